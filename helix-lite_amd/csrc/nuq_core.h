@@ -1,0 +1,96 @@
+// nuq_core.h -- per-thread nuq quantisation of 8 consecutive fp16 channels.
+//
+// Semantics (bit-exact with src/kvquant/triton_batched.py:53-82 / :204-232):
+//   outlier = v > upper || v < lower           (fp32 compare)
+//   code    = first argmin_l fl32(|v - pole_l|) (strict '<', ascending levels)
+// Fast path: decision-table binary search on packed fp16 lanes (2 elements per
+// VALU op).  Slow path (|v| beyond the table's safe range, NaN/inf, or a table
+// that failed the exactness criterion): the scan itself.
+#pragma once
+
+#include "hkv_common.h"
+
+struct SlowInfo {
+  const void* poles;
+  const void* upper;
+  const void* lower;
+  int pdt, tdt, L;
+};
+
+HKV_DEV SlowInfo slow_info(const hkv_nuq_scales& s) {
+  return SlowInfo{s.poles, s.upper, s.lower, s.poles_dtype, s.thr_dtype, s.levels};
+}
+
+HKV_DEV int64_t clamp_row(int64_t pos, int64_t rows) {
+  return pos > rows - 1 ? rows - 1 : (pos < 0 ? 0 : pos);
+}
+
+// Position of token t for per-token scales.
+HKV_DEV int64_t token_pos(const hkv_nuq_scales& s, int64_t t) {
+  return s.positions ? s.positions[t] : s.pos_offset + t;
+}
+
+// Exact scan of one element; returns code and sets *o to the outlier flag.
+HKV_DEV int slow_one(uint16_t xb, const SlowInfo& si, int64_t tab, int* o) {
+  float v = h2f(xb);
+  float up = load_scale(si.upper, si.tdt, tab), lo = load_scale(si.lower, si.tdt, tab);
+  *o = (v > up) || (v < lo);
+  return scan_code(v, si.poles, si.pdt, tab * si.L, si.L);
+}
+
+// Quantise 8 channels.  PT (per-token): S[0] holds the row's table broadcast;
+// otherwise S[j] holds the tables of channel pair j.  tab0: table index of
+// element 0 (per-channel: +e per element; per-token: shared).
+// code[j]: codes of elements 2j, 2j+1 in bits 0..3 / 16..19; om[j]: 0xffff lanes
+// for outliers.
+template <int NB, bool PT>
+HKV_DEV void quant8(const uint4 xv, const Search2<NB>* S, const SlowInfo& si, int64_t tab0,
+                    uint32_t code[4], uint32_t om[4]) {
+  const uint32_t x[4] = {xv.x, xv.y, xv.z, xv.w};
+  uint32_t uns = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) uns |= unsafe2<NB>(x[j], S[PT ? 0 : j]);
+  if (__builtin_expect(uns == 0, 1)) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      code[j] = search2<NB>(x[j], S[PT ? 0 : j]);
+      om[j] = outlier2<NB>(x[j], S[PT ? 0 : j]);
+    }
+  } else {
+#pragma unroll 1
+    for (int j = 0; j < 4; ++j) {
+      int o0, o1;
+      int c0 = slow_one((uint16_t)(x[j] & 0xffffu), si, PT ? tab0 : tab0 + 2 * j, &o0);
+      int c1 = slow_one((uint16_t)(x[j] >> 16), si, PT ? tab0 : tab0 + 2 * j + 1, &o1);
+      code[j] = (uint32_t)c0 | ((uint32_t)c1 << 16);
+      om[j] = (o0 ? 0xffffu : 0u) | (o1 ? 0xffff0000u : 0u);
+    }
+  }
+}
+
+// Two 16-bit lanes holding small values -> two bytes (lane0 -> byte0).
+HKV_DEV uint32_t lanes_to_bytes(uint32_t v) { return (v & 0xffu) | ((v >> 8) & 0xff00u); }
+
+// 8 codes (4 regs) -> 32 bits of nibbles, element e at bits 4e..4e+3.
+HKV_DEV uint32_t pack_nibbles(const uint32_t c[4]) {
+  uint32_t r = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) r |= ((c[j] & 0xfu) | ((c[j] >> 12) & 0xf0u)) << (8 * j);
+  return r;
+}
+
+// 8 codes -> 16 bits of crumbs, element e at bits 2e..2e+1.
+HKV_DEV uint32_t pack_crumbs(const uint32_t c[4]) {
+  uint32_t r = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) r |= ((c[j] & 0x3u) | ((c[j] >> 14) & 0xcu)) << (4 * j);
+  return r;
+}
+
+// 8 outlier lane masks -> 8-bit mask, element e at bit e.
+HKV_DEV uint32_t mask_bits(const uint32_t om[4]) {
+  uint32_t r = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) r |= ((om[j] & 1u) | ((om[j] >> 15) & 2u)) << (2 * j);
+  return r;
+}

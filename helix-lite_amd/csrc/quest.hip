@@ -1,0 +1,587 @@
+// quest.hip -- Quest page metadata, upper-bound scoring and top-K selection.
+//
+// Reference semantics: src/quest/reference.py:38-133 (stats, bound, top-K with
+// sinks), src/quest/triton_kernels.py:25-57 (fused bound, fp16 out),
+// src/kvquant/quest_selector.py:64-78 (selector path).
+//
+// Canonical bound evaluation (fixed so that the selected page sets are exact):
+// channels in chunks of 8, one lane per chunk; a lane sums its chunk left to
+// right (positive part sum_d clamp(q,0)*kmax and negative part
+// sum_d clamp(q,max=0)*kmin kept apart, products rounded before the add); the
+// chunk sums are combined by a xor-butterfly over the row's lanes (offsets
+// n/2 ... 1); bound = pos + neg, then + 0.0f so a zero bound is +0.
+#include "hkv_common.h"
+
+namespace {
+
+// --------------------------------------------------------------- a8: stats
+
+// Ordered fp16 keys on both lanes: x ^ ((x >> 15) & 0x7fff) (an involution).
+HKV_DEV uint32_t key2(uint32_t x) {
+  const uint32_t s = as_u32(as_s2(x) >> (s2_t){15, 15});
+  return x ^ (s & 0x7fff7fffu);
+}
+HKV_DEV uint32_t min2(uint32_t a, uint32_t b) {
+  s2_t x = as_s2(a), y = as_s2(b);
+  return as_u32((s2_t){x.x < y.x ? x.x : y.x, x.y < y.y ? x.y : y.y});
+}
+HKV_DEV uint32_t max2(uint32_t a, uint32_t b) {
+  s2_t x = as_s2(a), y = as_s2(b);
+  return as_u32((s2_t){x.x > y.x ? x.x : y.x, x.y > y.y ? x.y : y.y});
+}
+// 0xffff lanes where the fp16 value is NaN.
+HKV_DEV uint32_t nan2(uint32_t x) {
+  s2_t d = (s2_t){0x7c00, 0x7c00} - as_s2(x & 0x7fff7fffu);
+  return as_u32(d >> (s2_t){15, 15});
+}
+
+// fp16 (P,S,H,D), D % 8 == 0: one thread per 8 channels of one (page, head).
+__global__ void __launch_bounds__(256)
+page_stats_f16(const uint16_t* __restrict__ K, int64_t P, int S, int H, int D,
+               uint16_t* __restrict__ kmin, uint16_t* __restrict__ kmax) {
+  const int64_t HD8 = (int64_t)H * D / 8;
+  const int64_t n = P * HD8;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int64_t p = i / HD8, j = i - p * HD8;
+    const uint4* src = reinterpret_cast<const uint4*>(K + (p * S) * H * D) + j;
+    uint32_t mn[4], mx[4], nn[4] = {0, 0, 0, 0};
+    const uint4 v0 = src[0];
+    const uint32_t w0[4] = {v0.x, v0.y, v0.z, v0.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) { mn[q] = mx[q] = key2(w0[q]); nn[q] = nan2(w0[q]); }
+    for (int s = 1; s < S; ++s) {
+      const uint4 v = src[(int64_t)s * HD8];
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t k = key2(w[q]);
+        mn[q] = min2(mn[q], k);
+        mx[q] = max2(mx[q], k);
+        nn[q] |= nan2(w[q]);
+      }
+    }
+    uint32_t a[4], b[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      a[q] = bsel(nn[q], 0x7e007e00u, key2(mn[q]));
+      b[q] = bsel(nn[q], 0x7e007e00u, key2(mx[q]));
+    }
+    reinterpret_cast<uint4*>(kmin)[i] = make_uint4(a[0], a[1], a[2], a[3]);
+    reinterpret_cast<uint4*>(kmax)[i] = make_uint4(b[0], b[1], b[2], b[3]);
+  }
+}
+
+HKV_DEV int32_t fkey(float f) {
+  const int32_t b = __builtin_bit_cast(int32_t, f);
+  return b >= 0 ? b : (b ^ 0x7fffffff);
+}
+
+// Any dtype/D: one thread per (page, head, channel).
+template <typename T>
+__global__ void __launch_bounds__(256)
+page_stats_generic(const T* __restrict__ K, int64_t P, int S, int H, int D, T* __restrict__ kmin,
+                   T* __restrict__ kmax) {
+  const int64_t HD = (int64_t)H * D;
+  const int64_t n = P * HD;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int64_t p = i / HD, j = i - p * HD;
+    const T* src = K + p * S * HD + j;
+    float v = (float)src[0];
+    float mn = v, mx = v;
+    bool nan = __builtin_isnan(v);
+    for (int s = 1; s < S; ++s) {
+      v = (float)src[(int64_t)s * HD];
+      nan |= __builtin_isnan(v);
+      if (fkey(v) < fkey(mn)) mn = v;
+      if (fkey(v) > fkey(mx)) mx = v;
+    }
+    if (nan) mn = mx = __builtin_nanf("");
+    kmin[i] = (T)mn;
+    kmax[i] = (T)mx;
+  }
+}
+
+// --------------------------------------------------------------- a9: bound
+
+HKV_DEV float clamp_pos(float q) { return q < 0.0f ? 0.0f : q; }
+HKV_DEV float clamp_neg(float q) { return q > 0.0f ? 0.0f : q; }
+
+template <typename KT> HKV_DEV float kval(KT v);
+template <> HKV_DEV float kval<uint16_t>(uint16_t v) { return h2f(v); }
+template <> HKV_DEV float kval<float>(float v) { return v; }
+
+// Chunk c (8 channels) of one row: positive and negative partial sums.
+template <typename KT>
+HKV_DEV void chunk_sums(const KT* __restrict__ mn_row, const KT* __restrict__ mx_row, int D, int c,
+                        const float* qp, const float* qn, float& ps, float& ns) {
+  ps = 0.0f;
+  ns = 0.0f;
+  const int d0 = 8 * c;
+  if (d0 >= D) return;
+  KT a[8], b[8];
+  if (D % 8 == 0) {
+    if constexpr (sizeof(KT) == 2) {
+      *reinterpret_cast<uint4*>(a) = *reinterpret_cast<const uint4*>(mn_row + d0);
+      *reinterpret_cast<uint4*>(b) = *reinterpret_cast<const uint4*>(mx_row + d0);
+    } else {
+      reinterpret_cast<uint4*>(a)[0] = reinterpret_cast<const uint4*>(mn_row + d0)[0];
+      reinterpret_cast<uint4*>(a)[1] = reinterpret_cast<const uint4*>(mn_row + d0)[1];
+      reinterpret_cast<uint4*>(b)[0] = reinterpret_cast<const uint4*>(mx_row + d0)[0];
+      reinterpret_cast<uint4*>(b)[1] = reinterpret_cast<const uint4*>(mx_row + d0)[1];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      a[i] = d0 + i < D ? mn_row[d0 + i] : (KT)0;
+      b[i] = d0 + i < D ? mx_row[d0 + i] : (KT)0;
+    }
+  }
+  const int nd = D - d0 < 8 ? D - d0 : 8;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    if (i < nd) {
+      ps = __fadd_rn(ps, __fmul_rn(qp[i], kval<KT>(b[i])));
+      ns = __fadd_rn(ns, __fmul_rn(qn[i], kval<KT>(a[i])));
+    }
+  }
+}
+
+// Butterfly over n lanes (n | 64, lanes of a row contiguous and aligned).
+HKV_DEV float row_reduce(float v, int n) {
+  for (int off = n >> 1; off >= 1; off >>= 1) v = __fadd_rn(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+HKV_DEV int lanes_for(int D) {
+  int nch = (D + 7) / 8, n = 1;
+  while (n < nch) n <<= 1;
+  return n;
+}
+
+// q (Hq,D) -> per KV head clamp(q,0) / clamp(q,max=0) summed over its group in
+// ascending head order (group == 1: the clamps themselves).
+HKV_DEV void group_q(const void* q, int qdt, int g, int group, int D, int d, float& qp, float& qn) {
+  float a = 0.0f, b = 0.0f;
+  for (int j = 0; j < group; ++j) {
+    const float v = load_scale(q, qdt, (int64_t)(g * group + j) * D + d);
+    a = __fadd_rn(a, clamp_pos(v));
+    b = __fadd_rn(b, clamp_neg(v));
+  }
+  qp = a;
+  qn = b;
+}
+
+// Standalone bound: rows r = p*H + h; n lanes per row; q staged in LDS.
+template <typename KT>
+__global__ void __launch_bounds__(256)
+bound_kernel(const void* q, int qdt, int group, const KT* __restrict__ kmin,
+             const KT* __restrict__ kmax, int64_t P, int H, int D, void* out, int odt) {
+  extern __shared__ float qs[];  // [2][H][D]
+  for (int i = threadIdx.x; i < H * D; i += 256) {
+    float a, b;
+    group_q(q, qdt, i / D, group, D, i % D, a, b);
+    qs[i] = a;
+    qs[H * D + i] = b;
+  }
+  __syncthreads();
+  const int n = lanes_for(D);
+  const int rows_per_block = 256 / n;
+  const int c = threadIdx.x % n;
+  const int64_t nrows = P * H;
+  for (int64_t r0 = (int64_t)blockIdx.x * rows_per_block; r0 < nrows;
+       r0 += (int64_t)gridDim.x * rows_per_block) {
+    const int64_t r = r0 + threadIdx.x / n;
+    float ps = 0.0f, ns = 0.0f;
+    if (r < nrows) {
+      const int h = (int)(r % H);
+      float qp[8], qn[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int d = 8 * c + i;
+        qp[i] = d < D ? qs[h * D + d] : 0.0f;
+        qn[i] = d < D ? qs[H * D + h * D + d] : 0.0f;
+      }
+      chunk_sums<KT>(kmin + r * D, kmax + r * D, D, c, qp, qn, ps, ns);
+    }
+    ps = row_reduce(ps, n);
+    ns = row_reduce(ns, n);
+    if (r < nrows && c == 0) {
+      const float b = __fadd_rn(__fadd_rn(ps, ns), 0.0f);
+      if (odt == HKV_DT_F16) ((uint16_t*)out)[r] = f2h(b);
+      else ((float*)out)[r] = b;
+    }
+  }
+}
+
+// --------------------------------------------------------- a10: top-K
+
+constexpr int kSelThreads = 1024;
+constexpr int kSelWaves = kSelThreads / 64;
+constexpr int kBins = 2048;
+
+// Ordered key: NaN above +inf, -0 == +0.
+HKV_DEV uint32_t ukey(float f) {
+  if (__builtin_isnan(f)) return 0xffffffffu;
+  if (f == 0.0f) f = 0.0f;
+  const uint32_t b = __builtin_bit_cast(uint32_t, f);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+struct SelShared {
+  uint32_t hist[kBins];
+  uint32_t wred[kSelWaves][4];
+  uint32_t bcast[8];
+};
+
+// Block-wide (1024 threads) reductions through LDS.
+HKV_DEV uint32_t block_min_u32(uint32_t v, SelShared& sh) {
+  for (int o = 32; o >= 1; o >>= 1) { uint32_t y = __shfl_xor(v, o, 64); v = y < v ? y : v; }
+  const int w = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) sh.wred[w][0] = v;
+  __syncthreads();
+  uint32_t r = sh.wred[0][0];
+  for (int i = 1; i < kSelWaves; ++i) r = sh.wred[i][0] < r ? sh.wred[i][0] : r;
+  return r;
+}
+HKV_DEV uint32_t block_max_u32(uint32_t v, SelShared& sh) {
+  for (int o = 32; o >= 1; o >>= 1) { uint32_t y = __shfl_xor(v, o, 64); v = y > v ? y : v; }
+  const int w = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) sh.wred[w][1] = v;
+  __syncthreads();
+  uint32_t r = sh.wred[0][1];
+  for (int i = 1; i < kSelWaves; ++i) r = sh.wred[i][1] > r ? sh.wred[i][1] : r;
+  return r;
+}
+
+// Key of candidate i (i in [0, n)) of the column; column element p = s + i.
+struct ColumnF32 {
+  const float* base;
+  int64_t stride;
+  HKV_DEV uint32_t key(int64_t p) const { return ukey(base[p * stride]); }
+};
+struct ColumnF16 {
+  const uint16_t* base;
+  int64_t stride;
+  HKV_DEV uint32_t key(int64_t p) const { return ukey(h2f(base[p * stride])); }
+};
+
+// Select, for one column of P scores, the sinks plus the k_eff highest non-sink
+// pages (ties to the lower page), ascending, into out[i*ostride].  Candidate
+// pages [s, P) are split into 16 contiguous wave chunks walked in rounds of 64
+// consecutive pages (coalesced); ordering within a chunk comes from ballots.
+template <typename Col>
+HKV_DEV void select_column(const Col& col, int64_t P, int64_t s, int64_t keff, int64_t* out,
+                           int64_t ostride, SelShared& sh) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  for (int64_t i = tid; i < s; i += kSelThreads) out[i * ostride] = i;
+  if (keff <= 0) return;
+  const int64_t n = P - s;
+  const int64_t chunk = ((n + kSelWaves - 1) / kSelWaves + 63) / 64 * 64;
+  const int64_t c0 = s + (int64_t)w * chunk;
+  const int64_t c1 = (c0 + chunk < P) ? c0 + chunk : P;
+
+  // 1. key range
+  uint32_t kmn = 0xffffffffu, kmx = 0;
+  for (int64_t p = c0 + lane; p < c1; p += 64) {
+    const uint32_t k = col.key(p);
+    kmn = k < kmn ? k : kmn;
+    kmx = k > kmx ? k : kmx;
+  }
+  kmn = block_min_u32(kmn, sh);
+  kmx = block_max_u32(kmx, sh);
+
+  // 2. radix select of the keff-th largest key T, digits of <= 11 bits
+  //    starting at the highest bit where the keys differ.
+  uint32_t prefix = kmx, pmask = 0xffffffffu;  // keys matching prefix under pmask
+  uint32_t krem = (uint32_t)keff, gt = 0;
+  if (kmn != kmx) {
+    int hb = 31 - __builtin_clz(kmn ^ kmx);
+    pmask = hb == 31 ? 0u : ~((2u << hb) - 1u);
+    prefix = kmx & pmask;
+    while (true) {
+      const int lo = hb >= 10 ? hb - 10 : 0;
+      const uint32_t nb = 1u << (hb - lo + 1);
+      for (int i = tid; i < (int)nb; i += kSelThreads) sh.hist[i] = 0;
+      if (tid == 0) { sh.bcast[0] = 0; sh.bcast[1] = 0; }
+      __syncthreads();
+      for (int64_t p = c0 + lane; p < c1; p += 64) {
+        const uint32_t k = col.key(p);
+        if ((k & pmask) == prefix) atomicAdd(&sh.hist[(k >> lo) & (nb - 1)], 1u);
+      }
+      __syncthreads();
+      // find bin b (from the top) where the running count reaches krem:
+      // thread t owns bins 2t, 2t+1; suffix sums by a reversed block scan.
+      {
+        const uint32_t h0 = 2 * tid < (int)nb ? sh.hist[2 * tid] : 0u;
+        const uint32_t h1 = 2 * tid + 1 < (int)nb ? sh.hist[2 * tid + 1] : 0u;
+        const uint32_t loc = h0 + h1;
+        uint32_t inc = loc;  // inclusive suffix within the wave
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+          const uint32_t y = __shfl_down(inc, o, 64);
+          if (lane + o < 64) inc += y;
+        }
+        if (lane == 0) sh.wred[w][0] = inc;
+        __syncthreads();
+        uint32_t later = 0;
+        for (int i = w + 1; i < kSelWaves; ++i) later += sh.wred[i][0];
+        const uint32_t sfx = later + inc - loc;  // count in bins above 2t+1
+        if (sfx < krem && krem <= sfx + loc) {
+          if (sfx + h1 >= krem) { sh.bcast[0] = 2 * tid + 1; sh.bcast[1] = sfx; }
+          else { sh.bcast[0] = 2 * tid; sh.bcast[1] = sfx + h1; }
+        }
+        __syncthreads();
+      }
+      const uint32_t b = sh.bcast[0], above = sh.bcast[1];
+      gt += above;
+      krem -= above;
+      prefix |= b << lo;
+      pmask |= (nb - 1) << lo;
+      if (lo == 0) break;
+      hb = lo - 1;
+      __syncthreads();
+    }
+  }
+  const uint32_t T = prefix;
+  const uint32_t need_eq = krem;  // keys == T to take, lowest pages first
+
+  // 3. per-wave counts of > T and == T, then wave offsets
+  uint32_t cgt = 0, ceq = 0;
+  for (int64_t p = c0 + lane; p < c1; p += 64) {
+    const uint32_t k = col.key(p);
+    cgt += k > T;
+    ceq += k == T;
+  }
+  for (int o = 32; o >= 1; o >>= 1) {
+    cgt += __shfl_xor(cgt, o, 64);
+    ceq += __shfl_xor(ceq, o, 64);
+  }
+  __syncthreads();
+  if (lane == 0) { sh.wred[w][2] = cgt; sh.wred[w][3] = ceq; }
+  __syncthreads();
+  uint32_t eq_before = 0, out_before = 0;
+  for (int i = 0; i < w; ++i) {
+    const uint32_t e = sh.wred[i][3];
+    const uint32_t take = eq_before >= need_eq ? 0u : (need_eq - eq_before < e ? need_eq - eq_before : e);
+    out_before += sh.wred[i][2] + take;
+    eq_before += e;
+  }
+  (void)gt;
+
+  // 4. ordered write within the chunk
+  uint32_t run_out = 0, run_eq = 0;
+  const uint64_t lanemask_lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  for (int64_t p0 = c0; p0 < c1; p0 += 64) {
+    const int64_t p = p0 + lane;
+    const uint32_t k = p < c1 ? col.key(p) : 0u;
+    const bool is_eq = p < c1 && k == T;
+    const uint64_t eqm = __ballot(is_eq);
+    const uint32_t eq_rank = eq_before + run_eq + __builtin_popcountll(eqm & lanemask_lt);
+    const bool sel = p < c1 && (k > T || (is_eq && eq_rank < need_eq));
+    const uint64_t selm = __ballot(sel);
+    if (sel) {
+      const uint32_t pos = out_before + run_out + __builtin_popcountll(selm & lanemask_lt);
+      if (pos < (uint64_t)keff) out[(s + (int64_t)pos) * ostride] = p;
+    }
+    run_out += __builtin_popcountll(selm);
+    run_eq += __builtin_popcountll(eqm);
+  }
+}
+
+template <typename Col>
+__global__ void __launch_bounds__(kSelThreads)
+topk_kernel(Col col0, int64_t P, int H, int64_t s, int64_t keff, int64_t* out) {
+  __shared__ SelShared sh;
+  const int h = blockIdx.x;
+  Col col = col0;
+  col.base += h;
+  select_column(col, P, s, keff, out + h, H, sh);
+}
+
+// ----------------------------------------------- fused score + select (cfg3)
+
+struct SelectWs {
+  uint32_t done[64];  // per-head block completion counters
+};
+
+// grid (page blocks, H); 1024 threads; rows are pages of head h.  Scores go to
+// scores[h*P + p] (head-major).  The last block of head h selects for head h.
+template <typename KT>
+__global__ void __launch_bounds__(kSelThreads)
+select_fused_kernel(const void* q, int qdt, int group, const KT* __restrict__ kmin,
+                    const KT* __restrict__ kmax, int64_t P, int H, int D, int64_t pages_per_block,
+                    float* __restrict__ scores, int64_t s, int64_t keff, int64_t* out,
+                    SelectWs* ws) {
+  __shared__ SelShared sh;
+  __shared__ uint32_t s_last;
+  const int h = blockIdx.y;
+  const int n = lanes_for(D);
+  const int c = threadIdx.x % n;
+  const int rows = kSelThreads / n;
+  float qp[8], qn[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int d = 8 * c + i;
+    if (d < D) group_q(q, qdt, h, group, D, d, qp[i], qn[i]);
+    else { qp[i] = 0.0f; qn[i] = 0.0f; }
+  }
+  const int64_t pb0 = (int64_t)blockIdx.x * pages_per_block;
+  const int64_t pb1 = pb0 + pages_per_block < P ? pb0 + pages_per_block : P;
+  for (int64_t p0 = pb0; p0 < pb1; p0 += rows) {
+    const int64_t p = p0 + threadIdx.x / n;
+    float ps = 0.0f, ns = 0.0f;
+    if (p < pb1) {
+      const int64_t row = p * H + h;
+      chunk_sums<KT>(kmin + row * D, kmax + row * D, D, c, qp, qn, ps, ns);
+    }
+    ps = row_reduce(ps, n);
+    ns = row_reduce(ns, n);
+    if (p < pb1 && c == 0) scores[(int64_t)h * P + p] = __fadd_rn(__fadd_rn(ps, ns), 0.0f);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t prev = atomicAdd(&ws->done[h], 1u);
+    s_last = prev == gridDim.x - 1;
+    if (s_last) ws->done[h] = 0;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  ColumnF32 col{scores + (int64_t)h * P, 1};
+  select_column(col, P, s, keff, out + h, H, sh);
+}
+
+int num_cus() {
+  static int n = 0;
+  if (!n) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+  }
+  return n;
+}
+
+bool fdt(int dt) { return dt == HKV_DT_F16 || dt == HKV_DT_F32; }
+
+}  // namespace
+
+extern "C" int hkv_quest_page_stats(const void* k_pages, int dtype, int64_t P, int S, int H, int D,
+                                    void* kmin, void* kmax, void* stream) {
+  if (!fdt(dtype)) return HKV_ERR_DTYPE;
+  if (P < 0 || S < 1 || H < 1 || D < 1) return HKV_ERR_SHAPE;
+  if (P == 0) return HKV_OK;
+  if (!k_pages || !kmin || !kmax) return HKV_ERR_ARG;
+  hipStream_t s = (hipStream_t)stream;
+  const bool vec = dtype == HKV_DT_F16 && D % 8 == 0 && !((uintptr_t)k_pages & 15u) &&
+                   !((uintptr_t)kmin & 15u) && !((uintptr_t)kmax & 15u);
+  const int64_t n = vec ? P * H * D / 8 : P * H * D;
+  const unsigned grid = (unsigned)std::min<int64_t>((n + 255) / 256, (int64_t)num_cus() * 16);
+  if (vec)
+    hipLaunchKernelGGL(page_stats_f16, dim3(grid), dim3(256), 0, s, (const uint16_t*)k_pages, P, S,
+                       H, D, (uint16_t*)kmin, (uint16_t*)kmax);
+  else if (dtype == HKV_DT_F16)
+    hipLaunchKernelGGL(page_stats_generic<_Float16>, dim3(grid), dim3(256), 0, s,
+                       (const _Float16*)k_pages, P, S, H, D, (_Float16*)kmin, (_Float16*)kmax);
+  else
+    hipLaunchKernelGGL(page_stats_generic<float>, dim3(grid), dim3(256), 0, s,
+                       (const float*)k_pages, P, S, H, D, (float*)kmin, (float*)kmax);
+  HKV_CHECK_LAUNCH();
+  return HKV_OK;
+}
+
+extern "C" int hkv_quest_page_bound(const void* q, int q_dtype, int Hq, const void* kmin,
+                                    const void* kmax, int k_dtype, int64_t P, int H, int D,
+                                    void* out, int out_dtype, void* stream) {
+  if (!fdt(q_dtype) && q_dtype != HKV_DT_BF16) return HKV_ERR_DTYPE;
+  if (!fdt(k_dtype) || !fdt(out_dtype)) return HKV_ERR_DTYPE;
+  if (P < 0 || H < 1 || D < 1 || D > 512 || Hq < H || Hq % H) return HKV_ERR_SHAPE;
+  if (P == 0) return HKV_OK;
+  if (!q || !kmin || !kmax || !out) return HKV_ERR_ARG;
+  const int esz = k_dtype == HKV_DT_F16 ? 2 : 4;
+  if (D % 8 == 0 && (((uintptr_t)kmin | (uintptr_t)kmax) & 15u)) return HKV_ERR_ARG;
+  (void)esz;
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t rows = P * H;
+  int n = 1;
+  while (n < (D + 7) / 8) n <<= 1;
+  const int rpb = 256 / n;
+  const unsigned grid = (unsigned)std::min<int64_t>((rows + rpb - 1) / rpb, (int64_t)num_cus() * 8);
+  const size_t lds = sizeof(float) * 2 * H * D;
+  if (lds > 64 * 1024) return HKV_ERR_SHAPE;
+  if (k_dtype == HKV_DT_F16)
+    hipLaunchKernelGGL(bound_kernel<uint16_t>, dim3(grid), dim3(256), lds, s, q, q_dtype, Hq / H,
+                       (const uint16_t*)kmin, (const uint16_t*)kmax, P, H, D, out, out_dtype);
+  else
+    hipLaunchKernelGGL(bound_kernel<float>, dim3(grid), dim3(256), lds, s, q, q_dtype, Hq / H,
+                       (const float*)kmin, (const float*)kmax, P, H, D, out, out_dtype);
+  HKV_CHECK_LAUNCH();
+  return HKV_OK;
+}
+
+extern "C" size_t hkv_quest_topk_workspace_bytes(int64_t P, int H) {
+  (void)P;
+  (void)H;
+  return sizeof(SelectWs);
+}
+
+extern "C" int hkv_quest_topk(const void* bound, int b_dtype, int64_t P, int H, int64_t k,
+                              int64_t sink_pages, int64_t* out, int64_t* n_out, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  if (!fdt(b_dtype)) return HKV_ERR_DTYPE;
+  if (P < 0 || H < 1) return HKV_ERR_SHAPE;
+  const int64_t s = sink_pages < 0 ? 0 : (sink_pages > P ? P : sink_pages);
+  const int64_t keff = k < 0 ? 0 : (k > P - s ? P - s : k);
+  if (n_out) *n_out = s + keff;
+  if (s + keff == 0) return HKV_OK;
+  if (!bound || !out) return HKV_ERR_ARG;
+  (void)workspace;
+  (void)workspace_bytes;
+  hipStream_t st = (hipStream_t)stream;
+  if (b_dtype == HKV_DT_F32)
+    hipLaunchKernelGGL(topk_kernel<ColumnF32>, dim3(H), dim3(kSelThreads), 0, st,
+                       ColumnF32{(const float*)bound, H}, P, H, s, keff, out);
+  else
+    hipLaunchKernelGGL(topk_kernel<ColumnF16>, dim3(H), dim3(kSelThreads), 0, st,
+                       ColumnF16{(const uint16_t*)bound, H}, P, H, s, keff, out);
+  HKV_CHECK_LAUNCH();
+  return HKV_OK;
+}
+
+extern "C" int hkv_quest_select(const void* q, int q_dtype, int Hq, const void* kmin,
+                                const void* kmax, int k_dtype, int64_t P, int H, int D, int64_t k,
+                                int64_t sink_pages, float* scores, int64_t* out, int64_t* n_out,
+                                void* workspace, size_t workspace_bytes, void* stream) {
+  if (!fdt(q_dtype) && q_dtype != HKV_DT_BF16) return HKV_ERR_DTYPE;
+  if (!fdt(k_dtype)) return HKV_ERR_DTYPE;
+  if (P < 0 || H < 1 || H > 64 || D < 1 || D > 512 || Hq < H || Hq % H) return HKV_ERR_SHAPE;
+  const int64_t s = sink_pages < 0 ? 0 : (sink_pages > P ? P : sink_pages);
+  const int64_t keff = k < 0 ? 0 : (k > P - s ? P - s : k);
+  if (n_out) *n_out = s + keff;
+  if (P == 0) return HKV_OK;
+  if (!q || !kmin || !kmax || !scores || !out) return HKV_ERR_ARG;
+  if (!workspace || workspace_bytes < sizeof(SelectWs)) return HKV_ERR_WORKSPACE;
+  if (D % 8 == 0 && (((uintptr_t)kmin | (uintptr_t)kmax) & 15u)) return HKV_ERR_ARG;
+  hipStream_t st = (hipStream_t)stream;
+  int n = 1;
+  while (n < (D + 7) / 8) n <<= 1;
+  const int64_t rows = kSelThreads / n;
+  // enough blocks to fill the chip, each a multiple of the block's row count
+  int64_t target = std::max<int64_t>(1, (int64_t)num_cus() * 2 / H);
+  int64_t ppb = (P + target - 1) / target;
+  ppb = std::max<int64_t>(rows, (ppb + rows - 1) / rows * rows);
+  const unsigned gx = (unsigned)((P + ppb - 1) / ppb);
+  if (k_dtype == HKV_DT_F16)
+    hipLaunchKernelGGL(select_fused_kernel<uint16_t>, dim3(gx, H), dim3(kSelThreads), 0, st, q,
+                       q_dtype, Hq / H, (const uint16_t*)kmin, (const uint16_t*)kmax, P, H, D, ppb,
+                       scores, s, keff, out, (SelectWs*)workspace);
+  else
+    hipLaunchKernelGGL(select_fused_kernel<float>, dim3(gx, H), dim3(kSelThreads), 0, st, q,
+                       q_dtype, Hq / H, (const float*)kmin, (const float*)kmax, P, H, D, ppb,
+                       scores, s, keff, out, (SelectWs*)workspace);
+  HKV_CHECK_LAUNCH();
+  return HKV_OK;
+}

@@ -1,0 +1,367 @@
+"""Tensor-level wrappers over the helix_kv C ABI.
+
+Every function validates shapes/dtypes on the host (raising the exception types
+the reference raises for the same misuse), allocates outputs with
+``torch.empty`` like the reference wrappers do, and launches on torch's current
+stream.  Nothing here computes on the CPU.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import _native as N
+
+
+# ------------------------------------------------------------ decision tables
+
+def build_tables(poles: torch.Tensor, upper: torch.Tensor, lower: torch.Tensor) -> torch.Tensor:
+    """Decision tables for poles (..., L) and thresholds (...) -> uint8 (n, 80)."""
+    N.require_gpu(poles, upper, lower)
+    L = int(poles.shape[-1])
+    n = poles.numel() // max(L, 1)
+    if upper.numel() != n or lower.numel() != n:
+        raise AssertionError("thresholds must have one entry per pole row")
+    p = poles.contiguous()
+    up = upper.contiguous()
+    lo = lower.contiguous()
+    out = torch.empty((n, N.TABLE_BYTES), dtype=torch.uint8, device=poles.device)
+    st = N.lib().hkv_nuq_build_tables(N.ptr(p), N.dtype_code(p), N.ptr(up), N.ptr(lo),
+                                      N.dtype_code(up), n, L, N.ptr(out), N.stream_of(p))
+    N.check(st, "hkv_nuq_build_tables", AssertionError)
+    return out
+
+
+@dataclass
+class NuqLayerTables:
+    """One layer's K (per-channel) or V (per-token) scales on the device, with
+    their decision tables.
+
+    per-channel: poles (H,D,L), thresholds (H,D)  (src/kvquant/scales.py:13-39)
+    per-token:   poles (H,rows,L), thresholds (H,rows)  (src/kvquant/scales.py:42-69)
+    """
+
+    poles: torch.Tensor
+    upper: torch.Tensor
+    lower: torch.Tensor
+    per_token: bool
+    tables: torch.Tensor | None = None
+
+    def __post_init__(self) -> None:
+        N.require_gpu(self.poles, self.upper, self.lower)
+        if self.poles.dim() != 3:
+            raise AssertionError(f"poles must be 3-D, got {tuple(self.poles.shape)}")
+        if tuple(self.upper.shape) != tuple(self.poles.shape[:2]) or \
+                tuple(self.lower.shape) != tuple(self.poles.shape[:2]):
+            raise AssertionError("thresholds must match poles[..., 0]")
+        self.poles = self.poles.contiguous()
+        self.upper = self.upper.contiguous()
+        self.lower = self.lower.contiguous()
+        if self.upper.dtype != self.lower.dtype:
+            self.lower = self.lower.to(self.upper.dtype)
+
+    @property
+    def levels(self) -> int:
+        return int(self.poles.shape[-1])
+
+    @property
+    def rows(self) -> int:
+        return int(self.poles.shape[1]) if self.per_token else 0
+
+    def ensure_tables(self) -> torch.Tensor:
+        if self.tables is None:
+            self.tables = build_tables(self.poles, self.upper, self.lower)
+        return self.tables
+
+    def struct(self, positions: torch.Tensor | None = None, pos_offset: int = 0,
+               with_tables: bool = True) -> N.NuqScales:
+        s = N.NuqScales()
+        s.tables = self.ensure_tables().data_ptr() if with_tables else None
+        s.poles = self.poles.data_ptr()
+        s.upper = self.upper.data_ptr()
+        s.lower = self.lower.data_ptr()
+        s.poles_dtype = N.dtype_code(self.poles)
+        s.thr_dtype = N.dtype_code(self.upper)
+        s.levels = self.levels
+        s.per_token = 1 if self.per_token else 0
+        s.rows = self.rows
+        s.positions = positions.data_ptr() if positions is not None else None
+        s.pos_offset = int(pos_offset)
+        return s
+
+
+def _positions(positions, T: int, device) -> torch.Tensor | None:
+    if positions is None:
+        return None
+    p = positions.to(device=device, dtype=torch.int64).contiguous()
+    if p.numel() != T:
+        raise AssertionError(f"positions must have {T} entries, got {p.numel()}")
+    return p
+
+
+def _check_values(values: torch.Tensor, H: int, D: int) -> None:
+    N.require_gpu(values)
+    assert values.dtype == torch.float16, "values must be fp16"
+    assert values.is_contiguous(), "values must be contiguous (T, H, D)"
+    if values.dim() != 3 or values.shape[1] != H or values.shape[2] != D:
+        raise AssertionError(f"values shape {tuple(values.shape)} does not match scales (H={H}, D={D})")
+
+
+def _HD(t: NuqLayerTables, values: torch.Tensor) -> tuple[int, int]:
+    H = int(t.poles.shape[0])
+    D = int(values.shape[-1]) if t.per_token else int(t.poles.shape[1])
+    return H, D
+
+
+# ---------------------------------------------------------------- dense (a3/a6)
+
+def nuq_pack_dense(values: torch.Tensor, t: NuqLayerTables, positions=None, pos_offset: int = 0):
+    """(T,H,D) fp16 -> (codes u8, outlier_v fp16, outlier_m u8), the reference format."""
+    H, D = _HD(t, values)
+    _check_values(values, H, D)
+    T = int(values.shape[0])
+    pos = _positions(positions, T, values.device)
+    codes = torch.empty((T, H, D), dtype=torch.uint8, device=values.device)
+    outv = torch.empty((T, H, D), dtype=torch.float16, device=values.device)
+    outm = torch.empty((T, H, D), dtype=torch.uint8, device=values.device)
+    if T == 0:
+        return codes, outv, outm
+    s = t.struct(pos, pos_offset)
+    st = N.lib().hkv_nuq_pack_dense(N.ptr(values), T, H, D, s, N.ptr(codes), N.ptr(outv),
+                                    N.ptr(outm), N.stream_of(values))
+    N.check(st, "hkv_nuq_pack_dense", AssertionError)
+    return codes, outv, outm
+
+
+def nuq_unpack_dense(codes: torch.Tensor, outlier_v: torch.Tensor, outlier_m: torch.Tensor,
+                     t: NuqLayerTables, positions=None, pos_offset: int = 0) -> torch.Tensor:
+    N.require_gpu(codes, outlier_v, outlier_m)
+    assert codes.dtype == torch.uint8, "codes must be uint8"
+    assert codes.is_contiguous(), "codes must be contiguous"
+    T, H, D = (int(x) for x in codes.shape)
+    ov = outlier_v.to(torch.float16).contiguous()
+    om = outlier_m.to(torch.uint8).contiguous()
+    if ov.shape != codes.shape or om.shape != codes.shape:
+        raise AssertionError("codes / outlier_v / outlier_m shapes differ")
+    pos = _positions(positions, T, codes.device)
+    out = torch.empty((T, H, D), dtype=torch.float16, device=codes.device)
+    if T == 0:
+        return out
+    s = t.struct(pos, pos_offset, with_tables=False)
+    st = N.lib().hkv_nuq_unpack_dense(N.ptr(codes), N.ptr(ov), N.ptr(om), T, H, D, s, N.ptr(out),
+                                      N.stream_of(codes))
+    N.check(st, "hkv_nuq_unpack_dense", AssertionError)
+    return out
+
+
+# ----------------------------------------------------------- compact (a5/a6)
+
+@dataclass
+class CompactCodes:
+    """Bit-packed codes + CSR outliers of one (T,H,D) tensor.
+
+    packed (T,H,D*bits/8) u8; row_ptr (T*H+1) int32 over rows t*H+h;
+    col (>= nnz) u8; val (>= nnz) fp16.  ``nnz`` is None until read.
+    """
+
+    packed: torch.Tensor
+    row_ptr: torch.Tensor
+    col: torch.Tensor
+    val: torch.Tensor
+    bits: int
+    nnz: int | None = None
+
+    @property
+    def shape(self) -> tuple[int, int, int]:
+        T, H, B = self.packed.shape
+        return int(T), int(H), int(B) * 8 // self.bits
+
+    @staticmethod
+    def empty(T: int, H: int, D: int, bits: int, capacity: int, device) -> "CompactCodes":
+        return CompactCodes(
+            packed=torch.empty((T, H, D * bits // 8), dtype=torch.uint8, device=device),
+            row_ptr=torch.empty((T * H + 1,), dtype=torch.int32, device=device),
+            col=torch.empty((max(capacity, 1),), dtype=torch.uint8, device=device),
+            val=torch.empty((max(capacity, 1),), dtype=torch.float16, device=device),
+            bits=bits)
+
+    def read_nnz(self) -> int:
+        self.nnz = int(self.row_ptr[-1].item())
+        return self.nnz
+
+
+def pack_workspace(T: int, H: int, D: int, device) -> torch.Tensor:
+    nb = int(N.lib().hkv_nuq_pack_compact_workspace_bytes(T, H, D))
+    return N.workspace("nuq_pack", nb, device)
+
+
+def nuq_pack_compact(values: torch.Tensor, t: NuqLayerTables, bits: int, *,
+                     capacity: int | None = None, positions=None, pos_offset: int = 0,
+                     out: CompactCodes | None = None, sync: bool = True) -> CompactCodes:
+    """(T,H,D) fp16 -> CompactCodes.  With sync=True the true nnz is read back and
+    the call is re-issued with a larger capacity if needed (the returned col/val
+    are trimmed to nnz).  With sync=False nothing is read back."""
+    H, D = _HD(t, values)
+    _check_values(values, H, D)
+    if bits not in (2, 4):
+        raise AssertionError("bits must be 2 or 4")
+    if t.levels > (1 << bits):
+        raise AssertionError(f"{t.levels} levels do not fit in {bits} bits")
+    T = int(values.shape[0])
+    if capacity is None:
+        capacity = max(1024, (T * H * D) // 8)
+    if out is None:
+        out = CompactCodes.empty(T, H, D, bits, capacity, values.device)
+    pos = _positions(positions, T, values.device)
+    ws = pack_workspace(T, H, D, values.device)
+    s = t.struct(pos, pos_offset)
+
+    def launch(cc: CompactCodes) -> None:
+        st = N.lib().hkv_nuq_pack_compact(
+            N.ptr(values), T, H, D, bits, s, N.ptr(cc.packed), N.ptr(cc.row_ptr), N.ptr(cc.col),
+            N.ptr(cc.val), int(cc.col.numel()), N.ptr(ws), ws.numel(), N.stream_of(values))
+        N.check(st, "hkv_nuq_pack_compact", AssertionError)
+
+    launch(out)
+    if not sync:
+        return out
+    nnz = out.read_nnz()
+    if nnz > out.col.numel():
+        bigger = CompactCodes.empty(T, H, D, bits, nnz, values.device)
+        launch(bigger)
+        bigger.read_nnz()
+        out = bigger
+    err = N.lib().hkv_nuq_pack_compact_status(N.ptr(ws), N.stream_of(values))
+    if err:
+        raise RuntimeError(f"hkv_nuq_pack_compact: device reported error word {err}")
+    out.col = out.col[: out.nnz]
+    out.val = out.val[: out.nnz]
+    return out
+
+
+def nuq_unpack_compact(cc: CompactCodes, t: NuqLayerTables, *, positions=None, pos_offset: int = 0,
+                       out: torch.Tensor | None = None) -> torch.Tensor:
+    N.require_gpu(cc.packed, cc.row_ptr)
+    T, H, D = cc.shape
+    if out is None:
+        out = torch.empty((T, H, D), dtype=torch.float16, device=cc.packed.device)
+    if T == 0:
+        return out
+    pos = _positions(positions, T, cc.packed.device)
+    s = t.struct(pos, pos_offset)
+    st = N.lib().hkv_nuq_unpack_compact(
+        N.ptr(cc.packed), N.ptr(cc.row_ptr), N.ptr(cc.col), N.ptr(cc.val), T, H, D, cc.bits, s,
+        N.ptr(out), N.stream_of(out))
+    N.check(st, "hkv_nuq_unpack_compact", AssertionError)
+    return out
+
+
+# ------------------------------------------------------------------ Quest
+
+def _fdt(t: torch.Tensor) -> int:
+    if t.dtype not in (torch.float16, torch.float32):
+        raise TypeError(f"unsupported dtype {t.dtype}")
+    return N.dtype_code(t)
+
+
+def quest_page_stats(K_pages: torch.Tensor):
+    """(P,S,H,D) -> (K_min, K_max) (P,H,D), same dtype.  src/quest/reference.py:38-56."""
+    if K_pages.dim() != 4:
+        raise ValueError(f"expected (P, page, H, D), got {tuple(K_pages.shape)}")
+    N.require_gpu(K_pages)
+    K = K_pages.contiguous()
+    P, S, H, D = (int(x) for x in K.shape)
+    kmin = torch.empty((P, H, D), dtype=K.dtype, device=K.device)
+    kmax = torch.empty((P, H, D), dtype=K.dtype, device=K.device)
+    if P == 0:
+        return kmin, kmax
+    if S == 0:
+        raise ValueError("pages must hold at least one slot")
+    st = N.lib().hkv_quest_page_stats(N.ptr(K), _fdt(K), P, S, H, D, N.ptr(kmin), N.ptr(kmax),
+                                      N.stream_of(K))
+    N.check(st, "hkv_quest_page_stats", ValueError)
+    return kmin, kmax
+
+
+def quest_page_bound(query: torch.Tensor, K_min: torch.Tensor, K_max: torch.Tensor,
+                     out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """(Hq,D) query, (P,H,D) stats -> (P,H) bound (canonical fp32 order).
+
+    Hq == H: src/quest/reference.py:59-93; Hq = g*H: the group's bounds summed.
+    """
+    if query.dim() != 2:
+        raise ValueError(f"query should be (H, D), got {tuple(query.shape)}")
+    if K_min.shape != K_max.shape or K_min.dim() != 3:
+        raise ValueError(
+            f"K_min/K_max should be (P, H, D), got {tuple(K_min.shape)} and {tuple(K_max.shape)}")
+    N.require_gpu(query, K_min, K_max)
+    P, H, D = (int(x) for x in K_min.shape)
+    Hq = int(query.shape[0])
+    if int(query.shape[1]) != D or Hq % H != 0:
+        raise ValueError(f"query {tuple(query.shape)} incompatible with stats {tuple(K_min.shape)}")
+    kmin = K_min.contiguous()
+    kmax = K_max.to(kmin.dtype).contiguous()
+    q = query.contiguous()
+    out = torch.empty((P, H), dtype=out_dtype, device=kmin.device)
+    if P == 0:
+        return out
+    st = N.lib().hkv_quest_page_bound(N.ptr(q), N.dtype_code(q), Hq, N.ptr(kmin), N.ptr(kmax),
+                                      _fdt(kmin), P, H, D, N.ptr(out), N.dtype_code(out),
+                                      N.stream_of(q))
+    N.check(st, "hkv_quest_page_bound", ValueError)
+    return out
+
+
+def quest_topk(bound: torch.Tensor, k: int, sink_pages: int = 1) -> torch.Tensor:
+    """(P,H) bound -> (sinks + k_eff, H) int64 (src/quest/reference.py:96-133)."""
+    if bound.dim() != 2:
+        raise ValueError(f"bound should be (P, H), got {tuple(bound.shape)}")
+    N.require_gpu(bound)
+    b = bound if bound.dtype in (torch.float16, torch.float32) else bound.float()
+    b = b.contiguous()
+    P, H = (int(x) for x in b.shape)
+    s = max(0, min(int(sink_pages), P))
+    keff = max(0, min(int(k), P - s))
+    out = torch.empty((s + keff, H), dtype=torch.int64, device=b.device)
+    if s + keff == 0:
+        return out
+    ws = N.workspace("quest_topk", int(N.lib().hkv_quest_topk_workspace_bytes(P, H)), b.device)
+    n_out = N._i64(0)
+    st = N.lib().hkv_quest_topk(N.ptr(b), N.dtype_code(b), P, H, int(k), int(sink_pages), N.ptr(out),
+                                n_out, N.ptr(ws), ws.numel(), N.stream_of(b))
+    N.check(st, "hkv_quest_topk", ValueError)
+    return out
+
+
+def quest_select(query: torch.Tensor, K_min: torch.Tensor, K_max: torch.Tensor, k: int,
+                 sink_pages: int, *, scores: torch.Tensor | None = None,
+                 out: torch.Tensor | None = None):
+    """Fused bound + top-K for one decode step.
+
+    query (Hq,D) with Hq a multiple of H; stats (P,H,D) fp16/fp32.  Returns
+    (indices (sinks + k_eff, H) int64, scores (H,P) fp32 head-major).
+    """
+    N.require_gpu(query, K_min, K_max)
+    if K_min.dim() != 3 or K_min.shape != K_max.shape:
+        raise ValueError("K_min/K_max should be (P, H, D)")
+    P, H, D = (int(x) for x in K_min.shape)
+    Hq = int(query.shape[0])
+    if query.dim() != 2 or int(query.shape[1]) != D or Hq % H:
+        raise ValueError(f"query {tuple(query.shape)} incompatible with stats {tuple(K_min.shape)}")
+    kmin = K_min.contiguous()
+    kmax = K_max.to(kmin.dtype).contiguous()
+    q = query.contiguous()
+    s = max(0, min(int(sink_pages), P))
+    keff = max(0, min(int(k), P - s))
+    if out is None:
+        out = torch.empty((s + keff, H), dtype=torch.int64, device=kmin.device)
+    if scores is None:
+        scores = torch.empty((H, P), dtype=torch.float32, device=kmin.device)
+    ws = N.workspace("quest_select", 256, kmin.device)
+    n_out = N._i64(0)
+    st = N.lib().hkv_quest_select(N.ptr(q), N.dtype_code(q), Hq, N.ptr(kmin), N.ptr(kmax),
+                                  _fdt(kmin), P, H, D, int(k), int(sink_pages), N.ptr(scores),
+                                  N.ptr(out), n_out, N.ptr(ws), ws.numel(), N.stream_of(q))
+    N.check(st, "hkv_quest_select", ValueError)
+    return out, scores

@@ -1,0 +1,224 @@
+/*
+ * helix_kv.h -- C ABI of the MI355X (gfx950) KV-cache hot-path library
+ * (libhelix_kv.so).
+ *
+ * Plain pointers and sizes only.  Every pointer argument named as device data
+ * is device memory; `stream` is a hipStream_t (NULL = the default stream).
+ * Calls are asynchronous on `stream`, never allocate device memory, never
+ * synchronise, and return an hkv_status (0 = success).  Shapes are checked
+ * before anything is launched.  Layouts are contiguous row-major.
+ *
+ * Each entry point names the reference interface it replaces (paths relative to
+ * the helix-lite checkout).
+ */
+#ifndef HELIX_KV_H
+#define HELIX_KV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum hkv_status {
+  HKV_OK = 0,
+  HKV_ERR_ARG = 1,       /* null pointer / bad enum / negative size */
+  HKV_ERR_SHAPE = 2,     /* unsupported or inconsistent shape */
+  HKV_ERR_DTYPE = 3,     /* unsupported dtype */
+  HKV_ERR_CAPACITY = 4,  /* output capacity too small (result still sized) */
+  HKV_ERR_LAUNCH = 5,    /* kernel launch failed */
+  HKV_ERR_WORKSPACE = 6  /* workspace missing or too small */
+};
+
+enum hkv_dtype {
+  HKV_DT_F16 = 0, HKV_DT_F32 = 1, HKV_DT_BF16 = 2,
+  HKV_DT_I64 = 3, HKV_DT_U8 = 4, HKV_DT_I32 = 5 /* index / mask tensors */
+};
+
+/* A strided view: element i of a broadcast shape is at data + sum_d k_d *
+ * strides[d] (in elements; stride 0 broadcasts). */
+typedef struct hkv_tensor_desc {
+  const void *data;
+  int32_t dtype;
+  int32_t reserved;
+  int64_t strides[6];
+} hkv_tensor_desc;
+
+/* Bytes of one nearest-pole decision table (device record). */
+#define HKV_TABLE_BYTES 80
+
+const char *hkv_version(void);
+const char *hkv_status_string(int status);
+
+/*
+ * Scale description shared by the nuq entry points.  A "table" is one row of
+ * poles (levels entries) with its two thresholds:
+ *   per_token == 0 (Keys, per-channel): table index = h*D + d; poles (H,D,L),
+ *       thresholds (H,D).  src/kvquant/scales.py:13-39.
+ *   per_token == 1 (Values, per-token): table index = h*rows + min(pos, rows-1)
+ *       with pos = positions[t] if positions else pos_offset + t; poles
+ *       (H,rows,L), thresholds (H,rows).  src/kvquant/scales.py:42-69, clamp as
+ *       src/kvquant/compact_pool.py:467 / src/kvquant/vllm_backend.py:151-155.
+ * `tables` (optional for the dense pack, required for the compact path) are
+ * built from the same poles/thresholds by hkv_nuq_build_tables; the original
+ * poles/thresholds are still required (they decide the rare inputs the tables
+ * do not cover, bit-exactly).
+ */
+typedef struct hkv_nuq_scales {
+  const void *tables;   /* n_tables * HKV_TABLE_BYTES, or NULL */
+  const void *poles;    /* n_tables * levels */
+  const void *upper;    /* n_tables */
+  const void *lower;    /* n_tables */
+  int32_t poles_dtype;  /* hkv_dtype */
+  int32_t thr_dtype;    /* hkv_dtype */
+  int32_t levels;       /* 1..16 */
+  int32_t per_token;    /* 0 = per-channel (K), 1 = per-token (V) */
+  int64_t rows;         /* per-token scale rows (T_cal); unused for per-channel */
+  const int64_t *positions; /* (T,) absolute positions or NULL */
+  int64_t pos_offset;   /* absolute position of token 0 when positions == NULL */
+} hkv_nuq_scales;
+
+/*
+ * Build n_tables decision tables (nearest-pole breakpoints, canonical fp16
+ * thresholds, fp16 dequant poles).  Replaces the per-element level scan of
+ * src/kvquant/triton_batched.py:65-72 with an equivalent breakpoint search;
+ * tables that do not meet the exactness criterion are flagged and scanned.
+ * Host-side cost: none; device: one thread per table.
+ */
+int hkv_nuq_build_tables(const void *poles, int poles_dtype, const void *upper,
+                         const void *lower, int thr_dtype, int64_t n_tables, int levels,
+                         void *tables_out, void *stream);
+
+/*
+ * Dense-outlier pack (the reference's byte-per-code format): values (T,H,D)
+ * fp16 -> codes u8, outlier_v fp16 (0 where not an outlier), outlier_m u8, each
+ * (T,H,D).  Replaces pack_keys_per_channel_batched / pack_values_per_token_
+ * batched (src/kvquant/triton_batched.py:125-148, :275-303) and, with H = 1,
+ * pack_keys_per_channel / pack_values_per_token (src/kvquant/triton_kernels.py:
+ * 96-125, :258-280).
+ */
+int hkv_nuq_pack_dense(const void *values, int64_t T, int H, int D,
+                       const hkv_nuq_scales *scales, void *codes, void *outlier_v,
+                       void *outlier_m, void *stream);
+
+/*
+ * Dense unpack: where(outlier_m, outlier_v, fp16(pole[code])) -> out (T,H,D)
+ * fp16.  Replaces unpack_*_batched (src/kvquant/triton_batched.py:151-171,
+ * :306-326) and unpack_* (src/kvquant/triton_kernels.py:175-194, :321-339).
+ * Uses scales->poles only (tables may be NULL).
+ */
+int hkv_nuq_unpack_dense(const void *codes, const void *outlier_v, const void *outlier_m,
+                         int64_t T, int H, int D, const hkv_nuq_scales *scales, void *out,
+                         void *stream);
+
+/*
+ * Compact pack: values (T,H,D) fp16 -> bit-packed codes (T,H,D*bits/8) u8
+ * (nuq4: byte j = c[2j] | c[2j+1]<<4; nuq2: byte j = c[4j] | c[4j+1]<<2 |
+ * c[4j+2]<<4 | c[4j+3]<<6) plus CSR outliers over rows r = t*H + h:
+ * row_ptr (T*H+1) int32, col u8 (channel d), val fp16 (original value), in
+ * ascending (row, col) order.  Entries beyond `capacity` are not written;
+ * row_ptr is always complete, so row_ptr[T*H] is the true nnz and the call
+ * returns HKV_ERR_CAPACITY only after the stream has run (see
+ * hkv_nuq_pack_compact_status).  bits = 2 or 4 (levels <= 2^bits).  Requires
+ * scales->tables, D % 8 == 0, D <= 256.  The planned format of
+ * src/kvquant/triton_kernels.py:7-18 and src/kvquant/compact_pool.py:11-12
+ * (the reference never implemented it).  Single pass: the CSR offsets come
+ * from a decoupled look-back over tiles, so `workspace` (zero-filled once
+ * before first use, then reused as-is) must hold
+ * hkv_nuq_pack_compact_workspace_bytes(T, H, D) bytes and must not be shared by
+ * calls that may overlap.
+ */
+size_t hkv_nuq_pack_compact_workspace_bytes(int64_t T, int H, int D);
+int hkv_nuq_pack_compact(const void *values, int64_t T, int H, int D, int bits,
+                         const hkv_nuq_scales *scales, void *packed, int32_t *row_ptr,
+                         uint8_t *col, uint16_t *val, int64_t capacity, void *workspace,
+                         size_t workspace_bytes, void *stream);
+/* Device-side error word of a pack workspace (0 = fine; bit 0: look-back
+ * wait exceeded its limit).  Reads device memory: synchronises `stream`. */
+int hkv_nuq_pack_compact_status(const void *workspace, void *stream);
+
+/*
+ * Compact unpack: packed codes + CSR -> out (T,H,D) fp16.  Inverse of
+ * hkv_nuq_pack_compact; requires scales->tables.
+ */
+int hkv_nuq_unpack_compact(const void *packed, const int32_t *row_ptr, const uint8_t *col,
+                           const uint16_t *val, int64_t T, int H, int D, int bits,
+                           const hkv_nuq_scales *scales, void *out, void *stream);
+
+/*
+ * Broadcasting quantise with the CPU spec's dtype semantics: over a shape of
+ * up to 6 dims, code = first argmin_l |round_cdt(v - pole_l)| (NaN differences
+ * win, first one first), mask = v < lower || v > upper (omit both thresholds
+ * for no mask), recon = mask ? v : pole[code] in recon_dtype.  Any output may
+ * be NULL (codes int64, mask u8, recon contiguous).  Pole l of element i is at
+ * poles->data + offset_i + l*level_stride.  src/kvquant/nuq.py:22-38
+ * (round_to_nearest_pole), :41-94 (find_outliers, without the cap/first-N
+ * options), :97-132 (quantize_nuq).
+ */
+int hkv_nuq_quantize_generic(int ndim, const int64_t *shape, const hkv_tensor_desc *values,
+                             const hkv_tensor_desc *poles, int64_t level_stride, int levels,
+                             const hkv_tensor_desc *upper, const hkv_tensor_desc *lower,
+                             int compute_dtype, int64_t *codes, void *recon, int recon_dtype,
+                             uint8_t *mask, void *stream);
+
+/*
+ * Broadcasting dequantise: out = mask ? outliers : round_out(pole[code]) in
+ * out_dtype (contiguous).  Codes outside [0, levels) set *err (device int32)
+ * and read pole 0.  src/kvquant/nuq.py:135-156.
+ */
+int hkv_nuq_dequantize_generic(int ndim, const int64_t *shape, const hkv_tensor_desc *codes,
+                               const hkv_tensor_desc *outliers, const hkv_tensor_desc *outlier_mask,
+                               const hkv_tensor_desc *poles, int64_t level_stride, int levels,
+                               void *out, int out_dtype, int32_t *err, void *stream);
+
+/*
+ * Quest page statistics: K_pages (P,S,H,D) -> kmin, kmax (P,H,D), same dtype
+ * (f16 or f32).  -0 orders below +0; a NaN in a page-channel gives NaN.
+ * src/quest/reference.py:38-56.
+ */
+int hkv_quest_page_stats(const void *k_pages, int dtype, int64_t P, int S, int H, int D,
+                         void *kmin, void *kmax, void *stream);
+
+/*
+ * Quest upper bound per (page, KV head):
+ *   sum_d clamp(q,0)*kmax + clamp(q,max=0)*kmin   (fp32, fixed order)
+ * q is (Hq,D); gqa_group = Hq / H: 1 = one query per KV head
+ * (src/quest/reference.py:59-93, src/kvquant/quest_selector.py:68-70);
+ * > 1 = the group's per-head bounds summed (query head h -> KV head h / group).
+ * kmin/kmax (P,H,D) f16 or f32; out (P,H) f32 or f16 (f16 = the rounding of
+ * page_upper_bound_triton, src/quest/triton_kernels.py:57).
+ */
+int hkv_quest_page_bound(const void *q, int q_dtype, int Hq, const void *kmin,
+                         const void *kmax, int k_dtype, int64_t P, int H, int D,
+                         void *out, int out_dtype, void *stream);
+
+/*
+ * Quest top-K with sinks over a bound (P,H) (f32 or f16):
+ * sinks = clamp(sink_pages, 0, P); k_eff = clamp(k, 0, P - sinks); out
+ * (sinks + k_eff, H) int64, per head the sinks then the k_eff highest-bound
+ * non-sink pages, ascending; ties go to the lower page index; NaN ranks highest.
+ * src/quest/reference.py:96-133.  Returns sinks + k_eff through *n_out.
+ * workspace: hkv_quest_topk_workspace_bytes(P, H) bytes, zero-filled once.
+ */
+size_t hkv_quest_topk_workspace_bytes(int64_t P, int H);
+int hkv_quest_topk(const void *bound, int b_dtype, int64_t P, int H, int64_t k,
+                   int64_t sink_pages, int64_t *out, int64_t *n_out, void *workspace,
+                   size_t workspace_bytes, void *stream);
+
+/*
+ * Fused Quest selection for one decode step: bound (as hkv_quest_page_bound,
+ * f32) + top-K with sinks (as hkv_quest_topk) in one launch.  scores (P,H) f32
+ * receives the bounds.  The per-layer path of src/kvquant/quest_selector.py:
+ * 64-78 without the union.
+ */
+int hkv_quest_select(const void *q, int q_dtype, int Hq, const void *kmin, const void *kmax,
+                     int k_dtype, int64_t P, int H, int D, int64_t k, int64_t sink_pages,
+                     float *scores, int64_t *out, int64_t *n_out, void *workspace,
+                     size_t workspace_bytes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HELIX_KV_H */

@@ -1,0 +1,363 @@
+"""CPU oracle for helix-lite's KV-cache hot path.
+
+TEST INFRASTRUCTURE ONLY.  Only ``tests/``, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` may import this package, and only as the
+checker -- never as the thing measured or shipped.  The product (the HIP
+library under ``helix-lite_amd/csrc`` and the drop-in Python packages) never
+imports it and has no CPU fallback.
+
+The integer/byte semantics live in ``oracle.c`` (built to ``liboracle.so`` by
+``oracle/Makefile``); this module wraps it with numpy and adds the byte-format
+helpers (bit packing, CSR) and the attention reference in float64.
+
+Reference files are cited as ``file:line`` relative to the reference checkout.
+Every function here is pinned by at least one test in ``tests/test_oracle_*.py``
+against the reference's own known answers, torch library routines, or
+exhaustive enumeration; see each docstring.
+"""
+from __future__ import annotations
+
+import ctypes
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+_HERE = Path(__file__).resolve().parent
+_LIB_PATH = _HERE / "liboracle.so"
+_lib = None
+
+
+def build(force: bool = False) -> Path:
+    """Compile ``liboracle.so`` with the committed Makefile."""
+    if force or not _LIB_PATH.exists() or (
+        _LIB_PATH.stat().st_mtime < (_HERE / "oracle.c").stat().st_mtime
+    ):
+        subprocess.run(["make", "-s", "-B" if force else "liboracle.so"], cwd=_HERE, check=True)
+    return _LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        build()
+        _lib = ctypes.CDLL(str(_LIB_PATH))
+        _declare(_lib)
+    return _lib
+
+
+_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int
+
+
+def _declare(L: ctypes.CDLL) -> None:
+    L.orc_nearest_code.argtypes = [ctypes.c_float, _p, _i32]
+    L.orc_nearest_code.restype = _i32
+    L.orc_pack_k.argtypes = [_p, _i64, _i32, _i32, _p, _p, _p, _i32, _p, _p, _p]
+    L.orc_pack_v.argtypes = [_p, _i64, _i32, _i32, _p, _p, _p, _i32, _i64, _p, _p, _p, _p]
+    L.orc_unpack.argtypes = [_p, _p, _p, _i64, _i32, _i32, _p, _i32, _i32, _i64, _p, _p]
+    L.orc_prep_tables.argtypes = [_p, _p, _p, _i64, _i32, _p]
+    L.orc_check_table_exhaustive.argtypes = [_p, _i32, ctypes.c_float, ctypes.c_float,
+                                             ctypes.POINTER(_i64)]
+    L.orc_check_table_exhaustive.restype = _i64
+    L.orc_page_stats.argtypes = [_p, _i64, _i32, _i32, _i32, _p, _p]
+    L.orc_page_bound.argtypes = [_p, _p, _p, _i64, _i32, _i32, _p]
+    L.orc_page_bound_group.argtypes = [_p, _p, _p, _i64, _i32, _i32, _i32, _p]
+    L.orc_topk_sinks.argtypes = [_p, _i64, _i32, _i64, _i64, _p]
+    L.orc_topk_sinks.restype = _i64
+
+
+def _ptr(a: np.ndarray | None):
+    if a is None:
+        return None
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, dtype=np.float32))
+
+
+def _h16(a) -> np.ndarray:
+    """fp16 values as a contiguous uint16 bit array."""
+    a = np.asarray(a)
+    if a.dtype == np.uint16:
+        return np.ascontiguousarray(a)
+    return np.ascontiguousarray(a.astype(np.float16)).view(np.uint16)
+
+
+# Table record layout shared with the GPU tables (80 bytes, see oracle.c).
+TABLE_DTYPE = np.dtype([
+    ("bp", np.uint16, 16), ("pf16", np.uint16, 16), ("lo", np.uint16), ("up", np.uint16),
+    ("xsafe", np.uint16), ("flags", np.uint16), ("levels", np.uint16), ("pad", np.uint16, 3),
+])
+assert TABLE_DTYPE.itemsize == 80
+
+
+# --------------------------------------------------------------- nuq (a1-a6)
+
+def nearest_code(v: float, poles) -> int:
+    """Strict-< ascending scan over fp32 |v - pole| (src/kvquant/triton_batched.py:65-72)."""
+    p = _f32(poles)
+    return int(lib().orc_nearest_code(ctypes.c_float(float(np.float32(v))), _ptr(p), p.size))
+
+
+def pack_k(values, poles, upper, lower):
+    """K per-channel pack, dense outliers (src/kvquant/triton_batched.py:28-82).
+
+    values (T,H,D) fp16; poles (H,D,L); upper/lower (H,D).  Returns
+    (codes u8, outlier_v fp16-bits u16, outlier_m u8), each (T,H,D).
+    """
+    x = _h16(values)
+    T, H, D = x.shape
+    p, up, lo = _f32(poles), _f32(upper), _f32(lower)
+    L = p.shape[-1]
+    assert p.shape == (H, D, L) and up.shape == (H, D) and lo.shape == (H, D)
+    codes = np.empty((T, H, D), np.uint8)
+    outv = np.empty((T, H, D), np.uint16)
+    outm = np.empty((T, H, D), np.uint8)
+    lib().orc_pack_k(_ptr(x), T, H, D, _ptr(p), _ptr(up), _ptr(lo), L, _ptr(codes),
+                     _ptr(outv), _ptr(outm))
+    return codes, outv, outm
+
+
+def pack_v(values, poles, upper, lower, positions=None):
+    """V per-token pack, dense outliers.
+
+    poles (H,Tt,L), upper/lower (H,Tt); row t uses scale row
+    min(positions[t], Tt-1) (positions default to arange(T)).
+    src/kvquant/triton_batched.py:179-232; clamp src/kvquant/compact_pool.py:467.
+    """
+    x = _h16(values)
+    T, H, D = x.shape
+    p, up, lo = _f32(poles), _f32(upper), _f32(lower)
+    L = p.shape[-1]
+    Tt = p.shape[1]
+    assert p.shape == (H, Tt, L) and up.shape == (H, Tt) and lo.shape == (H, Tt)
+    pos = None if positions is None else np.ascontiguousarray(np.asarray(positions, np.int64))
+    codes = np.empty((T, H, D), np.uint8)
+    outv = np.empty((T, H, D), np.uint16)
+    outm = np.empty((T, H, D), np.uint8)
+    lib().orc_pack_v(_ptr(x), T, H, D, _ptr(p), _ptr(up), _ptr(lo), L, Tt, _ptr(pos),
+                     _ptr(codes), _ptr(outv), _ptr(outm))
+    return codes, outv, outm
+
+
+def unpack(codes, outv, outm, poles, mode: str, positions=None):
+    """where(outlier_m, outlier_v, fp16(pole[code])) -> fp16 bits (T,H,D).
+
+    mode "k": poles (H,D,L); mode "v": poles (H,Tt,L) with the clamp above.
+    src/kvquant/triton_batched.py:85-122, :235-272; src/kvquant/nuq.py:155-156.
+    """
+    c = np.ascontiguousarray(codes, dtype=np.uint8)
+    v = _h16(outv)
+    m = np.ascontiguousarray(outm, dtype=np.uint8)
+    T, H, D = c.shape
+    p = _f32(poles)
+    L = p.shape[-1]
+    Tt = p.shape[1] if mode == "v" else 0
+    pos = None if positions is None else np.ascontiguousarray(np.asarray(positions, np.int64))
+    out = np.empty((T, H, D), np.uint16)
+    lib().orc_unpack(_ptr(c), _ptr(v), _ptr(m), T, H, D, _ptr(p), L, 0 if mode == "k" else 1,
+                     Tt, _ptr(pos), _ptr(out))
+    return out
+
+
+def nuq_py_semantics(values, poles, upper, lower):
+    """``quantize_nuq`` exactly as src/kvquant/nuq.py:36-38,72,131 computes it.
+
+    The difference ``values - poles`` is formed in torch's promoted dtype: for
+    fp16 inputs and fp16 poles the fp32 difference is rounded to fp16 before
+    ``abs`` and ``argmin`` (first index on ties).  Returns (codes, recon, mask)
+    with recon in the promoted dtype.  Broadcasting follows numpy rules.
+    """
+    v = np.asarray(values)
+    p = np.asarray(poles)
+    dt = np.result_type(v.dtype, p.dtype)
+    diff = (v.astype(np.float32)[..., None] - p.astype(np.float32)).astype(dt)
+    codes = np.abs(diff).argmin(axis=-1)
+    q = np.take_along_axis(np.broadcast_to(p, codes.shape + (p.shape[-1],)),
+                           codes[..., None], axis=-1)[..., 0].astype(dt)
+    mask = (v < np.asarray(lower)) | (v > np.asarray(upper))
+    recon = np.where(mask, v.astype(dt), q)
+    return codes, recon, mask
+
+
+# ----------------------------------------------------- fast decision tables
+
+def prep_tables(poles, upper, lower) -> np.ndarray:
+    """Decision tables (TABLE_DTYPE records) for poles (N,L), thresholds (N,)."""
+    p, up, lo = _f32(poles), _f32(upper), _f32(lower)
+    n, L = p.shape
+    out = np.zeros(n, TABLE_DTYPE)
+    lib().orc_prep_tables(_ptr(p), _ptr(up), _ptr(lo), n, L, _ptr(out))
+    return out
+
+
+def check_table_exhaustive(poles, upper: float, lower: float) -> tuple[int, int]:
+    """(mismatches, covered inputs) of the fast path over all 65,536 fp16 inputs."""
+    p = _f32(poles)
+    cov = _i64(0)
+    bad = lib().orc_check_table_exhaustive(_ptr(p), p.size, ctypes.c_float(upper),
+                                           ctypes.c_float(lower), ctypes.byref(cov))
+    return int(bad), int(cov.value)
+
+
+# ---------------------------------------------- a5: bit packing and CSR
+
+def bitpack(codes, bits: int) -> np.ndarray:
+    """Pack codes (..., D) into little-endian bytes (..., D*bits/8).
+
+    nuq4: byte j = c[2j] | c[2j+1] << 4; nuq2: byte j = c[4j] | c[4j+1] << 2 |
+    c[4j+2] << 4 | c[4j+3] << 6.  (Format of this build; the reference stores
+    one byte per code, src/kvquant/compact_pool.py:427-432.)
+    """
+    c = np.asarray(codes, dtype=np.uint8)
+    per = 8 // bits
+    assert c.shape[-1] % per == 0
+    c = c.reshape(c.shape[:-1] + (c.shape[-1] // per, per)).astype(np.uint16)
+    out = np.zeros(c.shape[:-1], np.uint16)
+    for j in range(per):
+        out |= (c[..., j] & ((1 << bits) - 1)) << (bits * j)
+    return out.astype(np.uint8)
+
+
+def bitunpack(packed, bits: int, D: int) -> np.ndarray:
+    b = np.asarray(packed, dtype=np.uint8)
+    per = 8 // bits
+    out = np.empty(b.shape + (per,), np.uint8)
+    for j in range(per):
+        out[..., j] = (b >> (bits * j)) & ((1 << bits) - 1)
+    return out.reshape(b.shape[:-1] + (D,))
+
+
+def csr_encode(outm, outv):
+    """Dense (R,D) outlier mask/values -> CSR (row_ptr int32 (R+1,), col u8, val fp16 bits).
+
+    Rows are the flattened (token, head) rows; within a row columns ascend.
+    """
+    m = np.asarray(outm).astype(bool)
+    R = m.shape[0]
+    m2 = m.reshape(R, -1)
+    v2 = _h16(outv).reshape(R, -1)
+    counts = m2.sum(axis=1)
+    row_ptr = np.zeros(R + 1, np.int64)
+    np.cumsum(counts, out=row_ptr[1:])
+    r, c = np.nonzero(m2)
+    return row_ptr.astype(np.int32), c.astype(np.uint8), v2[r, c]
+
+
+def csr_decode(row_ptr, col, val, R: int, D: int):
+    m = np.zeros((R, D), np.uint8)
+    v = np.zeros((R, D), np.uint16)
+    rp = np.asarray(row_ptr, np.int64)
+    rows = np.repeat(np.arange(R), np.diff(rp))
+    m[rows, np.asarray(col, np.int64)] = 1
+    v[rows, np.asarray(col, np.int64)] = np.asarray(val, np.uint16)
+    return m, v
+
+
+def pack_compact(codes, outv, outm, bits: int):
+    """Dense (T,H,D) pack outputs -> (packed codes (T,H,D*bits/8), row_ptr, col, val)."""
+    T, H, D = np.asarray(codes).shape
+    rp, col, val = csr_encode(np.asarray(outm).reshape(T * H, D), np.asarray(outv).reshape(T * H, D))
+    return bitpack(codes, bits), rp, col, val
+
+
+# ------------------------------------------------------------ Quest a8-a11
+
+def page_stats(K_pages):
+    """(P,S,H,D) -> (min, max) (P,H,D) in K's dtype; -0 < +0; NaN propagates.
+
+    src/quest/reference.py:38-56.
+    """
+    K = np.asarray(K_pages)
+    P, S, H, D = K.shape
+    k32 = _f32(K)
+    mn = np.empty((P, H, D), np.float32)
+    mx = np.empty((P, H, D), np.float32)
+    lib().orc_page_stats(_ptr(k32), P, S, H, D, _ptr(mn), _ptr(mx))
+    return mn.astype(K.dtype), mx.astype(K.dtype)
+
+
+def page_bound(query, kmin, kmax):
+    """(H,D) query, (P,H,D) stats -> (P,H) fp32 bound in the canonical order.
+
+    src/quest/reference.py:59-93, src/quest/triton_kernels.py:25-57.
+    """
+    q, mn, mx = _f32(query), _f32(kmin), _f32(kmax)
+    P, H, D = mn.shape
+    out = np.empty((P, H), np.float32)
+    lib().orc_page_bound(_ptr(q), _ptr(mn), _ptr(mx), P, H, D, _ptr(out))
+    return out
+
+
+def page_bound_group(query, kmin, kmax, group: int):
+    """(Hq,D) query with Hq = Hkv*group -> (P,Hkv) group-sum bound (factorised order)."""
+    q, mn, mx = _f32(query), _f32(kmin), _f32(kmax)
+    P, H, D = mn.shape
+    assert q.shape == (H * group, D)
+    out = np.empty((P, H), np.float32)
+    lib().orc_page_bound_group(_ptr(q), _ptr(mn), _ptr(mx), P, H, group, D, _ptr(out))
+    return out
+
+
+def topk_sinks(bound, k: int, sink_pages: int):
+    """src/quest/reference.py:96-133 with lowest-index tie-break -> (s+k_eff, H) int64."""
+    b = _f32(bound)
+    P, H = b.shape
+    s = max(0, min(sink_pages, P))
+    keff = max(0, min(k, P - s))
+    out = np.empty((s + keff, H), np.int64)
+    lib().orc_topk_sinks(_ptr(b), P, H, k, sink_pages, _ptr(out))
+    return out
+
+
+def select_union(bound, used_block_ids, top_k: int, sink_blocks: int, block_size: int):
+    """src/kvquant/quest_selector.py:38-90: union over heads, mapped to block ids, sorted."""
+    used = np.asarray(used_block_ids, np.int64)
+    NU = used.shape[0]
+    sinks = max(0, min(sink_blocks, NU))
+    keep = max(0, min(top_k, NU - sinks))
+    sel = topk_sinks(bound, keep, sinks)
+    uniq = np.unique(sel.reshape(-1))
+    ids = np.sort(used[uniq])
+    return ids, ids * block_size
+
+
+def selected_attention(query, K_pages, V_pages, page_indices, kv_of_head):
+    """softmax(q.K^T/sqrt(D)).V over each head's selected pages, in float64.
+
+    query (Hq,D); K_pages/V_pages (P,S,Hkv,D); page_indices (n,Hsel) where
+    column j selects pages for KV head j (Hsel == Hkv) or for query head j
+    (Hsel == Hq); kv_of_head(h) maps a query head to its KV head.
+    src/quest/reference.py:136-168 (fp32 softmax there; float64 here, compared
+    with a tolerance).
+    """
+    q = np.asarray(query, np.float64)
+    K = np.asarray(K_pages, np.float64)
+    V = np.asarray(V_pages, np.float64)
+    idx = np.asarray(page_indices, np.int64)
+    Hq, D = q.shape
+    out = np.zeros((Hq, V.shape[-1]))
+    for h in range(Hq):
+        g = kv_of_head(h)
+        col = idx[:, h] if idx.shape[1] == Hq else idx[:, g]
+        Kh = K[col, :, g, :].reshape(-1, D)
+        Vh = V[col, :, g, :].reshape(-1, V.shape[-1])
+        s = Kh @ q[h] / np.sqrt(D)
+        s = np.exp(s - s.max())
+        out[h] = (s / s.sum()) @ Vh
+    return out
+
+
+def h2f(bits) -> np.ndarray:
+    return np.asarray(bits, np.uint16).view(np.float16).astype(np.float32)
+
+
+def f2h(x) -> np.ndarray:
+    return np.asarray(x, np.float32).astype(np.float16).view(np.uint16)
+
+
+__all__ = [n for n in dir() if not n.startswith("_")]

@@ -1,0 +1,61 @@
+"""The C-ABI library loads and exports every entry point its header declares.
+
+Host-only: no device memory is touched and no kernel is launched.
+"""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "helix_kv.h"
+
+
+def declared_functions() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(hkv_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    from helix_kv import _native
+
+    L = _native.lib()
+    names = declared_functions()
+    assert len(names) >= 16
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, missing
+    # the Python binding declares a signature for every exported entry point
+    assert sorted(_native.exported_symbols()) == names
+
+
+def test_host_only_entry_points():
+    from helix_kv import _native
+
+    L = _native.lib()
+    assert b"gfx950" in L.hkv_version()
+    assert L.hkv_status_string(0) == b"ok"
+    assert L.hkv_status_string(4) == b"output capacity too small"
+    # pack workspace: 64-byte header + one status word per tile of 64 rows (D=128)
+    assert L.hkv_nuq_pack_compact_workspace_bytes(131072, 4, 128) == 64 + 8 * (131072 * 4 // 64)
+    assert L.hkv_nuq_pack_compact_workspace_bytes(10, 4, 128) == 64 + 8
+    assert L.hkv_nuq_pack_compact_workspace_bytes(10, 4, 100) == 0  # unsupported D
+    assert L.hkv_quest_topk_workspace_bytes(65536, 4) >= 64
+
+
+def test_struct_layouts_match_header():
+    from helix_kv import _native
+
+    assert ctypes.sizeof(_native.NuqScales) == 4 * 8 + 4 * 4 + 8 + 8 + 8
+    assert ctypes.sizeof(_native.TensorDesc) == 8 + 4 + 4 + 6 * 8
+    assert "#define HKV_TABLE_BYTES 80" in HEADER.read_text()
+    assert _native.TABLE_BYTES == 80
+
+
+def test_oracle_table_record_matches_device_layout():
+    import oracle
+
+    assert oracle.TABLE_DTYPE.itemsize == 80
+    assert oracle.TABLE_DTYPE.fields["lo"][1] == 64
+    assert oracle.TABLE_DTYPE.fields["xsafe"][1] == 68
+    assert oracle.TABLE_DTYPE.fields["flags"][1] == 70

@@ -1,0 +1,161 @@
+"""Pins of the CPU oracle's Quest functions (no GPU).
+
+Checked against the reference's known-answer tests (src/quest/tests/
+test_reference.py, src/kvquant/tests/test_quest_selector.py), numpy/torch
+reductions, torch.topk on distinct keys, and closed forms.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+
+RNG = np.random.default_rng(7)
+
+
+def test_page_stats_match_numpy_and_spot_check():
+    # src/quest/tests/test_reference.py:34-42
+    K = RNG.standard_normal((4, 16, 2, 8)).astype(np.float32)
+    mn, mx = O.page_stats(K)
+    assert np.array_equal(mn, K.min(axis=1)) and np.array_equal(mx, K.max(axis=1))
+    assert mn[1, 0, 3] == K[1, :, 0, 3].min() and mx[1, 0, 3] == K[1, :, 0, 3].max()
+    Kh = K.astype(np.float16)
+    mn16, mx16 = O.page_stats(Kh)
+    assert mn16.dtype == np.float16
+    assert np.array_equal(mn16, Kh.min(axis=1)) and np.array_equal(mx16, Kh.max(axis=1))
+
+
+def test_page_stats_signed_zero_and_nan_rules():
+    K = np.zeros((2, 4, 1, 2), np.float32)
+    K[0, :, 0, 0] = [0.0, -0.0, 0.0, 1.0]
+    K[0, :, 0, 1] = [-0.0, 0.0, -1.0, -0.0]
+    K[1, 2, 0, 0] = np.nan
+    mn, mx = O.page_stats(K)
+    assert np.signbit(mn[0, 0, 0]) and mn[0, 0, 0] == 0.0 and mx[0, 0, 0] == 1.0
+    assert mn[0, 0, 1] == -1.0 and not np.signbit(mx[0, 0, 1]) and mx[0, 0, 1] == 0.0
+    assert np.isnan(mn[1, 0, 0]) and np.isnan(mx[1, 0, 0]) and mn[1, 0, 1] == 0.0
+
+
+def test_bound_is_an_upper_bound():
+    # src/quest/tests/test_reference.py:45-63
+    P, page, H, D = 8, 16, 4, 32
+    K = RNG.standard_normal((P, page, H, D)).astype(np.float32)
+    q = RNG.standard_normal((H, D)).astype(np.float32)
+    mn, mx = O.page_stats(K)
+    bound = O.page_bound(q, mn, mx)
+    true_max = np.einsum("pthd,hd->pth", K, q).max(axis=1)
+    assert (bound - true_max >= -1e-4).all()
+
+
+def test_bound_matches_torch_formula():
+    """Same value as the reference's torch expression up to summation order."""
+    P, H, D = 64, 4, 128
+    q = torch.randn(H, D)
+    kmin = torch.randn(P, H, D)
+    kmax = kmin + torch.rand(P, H, D)
+    ref = (q.clamp(min=0) * kmax).sum(-1) + (q.clamp(max=0) * kmin).sum(-1)  # reference.py:88-92
+    got = O.page_bound(q.numpy(), kmin.numpy(), kmax.numpy())
+    mag = (q.abs().unsqueeze(0) * torch.maximum(kmin.abs(), kmax.abs())).sum(-1)
+    assert np.all(np.abs(got - ref.numpy()) <= 4 * np.finfo(np.float32).eps * mag.numpy())
+
+
+def test_bound_exact_for_one_hot_query():
+    P, H, D = 16, 2, 40
+    mn = RNG.standard_normal((P, H, D)).astype(np.float16).astype(np.float32)
+    mx = mn + RNG.random((P, H, D)).astype(np.float16).astype(np.float32)
+    for d, c in [(0, 2.5), (17, -3.0), (39, 0.125)]:
+        q = np.zeros((H, D), np.float32)
+        q[:, d] = c
+        want = c * (mx[:, :, d] if c > 0 else mn[:, :, d])
+        assert np.array_equal(O.page_bound(q, mn, mx), want.astype(np.float32))
+
+
+def test_group_bound_is_sum_of_head_bounds():
+    P, Hkv, g, D = 32, 4, 7, 128
+    q = RNG.standard_normal((Hkv * g, D)).astype(np.float16).astype(np.float32)
+    mn = RNG.standard_normal((P, Hkv, D)).astype(np.float16).astype(np.float32)
+    mx = mn + RNG.random((P, Hkv, D)).astype(np.float16).astype(np.float32)
+    got = O.page_bound_group(q, mn, mx, g).astype(np.float64)
+    per_head = np.stack([O.page_bound(q[h:h + 1], mn[:, h // g:h // g + 1],
+                                      mx[:, h // g:h // g + 1])[:, 0] for h in range(Hkv * g)], 1)
+    want = per_head.astype(np.float64).reshape(P, Hkv, g).sum(-1)
+    assert np.allclose(got, want, rtol=1e-5, atol=1e-4)
+    assert np.array_equal(O.page_bound_group(q[:Hkv], mn, mx, 1), O.page_bound(q[:Hkv], mn, mx))
+
+
+def test_topk_known_answers():
+    # src/quest/tests/test_reference.py:66-92
+    bound = RNG.standard_normal((16, 4)).astype(np.float32)
+    bound[0, :] = -100.0
+    sel = O.topk_sinks(bound, 4, 2)
+    assert sel.shape == (6, 4)
+    for h in range(4):
+        assert {0, 1} <= set(sel[:, h].tolist())
+        assert np.all(np.diff(sel[:, h]) > 0)
+    assert O.topk_sinks(RNG.standard_normal((3, 2)).astype(np.float32), 10, 1).shape == (3, 2)
+
+
+@pytest.mark.parametrize("P,k,s", [(1000, 250, 4), (257, 1, 0), (64, 60, 4), (5, 0, 2), (3, 1, 7)])
+def test_topk_equals_torch_topk_on_distinct_keys(P, k, s):
+    H = 3
+    b = torch.randperm(P * H).float().reshape(P, H) * 0.25 - 100.0
+    sel = O.topk_sinks(b.numpy(), k, s)
+    sp = max(0, min(s, P))
+    keff = max(0, min(k, P - sp))
+    masked = b.clone()
+    masked[:sp] = float("-inf")
+    top = torch.topk(masked, keff, dim=0).indices if keff else torch.empty(0, H, dtype=torch.long)
+    want = torch.cat([torch.arange(sp).unsqueeze(1).expand(-1, H), top], 0).sort(0).values
+    assert np.array_equal(sel, want.numpy())
+
+
+def test_topk_ties_go_to_lower_pages_and_nan_ranks_highest():
+    b = np.zeros((20, 2), np.float32)
+    sel = O.topk_sinks(b, 5, 2)
+    assert sel[:, 0].tolist() == [0, 1, 2, 3, 4, 5, 6]
+    b[15, 1] = np.nan
+    b[9, 1] = 1.0
+    b[3, 1] = -0.0
+    sel = O.topk_sinks(b, 3, 0)
+    assert sel[:, 1].tolist() == [0, 9, 15]
+
+
+def _pool_stats(key, poles, up, lo, BS):
+    """Reconstructed-K page stats as the reference pool keeps them (compact_pool.py:258-287)."""
+    c, v, m = O.pack_k(key, poles, up, lo)
+    rec = O.h2f(O.unpack(c, v, m, poles, "k"))
+    T, H, D = rec.shape
+    return O.page_stats(rec.reshape(T // BS, BS, H, D))
+
+
+def test_select_union_known_answers():
+    # src/kvquant/tests/test_quest_selector.py:41-95
+    H, D, BS = 2, 8, 4
+    poles = np.broadcast_to(np.linspace(-1.5, 1.5, 16, dtype=np.float16).astype(np.float32),
+                            (H, D, 16)).copy()
+    up, lo = np.full((H, D), 2.0), np.full((H, D), -2.0)
+    key = np.zeros((5 * BS, H, D), np.float16)
+    key[3 * BS:4 * BS] = 1.0
+    mn, mx = _pool_stats(key, poles, up, lo, BS)
+    q = np.ones((H, D), np.float32)
+    ids, first = O.select_union(O.page_bound(q, mn, mx), np.arange(5), 1, 0, BS)
+    assert ids.tolist() == [3] and first.tolist() == [12]
+    key0 = np.zeros((5 * BS, H, D), np.float16)
+    mn, mx = _pool_stats(key0, poles, up, lo, BS)
+    ids, _ = O.select_union(O.page_bound(q, mn, mx), np.arange(5), 1, 2, BS)
+    assert {0, 1} <= set(ids.tolist())
+
+
+def test_attention_all_pages_equals_dense():
+    # src/quest/tests/test_reference.py:95-117 (float64 oracle vs torch fp32 dense)
+    P, page, H, D = 4, 8, 2, 16
+    K = RNG.standard_normal((P, page, H, D))
+    V = RNG.standard_normal((P, page, H, D))
+    q = RNG.standard_normal((H, D))
+    out = O.selected_attention(q, K, V, np.arange(P)[:, None].repeat(H, 1), lambda h: h)
+    Kf, Vf = torch.tensor(K).reshape(P * page, H, D), torch.tensor(V).reshape(P * page, H, D)
+    for h in range(H):
+        a = torch.softmax(Kf[:, h] @ torch.tensor(q[h]) / np.sqrt(D), 0)
+        assert np.allclose(out[h], (a @ Vf[:, h]).numpy(), atol=1e-9)
