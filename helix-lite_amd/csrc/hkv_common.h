@@ -77,8 +77,14 @@ HKV_DEV uint32_t lt2(uint32_t a, uint32_t b) {
   return as_u32(as_s2(as_u32(d)) >> (s2_t){15, 15});
 }
 
-// Bitwise select: m ? a : b per bit (lowered to v_bfi_b32).
-HKV_DEV uint32_t bsel(uint32_t m, uint32_t a, uint32_t b) { return (m & a) | (~m & b); }
+// Bitwise select: m ? a : b per bit, as one v_bfi_b32.  Written as inline
+// asm: when m is a per-16-bit sign splat, the compiler otherwise rewrites the
+// and/or form into per-half selects (two shifts, two v_cndmask and a v_perm).
+HKV_DEV uint32_t bsel(uint32_t m, uint32_t a, uint32_t b) {
+  uint32_t r;
+  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "v"(m), "v"(a), "v"(b));
+  return r;
+}
 
 // Pack the low halves of a and b into one register (a -> lane 0, b -> lane 1).
 HKV_DEV uint32_t pack_lo(uint32_t a, uint32_t b) { return (a & 0xffffu) | (b << 16); }

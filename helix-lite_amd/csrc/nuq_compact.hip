@@ -8,253 +8,305 @@
 //   CSR outliers over rows r = t*H + h: row_ptr (T*H+1) int32, col u8 = d,
 //   val fp16 = the original value; (row, col) ascending.
 //
-// Pack is one pass over the fp16 input.  The CSR offsets need a global
-// exclusive scan of per-row outlier counts; tiles of rows obtain their offset
-// by a decoupled look-back: each tile publishes its count, then its inclusive
-// prefix once known, and a tile sums its predecessors' published values.
-// Tiles take ids from an atomic ticket, so every tile waited on is already
-// running.  Status words carry a launch epoch so the workspace never needs
-// clearing between calls; the last tile to finish advances the epoch.
+// Pack runs as two kernels.  pack_stage_kernel streams the fp16 input once:
+// it writes the packed codes, each row's outlier offset within its tile (into
+// row_ptr), the tile's outliers into the tile's own region of a staging
+// buffer, and the tile's outlier count.  compact_kernel then turns the tile
+// counts into tile offsets, adds them to row_ptr and copies the staged
+// outliers into the dense col/val arrays.  No block ever waits on another:
+// on gfx950 the eight XCDs' L2 caches are not coherent, so a single-pass scan
+// whose tiles wait on their predecessors pays a memory round trip per step.
 #include "nuq_core.h"
 
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kPasses = 4;               // passes of kThreads*8 elements per tile
-constexpr uint32_t kSpinLimit = 1u << 22;
+constexpr int kPasses = 8;  // passes of kThreads*8 elements per tile
 
-struct PackWs {
-  uint32_t ticket;
-  uint32_t done;
-  uint32_t epoch;
-  uint32_t err;
-  uint32_t pad[12];
+// Workspace: header, per-tile counts, then the staging columns and values,
+// each region 256-byte aligned.  Staging holds a whole tile per tile, so no
+// input can overflow it.
+struct PackLayout {
+  int64_t ntiles, tile_elems;
+  size_t cnt_off, col_off, val_off, bytes;
 };
-static_assert(sizeof(PackWs) == 64, "workspace header");
 
-constexpr uint32_t kFlagAgg = 1, kFlagPrefix = 2;
+__host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-HKV_DEV uint64_t status_word(uint32_t epoch, uint32_t flag, uint32_t value) {
-  return ((uint64_t)(((epoch & 0x3fffffffu) << 2) | flag) << 32) | value;
-}
-
-HKV_DEV void publish(uint64_t* st, uint32_t tile, uint64_t w) {
-  __hip_atomic_store(st + tile, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Sum of the counts of all tiles before `tile`.
-HKV_DEV uint32_t look_back(uint64_t* st, uint32_t tile, uint32_t epoch, PackWs* ws) {
-  uint32_t sum = 0, spins = 0;
-  int64_t j = (int64_t)tile - 1;
-  const uint32_t e30 = epoch & 0x3fffffffu;
-  while (j >= 0) {
-    const uint64_t s = __hip_atomic_load(st + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const uint32_t hi = (uint32_t)(s >> 32);
-    if ((hi >> 2) == e30 && (hi & 3u) != 0) {
-      sum += (uint32_t)s;
-      if ((hi & 3u) == kFlagPrefix) return sum;
-      --j;
-      continue;
-    }
-    if (++spins > kSpinLimit) {  // never expected; reported to the host
-      atomicOr(&ws->err, 1u);
-      return sum;
-    }
-    __builtin_amdgcn_s_sleep(2);
-  }
-  return sum;
-}
-
+// KFIX: the rows per pass are a multiple of H, so a thread's head is fixed
+// (rl % H) and its token advances by R / H per pass (no 64-bit division in
+// the loop).
 template <int NB, bool PT, int G, int BITS, bool KFIX>
 __global__ void __launch_bounds__(kThreads)
-pack_compact_kernel(const uint16_t* __restrict__ x, int64_t nrows, int H, hkv_nuq_scales sc,
-                    uint8_t* __restrict__ packed, int32_t* __restrict__ row_ptr,
-                    uint8_t* __restrict__ col, uint16_t* __restrict__ val, uint32_t cap,
-                    PackWs* ws, uint64_t* st, uint32_t ntiles) {
-  constexpr int R = kThreads / G;
-  constexpr int TR = R * kPasses;
+pack_stage_kernel(const uint16_t* __restrict__ x, int64_t nrows, int H, hkv_nuq_scales sc,
+                  uint8_t* __restrict__ packed, int32_t* __restrict__ row_ptr,
+                  uint8_t* __restrict__ scol, uint16_t* __restrict__ sval,
+                  uint32_t* __restrict__ tile_cnt, uint32_t ntiles) {
+  constexpr int R = kThreads / G;   // rows per pass
+  constexpr int TR = R * kPasses;   // rows per tile
   constexpr int D = 8 * G;
   constexpr int RB = D * BITS / 8;  // packed bytes per row
-  __shared__ uint32_t s_ticket, s_epoch, s_off;
-  __shared__ uint32_t s_wave[kPasses][kThreads / 64];
+  constexpr int NW = kThreads / 64;
+  // Per-token tables of the tile's rows are staged in LDS when they fit in
+  // 16 KiB (D >= 128); otherwise each row reads its table through L1.
+  constexpr bool STAGE = PT && TR * 80 <= 16384;
+  __shared__ uint32_t s_wave[kPasses][NW];
+  __shared__ uint4 s_tab[STAGE ? TR * 5 : 1];
 
   const int tid = threadIdx.x, cg = tid % G, rl = tid / G;
-  const int lane = tid & 63, wv = tid >> 6;
-  if (tid == 0) {
-    const uint32_t tk = atomicAdd(&ws->ticket, 1u);
-    s_ticket = tk;
-    s_epoch = __hip_atomic_load(&ws->epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (tk == ntiles - 1) atomicExch(&ws->ticket, 0u);  // last ticket handed out
-  }
-  __syncthreads();
-  const uint32_t tile = s_ticket, epoch = s_epoch;
-  const int64_t r0 = (int64_t)tile * TR;
+  const int wv = tid >> 6, lane = tid & 63;
   const hkv_table_t* tabs = (const hkv_table_t*)sc.tables;
   const SlowInfo si = slow_info(sc);
+  const int hfix = KFIX ? rl % H : 0;
 
   Search2<NB> S[PT ? 1 : 4];
-  int64_t tab0 = 0;
   if constexpr (!PT && KFIX) {
-    tab0 = (int64_t)(rl % H) * D + 8 * cg;
+    const int64_t tab0 = (int64_t)hfix * D + 8 * cg;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       load_search_pair<NB>(tabs + tab0 + 2 * j, tabs + tab0 + 2 * j + 1, S[j]);
   }
 
-  uint32_t xs[kPasses][4];
-  uint32_t mk[kPasses];
-  uint32_t excl[kPasses];
-#pragma unroll
-  for (int p = 0; p < kPasses; ++p) {
-    const int64_t r = r0 + p * R + rl;
-    mk[p] = 0;
-    xs[p][0] = xs[p][1] = xs[p][2] = xs[p][3] = 0;
-    if (r < nrows) {
-      const int64_t t = r / H;
-      const int h = (int)(r - t * H);
-      if constexpr (PT) {
-        tab0 = (int64_t)h * sc.rows + clamp_row(token_pos(sc, t), sc.rows);
-        load_search_bcast<NB>(tabs + tab0, S[0]);
-      } else if constexpr (!KFIX) {
-        tab0 = (int64_t)h * D + 8 * cg;
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          load_search_pair<NB>(tabs + tab0 + 2 * j, tabs + tab0 + 2 * j + 1, S[j]);
-      }
-      const uint4 xv = *reinterpret_cast<const uint4*>(x + r * D + 8 * cg);
-      uint32_t c[4], om[4];
-      quant8<NB, PT>(xv, S, si, tab0, c, om);
-      if constexpr (BITS == 4) {
-        *reinterpret_cast<uint32_t*>(packed + r * RB + 4 * cg) = pack_nibbles(c);
-      } else {
-        *reinterpret_cast<uint16_t*>(packed + r * RB + 2 * cg) = (uint16_t)pack_crumbs(c);
-      }
-      mk[p] = mask_bits(om);
-      xs[p][0] = xv.x; xs[p][1] = xv.y; xs[p][2] = xv.z; xs[p][3] = xv.w;
-    }
-    // wave-inclusive scan of this pass's counts
-    const uint32_t cnt = __builtin_popcount(mk[p]);
-    uint32_t inc = cnt;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const uint32_t y = __shfl_up(inc, o, 64);
-      if (lane >= o) inc += y;
-    }
-    excl[p] = inc - cnt;
-    if (lane == 63) s_wave[p][wv] = inc;
-  }
-  __syncthreads();
-
-  // Tile-local offsets in (pass, wave) order, and the tile total.
-  uint32_t base[kPasses];
-  uint32_t total = 0;
-#pragma unroll
-  for (int p = 0; p < kPasses; ++p) {
-#pragma unroll
-    for (int w = 0; w < kThreads / 64; ++w) {
-      if (w == wv) base[p] = total;
-      total += s_wave[p][w];
-    }
-  }
-
-  if (tid == 0) {
-    uint32_t off = 0;
-    if (tile == 0) {
-      publish(st, tile, status_word(epoch, kFlagPrefix, total));
-    } else {
-      publish(st, tile, status_word(epoch, kFlagAgg, total));
-      off = look_back(st, tile, epoch, ws);
-      publish(st, tile, status_word(epoch, kFlagPrefix, off + total));
-    }
-    s_off = off;
-  }
-  __syncthreads();
-  const uint32_t off = s_off;
-
-#pragma unroll
-  for (int p = 0; p < kPasses; ++p) {
-    const int64_t r = r0 + p * R + rl;
-    if (r >= nrows) continue;
-    uint32_t pos = off + base[p] + excl[p];
-    if (cg == 0) row_ptr[r] = (int32_t)pos;
-    const uint32_t m = mk[p];
-    if (m) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        if ((m >> e) & 1u) {
-          if (pos < cap) {
-            col[pos] = (uint8_t)(8 * cg + e);
-            val[pos] = (uint16_t)(xs[p][e >> 1] >> (16 * (e & 1)));
-          }
-          ++pos;
-        }
-      }
-    }
-  }
-  if (tile == ntiles - 1 && tid == 0) row_ptr[nrows] = (int32_t)(off + total);
-
-  if (tid == 0) {
-    __threadfence();
-    const uint32_t prev = atomicAdd(&ws->done, 1u);
-    if (prev == ntiles - 1) {
-      atomicExch(&ws->done, 0u);
-      __hip_atomic_store(&ws->epoch, epoch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
-}
-
-// Compact unpack.  Blocks loop over tiles of rows; each tile is dequantised
-// into LDS, the tile's CSR entries are scattered into it, and it is written
-// out with 128-bit stores.  Per-channel fp16 poles for all heads sit in LDS
-// for the block's lifetime when they fit (KLDS), else are read through L1.
-template <bool PT, int G, int BITS, bool KLDS>
-__global__ void __launch_bounds__(kThreads)
-unpack_compact_kernel(const uint8_t* __restrict__ packed, const int32_t* __restrict__ row_ptr,
-                      const uint8_t* __restrict__ col, const uint16_t* __restrict__ val,
-                      int64_t nrows, int H, hkv_nuq_scales sc, uint16_t* __restrict__ out,
-                      uint32_t ntiles) {
-  constexpr int R = kThreads / G;
-  constexpr int TR = R * kPasses;
-  constexpr int D = 8 * G;
-  constexpr int RB = D * BITS / 8;
-  extern __shared__ uint16_t dyn[];
-  uint16_t* tile_lds = dyn;                 // TR * D
-  uint16_t* pole_lds = dyn + TR * D;        // PT: TR*16; K: H*16*D when KLDS
-  const int tid = threadIdx.x, cg = tid % G, rl = tid / G;
-  const hkv_table_t* tabs = (const hkv_table_t*)sc.tables;
-
-  if constexpr (!PT && KLDS) {
-    for (int i = tid; i < H * 16 * D; i += kThreads) {
-      const int d = i % D, l = (i / D) % 16, h = i / (16 * D);
-      pole_lds[i] = tabs[(int64_t)h * D + d].pf16[l];
-    }
-  }
-
   for (uint32_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
     const int64_t r0 = (int64_t)tile * TR;
-    __syncthreads();  // previous tile fully written out; K poles staged
-    if constexpr (PT) {
-      for (int i = tid; i < TR * 16; i += kThreads) {
-        const int rr = i / 16, l = i % 16;
+    const int64_t t0 = KFIX ? r0 / H : 0;  // token of row r0 (H divides r0)
+    uint32_t xs[kPasses][4];
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p) {
+      const int64_t r = r0 + p * R + rl;
+      uint4 v = make_uint4(0u, 0u, 0u, 0u);
+      if (r < nrows) v = *reinterpret_cast<const uint4*>(x + r * D + 8 * cg);
+      xs[p][0] = v.x; xs[p][1] = v.y; xs[p][2] = v.z; xs[p][3] = v.w;
+    }
+    if constexpr (STAGE) {
+      for (int i = tid; i < TR * 5; i += kThreads) {
+        const int rr = i / 5, part = i - rr * 5;
         const int64_t r = r0 + rr;
         if (r < nrows) {
           const int64_t t = r / H;
           const int h = (int)(r - t * H);
           const int64_t tab = (int64_t)h * sc.rows + clamp_row(token_pos(sc, t), sc.rows);
-          pole_lds[i] = tabs[tab].pf16[l];
+          s_tab[i] = reinterpret_cast<const uint4*>(tabs + tab)[part];
         }
       }
       __syncthreads();
     }
+
+    uint32_t mk[kPasses], excl[kPasses];
 #pragma unroll
     for (int p = 0; p < kPasses; ++p) {
       const int rr = p * R + rl;
       const int64_t r = r0 + rr;
+      mk[p] = 0;
+      if (r < nrows) {
+        int64_t t;
+        int h;
+        if constexpr (KFIX) {
+          t = t0 + p * (R / H) + rl / H;
+          h = hfix;
+        } else {
+          t = r / H;
+          h = (int)(r - t * H);
+        }
+        const uint4 xv = make_uint4(xs[p][0], xs[p][1], xs[p][2], xs[p][3]);
+        uint32_t c[4], om[4];
+        if constexpr (PT) {
+          const int64_t tab = (int64_t)h * sc.rows + clamp_row(token_pos(sc, t), sc.rows);
+          if constexpr (STAGE) load_search_bcast<NB>(reinterpret_cast<const hkv_table_t*>(s_tab + rr * 5), S[0]);
+          else load_search_bcast<NB>(tabs + tab, S[0]);
+          quant8<NB, PT>(xv, S, si, RowTab{tab}, c, om);
+        } else {
+          const int64_t tab0 = (int64_t)h * D + 8 * cg;
+          if constexpr (!KFIX) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              load_search_pair<NB>(tabs + tab0 + 2 * j, tabs + tab0 + 2 * j + 1, S[j]);
+          }
+          quant8<NB, PT>(xv, S, si, ChanTab{tab0}, c, om);
+        }
+        if constexpr (BITS == 4) {
+          *reinterpret_cast<uint32_t*>(packed + r * RB + 4 * cg) = pack_nibbles(c);
+        } else {
+          *reinterpret_cast<uint16_t*>(packed + r * RB + 2 * cg) = (uint16_t)pack_crumbs(c);
+        }
+        mk[p] = mask_bits(om);
+      }
+      uint32_t tot;
+      excl[p] = wave_excl_count(__builtin_popcount(mk[p]), &tot);
+      if (lane == 0) s_wave[p][wv] = tot;
+    }
+    __syncthreads();
+
+    // Offsets within the tile in (pass, wave, lane) order = (row, col) order.
+    uint32_t total = 0;
+    const int64_t sbase = r0 * D;  // the tile's staging region
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p) {
+      uint32_t before = 0;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) before += w < wv ? s_wave[p][w] : 0u;
+      uint32_t pos = total + before + excl[p];
+#pragma unroll
+      for (int w = 0; w < NW; ++w) total += s_wave[p][w];
+      const int64_t r = r0 + p * R + rl;
+      if (r >= nrows) continue;
+      if (cg == 0) row_ptr[r] = (int32_t)pos;
+      uint32_t m = mk[p];
+      while (m) {
+        const int e = __builtin_ctz(m);
+        m &= m - 1u;
+        const uint32_t w = pick4(xs[p][0], xs[p][1], xs[p][2], xs[p][3], e >> 1);
+        scol[sbase + pos] = (uint8_t)(8 * cg + e);
+        sval[sbase + pos] = (uint16_t)(w >> (16 * (e & 1)));
+        ++pos;
+      }
+    }
+    if (tid == 0) tile_cnt[tile] = total;
+    __syncthreads();  // s_wave / s_tab are reused by the next tile
+  }
+}
+
+// Tile offsets from the tile counts, then the dense CSR.  One wave per tile
+// (kCompactTiles per block); a block first sums the counts of all tiles before
+// its own with every thread loading in parallel.
+constexpr int kCompactTiles = kThreads / 64;
+constexpr int kCopyUnroll = 4;
+
+__global__ void __launch_bounds__(kThreads)
+compact_kernel(const uint32_t* __restrict__ tile_cnt, uint32_t ntiles, int64_t TR, int64_t D,
+               int64_t nrows, const uint8_t* __restrict__ scol, const uint16_t* __restrict__ sval,
+               int32_t* __restrict__ row_ptr, uint8_t* __restrict__ col,
+               uint16_t* __restrict__ val, uint32_t cap) {
+  __shared__ uint32_t s_red[kThreads / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const uint32_t t0 = blockIdx.x * kCompactTiles;
+  uint32_t acc = 0;
+  for (uint32_t i = tid; i < t0; i += kThreads) acc += tile_cnt[i];
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, 64);
+  if (lane == 0) s_red[wv] = acc;
+  __syncthreads();
+  uint32_t base = 0;
+#pragma unroll
+  for (int w = 0; w < kThreads / 64; ++w) base += s_red[w];
+  const uint32_t tile = t0 + wv;
+  if (tile >= ntiles) return;
+  // counts of the block's earlier tiles, and this tile's
+  const uint32_t mine = lane < kCompactTiles && t0 + lane < ntiles ? tile_cnt[t0 + lane] : 0u;
+#pragma unroll
+  for (int w = 0; w < kCompactTiles; ++w) {
+    const uint32_t c = __shfl(mine, w, 64);
+    if (w < wv) base += c;
+  }
+  const uint32_t n = __shfl(mine, wv, 64);
+  const int64_t r0 = (int64_t)tile * TR;
+  for (int64_t i = lane; i < TR; i += 64) {
+    const int64_t r = r0 + i;
+    if (r < nrows) row_ptr[r] += (int32_t)base;
+  }
+  if (tile == ntiles - 1 && lane == 0) row_ptr[nrows] = (int32_t)(base + n);
+  const int64_t src = r0 * D;
+  for (uint32_t i0 = 0; i0 < n; i0 += 64 * kCopyUnroll) {
+    uint8_t cv[kCopyUnroll];
+    uint16_t vv[kCopyUnroll];
+#pragma unroll
+    for (int u = 0; u < kCopyUnroll; ++u) {
+      const uint32_t i = i0 + u * 64 + lane;
+      if (i < n) { cv[u] = scol[src + i]; vv[u] = sval[src + i]; }
+    }
+#pragma unroll
+    for (int u = 0; u < kCopyUnroll; ++u) {
+      const uint32_t i = i0 + u * 64 + lane;
+      if (i < n && base + i < cap) { col[base + i] = cv[u]; val[base + i] = vv[u]; }
+    }
+  }
+}
+
+// Compact unpack.  Each wave owns a private LDS segment of kUPasses * RW
+// rows (RW = 64 / G rows per pass): it dequantises its rows into the
+// segment, scatters the rows' CSR entries into it, and writes the rows out
+// with 128-bit stores.  Only wave-level ordering is needed between those
+// steps (LDS operations of one wave complete in order), so waves proceed
+// independently.  Blocks are persistent and loop over wave tiles.  Per-channel
+// poles of all heads are staged once per block in LDS as [h][level][d] fp16
+// when they fit (KLDS); per-token poles are staged per row.  CSR entries at or
+// beyond `cap` (the col/val capacity) are never read.
+constexpr int kUPasses = 4;
+
+HKV_DEV void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <bool PT, int G, int BITS, bool KLDS>
+__global__ void __launch_bounds__(kThreads)
+unpack_compact_kernel(const uint8_t* __restrict__ packed, const int32_t* __restrict__ row_ptr,
+                      const uint8_t* __restrict__ col, const uint16_t* __restrict__ val,
+                      int64_t cap, int64_t nrows, int H, hkv_nuq_scales sc,
+                      uint16_t* __restrict__ out, int64_t nwtiles) {
+  constexpr int D = 8 * G;
+  constexpr int RW = 64 / G;           // rows per wave per pass
+  constexpr int WR = RW * kUPasses;    // rows per wave tile
+  constexpr int RB = D * BITS / 8;     // packed bytes per row
+  constexpr int NW = kThreads / 64;
+  extern __shared__ uint16_t dyn[];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int cg = lane % G, rw = lane / G;
+  uint16_t* seg = dyn + wv * (WR * D);
+  uint16_t* prow = dyn + NW * WR * D + wv * (WR * 16);  // PT: poles of each row
+  uint16_t* kp = dyn + NW * WR * D;                     // KLDS: [h][16][D]
+  const hkv_table_t* tabs = (const hkv_table_t*)sc.tables;
+
+  if constexpr (!PT && KLDS) {
+    for (int i = tid; i < H * D; i += kThreads) {
+      const uint4* src = reinterpret_cast<const uint4*>(tabs[i].pf16);
+      const uint4 a = src[0], b = src[1];
+      const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+      const int h = i / D, d = i - h * D;
+#pragma unroll
+      for (int l = 0; l < 16; ++l) kp[(h * 16 + l) * D + d] = (uint16_t)(w[l >> 1] >> (16 * (l & 1)));
+    }
+    __syncthreads();
+  }
+
+  const int64_t nwaves = (int64_t)gridDim.x * NW;
+  for (int64_t wt = (int64_t)blockIdx.x * NW + wv; wt < nwtiles; wt += nwaves) {
+    const int64_t r0 = wt * WR;
+    uint32_t cw[kUPasses];
+    int32_t ra[kUPasses], rb[kUPasses];
+#pragma unroll
+    for (int p = 0; p < kUPasses; ++p) {
+      const int64_t r = r0 + p * RW + rw;
+      cw[p] = 0;
+      ra[p] = rb[p] = 0;
+      if (r < nrows) {
+        if constexpr (BITS == 4) cw[p] = *reinterpret_cast<const uint32_t*>(packed + r * RB + 4 * cg);
+        else cw[p] = *reinterpret_cast<const uint16_t*>(packed + r * RB + 2 * cg);
+        ra[p] = row_ptr[r];
+        rb[p] = row_ptr[r + 1];
+      }
+    }
+    if constexpr (PT) {
+#pragma unroll
+      for (int p = 0; p < kUPasses; ++p) {
+        const int64_t r = r0 + p * RW + rw;
+        if (r < nrows && cg < 2) {
+          const int64_t t = r / H;
+          const int h = (int)(r - t * H);
+          const int64_t tab = (int64_t)h * sc.rows + clamp_row(token_pos(sc, t), sc.rows);
+          const uint4 v = reinterpret_cast<const uint4*>(tabs[tab].pf16)[cg];
+          *reinterpret_cast<uint4*>(prow + (p * RW + rw) * 16 + 8 * cg) = v;
+        }
+      }
+      wave_sync();
+    }
+#pragma unroll
+    for (int p = 0; p < kUPasses; ++p) {
+      const int rr = p * RW + rw;
+      const int64_t r = r0 + rr;
       if (r >= nrows) continue;
       const int h = (int)(r % H);
-      uint32_t cw;
-      if constexpr (BITS == 4) cw = *reinterpret_cast<const uint32_t*>(packed + r * RB + 4 * cg);
-      else cw = *reinterpret_cast<const uint16_t*>(packed + r * RB + 2 * cg);
       uint32_t res[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -262,38 +314,38 @@ unpack_compact_kernel(const uint8_t* __restrict__ packed, const int32_t* __restr
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
           const int e = 2 * j + k;
-          const uint32_t c = (cw >> (BITS * e)) & ((1u << BITS) - 1u);
+          const uint32_t c = (cw[p] >> (BITS * e)) & ((1u << BITS) - 1u);
           uint16_t v;
-          if constexpr (PT) v = pole_lds[rr * 16 + c];
-          else if constexpr (KLDS) v = pole_lds[(h * 16 + c) * D + 8 * cg + e];
+          if constexpr (PT) v = prow[rr * 16 + c];
+          else if constexpr (KLDS) v = kp[(h * 16 + c) * D + 8 * cg + e];
           else v = tabs[(int64_t)h * D + 8 * cg + e].pf16[c];
           pr |= (uint32_t)v << (16 * k);
         }
         res[j] = pr;
       }
-      *reinterpret_cast<uint4*>(tile_lds + rr * D + 8 * cg) = make_uint4(res[0], res[1], res[2], res[3]);
+      *reinterpret_cast<uint4*>(seg + rr * D + 8 * cg) = make_uint4(res[0], res[1], res[2], res[3]);
     }
-    __syncthreads();
+    wave_sync();
 #pragma unroll
-    for (int p = 0; p < kPasses; ++p) {
-      const int rr = p * R + rl;
-      const int64_t r = r0 + rr;
-      if (r >= nrows) continue;
-      const int32_t a = row_ptr[r], b = row_ptr[r + 1];
-      for (int32_t i = a + cg; i < b; i += G) {
+    for (int p = 0; p < kUPasses; ++p) {
+      const int rr = p * RW + rw;
+      const int32_t lo = ra[p] > 0 ? ra[p] : 0;
+      const int32_t hi = (int64_t)rb[p] < cap ? rb[p] : (int32_t)cap;
+      for (int32_t i = lo + cg; i < hi; i += G) {
         const uint32_t d = col[i];
-        if (d < (uint32_t)D) tile_lds[rr * D + d] = val[i];
+        if (d < (uint32_t)D) seg[rr * D + d] = val[i];
       }
     }
-    __syncthreads();
+    wave_sync();
 #pragma unroll
-    for (int p = 0; p < kPasses; ++p) {
-      const int rr = p * R + rl;
+    for (int p = 0; p < kUPasses; ++p) {
+      const int rr = p * RW + rw;
       const int64_t r = r0 + rr;
       if (r >= nrows) continue;
       *reinterpret_cast<uint4*>(out + r * D + 8 * cg) =
-          *reinterpret_cast<const uint4*>(tile_lds + rr * D + 8 * cg);
+          *reinterpret_cast<const uint4*>(seg + rr * D + 8 * cg);
     }
+    wave_sync();
   }
 }
 
@@ -301,48 +353,16 @@ __global__ void write_zero_rowptr(int32_t* row_ptr) { row_ptr[0] = 0; }
 
 bool pow2_G(int D) { return D % 8 == 0 && D >= 8 && D <= 256 && ((D / 8) & (D / 8 - 1)) == 0; }
 
-int64_t tiles_for(int64_t nrows, int D) {
+PackLayout pack_layout(int64_t nrows, int D) {
+  PackLayout L;
   const int64_t TR = (int64_t)(kThreads / (D / 8)) * kPasses;
-  return (nrows + TR - 1) / TR;
-}
-
-template <int NB, bool PT, int BITS, bool KFIX>
-void launch_pack_g(int G, unsigned ntiles, hipStream_t s, const uint16_t* x, int64_t nrows, int H,
-                   const hkv_nuq_scales& sc, uint8_t* pk, int32_t* rp, uint8_t* col,
-                   uint16_t* val, uint32_t cap, PackWs* ws, uint64_t* st) {
-  switch (G) {
-#define HKV_CASE(g)                                                                         \
-  case g:                                                                                   \
-    hipLaunchKernelGGL((pack_compact_kernel<NB, PT, g, BITS, KFIX>), dim3(ntiles),          \
-                       dim3(kThreads), 0, s, x, nrows, H, sc, pk, rp, col, val, cap, ws, st, \
-                       ntiles);                                                             \
-    break;
-    HKV_CASE(1) HKV_CASE(2) HKV_CASE(4) HKV_CASE(8) HKV_CASE(16) HKV_CASE(32)
-#undef HKV_CASE
-  }
-}
-
-template <int NB, bool PT, int BITS>
-void launch_pack_k(bool kfix, int G, unsigned ntiles, hipStream_t s, const uint16_t* x,
-                   int64_t nrows, int H, const hkv_nuq_scales& sc, uint8_t* pk, int32_t* rp,
-                   uint8_t* col, uint16_t* val, uint32_t cap, PackWs* ws, uint64_t* st) {
-  if (kfix) launch_pack_g<NB, PT, BITS, true>(G, ntiles, s, x, nrows, H, sc, pk, rp, col, val, cap, ws, st);
-  else launch_pack_g<NB, PT, BITS, false>(G, ntiles, s, x, nrows, H, sc, pk, rp, col, val, cap, ws, st);
-}
-
-template <bool PT, int BITS, bool KLDS>
-void launch_unpack_g(int G, unsigned grid, size_t lds, hipStream_t s, const uint8_t* pk,
-                     const int32_t* rp, const uint8_t* col, const uint16_t* val, int64_t nrows,
-                     int H, const hkv_nuq_scales& sc, uint16_t* out, uint32_t ntiles) {
-  switch (G) {
-#define HKV_CASE(g)                                                                            \
-  case g:                                                                                      \
-    hipLaunchKernelGGL((unpack_compact_kernel<PT, g, BITS, KLDS>), dim3(grid), dim3(kThreads), \
-                       lds, s, pk, rp, col, val, nrows, H, sc, out, ntiles);                   \
-    break;
-    HKV_CASE(1) HKV_CASE(2) HKV_CASE(4) HKV_CASE(8) HKV_CASE(16) HKV_CASE(32)
-#undef HKV_CASE
-  }
+  L.ntiles = (nrows + TR - 1) / TR;
+  L.tile_elems = TR * D;
+  L.cnt_off = 256;
+  L.col_off = L.cnt_off + align256(sizeof(uint32_t) * (size_t)L.ntiles);
+  L.val_off = L.col_off + align256((size_t)(L.ntiles * L.tile_elems));
+  L.bytes = L.val_off + sizeof(uint16_t) * (size_t)(L.ntiles * L.tile_elems);
+  return L;
 }
 
 int num_cus() {
@@ -356,11 +376,88 @@ int num_cus() {
   return n;
 }
 
+// Persistent grid: as many blocks as fit on the device at once (at most one
+// per tile).
+template <typename K>
+unsigned resident_grid(K kernel, int64_t ntiles) {
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kThreads, 0) != hipSuccess ||
+      per_cu < 1)
+    per_cu = 1;
+  return (unsigned)std::min<int64_t>(ntiles, (int64_t)per_cu * num_cus());
+}
+
+struct PackArgs {
+  const uint16_t* x;
+  int64_t nrows;
+  int H;
+  hkv_nuq_scales sc;
+  uint8_t* pk;
+  int32_t* rp;
+  uint8_t* scol;
+  uint16_t* sval;
+  uint32_t* cnt;
+  uint32_t ntiles;
+  hipStream_t s;
+};
+
+template <int NB, bool PT, int G, int BITS, bool KFIX>
+void launch_stage(const PackArgs& a) {
+  auto k = pack_stage_kernel<NB, PT, G, BITS, KFIX>;
+  hipLaunchKernelGGL(k, dim3(resident_grid(k, a.ntiles)), dim3(kThreads), 0, a.s, a.x, a.nrows,
+                     a.H, a.sc, a.pk, a.rp, a.scol, a.sval, a.cnt, a.ntiles);
+}
+
+template <int NB, bool PT, int BITS, bool KFIX>
+void launch_stage_g(int G, const PackArgs& a) {
+  switch (G) {
+    case 1: launch_stage<NB, PT, 1, BITS, KFIX>(a); break;
+    case 2: launch_stage<NB, PT, 2, BITS, KFIX>(a); break;
+    case 4: launch_stage<NB, PT, 4, BITS, KFIX>(a); break;
+    case 8: launch_stage<NB, PT, 8, BITS, KFIX>(a); break;
+    case 16: launch_stage<NB, PT, 16, BITS, KFIX>(a); break;
+    default: launch_stage<NB, PT, 32, BITS, KFIX>(a); break;
+  }
+}
+
+template <int NB, bool PT, int BITS>
+void launch_stage_k(bool kfix, int G, const PackArgs& a) {
+  if (kfix) launch_stage_g<NB, PT, BITS, true>(G, a);
+  else launch_stage_g<NB, PT, BITS, false>(G, a);
+}
+
+template <bool PT, int BITS>
+void launch_stage_nb(int nb, bool kfix, int G, const PackArgs& a) {
+  switch (nb) {
+    case 0: launch_stage_k<0, PT, BITS>(kfix, G, a); break;
+    case 1: launch_stage_k<1, PT, BITS>(kfix, G, a); break;
+    case 2: launch_stage_k<2, PT, BITS>(kfix, G, a); break;
+    case 3: if constexpr (BITS == 4) launch_stage_k<3, PT, BITS>(kfix, G, a); break;
+    default: if constexpr (BITS == 4) launch_stage_k<4, PT, BITS>(kfix, G, a); break;
+  }
+}
+
+template <bool PT, int BITS, bool KLDS>
+void launch_unpack_g(int G, unsigned grid, size_t lds, hipStream_t s, const uint8_t* pk,
+                     const int32_t* rp, const uint8_t* col, const uint16_t* val, int64_t cap,
+                     int64_t nrows, int H, const hkv_nuq_scales& sc, uint16_t* out,
+                     int64_t nwtiles) {
+  switch (G) {
+#define HKV_CASE(g)                                                                            \
+  case g:                                                                                      \
+    hipLaunchKernelGGL((unpack_compact_kernel<PT, g, BITS, KLDS>), dim3(grid), dim3(kThreads), \
+                       lds, s, pk, rp, col, val, cap, nrows, H, sc, out, nwtiles);             \
+    break;
+    HKV_CASE(1) HKV_CASE(2) HKV_CASE(4) HKV_CASE(8) HKV_CASE(16) HKV_CASE(32)
+#undef HKV_CASE
+  }
+}
+
 }  // namespace
 
 extern "C" size_t hkv_nuq_pack_compact_workspace_bytes(int64_t T, int H, int D) {
   if (T < 0 || H < 1 || !pow2_G(D)) return 0;
-  return sizeof(PackWs) + sizeof(uint64_t) * (size_t)tiles_for(T * H, D);
+  return pack_layout(T * H, D).bytes;
 }
 
 extern "C" int hkv_nuq_pack_compact(const void* values, int64_t T, int H, int D, int bits,
@@ -385,102 +482,89 @@ extern "C" int hkv_nuq_pack_compact(const void* values, int64_t T, int H, int D,
   }
   if (!values || !packed || (capacity > 0 && (!col || !val))) return HKV_ERR_ARG;
   if (((uintptr_t)values & 15u) || ((uintptr_t)packed & 3u)) return HKV_ERR_ARG;
-  const size_t need = hkv_nuq_pack_compact_workspace_bytes(T, H, D);
-  if (!workspace || workspace_bytes < need) return HKV_ERR_WORKSPACE;
+  const PackLayout lay = pack_layout(nrows, D);
+  if (!workspace || workspace_bytes < lay.bytes || ((uintptr_t)workspace & 255u))
+    return HKV_ERR_WORKSPACE;
   const int G = D / 8, R = kThreads / G;
-  const unsigned ntiles = (unsigned)tiles_for(nrows, D);
+  char* ws = (char*)workspace;
+  PackArgs a;
+  a.x = (const uint16_t*)values;
+  a.nrows = nrows;
+  a.H = H;
+  a.sc = *scales;
+  a.pk = (uint8_t*)packed;
+  a.rp = row_ptr;
+  a.scol = (uint8_t*)(ws + lay.col_off);
+  a.sval = (uint16_t*)(ws + lay.val_off);
+  a.cnt = (uint32_t*)(ws + lay.cnt_off);
+  a.ntiles = (uint32_t)lay.ntiles;
+  a.s = s;
   const bool kfix = (R % H) == 0;
-  const uint32_t cap = (uint32_t)std::min<int64_t>(capacity, 0x7fffffff);
-  PackWs* ws = (PackWs*)workspace;
-  uint64_t* st = (uint64_t*)((char*)workspace + sizeof(PackWs));
-  const hkv_nuq_scales sc = *scales;
-  const int nb = nb_for_levels_host(sc.levels);
-  auto x = (const uint16_t*)values;
-  auto pk = (uint8_t*)packed;
-#define HKV_ARGS kfix, G, ntiles, s, x, nrows, H, sc, pk, row_ptr, col, val, cap, ws, st
+  const int nb = nb_for_levels_host(a.sc.levels);
   if (bits == 4) {
-    if (sc.per_token) {
-      switch (nb) {
-        case 0: launch_pack_k<0, true, 4>(HKV_ARGS); break;
-        case 1: launch_pack_k<1, true, 4>(HKV_ARGS); break;
-        case 2: launch_pack_k<2, true, 4>(HKV_ARGS); break;
-        case 3: launch_pack_k<3, true, 4>(HKV_ARGS); break;
-        default: launch_pack_k<4, true, 4>(HKV_ARGS); break;
-      }
-    } else {
-      switch (nb) {
-        case 0: launch_pack_k<0, false, 4>(HKV_ARGS); break;
-        case 1: launch_pack_k<1, false, 4>(HKV_ARGS); break;
-        case 2: launch_pack_k<2, false, 4>(HKV_ARGS); break;
-        case 3: launch_pack_k<3, false, 4>(HKV_ARGS); break;
-        default: launch_pack_k<4, false, 4>(HKV_ARGS); break;
-      }
-    }
+    if (a.sc.per_token) launch_stage_nb<true, 4>(nb, kfix, G, a);
+    else launch_stage_nb<false, 4>(nb, kfix, G, a);
   } else {
-    if (sc.per_token) {
-      switch (nb) {
-        case 0: launch_pack_k<0, true, 2>(HKV_ARGS); break;
-        case 1: launch_pack_k<1, true, 2>(HKV_ARGS); break;
-        default: launch_pack_k<2, true, 2>(HKV_ARGS); break;
-      }
-    } else {
-      switch (nb) {
-        case 0: launch_pack_k<0, false, 2>(HKV_ARGS); break;
-        case 1: launch_pack_k<1, false, 2>(HKV_ARGS); break;
-        default: launch_pack_k<2, false, 2>(HKV_ARGS); break;
-      }
-    }
+    if (a.sc.per_token) launch_stage_nb<true, 2>(nb, kfix, G, a);
+    else launch_stage_nb<false, 2>(nb, kfix, G, a);
   }
-#undef HKV_ARGS
+  HKV_CHECK_LAUNCH();
+  const uint32_t cap = (uint32_t)std::min<int64_t>(capacity, 0x7fffffff);
+  const unsigned cgrid = (unsigned)((lay.ntiles + kCompactTiles - 1) / kCompactTiles);
+  hipLaunchKernelGGL(compact_kernel, dim3(cgrid), dim3(kThreads), 0, s, a.cnt, a.ntiles,
+                     (int64_t)R * kPasses, (int64_t)D, nrows, a.scol, a.sval, row_ptr, col, val,
+                     cap);
   HKV_CHECK_LAUNCH();
   return HKV_OK;
 }
 
 extern "C" int hkv_nuq_pack_compact_status(const void* workspace, void* stream) {
-  if (!workspace) return HKV_ERR_ARG;
-  uint32_t err = 0;
-  if (hipMemcpyAsync(&err, (const char*)workspace + offsetof(PackWs, err), sizeof(err),
-                     hipMemcpyDeviceToHost, (hipStream_t)stream) != hipSuccess)
-    return -1;
-  if (hipStreamSynchronize((hipStream_t)stream) != hipSuccess) return -1;
-  return (int)err;
+  // The two-kernel pack has no device-side failure mode; kept for callers
+  // that check it.
+  (void)stream;
+  return workspace ? 0 : HKV_ERR_ARG;
 }
 
 extern "C" int hkv_nuq_unpack_compact(const void* packed, const int32_t* row_ptr,
-                                      const uint8_t* col, const uint16_t* val, int64_t T, int H,
-                                      int D, int bits, const hkv_nuq_scales* scales, void* out,
-                                      void* stream) {
+                                      const uint8_t* col, const uint16_t* val, int64_t capacity,
+                                      int64_t T, int H, int D, int bits,
+                                      const hkv_nuq_scales* scales, void* out, void* stream) {
   if (!scales || !scales->tables) return HKV_ERR_ARG;
   if (bits != 2 && bits != 4) return HKV_ERR_ARG;
   if (scales->per_token && scales->rows < 1) return HKV_ERR_SHAPE;
   if (T < 0 || H < 1 || !pow2_G(D)) return HKV_ERR_SHAPE;
+  if (capacity < 0) return HKV_ERR_ARG;
   if (T == 0) return HKV_OK;
-  if (!packed || !row_ptr || !out) return HKV_ERR_ARG;
+  if (!packed || !row_ptr || !out || (capacity > 0 && (!col || !val))) return HKV_ERR_ARG;
   if (((uintptr_t)out & 15u) || ((uintptr_t)packed & 3u)) return HKV_ERR_ARG;
   hipStream_t s = (hipStream_t)stream;
   const int64_t nrows = T * H;
   const int G = D / 8;
-  const int TR = (kThreads / G) * kPasses;
-  const unsigned ntiles = (unsigned)tiles_for(nrows, D);
-  const unsigned grid = (unsigned)std::min<int64_t>(ntiles, (int64_t)num_cus() * 8);
+  constexpr int NW = kThreads / 64;
+  const int64_t WR = (int64_t)(64 / G) * kUPasses;  // rows per wave tile
+  const int64_t nwtiles = (nrows + WR - 1) / WR;
+  const unsigned grid =
+      (unsigned)std::min<int64_t>((nwtiles + NW - 1) / NW, (int64_t)num_cus() * 8);
   const hkv_nuq_scales sc = *scales;
-  const size_t tile_bytes = (size_t)TR * D * 2;
+  const size_t seg_bytes = (size_t)NW * WR * D * 2;
   const size_t kpole_bytes = (size_t)H * 16 * D * 2;
   auto pk = (const uint8_t*)packed;
   auto o = (uint16_t*)out;
+#define HKV_UARGS G, grid, lds, s, pk, row_ptr, col, val, capacity, nrows, H, sc, o, nwtiles
   if (sc.per_token) {
-    const size_t lds = tile_bytes + (size_t)TR * 16 * 2;
-    if (bits == 4) launch_unpack_g<true, 4, false>(G, grid, lds, s, pk, row_ptr, col, val, nrows, H, sc, o, ntiles);
-    else launch_unpack_g<true, 2, false>(G, grid, lds, s, pk, row_ptr, col, val, nrows, H, sc, o, ntiles);
-  } else if (tile_bytes + kpole_bytes <= 64 * 1024) {
-    const size_t lds = tile_bytes + kpole_bytes;
-    if (bits == 4) launch_unpack_g<false, 4, true>(G, grid, lds, s, pk, row_ptr, col, val, nrows, H, sc, o, ntiles);
-    else launch_unpack_g<false, 2, true>(G, grid, lds, s, pk, row_ptr, col, val, nrows, H, sc, o, ntiles);
+    const size_t lds = seg_bytes + (size_t)NW * WR * 16 * 2;
+    if (bits == 4) launch_unpack_g<true, 4, false>(HKV_UARGS);
+    else launch_unpack_g<true, 2, false>(HKV_UARGS);
+  } else if (seg_bytes + kpole_bytes <= 48 * 1024) {
+    const size_t lds = seg_bytes + kpole_bytes;
+    if (bits == 4) launch_unpack_g<false, 4, true>(HKV_UARGS);
+    else launch_unpack_g<false, 2, true>(HKV_UARGS);
   } else {
-    const size_t lds = tile_bytes;
-    if (bits == 4) launch_unpack_g<false, 4, false>(G, grid, lds, s, pk, row_ptr, col, val, nrows, H, sc, o, ntiles);
-    else launch_unpack_g<false, 2, false>(G, grid, lds, s, pk, row_ptr, col, val, nrows, H, sc, o, ntiles);
+    const size_t lds = seg_bytes;
+    if (bits == 4) launch_unpack_g<false, 4, false>(HKV_UARGS);
+    else launch_unpack_g<false, 2, false>(HKV_UARGS);
   }
+#undef HKV_UARGS
   HKV_CHECK_LAUNCH();
   return HKV_OK;
 }

@@ -39,12 +39,12 @@ HKV_DEV int slow_one(uint16_t xb, const SlowInfo& si, int64_t tab, int* o) {
 }
 
 // Quantise 8 channels.  PT (per-token): S[0] holds the row's table broadcast;
-// otherwise S[j] holds the tables of channel pair j.  tab0: table index of
-// element 0 (per-channel: +e per element; per-token: shared).
+// otherwise S[j] holds the tables of channel pair j.  tab(e) gives the table
+// index of element e (0..7); it is evaluated only on the exact-scan path.
 // code[j]: codes of elements 2j, 2j+1 in bits 0..3 / 16..19; om[j]: 0xffff lanes
 // for outliers.
-template <int NB, bool PT>
-HKV_DEV void quant8(const uint4 xv, const Search2<NB>* S, const SlowInfo& si, int64_t tab0,
+template <int NB, bool PT, typename TabFn>
+HKV_DEV void quant8(const uint4 xv, const Search2<NB>* S, const SlowInfo& si, TabFn tab,
                     uint32_t code[4], uint32_t om[4]) {
   const uint32_t x[4] = {xv.x, xv.y, xv.z, xv.w};
   uint32_t uns = 0;
@@ -60,12 +60,47 @@ HKV_DEV void quant8(const uint4 xv, const Search2<NB>* S, const SlowInfo& si, in
 #pragma unroll 1
     for (int j = 0; j < 4; ++j) {
       int o0, o1;
-      int c0 = slow_one((uint16_t)(x[j] & 0xffffu), si, PT ? tab0 : tab0 + 2 * j, &o0);
-      int c1 = slow_one((uint16_t)(x[j] >> 16), si, PT ? tab0 : tab0 + 2 * j + 1, &o1);
+      int c0 = slow_one((uint16_t)(x[j] & 0xffffu), si, tab(2 * j), &o0);
+      int c1 = slow_one((uint16_t)(x[j] >> 16), si, tab(2 * j + 1), &o1);
       code[j] = (uint32_t)c0 | ((uint32_t)c1 << 16);
       om[j] = (o0 ? 0xffffu : 0u) | (o1 ? 0xffff0000u : 0u);
     }
   }
+}
+
+// Per-channel tables: element e of the chunk starting at table index tab0.
+struct ChanTab {
+  int64_t tab0;
+  HKV_DEV int64_t operator()(int e) const { return tab0 + e; }
+};
+// Per-token tables: one table for the whole row.
+struct RowTab {
+  int64_t tab;
+  HKV_DEV int64_t operator()(int) const { return tab; }
+};
+
+// Word k (0..3) of a 4-word register group, by an explicit select tree (a
+// dynamic index into a register array becomes a compare chain over all of
+// the array's registers).
+HKV_DEV uint32_t pick4(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3, int k) {
+  const uint32_t lo = (k & 1) ? w1 : w0, hi = (k & 1) ? w3 : w2;
+  return (k & 2) ? hi : lo;
+}
+
+// Wave-wide exclusive prefix of a per-lane count in [0, 15] and the wave
+// total, from ballots of its bits (no LDS traffic).
+HKV_DEV uint32_t wave_excl_count(uint32_t cnt, uint32_t* total) {
+  const uint32_t lane = __lane_id();
+  const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  uint32_t ex = 0, tot = 0;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const uint64_t m = __ballot((cnt >> b) & 1u);
+    ex += (uint32_t)__builtin_popcountll(m & lt) << b;
+    tot += (uint32_t)__builtin_popcountll(m) << b;
+  }
+  *total = tot;
+  return ex;
 }
 
 // Two 16-bit lanes holding small values -> two bytes (lane0 -> byte0).

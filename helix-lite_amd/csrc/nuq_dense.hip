@@ -42,7 +42,8 @@ pack_dense_kernel(const uint16_t* __restrict__ x, int64_t T, int H, hkv_nuq_scal
     const int64_t off = (t * H + h) * D + 8 * cg;
     const uint4 xv = *reinterpret_cast<const uint4*>(x + off);
     uint32_t c[4], om[4];
-    quant8<NB, PT>(xv, S, si, tab0, c, om);
+    if constexpr (PT) quant8<NB, PT>(xv, S, si, RowTab{tab0}, c, om);
+    else quant8<NB, PT>(xv, S, si, ChanTab{tab0}, c, om);
     uint2 cb, mb;
     cb.x = lanes_to_bytes(c[0]) | (lanes_to_bytes(c[1]) << 16);
     cb.y = lanes_to_bytes(c[2]) | (lanes_to_bytes(c[3]) << 16);

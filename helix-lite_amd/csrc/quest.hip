@@ -171,7 +171,10 @@ HKV_DEV void group_q(const void* q, int qdt, int g, int group, int D, int d, flo
   qn = b;
 }
 
-// Standalone bound: rows r = p*H + h; n lanes per row; q staged in LDS.
+// Standalone bound: rows r = p*H + h; n lanes per row; q staged in LDS; each
+// thread has the loads of kBoundUnroll rows in flight.
+constexpr int kBoundUnroll = 4;
+
 template <typename KT>
 __global__ void __launch_bounds__(256)
 bound_kernel(const void* q, int qdt, int group, const KT* __restrict__ kmin,
@@ -188,27 +191,36 @@ bound_kernel(const void* q, int qdt, int group, const KT* __restrict__ kmin,
   const int rows_per_block = 256 / n;
   const int c = threadIdx.x % n;
   const int64_t nrows = P * H;
-  for (int64_t r0 = (int64_t)blockIdx.x * rows_per_block; r0 < nrows;
-       r0 += (int64_t)gridDim.x * rows_per_block) {
-    const int64_t r = r0 + threadIdx.x / n;
-    float ps = 0.0f, ns = 0.0f;
-    if (r < nrows) {
-      const int h = (int)(r % H);
-      float qp[8], qn[8];
+  const int64_t span = (int64_t)rows_per_block * kBoundUnroll;
+  for (int64_t r0 = (int64_t)blockIdx.x * span; r0 < nrows; r0 += (int64_t)gridDim.x * span) {
+    float ps[kBoundUnroll], ns[kBoundUnroll];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int d = 8 * c + i;
-        qp[i] = d < D ? qs[h * D + d] : 0.0f;
-        qn[i] = d < D ? qs[H * D + h * D + d] : 0.0f;
+    for (int u = 0; u < kBoundUnroll; ++u) {
+      const int64_t r = r0 + (int64_t)u * rows_per_block + threadIdx.x / n;
+      ps[u] = 0.0f;
+      ns[u] = 0.0f;
+      if (r < nrows) {
+        const int h = (int)(r % H);
+        float qp[8], qn[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int d = 8 * c + i;
+          qp[i] = d < D ? qs[h * D + d] : 0.0f;
+          qn[i] = d < D ? qs[H * D + h * D + d] : 0.0f;
+        }
+        chunk_sums<KT>(kmin + r * D, kmax + r * D, D, c, qp, qn, ps[u], ns[u]);
       }
-      chunk_sums<KT>(kmin + r * D, kmax + r * D, D, c, qp, qn, ps, ns);
     }
-    ps = row_reduce(ps, n);
-    ns = row_reduce(ns, n);
-    if (r < nrows && c == 0) {
-      const float b = __fadd_rn(__fadd_rn(ps, ns), 0.0f);
-      if (odt == HKV_DT_F16) ((uint16_t*)out)[r] = f2h(b);
-      else ((float*)out)[r] = b;
+#pragma unroll
+    for (int u = 0; u < kBoundUnroll; ++u) {
+      const int64_t r = r0 + (int64_t)u * rows_per_block + threadIdx.x / n;
+      const float a = row_reduce(ps[u], n);
+      const float b2 = row_reduce(ns[u], n);
+      if (r < nrows && c == 0) {
+        const float b = __fadd_rn(__fadd_rn(a, b2), 0.0f);
+        if (odt == HKV_DT_F16) ((uint16_t*)out)[r] = f2h(b);
+        else ((float*)out)[r] = b;
+      }
     }
   }
 }
@@ -390,14 +402,161 @@ HKV_DEV void select_column(const Col& col, int64_t P, int64_t s, int64_t keff, i
   }
 }
 
-template <typename Col>
+// Radix search shared by both selectors: the keff-th largest key T among
+// the candidates and how many keys equal to T are taken (lowest pages first).
+// `count(pmask, prefix, lo, nb)` adds, into sh.hist, the digit (k >> lo) &
+// (nb-1) of every candidate key k with (k & pmask) == prefix.
+template <typename CountFn>
+HKV_DEV void radix_threshold(uint32_t kmn, uint32_t kmx, int64_t keff, SelShared& sh,
+                             CountFn count, uint32_t& T_out, uint32_t& need_eq) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  uint32_t prefix = kmx, pmask = 0xffffffffu;
+  uint32_t krem = (uint32_t)keff;
+  if (kmn != kmx) {
+    int hb = 31 - __builtin_clz(kmn ^ kmx);
+    pmask = hb == 31 ? 0u : ~((2u << hb) - 1u);
+    prefix = kmx & pmask;
+    while (true) {
+      const int lo = hb >= 10 ? hb - 10 : 0;
+      const uint32_t nb = 1u << (hb - lo + 1);
+      for (int i = tid; i < (int)nb; i += kSelThreads) sh.hist[i] = 0;
+      __syncthreads();
+      count(pmask, prefix, lo, nb);
+      __syncthreads();
+      {
+        const uint32_t h0 = 2 * tid < (int)nb ? sh.hist[2 * tid] : 0u;
+        const uint32_t h1 = 2 * tid + 1 < (int)nb ? sh.hist[2 * tid + 1] : 0u;
+        const uint32_t loc = h0 + h1;
+        uint32_t inc = loc;  // inclusive suffix within the wave
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+          const uint32_t y = __shfl_down(inc, o, 64);
+          if (lane + o < 64) inc += y;
+        }
+        if (lane == 0) sh.wred[w][0] = inc;
+        __syncthreads();
+        uint32_t later = 0;
+        for (int i = w + 1; i < kSelWaves; ++i) later += sh.wred[i][0];
+        const uint32_t sfx = later + inc - loc;  // count in bins above 2t+1
+        if (sfx < krem && krem <= sfx + loc) {
+          if (sfx + h1 >= krem) { sh.bcast[0] = 2 * tid + 1; sh.bcast[1] = sfx; }
+          else { sh.bcast[0] = 2 * tid; sh.bcast[1] = sfx + h1; }
+        }
+        __syncthreads();
+      }
+      const uint32_t b = sh.bcast[0], above = sh.bcast[1];
+      krem -= above;
+      prefix |= b << lo;
+      pmask |= (nb - 1) << lo;
+      __syncthreads();
+      if (lo == 0) break;
+      hb = lo - 1;
+    }
+  }
+  T_out = prefix;
+  need_eq = krem;
+}
+
+// Register-resident selector for n = P - s <= 1024 * KPT candidates: wave w
+// holds pages s + w*64*KPT + i*64 + lane (i < KPT) as keys; the radix passes
+// and the ordered write read only registers.  Same contract as
+// select_column.
+template <int KPT, typename Col>
+HKV_DEV void select_column_regs(const Col& col, int64_t P, int64_t s, int64_t keff, int64_t* out,
+                                int64_t ostride, SelShared& sh) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  for (int64_t i = tid; i < s; i += kSelThreads) out[i * ostride] = i;
+  if (keff <= 0) return;
+  const int64_t c0 = s + (int64_t)w * (64 * KPT) + lane;  // page of key[0]
+  // key[i] is a candidate iff i*64 < lim
+  const int64_t lim = P - c0;
+  uint32_t key[KPT];
+  uint32_t kmn = 0xffffffffu, kmx = 0;
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) key[i] = (int64_t)i * 64 < lim ? col.key(c0 + (int64_t)i * 64) : 0u;
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) {
+    if ((int64_t)i * 64 < lim) {
+      kmn = key[i] < kmn ? key[i] : kmn;
+      kmx = key[i] > kmx ? key[i] : kmx;
+    }
+  }
+  kmn = block_min_u32(kmn, sh);
+  kmx = block_max_u32(kmx, sh);
+  uint32_t T, need_eq;
+  radix_threshold(kmn, kmx, keff, sh,
+                  [&](uint32_t pmask, uint32_t prefix, int lo, uint32_t nb) {
+#pragma unroll
+                    for (int i = 0; i < KPT; ++i)
+                      if ((int64_t)i * 64 < lim && (key[i] & pmask) == prefix)
+                        atomicAdd(&sh.hist[(key[i] >> lo) & (nb - 1)], 1u);
+                  },
+                  T, need_eq);
+
+  uint32_t cgt = 0, ceq = 0;
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) {
+    const bool v = (int64_t)i * 64 < lim;
+    cgt += v && key[i] > T;
+    ceq += v && key[i] == T;
+  }
+  for (int o = 32; o >= 1; o >>= 1) {
+    cgt += __shfl_xor(cgt, o, 64);
+    ceq += __shfl_xor(ceq, o, 64);
+  }
+  __syncthreads();
+  if (lane == 0) { sh.wred[w][2] = cgt; sh.wred[w][3] = ceq; }
+  __syncthreads();
+  uint32_t eq_before = 0, out_before = 0;
+  for (int i = 0; i < w; ++i) {
+    const uint32_t e = sh.wred[i][3];
+    const uint32_t take = eq_before >= need_eq ? 0u : (need_eq - eq_before < e ? need_eq - eq_before : e);
+    out_before += sh.wred[i][2] + take;
+    eq_before += e;
+  }
+  uint32_t run_out = 0, run_eq = 0;
+  const uint64_t lanemask_lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) {
+    const bool v = (int64_t)i * 64 < lim;
+    const bool is_eq = v && key[i] == T;
+    const uint64_t eqm = __ballot(is_eq);
+    const uint32_t eq_rank = eq_before + run_eq + __builtin_popcountll(eqm & lanemask_lt);
+    const bool sel = v && (key[i] > T || (is_eq && eq_rank < need_eq));
+    const uint64_t selm = __ballot(sel);
+    if (sel) {
+      const uint32_t pos = out_before + run_out + __builtin_popcountll(selm & lanemask_lt);
+      if (pos < (uint64_t)keff) out[(s + (int64_t)pos) * ostride] = c0 + (int64_t)i * 64;
+    }
+    run_out += __builtin_popcountll(selm);
+    run_eq += __builtin_popcountll(eqm);
+  }
+}
+
+// KPT == 0: streaming selector (any P); else register-resident.
+template <int KPT, typename Col>
+HKV_DEV void select_any(const Col& col, int64_t P, int64_t s, int64_t keff, int64_t* out,
+                        int64_t ostride, SelShared& sh) {
+  if constexpr (KPT == 0) select_column(col, P, s, keff, out, ostride, sh);
+  else select_column_regs<KPT>(col, P, s, keff, out, ostride, sh);
+}
+
+// Smallest register tile that holds n candidates (0: too many, stream).
+int kpt_for(int64_t n) {
+  if (n <= (int64_t)kSelThreads * 4) return 4;
+  if (n <= (int64_t)kSelThreads * 16) return 16;
+  if (n <= (int64_t)kSelThreads * 64) return 64;
+  return 0;
+}
+
+template <int KPT, typename Col>
 __global__ void __launch_bounds__(kSelThreads)
 topk_kernel(Col col0, int64_t P, int H, int64_t s, int64_t keff, int64_t* out) {
   __shared__ SelShared sh;
   const int h = blockIdx.x;
   Col col = col0;
   col.base += h;
-  select_column(col, P, s, keff, out + h, H, sh);
+  select_any<KPT>(col, P, s, keff, out + h, H, sh);
 }
 
 // ----------------------------------------------- fused score + select (cfg3)
@@ -406,9 +565,11 @@ struct SelectWs {
   uint32_t done[64];  // per-head block completion counters
 };
 
+constexpr int kScoreUnroll = 4;
+
 // grid (page blocks, H); 1024 threads; rows are pages of head h.  Scores go to
 // scores[h*P + p] (head-major).  The last block of head h selects for head h.
-template <typename KT>
+template <int KPT, typename KT>
 __global__ void __launch_bounds__(kSelThreads)
 select_fused_kernel(const void* q, int qdt, int group, const KT* __restrict__ kmin,
                     const KT* __restrict__ kmax, int64_t P, int H, int D, int64_t pages_per_block,
@@ -429,16 +590,25 @@ select_fused_kernel(const void* q, int qdt, int group, const KT* __restrict__ km
   }
   const int64_t pb0 = (int64_t)blockIdx.x * pages_per_block;
   const int64_t pb1 = pb0 + pages_per_block < P ? pb0 + pages_per_block : P;
-  for (int64_t p0 = pb0; p0 < pb1; p0 += rows) {
-    const int64_t p = p0 + threadIdx.x / n;
-    float ps = 0.0f, ns = 0.0f;
-    if (p < pb1) {
-      const int64_t row = p * H + h;
-      chunk_sums<KT>(kmin + row * D, kmax + row * D, D, c, qp, qn, ps, ns);
+  for (int64_t p0 = pb0; p0 < pb1; p0 += (int64_t)rows * kScoreUnroll) {
+    float ps[kScoreUnroll], ns[kScoreUnroll];
+#pragma unroll
+    for (int u = 0; u < kScoreUnroll; ++u) {
+      const int64_t p = p0 + (int64_t)u * rows + threadIdx.x / n;
+      ps[u] = 0.0f;
+      ns[u] = 0.0f;
+      if (p < pb1) {
+        const int64_t row = p * H + h;
+        chunk_sums<KT>(kmin + row * D, kmax + row * D, D, c, qp, qn, ps[u], ns[u]);
+      }
     }
-    ps = row_reduce(ps, n);
-    ns = row_reduce(ns, n);
-    if (p < pb1 && c == 0) scores[(int64_t)h * P + p] = __fadd_rn(__fadd_rn(ps, ns), 0.0f);
+#pragma unroll
+    for (int u = 0; u < kScoreUnroll; ++u) {
+      const int64_t p = p0 + (int64_t)u * rows + threadIdx.x / n;
+      const float a = row_reduce(ps[u], n);
+      const float b = row_reduce(ns[u], n);
+      if (p < pb1 && c == 0) scores[(int64_t)h * P + p] = __fadd_rn(__fadd_rn(a, b), 0.0f);
+    }
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
   __syncthreads();
@@ -451,7 +621,7 @@ select_fused_kernel(const void* q, int qdt, int group, const KT* __restrict__ km
   if (!s_last) return;
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   ColumnF32 col{scores + (int64_t)h * P, 1};
-  select_column(col, P, s, keff, out + h, H, sh);
+  select_any<KPT>(col, P, s, keff, out + h, H, sh);
 }
 
 int num_cus() {
@@ -509,7 +679,8 @@ extern "C" int hkv_quest_page_bound(const void* q, int q_dtype, int Hq, const vo
   int n = 1;
   while (n < (D + 7) / 8) n <<= 1;
   const int rpb = 256 / n;
-  const unsigned grid = (unsigned)std::min<int64_t>((rows + rpb - 1) / rpb, (int64_t)num_cus() * 8);
+  const int64_t span = (int64_t)rpb * kBoundUnroll;
+  const unsigned grid = (unsigned)std::min<int64_t>((rows + span - 1) / span, (int64_t)num_cus() * 8);
   const size_t lds = sizeof(float) * 2 * H * D;
   if (lds > 64 * 1024) return HKV_ERR_SHAPE;
   if (k_dtype == HKV_DT_F16)
@@ -541,12 +712,21 @@ extern "C" int hkv_quest_topk(const void* bound, int b_dtype, int64_t P, int H, 
   (void)workspace;
   (void)workspace_bytes;
   hipStream_t st = (hipStream_t)stream;
-  if (b_dtype == HKV_DT_F32)
-    hipLaunchKernelGGL(topk_kernel<ColumnF32>, dim3(H), dim3(kSelThreads), 0, st,
-                       ColumnF32{(const float*)bound, H}, P, H, s, keff, out);
-  else
-    hipLaunchKernelGGL(topk_kernel<ColumnF16>, dim3(H), dim3(kSelThreads), 0, st,
+  const int kpt = kpt_for(P - s);
+#define HKV_TOPK(K)                                                                        \
+  if (b_dtype == HKV_DT_F32)                                                               \
+    hipLaunchKernelGGL((topk_kernel<K, ColumnF32>), dim3(H), dim3(kSelThreads), 0, st,     \
+                       ColumnF32{(const float*)bound, H}, P, H, s, keff, out);            \
+  else                                                                                     \
+    hipLaunchKernelGGL((topk_kernel<K, ColumnF16>), dim3(H), dim3(kSelThreads), 0, st,     \
                        ColumnF16{(const uint16_t*)bound, H}, P, H, s, keff, out);
+  switch (kpt) {
+    case 4: HKV_TOPK(4) break;
+    case 16: HKV_TOPK(16) break;
+    case 64: HKV_TOPK(64) break;
+    default: HKV_TOPK(0) break;
+  }
+#undef HKV_TOPK
   HKV_CHECK_LAUNCH();
   return HKV_OK;
 }
@@ -574,14 +754,23 @@ extern "C" int hkv_quest_select(const void* q, int q_dtype, int Hq, const void* 
   int64_t ppb = (P + target - 1) / target;
   ppb = std::max<int64_t>(rows, (ppb + rows - 1) / rows * rows);
   const unsigned gx = (unsigned)((P + ppb - 1) / ppb);
-  if (k_dtype == HKV_DT_F16)
-    hipLaunchKernelGGL(select_fused_kernel<uint16_t>, dim3(gx, H), dim3(kSelThreads), 0, st, q,
-                       q_dtype, Hq / H, (const uint16_t*)kmin, (const uint16_t*)kmax, P, H, D, ppb,
-                       scores, s, keff, out, (SelectWs*)workspace);
-  else
-    hipLaunchKernelGGL(select_fused_kernel<float>, dim3(gx, H), dim3(kSelThreads), 0, st, q,
-                       q_dtype, Hq / H, (const float*)kmin, (const float*)kmax, P, H, D, ppb,
-                       scores, s, keff, out, (SelectWs*)workspace);
+  const int kpt = kpt_for(P - s);
+#define HKV_SEL(K)                                                                             \
+  if (k_dtype == HKV_DT_F16)                                                                   \
+    hipLaunchKernelGGL((select_fused_kernel<K, uint16_t>), dim3(gx, H), dim3(kSelThreads), 0,  \
+                       st, q, q_dtype, Hq / H, (const uint16_t*)kmin, (const uint16_t*)kmax, P, \
+                       H, D, ppb, scores, s, keff, out, (SelectWs*)workspace);                 \
+  else                                                                                         \
+    hipLaunchKernelGGL((select_fused_kernel<K, float>), dim3(gx, H), dim3(kSelThreads), 0, st, \
+                       q, q_dtype, Hq / H, (const float*)kmin, (const float*)kmax, P, H, D,    \
+                       ppb, scores, s, keff, out, (SelectWs*)workspace);
+  switch (kpt) {
+    case 4: HKV_SEL(4) break;
+    case 16: HKV_SEL(16) break;
+    case 64: HKV_SEL(64) break;
+    default: HKV_SEL(0) break;
+  }
+#undef HKV_SEL
   HKV_CHECK_LAUNCH();
   return HKV_OK;
 }

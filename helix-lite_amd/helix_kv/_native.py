@@ -62,7 +62,7 @@ _SIGS = {
     "hkv_nuq_pack_compact": ([_p, _i64, _i32, _i32, _i32, ctypes.POINTER(NuqScales), _p, _p, _p,
                               _p, _i64, _p, _sz, _p], _i32),
     "hkv_nuq_pack_compact_status": ([_p, _p], _i32),
-    "hkv_nuq_unpack_compact": ([_p, _p, _p, _p, _i64, _i32, _i32, _i32,
+    "hkv_nuq_unpack_compact": ([_p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32,
                                 ctypes.POINTER(NuqScales), _p, _p], _i32),
     "hkv_nuq_quantize_generic": ([_i32, ctypes.POINTER(_i64), ctypes.POINTER(TensorDesc),
                                   ctypes.POINTER(TensorDesc), _i64, _i32, ctypes.POINTER(TensorDesc),

@@ -251,7 +251,8 @@ def nuq_unpack_compact(cc: CompactCodes, t: NuqLayerTables, *, positions=None, p
     pos = _positions(positions, T, cc.packed.device)
     s = t.struct(pos, pos_offset)
     st = N.lib().hkv_nuq_unpack_compact(
-        N.ptr(cc.packed), N.ptr(cc.row_ptr), N.ptr(cc.col), N.ptr(cc.val), T, H, D, cc.bits, s,
+        N.ptr(cc.packed), N.ptr(cc.row_ptr), N.ptr(cc.col), N.ptr(cc.val),
+        min(int(cc.col.numel()), int(cc.val.numel())), T, H, D, cc.bits, s,
         N.ptr(out), N.stream_of(out))
     N.check(st, "hkv_nuq_unpack_compact", AssertionError)
     return out

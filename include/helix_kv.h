@@ -140,11 +140,13 @@ int hkv_nuq_pack_compact_status(const void *workspace, void *stream);
 
 /*
  * Compact unpack: packed codes + CSR -> out (T,H,D) fp16.  Inverse of
- * hkv_nuq_pack_compact; requires scales->tables.
+ * hkv_nuq_pack_compact; requires scales->tables.  `capacity` is the length of
+ * col/val: CSR entries at or beyond it are never read (a row_ptr from a pack
+ * that overflowed its capacity then decodes those outliers as their poles).
  */
 int hkv_nuq_unpack_compact(const void *packed, const int32_t *row_ptr, const uint8_t *col,
-                           const uint16_t *val, int64_t T, int H, int D, int bits,
-                           const hkv_nuq_scales *scales, void *out, void *stream);
+                           const uint16_t *val, int64_t capacity, int64_t T, int H, int D,
+                           int bits, const hkv_nuq_scales *scales, void *out, void *stream);
 
 /*
  * Broadcasting quantise with the CPU spec's dtype semantics: over a shape of

@@ -36,9 +36,13 @@ def test_host_only_entry_points():
     assert b"gfx950" in L.hkv_version()
     assert L.hkv_status_string(0) == b"ok"
     assert L.hkv_status_string(4) == b"output capacity too small"
-    # pack workspace: 64-byte header + one status word per tile of 64 rows (D=128)
-    assert L.hkv_nuq_pack_compact_workspace_bytes(131072, 4, 128) == 64 + 8 * (131072 * 4 // 64)
-    assert L.hkv_nuq_pack_compact_workspace_bytes(10, 4, 128) == 64 + 8
+    # 256-byte header, one u32 count per tile of 128 rows (D = 128), then the
+    # staging columns (1 B) and values (2 B) of every element, 256-aligned
+    ntiles = 131072 * 4 // 128
+    assert L.hkv_nuq_pack_compact_workspace_bytes(131072, 4, 128) == \
+        256 + 4 * ntiles + 131072 * 4 * 128 * 3
+    # one partial tile: header, count (padded to 256), staging for 128 x 128
+    assert L.hkv_nuq_pack_compact_workspace_bytes(10, 4, 128) == 256 + 256 + 16384 * 3
     assert L.hkv_nuq_pack_compact_workspace_bytes(10, 4, 100) == 0  # unsupported D
     assert L.hkv_quest_topk_workspace_bytes(65536, 4) >= 64
 

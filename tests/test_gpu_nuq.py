@@ -249,6 +249,58 @@ def test_compact_values_vs_oracle(dev, T, Tcal, L, offset):
     assert torch.equal(cc2.packed, cc.packed) and torch.equal(cc2.row_ptr, cc.row_ptr)
 
 
+@pytest.mark.parametrize("per_token,L", [(False, 16), (True, 4)])
+def test_compact_many_tiles_vs_oracle(dev, per_token, L):
+    """65,536 tokens x 4 heads: thousands of tiles, so the CSR offsets cross
+    many look-back windows; every byte against the oracle."""
+    from helix_kv.ops import NuqLayerTables, nuq_pack_compact, nuq_unpack_compact
+
+    T, H, D = 65536, 4, 128
+    bits = 2 if L <= 4 else 4
+    x = RNG.standard_t(3, (T, H, D)).astype(np.float16)
+    rows = D if not per_token else 4096
+    poles = np.sort(RNG.standard_normal((H, rows, L)), axis=-1).astype(np.float16)
+    up = RNG.uniform(1.5, 3.0, (H, rows)).astype(np.float16)
+    t = NuqLayerTables(_t(poles, dev), _t(up, dev), _t(-up, dev), per_token=per_token)
+    cc = nuq_pack_compact(_t(x, dev), t, bits)
+    f32 = [a.astype(np.float32) for a in (poles, up, -up)]
+    if per_token:
+        wc, wv, wm = O.pack_v(x, *f32, positions=np.arange(T))
+    else:
+        wc, wv, wm = O.pack_k(x, *f32)
+    pk, rp, col, val = O.pack_compact(wc, wv, wm, bits)
+    assert cc.nnz == len(col) and 0.01 < cc.nnz / x.size < 0.5
+    assert np.array_equal(cc.row_ptr.cpu().numpy(), rp)
+    assert np.array_equal(cc.packed.cpu().numpy(), pk)
+    assert np.array_equal(cc.col.cpu().numpy(), col)
+    assert np.array_equal(_bits(cc.val), val)
+    out = nuq_unpack_compact(cc, t)
+    want = O.unpack(wc, wv, wm, f32[0], "v" if per_token else "k",
+                    positions=np.arange(T) if per_token else None)
+    assert np.array_equal(_bits(out), want)
+
+
+def test_compact_unpack_respects_capacity(dev):
+    """CSR entries beyond the col/val capacity are never read: those outliers
+    decode as their poles, everything else is unchanged."""
+    from helix_kv.ops import CompactCodes, NuqLayerTables, nuq_pack_compact, nuq_unpack_compact
+
+    T, H, D, L = 256, 4, 128, 16
+    x = RNG.standard_t(3, (T, H, D)).astype(np.float16)
+    poles, up, lo = _kscales(H, D, L, thr=1.0)
+    t = NuqLayerTables(_t(poles, dev), _t(up, dev), _t(lo, dev), per_token=False)
+    full = nuq_pack_compact(_t(x, dev), t, 4)
+    keep = full.nnz // 2
+    cut = CompactCodes(full.packed, full.row_ptr, full.col[:keep].clone(), full.val[:keep].clone(), 4)
+    got = _bits(nuq_unpack_compact(cut, t))
+    wc, wv, wm = O.pack_k(x, poles.astype(np.float32), up.astype(np.float32), lo.astype(np.float32))
+    flat_m = wm.reshape(-1).copy()
+    idx = np.flatnonzero(flat_m)
+    flat_m[idx[keep:]] = 0
+    want = O.unpack(wc, wv, flat_m.reshape(wm.shape), poles.astype(np.float32), "k")
+    assert np.array_equal(got, want)
+
+
 def test_compact_empty_and_repeat_calls(dev):
     """Empty input; and the look-back workspace is reused across calls."""
     from helix_kv.ops import NuqLayerTables, nuq_pack_compact
