@@ -162,6 +162,14 @@ HKV_DEV uint32_t outlier2(uint32_t x, const Search2<NB>& s) {
   return lt2(x, s.lo) | lt2(s.up, x);
 }
 
+// Outlier flags of two fp16 lanes in the sign bits (bit 15: lane 0, bit 31:
+// lane 1; other bits are garbage): the sign of x - lo or of up - x.
+template <int NB>
+HKV_DEV uint32_t outlier2_sign(uint32_t x, const Search2<NB>& s) {
+  const h2_t d1 = as_h2(x) - as_h2(s.lo), d2 = as_h2(s.up) - as_h2(x);
+  return as_u32(d1) | as_u32(d2);
+}
+
 // Nonzero if some lane of x has |x| > xsafe (fast path not applicable).
 // xsafe lanes are in [0, 0x7bff] or 0xffff (= -1: never applicable).
 template <int NB>

@@ -8,14 +8,16 @@
 //   CSR outliers over rows r = t*H + h: row_ptr (T*H+1) int32, col u8 = d,
 //   val fp16 = the original value; (row, col) ascending.
 //
-// Pack runs as two kernels.  pack_stage_kernel streams the fp16 input once:
-// it writes the packed codes, each row's outlier offset within its tile (into
-// row_ptr), the tile's outliers into the tile's own region of a staging
-// buffer, and the tile's outlier count.  compact_kernel then turns the tile
-// counts into tile offsets, adds them to row_ptr and copies the staged
-// outliers into the dense col/val arrays.  No block ever waits on another:
-// on gfx950 the eight XCDs' L2 caches are not coherent, so a single-pass scan
-// whose tiles wait on their predecessors pays a memory round trip per step.
+// Pack runs as three kernels.  pack_stage_kernel streams the fp16 input once;
+// its unit of work is a wave tile (kPasses passes of 64/G rows, G = D/8 lanes
+// per row), handled by one wave on its own: no block-level barrier.  A wave
+// writes the packed codes, each row's outlier offset within its wave tile
+// (into row_ptr), the tile's outliers into the tile's own staging region, and
+// the tile's outlier count.  scan_kernel turns the counts into offsets;
+// copy_kernel adds them to row_ptr and copies the staged outliers into the
+// dense col/val arrays.  No block ever waits on another: on gfx950 the eight XCDs' L2
+// caches are not coherent, so a single-pass scan whose tiles wait on their
+// predecessors pays a memory round trip per step.
 #include "nuq_core.h"
 
 namespace {
@@ -23,41 +25,46 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kPasses = 8;  // passes of kThreads*8 elements per tile
 
-// Workspace: header, per-tile counts, then the staging columns and values,
-// each region 256-byte aligned.  Staging holds a whole tile per tile, so no
-// input can overflow it.
+// Workspace: header, per-wave-tile counts and bases, then the staged entries
+// (u32: value | column << 16), each region 256-byte aligned.  Staging holds a
+// whole wave tile per wave tile, so no input can overflow it.
 struct PackLayout {
-  int64_t ntiles, tile_elems;
-  size_t cnt_off, col_off, val_off, bytes;
+  int64_t ntiles, tile_rows, tile_elems;
+  size_t cnt_off, base_off, ent_off, bytes;
 };
 
 __host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// KFIX: the rows per pass are a multiple of H, so a thread's head is fixed
-// (rl % H) and its token advances by R / H per pass (no 64-bit division in
-// the loop).
+HKV_DEV void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// KFIX: the rows of one pass of a wave (RW = 64/G) are a multiple of H, so a
+// lane's head is fixed (rw % H) and its token advances by RW / H per pass.
 template <int NB, bool PT, int G, int BITS, bool KFIX>
 __global__ void __launch_bounds__(kThreads)
 pack_stage_kernel(const uint16_t* __restrict__ x, int64_t nrows, int H, hkv_nuq_scales sc,
                   uint8_t* __restrict__ packed, int32_t* __restrict__ row_ptr,
-                  uint8_t* __restrict__ scol, uint16_t* __restrict__ sval,
-                  uint32_t* __restrict__ tile_cnt, uint32_t ntiles) {
-  constexpr int R = kThreads / G;   // rows per pass
-  constexpr int TR = R * kPasses;   // rows per tile
+                  uint32_t* __restrict__ sent, uint32_t* __restrict__ wt_cnt, int64_t nwt) {
+  constexpr int RW = 64 / G;        // rows per wave per pass
+  constexpr int WT = RW * kPasses;  // rows per wave tile
   constexpr int D = 8 * G;
   constexpr int RB = D * BITS / 8;  // packed bytes per row
   constexpr int NW = kThreads / 64;
-  // Per-token tables of the tile's rows are staged in LDS when they fit in
-  // 16 KiB (D >= 128); otherwise each row reads its table through L1.
-  constexpr bool STAGE = PT && TR * 80 <= 16384;
-  __shared__ uint32_t s_wave[kPasses][NW];
-  __shared__ uint4 s_tab[STAGE ? TR * 5 : 1];
+  // Per-token tables of a wave tile's rows are staged in the wave's LDS slice
+  // when they fit in 4 KiB (D >= 128); otherwise each row reads its table
+  // through L1.
+  constexpr bool STAGE = PT && WT * 80 <= 4096;
+  __shared__ uint4 s_tab[STAGE ? NW * WT * 5 : 1];
 
-  const int tid = threadIdx.x, cg = tid % G, rl = tid / G;
-  const int wv = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int cg = lane % G, rw = lane / G;
+  uint4* wtab = s_tab + (STAGE ? wv * WT * 5 : 0);
   const hkv_table_t* tabs = (const hkv_table_t*)sc.tables;
   const SlowInfo si = slow_info(sc);
-  const int hfix = KFIX ? rl % H : 0;
+  const int hfix = KFIX ? rw % H : 0;
 
   Search2<NB> S[PT ? 1 : 4];
   if constexpr (!PT && KFIX) {
@@ -67,42 +74,43 @@ pack_stage_kernel(const uint16_t* __restrict__ x, int64_t nrows, int H, hkv_nuq_
       load_search_pair<NB>(tabs + tab0 + 2 * j, tabs + tab0 + 2 * j + 1, S[j]);
   }
 
-  for (uint32_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
-    const int64_t r0 = (int64_t)tile * TR;
+  for (int64_t wt = (int64_t)blockIdx.x * NW + wv; wt < nwt; wt += (int64_t)gridDim.x * NW) {
+    const int64_t r0 = wt * WT;
     const int64_t t0 = KFIX ? r0 / H : 0;  // token of row r0 (H divides r0)
     uint32_t xs[kPasses][4];
 #pragma unroll
     for (int p = 0; p < kPasses; ++p) {
-      const int64_t r = r0 + p * R + rl;
+      const int64_t r = r0 + p * RW + rw;
       uint4 v = make_uint4(0u, 0u, 0u, 0u);
       if (r < nrows) v = *reinterpret_cast<const uint4*>(x + r * D + 8 * cg);
       xs[p][0] = v.x; xs[p][1] = v.y; xs[p][2] = v.z; xs[p][3] = v.w;
     }
     if constexpr (STAGE) {
-      for (int i = tid; i < TR * 5; i += kThreads) {
+      for (int i = lane; i < WT * 5; i += 64) {
         const int rr = i / 5, part = i - rr * 5;
         const int64_t r = r0 + rr;
         if (r < nrows) {
           const int64_t t = r / H;
           const int h = (int)(r - t * H);
           const int64_t tab = (int64_t)h * sc.rows + clamp_row(token_pos(sc, t), sc.rows);
-          s_tab[i] = reinterpret_cast<const uint4*>(tabs + tab)[part];
+          wtab[i] = reinterpret_cast<const uint4*>(tabs + tab)[part];
         }
       }
-      __syncthreads();
+      wave_sync();
     }
 
-    uint32_t mk[kPasses], excl[kPasses];
+    const int64_t sbase = r0 * D;  // the wave tile's staging region
+    uint32_t run = 0;              // outliers of the tile's earlier passes
 #pragma unroll
     for (int p = 0; p < kPasses; ++p) {
-      const int rr = p * R + rl;
+      const int rr = p * RW + rw;
       const int64_t r = r0 + rr;
-      mk[p] = 0;
+      uint32_t m = 0;
       if (r < nrows) {
         int64_t t;
         int h;
         if constexpr (KFIX) {
-          t = t0 + p * (R / H) + rl / H;
+          t = t0 + p * (RW / H) + rw / H;
           h = hfix;
         } else {
           t = r / H;
@@ -112,9 +120,9 @@ pack_stage_kernel(const uint16_t* __restrict__ x, int64_t nrows, int H, hkv_nuq_
         uint32_t c[4], om[4];
         if constexpr (PT) {
           const int64_t tab = (int64_t)h * sc.rows + clamp_row(token_pos(sc, t), sc.rows);
-          if constexpr (STAGE) load_search_bcast<NB>(reinterpret_cast<const hkv_table_t*>(s_tab + rr * 5), S[0]);
+          if constexpr (STAGE) load_search_bcast<NB>(reinterpret_cast<const hkv_table_t*>(wtab + rr * 5), S[0]);
           else load_search_bcast<NB>(tabs + tab, S[0]);
-          quant8<NB, PT>(xv, S, si, RowTab{tab}, c, om);
+          quant8<NB, PT, RowTab, true>(xv, S, si, RowTab{tab}, c, om);
         } else {
           const int64_t tab0 = (int64_t)h * D + 8 * cg;
           if constexpr (!KFIX) {
@@ -122,102 +130,133 @@ pack_stage_kernel(const uint16_t* __restrict__ x, int64_t nrows, int H, hkv_nuq_
             for (int j = 0; j < 4; ++j)
               load_search_pair<NB>(tabs + tab0 + 2 * j, tabs + tab0 + 2 * j + 1, S[j]);
           }
-          quant8<NB, PT>(xv, S, si, ChanTab{tab0}, c, om);
+          quant8<NB, PT, ChanTab, true>(xv, S, si, ChanTab{tab0}, c, om);
         }
         if constexpr (BITS == 4) {
           *reinterpret_cast<uint32_t*>(packed + r * RB + 4 * cg) = pack_nibbles(c);
         } else {
           *reinterpret_cast<uint16_t*>(packed + r * RB + 2 * cg) = (uint16_t)pack_crumbs(c);
         }
-        mk[p] = mask_bits(om);
+        m = mask_bits_sign(om);
       }
+      // lanes are in (row, channel) order, so the wave's exclusive count is
+      // the position in (row, col) order
       uint32_t tot;
-      excl[p] = wave_excl_count(__builtin_popcount(mk[p]), &tot);
-      if (lane == 0) s_wave[p][wv] = tot;
-    }
-    __syncthreads();
-
-    // Offsets within the tile in (pass, wave, lane) order = (row, col) order.
-    uint32_t total = 0;
-    const int64_t sbase = r0 * D;  // the tile's staging region
-#pragma unroll
-    for (int p = 0; p < kPasses; ++p) {
-      uint32_t before = 0;
-#pragma unroll
-      for (int w = 0; w < NW; ++w) before += w < wv ? s_wave[p][w] : 0u;
-      uint32_t pos = total + before + excl[p];
-#pragma unroll
-      for (int w = 0; w < NW; ++w) total += s_wave[p][w];
-      const int64_t r = r0 + p * R + rl;
-      if (r >= nrows) continue;
-      if (cg == 0) row_ptr[r] = (int32_t)pos;
-      uint32_t m = mk[p];
+      uint32_t pos = run + wave_excl_count(__builtin_popcount(m), &tot);
+      run += tot;
+      if (r < nrows && cg == 0) row_ptr[r] = (int32_t)pos;
       while (m) {
         const int e = __builtin_ctz(m);
         m &= m - 1u;
         const uint32_t w = pick4(xs[p][0], xs[p][1], xs[p][2], xs[p][3], e >> 1);
-        scol[sbase + pos] = (uint8_t)(8 * cg + e);
-        sval[sbase + pos] = (uint16_t)(w >> (16 * (e & 1)));
+        if (pos < (uint32_t)(WT * D))  // always true; keeps the region bound explicit
+          sent[sbase + pos] = ((w >> (16 * (e & 1))) & 0xffffu) | ((uint32_t)(8 * cg + e) << 16);
         ++pos;
       }
     }
-    if (tid == 0) tile_cnt[tile] = total;
-    __syncthreads();  // s_wave / s_tab are reused by the next tile
+    if (lane == 0) wt_cnt[wt] = run;
+    if constexpr (STAGE) wave_sync();  // the slice is refilled for the next tile
   }
 }
 
-// Tile offsets from the tile counts, then the dense CSR.  One wave per tile
-// (kCompactTiles per block); a block first sums the counts of all tiles before
-// its own with every thread loading in parallel.
-constexpr int kCompactTiles = kThreads / 64;
+// Offsets from the wave-tile counts: one block scans all counts into
+// exclusive bases (base[nwt] = nnz, also written to row_ptr[nrows]).  Counts
+// pass through LDS in windows of kScanWindow: coalesced loads, a sequential
+// scan of each thread's contiguous run, a block scan of the run totals, then
+// coalesced stores.
+constexpr int kScanThreads = 1024;
+constexpr int kScanPer = 16;
+constexpr int kScanWindow = kScanThreads * kScanPer;
+
+__global__ void __launch_bounds__(kScanThreads)
+scan_kernel(const uint32_t* __restrict__ wt_cnt, int64_t nwt, uint32_t* __restrict__ base,
+            int32_t* __restrict__ row_ptr, int64_t nrows) {
+  constexpr int NW = kScanThreads / 64;
+  __shared__ uint32_t s_v[kScanWindow];
+  __shared__ uint32_t s_w[NW];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  uint32_t carry = 0;
+  for (int64_t w0 = 0; w0 < nwt; w0 += kScanWindow) {
+    uint32_t v[kScanPer];
+#pragma unroll
+    for (int k = 0; k < kScanPer; ++k) {
+      const int64_t i = w0 + k * kScanThreads + tid;
+      v[k] = i < nwt ? wt_cnt[i] : 0u;
+    }
+#pragma unroll
+    for (int k = 0; k < kScanPer; ++k) s_v[k * kScanThreads + tid] = v[k];
+    __syncthreads();
+    uint32_t run[kScanPer], sum = 0;
+#pragma unroll
+    for (int k = 0; k < kScanPer; ++k) {
+      run[k] = sum;
+      sum += s_v[tid * kScanPer + k];
+    }
+    uint32_t inc = sum;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t y = __shfl_up(inc, o, 64);
+      if (lane >= o) inc += y;
+    }
+    if (lane == 63) s_w[wv] = inc;
+    __syncthreads();
+    uint32_t before = carry + inc - sum, total = carry;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      before += w < wv ? s_w[w] : 0u;
+      total += s_w[w];
+    }
+#pragma unroll
+    for (int k = 0; k < kScanPer; ++k) s_v[tid * kScanPer + k] = before + run[k];
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kScanPer; ++k) {
+      const int64_t i = w0 + k * kScanThreads + tid;
+      if (i < nwt) base[i] = s_v[k * kScanThreads + tid];
+    }
+    carry = total;
+    __syncthreads();  // s_v / s_w are reused by the next window
+  }
+  if (tid == 0) {
+    base[nwt] = carry;
+    row_ptr[nrows] = (int32_t)carry;
+  }
+}
+
+// The dense CSR: one wave per wave tile adds the tile's base to its rows'
+// row_ptr entries and copies its staged entries.
 constexpr int kCopyUnroll = 4;
 
 __global__ void __launch_bounds__(kThreads)
-compact_kernel(const uint32_t* __restrict__ tile_cnt, uint32_t ntiles, int64_t TR, int64_t D,
-               int64_t nrows, const uint8_t* __restrict__ scol, const uint16_t* __restrict__ sval,
-               int32_t* __restrict__ row_ptr, uint8_t* __restrict__ col,
-               uint16_t* __restrict__ val, uint32_t cap) {
-  __shared__ uint32_t s_red[kThreads / 64];
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const uint32_t t0 = blockIdx.x * kCompactTiles;
-  uint32_t acc = 0;
-  for (uint32_t i = tid; i < t0; i += kThreads) acc += tile_cnt[i];
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, 64);
-  if (lane == 0) s_red[wv] = acc;
-  __syncthreads();
-  uint32_t base = 0;
-#pragma unroll
-  for (int w = 0; w < kThreads / 64; ++w) base += s_red[w];
-  const uint32_t tile = t0 + wv;
-  if (tile >= ntiles) return;
-  // counts of the block's earlier tiles, and this tile's
-  const uint32_t mine = lane < kCompactTiles && t0 + lane < ntiles ? tile_cnt[t0 + lane] : 0u;
-#pragma unroll
-  for (int w = 0; w < kCompactTiles; ++w) {
-    const uint32_t c = __shfl(mine, w, 64);
-    if (w < wv) base += c;
-  }
-  const uint32_t n = __shfl(mine, wv, 64);
-  const int64_t r0 = (int64_t)tile * TR;
-  for (int64_t i = lane; i < TR; i += 64) {
+copy_kernel(const uint32_t* __restrict__ base_arr, int64_t nwt, int64_t WT, int64_t D,
+            int64_t nrows, const uint32_t* __restrict__ sent, int32_t* __restrict__ row_ptr,
+            uint8_t* __restrict__ col, uint16_t* __restrict__ val, uint32_t cap) {
+  constexpr int NW = kThreads / 64;
+  const int lane = threadIdx.x & 63;
+  const int64_t wt = (int64_t)blockIdx.x * NW + (threadIdx.x >> 6);
+  if (wt >= nwt) return;
+  const uint32_t base = base_arr[wt];
+  const uint32_t n = min(base_arr[wt + 1] - base, (uint32_t)(WT * D));  // staging region bound
+  const int64_t r0 = wt * WT;
+  for (int64_t i = lane; i < WT; i += 64) {
     const int64_t r = r0 + i;
     if (r < nrows) row_ptr[r] += (int32_t)base;
   }
-  if (tile == ntiles - 1 && lane == 0) row_ptr[nrows] = (int32_t)(base + n);
   const int64_t src = r0 * D;
   for (uint32_t i0 = 0; i0 < n; i0 += 64 * kCopyUnroll) {
-    uint8_t cv[kCopyUnroll];
-    uint16_t vv[kCopyUnroll];
+    uint32_t ev[kCopyUnroll];
 #pragma unroll
     for (int u = 0; u < kCopyUnroll; ++u) {
       const uint32_t i = i0 + u * 64 + lane;
-      if (i < n) { cv[u] = scol[src + i]; vv[u] = sval[src + i]; }
+      if (i < n) ev[u] = sent[src + i];
     }
 #pragma unroll
     for (int u = 0; u < kCopyUnroll; ++u) {
       const uint32_t i = i0 + u * 64 + lane;
-      if (i < n && base + i < cap) { col[base + i] = cv[u]; val[base + i] = vv[u]; }
+      if (i < n && base + i < cap) {
+        col[base + i] = (uint8_t)(ev[u] >> 16);
+        val[base + i] = (uint16_t)ev[u];
+      }
     }
   }
 }
@@ -232,12 +271,6 @@ compact_kernel(const uint32_t* __restrict__ tile_cnt, uint32_t ntiles, int64_t T
 // when they fit (KLDS); per-token poles are staged per row.  CSR entries at or
 // beyond `cap` (the col/val capacity) are never read.
 constexpr int kUPasses = 4;
-
-HKV_DEV void wave_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
 
 template <bool PT, int G, int BITS, bool KLDS>
 __global__ void __launch_bounds__(kThreads)
@@ -355,13 +388,13 @@ bool pow2_G(int D) { return D % 8 == 0 && D >= 8 && D <= 256 && ((D / 8) & (D / 
 
 PackLayout pack_layout(int64_t nrows, int D) {
   PackLayout L;
-  const int64_t TR = (int64_t)(kThreads / (D / 8)) * kPasses;
-  L.ntiles = (nrows + TR - 1) / TR;
-  L.tile_elems = TR * D;
+  L.tile_rows = (int64_t)(64 / (D / 8)) * kPasses;
+  L.ntiles = (nrows + L.tile_rows - 1) / L.tile_rows;
+  L.tile_elems = L.tile_rows * D;
   L.cnt_off = 256;
-  L.col_off = L.cnt_off + align256(sizeof(uint32_t) * (size_t)L.ntiles);
-  L.val_off = L.col_off + align256((size_t)(L.ntiles * L.tile_elems));
-  L.bytes = L.val_off + sizeof(uint16_t) * (size_t)(L.ntiles * L.tile_elems);
+  L.base_off = L.cnt_off + align256(sizeof(uint32_t) * (size_t)L.ntiles);
+  L.ent_off = L.base_off + align256(sizeof(uint32_t) * (size_t)(L.ntiles + 1));
+  L.bytes = L.ent_off + sizeof(uint32_t) * (size_t)(L.ntiles * L.tile_elems);
   return L;
 }
 
@@ -379,12 +412,12 @@ int num_cus() {
 // Persistent grid: as many blocks as fit on the device at once (at most one
 // per tile).
 template <typename K>
-unsigned resident_grid(K kernel, int64_t ntiles) {
+unsigned resident_grid(K kernel, int64_t nblocks, size_t lds = 0) {
   int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kThreads, 0) != hipSuccess ||
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kThreads, lds) != hipSuccess ||
       per_cu < 1)
     per_cu = 1;
-  return (unsigned)std::min<int64_t>(ntiles, (int64_t)per_cu * num_cus());
+  return (unsigned)std::min<int64_t>(nblocks, (int64_t)per_cu * num_cus());
 }
 
 struct PackArgs {
@@ -394,18 +427,18 @@ struct PackArgs {
   hkv_nuq_scales sc;
   uint8_t* pk;
   int32_t* rp;
-  uint8_t* scol;
-  uint16_t* sval;
+  uint32_t* sent;
   uint32_t* cnt;
-  uint32_t ntiles;
+  int64_t ntiles;  // wave tiles
   hipStream_t s;
 };
 
 template <int NB, bool PT, int G, int BITS, bool KFIX>
 void launch_stage(const PackArgs& a) {
   auto k = pack_stage_kernel<NB, PT, G, BITS, KFIX>;
-  hipLaunchKernelGGL(k, dim3(resident_grid(k, a.ntiles)), dim3(kThreads), 0, a.s, a.x, a.nrows,
-                     a.H, a.sc, a.pk, a.rp, a.scol, a.sval, a.cnt, a.ntiles);
+  const int64_t nblocks = (a.ntiles + kThreads / 64 - 1) / (kThreads / 64);
+  hipLaunchKernelGGL(k, dim3(resident_grid(k, nblocks)), dim3(kThreads), 0, a.s, a.x, a.nrows,
+                     a.H, a.sc, a.pk, a.rp, a.sent, a.cnt, a.ntiles);
 }
 
 template <int NB, bool PT, int BITS, bool KFIX>
@@ -485,7 +518,7 @@ extern "C" int hkv_nuq_pack_compact(const void* values, int64_t T, int H, int D,
   const PackLayout lay = pack_layout(nrows, D);
   if (!workspace || workspace_bytes < lay.bytes || ((uintptr_t)workspace & 255u))
     return HKV_ERR_WORKSPACE;
-  const int G = D / 8, R = kThreads / G;
+  const int G = D / 8, RW = 64 / G;
   char* ws = (char*)workspace;
   PackArgs a;
   a.x = (const uint16_t*)values;
@@ -494,12 +527,11 @@ extern "C" int hkv_nuq_pack_compact(const void* values, int64_t T, int H, int D,
   a.sc = *scales;
   a.pk = (uint8_t*)packed;
   a.rp = row_ptr;
-  a.scol = (uint8_t*)(ws + lay.col_off);
-  a.sval = (uint16_t*)(ws + lay.val_off);
+  a.sent = (uint32_t*)(ws + lay.ent_off);
   a.cnt = (uint32_t*)(ws + lay.cnt_off);
-  a.ntiles = (uint32_t)lay.ntiles;
+  a.ntiles = lay.ntiles;
   a.s = s;
-  const bool kfix = (R % H) == 0;
+  const bool kfix = (RW % H) == 0;
   const int nb = nb_for_levels_host(a.sc.levels);
   if (bits == 4) {
     if (a.sc.per_token) launch_stage_nb<true, 4>(nb, kfix, G, a);
@@ -510,10 +542,13 @@ extern "C" int hkv_nuq_pack_compact(const void* values, int64_t T, int H, int D,
   }
   HKV_CHECK_LAUNCH();
   const uint32_t cap = (uint32_t)std::min<int64_t>(capacity, 0x7fffffff);
-  const unsigned cgrid = (unsigned)((lay.ntiles + kCompactTiles - 1) / kCompactTiles);
-  hipLaunchKernelGGL(compact_kernel, dim3(cgrid), dim3(kThreads), 0, s, a.cnt, a.ntiles,
-                     (int64_t)R * kPasses, (int64_t)D, nrows, a.scol, a.sval, row_ptr, col, val,
-                     cap);
+  uint32_t* bases = (uint32_t*)(ws + lay.base_off);
+  hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(kScanThreads), 0, s, a.cnt, a.ntiles, bases,
+                     row_ptr, nrows);
+  HKV_CHECK_LAUNCH();
+  const unsigned cgrid = (unsigned)((lay.ntiles + kThreads / 64 - 1) / (kThreads / 64));
+  hipLaunchKernelGGL(copy_kernel, dim3(cgrid), dim3(kThreads), 0, s, bases, a.ntiles,
+                     lay.tile_rows, (int64_t)D, nrows, a.sent, row_ptr, col, val, cap);
   HKV_CHECK_LAUNCH();
   return HKV_OK;
 }

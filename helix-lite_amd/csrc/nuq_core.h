@@ -43,7 +43,9 @@ HKV_DEV int slow_one(uint16_t xb, const SlowInfo& si, int64_t tab, int* o) {
 // index of element e (0..7); it is evaluated only on the exact-scan path.
 // code[j]: codes of elements 2j, 2j+1 in bits 0..3 / 16..19; om[j]: 0xffff lanes
 // for outliers.
-template <int NB, bool PT, typename TabFn>
+// SIGN: om[j] flags outliers in its sign bits only (bits 15 and 31) instead of
+// whole 0xffff lanes.
+template <int NB, bool PT, typename TabFn, bool SIGN = false>
 HKV_DEV void quant8(const uint4 xv, const Search2<NB>* S, const SlowInfo& si, TabFn tab,
                     uint32_t code[4], uint32_t om[4]) {
   const uint32_t x[4] = {xv.x, xv.y, xv.z, xv.w};
@@ -54,7 +56,8 @@ HKV_DEV void quant8(const uint4 xv, const Search2<NB>* S, const SlowInfo& si, Ta
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       code[j] = search2<NB>(x[j], S[PT ? 0 : j]);
-      om[j] = outlier2<NB>(x[j], S[PT ? 0 : j]);
+      if constexpr (SIGN) om[j] = outlier2_sign<NB>(x[j], S[PT ? 0 : j]);
+      else om[j] = outlier2<NB>(x[j], S[PT ? 0 : j]);
     }
   } else {
 #pragma unroll 1
@@ -87,20 +90,27 @@ HKV_DEV uint32_t pick4(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3, int k
   return (k & 2) ? hi : lo;
 }
 
-// Wave-wide exclusive prefix of a per-lane count in [0, 15] and the wave
-// total, from ballots of its bits (no LDS traffic).
+// Wave-wide inclusive prefix sum (row scans by DPP row_shr, then
+// row_bcast:15 / row_bcast:31 across the four 16-lane rows).
+template <int CTRL, int ROW_MASK>
+HKV_DEV uint32_t dpp_shifted(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, 0xf, true);
+}
+HKV_DEV uint32_t wave_incl_sum(uint32_t v) {
+  v += dpp_shifted<0x111, 0xf>(v);  // row_shr:1
+  v += dpp_shifted<0x112, 0xf>(v);  // row_shr:2
+  v += dpp_shifted<0x114, 0xf>(v);  // row_shr:4
+  v += dpp_shifted<0x118, 0xf>(v);  // row_shr:8
+  v += dpp_shifted<0x142, 0xa>(v);  // row_bcast:15 into rows 1, 3
+  v += dpp_shifted<0x143, 0xc>(v);  // row_bcast:31 into rows 2, 3
+  return v;
+}
+
+// Wave-wide exclusive prefix of a per-lane count, and the wave total.
 HKV_DEV uint32_t wave_excl_count(uint32_t cnt, uint32_t* total) {
-  const uint32_t lane = __lane_id();
-  const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-  uint32_t ex = 0, tot = 0;
-#pragma unroll
-  for (int b = 0; b < 4; ++b) {
-    const uint64_t m = __ballot((cnt >> b) & 1u);
-    ex += (uint32_t)__builtin_popcountll(m & lt) << b;
-    tot += (uint32_t)__builtin_popcountll(m) << b;
-  }
-  *total = tot;
-  return ex;
+  const uint32_t inc = wave_incl_sum(cnt);
+  *total = (uint32_t)__builtin_amdgcn_readlane((int)inc, 63);
+  return inc - cnt;
 }
 
 // Two 16-bit lanes holding small values -> two bytes (lane0 -> byte0).
@@ -119,6 +129,14 @@ HKV_DEV uint32_t pack_crumbs(const uint32_t c[4]) {
   uint32_t r = 0;
 #pragma unroll
   for (int j = 0; j < 4; ++j) r |= ((c[j] & 0x3u) | ((c[j] >> 14) & 0xcu)) << (4 * j);
+  return r;
+}
+
+// 8 outlier sign-bit flags (quant8<..., SIGN>) -> 8-bit mask, element e at bit e.
+HKV_DEV uint32_t mask_bits_sign(const uint32_t om[4]) {
+  uint32_t r = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) r |= (((om[j] >> 15) & 1u) | ((om[j] >> 30) & 2u)) << (2 * j);
   return r;
 }
 

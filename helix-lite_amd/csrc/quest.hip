@@ -178,7 +178,8 @@ constexpr int kBoundUnroll = 4;
 template <typename KT>
 __global__ void __launch_bounds__(256)
 bound_kernel(const void* q, int qdt, int group, const KT* __restrict__ kmin,
-             const KT* __restrict__ kmax, int64_t P, int H, int D, void* out, int odt) {
+             const KT* __restrict__ kmax, int64_t P, int H, int D, void* out, int odt,
+             int head_major) {
   extern __shared__ float qs[];  // [2][H][D]
   for (int i = threadIdx.x; i < H * D; i += 256) {
     float a, b;
@@ -218,8 +219,94 @@ bound_kernel(const void* q, int qdt, int group, const KT* __restrict__ kmin,
       const float b2 = row_reduce(ns[u], n);
       if (r < nrows && c == 0) {
         const float b = __fadd_rn(__fadd_rn(a, b2), 0.0f);
-        if (odt == HKV_DT_F16) ((uint16_t*)out)[r] = f2h(b);
-        else ((float*)out)[r] = b;
+        const int64_t o = head_major ? (r % H) * P + r / H : r;
+        if (odt == HKV_DT_F16) ((uint16_t*)out)[o] = f2h(b);
+        else ((float*)out)[o] = b;
+      }
+    }
+  }
+}
+
+constexpr int kBoundUnrollF16 = 8;  // row groups of loads in flight per thread
+
+// fp16 stats with D = 8*G (G a power of two, G <= 64): lane c of a row owns
+// channels [8c, 8c+8) and loads them with one 128-bit load per array.  HFIX:
+// the rows of one wave (64/G) are a multiple of H, so a lane's head is fixed
+// and its clamped query sums live in registers.  Same summation order as
+// bound_kernel.
+template <int G, bool HFIX>
+__global__ void __launch_bounds__(256)
+bound_f16_kernel(const void* q, int qdt, int group, const uint16_t* __restrict__ kmin,
+                 const uint16_t* __restrict__ kmax, int64_t P, int H, void* out, int odt,
+                 int head_major) {
+  constexpr int D = 8 * G;
+  constexpr int RB = 256 / G;  // rows per block per step
+  extern __shared__ float qs[];  // [2][H][D]
+  const int c = threadIdx.x % G, rl = threadIdx.x / G;
+  const int64_t nrows = P * H;
+  // the block's clamped, group-summed query, [2][H][D] in LDS
+  for (int i = threadIdx.x; i < H * D; i += 256) {
+    float a, b;
+    group_q(q, qdt, i / D, group, D, i % D, a, b);
+    qs[i] = a;
+    qs[H * D + i] = b;
+  }
+  __syncthreads();
+  float qp[8], qn[8];
+  if constexpr (HFIX) {
+    const int h = rl % H;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      qp[i] = qs[h * D + 8 * c + i];
+      qn[i] = qs[H * D + h * D + 8 * c + i];
+    }
+  }
+  const int64_t span = (int64_t)RB * kBoundUnrollF16;
+  for (int64_t r0 = (int64_t)blockIdx.x * span; r0 < nrows; r0 += (int64_t)gridDim.x * span) {
+    uint4 a[kBoundUnrollF16], b[kBoundUnrollF16];
+#pragma unroll
+    for (int u = 0; u < kBoundUnrollF16; ++u) {
+      const int64_t r = r0 + (int64_t)u * RB + rl;
+      a[u] = b[u] = make_uint4(0u, 0u, 0u, 0u);
+      if (r < nrows) {
+        a[u] = reinterpret_cast<const uint4*>(kmin + r * D)[c];
+        b[u] = reinterpret_cast<const uint4*>(kmax + r * D)[c];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kBoundUnrollF16; ++u) {
+      const int64_t r = r0 + (int64_t)u * RB + rl;
+      int h;
+      int64_t p;
+      if constexpr (HFIX) {
+        h = rl % H;
+        p = (r0 + (int64_t)u * RB) / H + rl / H;
+      } else {
+        p = r / H;
+        h = (int)(r - p * H);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          qp[i] = qs[h * D + 8 * c + i];
+          qn[i] = qs[H * D + h * D + 8 * c + i];
+        }
+      }
+      const uint32_t wa[4] = {a[u].x, a[u].y, a[u].z, a[u].w};
+      const uint32_t wb[4] = {b[u].x, b[u].y, b[u].z, b[u].w};
+      float ps = 0.0f, ns = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float kmx = h2f((uint16_t)(wb[i >> 1] >> (16 * (i & 1))));
+        const float kmn = h2f((uint16_t)(wa[i >> 1] >> (16 * (i & 1))));
+        ps = __fadd_rn(ps, __fmul_rn(qp[i], kmx));
+        ns = __fadd_rn(ns, __fmul_rn(qn[i], kmn));
+      }
+      ps = row_reduce(ps, G);
+      ns = row_reduce(ns, G);
+      if (r < nrows && c == 0) {
+        const float v = __fadd_rn(__fadd_rn(ps, ns), 0.0f);
+        const int64_t o = head_major ? (int64_t)h * P + p : r;
+        if (odt == HKV_DT_F16) ((uint16_t*)out)[o] = f2h(v);
+        else ((float*)out)[o] = v;
       }
     }
   }
@@ -239,10 +326,14 @@ HKV_DEV uint32_t ukey(float f) {
   return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
+constexpr int kCand = 4096;  // keys of the first digit's bin kept in LDS
+
 struct SelShared {
   uint32_t hist[kBins];
   uint32_t wred[kSelWaves][4];
   uint32_t bcast[8];
+  uint32_t cand[kCand];
+  uint32_t ncand;
 };
 
 // Block-wide (1024 threads) reductions through LDS.
@@ -268,14 +359,15 @@ HKV_DEV uint32_t block_max_u32(uint32_t v, SelShared& sh) {
 }
 
 // Key of candidate i (i in [0, n)) of the column; column element p = s + i.
+// Column h of a score matrix: page p at base[h * hstride + p * stride].
 struct ColumnF32 {
   const float* base;
-  int64_t stride;
+  int64_t stride, hstride;
   HKV_DEV uint32_t key(int64_t p) const { return ukey(base[p * stride]); }
 };
 struct ColumnF16 {
   const uint16_t* base;
-  int64_t stride;
+  int64_t stride, hstride;
   HKV_DEV uint32_t key(int64_t p) const { return ukey(h2f(base[p * stride])); }
 };
 
@@ -402,65 +494,58 @@ HKV_DEV void select_column(const Col& col, int64_t P, int64_t s, int64_t keff, i
   }
 }
 
-// Radix search shared by both selectors: the keff-th largest key T among
-// the candidates and how many keys equal to T are taken (lowest pages first).
-// `count(pmask, prefix, lo, nb)` adds, into sh.hist, the digit (k >> lo) &
-// (nb-1) of every candidate key k with (k & pmask) == prefix.
+// One radix digit over bits [lo, hb] (lo = max(hb - 10, 0)) of the keys that
+// match `prefix` under `pmask`: finds the bin holding the krem-th largest such
+// key, narrows prefix / pmask to it and subtracts the keys in higher bins from
+// krem.  `count(pmask, prefix, lo, nb)` adds, into sh.hist, the digit
+// (k >> lo) & (nb - 1) of every candidate key k with (k & pmask) == prefix.
+// Returns lo; *inbin = the number of keys in the chosen bin.
 template <typename CountFn>
-HKV_DEV void radix_threshold(uint32_t kmn, uint32_t kmx, int64_t keff, SelShared& sh,
-                             CountFn count, uint32_t& T_out, uint32_t& need_eq) {
+HKV_DEV int radix_digit(int hb, uint32_t& prefix, uint32_t& pmask, uint32_t& krem, SelShared& sh,
+                        CountFn count, uint32_t* inbin) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  uint32_t prefix = kmx, pmask = 0xffffffffu;
-  uint32_t krem = (uint32_t)keff;
-  if (kmn != kmx) {
-    int hb = 31 - __builtin_clz(kmn ^ kmx);
-    pmask = hb == 31 ? 0u : ~((2u << hb) - 1u);
-    prefix = kmx & pmask;
-    while (true) {
-      const int lo = hb >= 10 ? hb - 10 : 0;
-      const uint32_t nb = 1u << (hb - lo + 1);
-      for (int i = tid; i < (int)nb; i += kSelThreads) sh.hist[i] = 0;
-      __syncthreads();
-      count(pmask, prefix, lo, nb);
-      __syncthreads();
-      {
-        const uint32_t h0 = 2 * tid < (int)nb ? sh.hist[2 * tid] : 0u;
-        const uint32_t h1 = 2 * tid + 1 < (int)nb ? sh.hist[2 * tid + 1] : 0u;
-        const uint32_t loc = h0 + h1;
-        uint32_t inc = loc;  // inclusive suffix within the wave
+  const int lo = hb >= 10 ? hb - 10 : 0;
+  const uint32_t nb = 1u << (hb - lo + 1);
+  for (int i = tid; i < (int)nb; i += kSelThreads) sh.hist[i] = 0;
+  __syncthreads();
+  count(pmask, prefix, lo, nb);
+  __syncthreads();
+  {
+    const uint32_t h0 = 2 * tid < (int)nb ? sh.hist[2 * tid] : 0u;
+    const uint32_t h1 = 2 * tid + 1 < (int)nb ? sh.hist[2 * tid + 1] : 0u;
+    const uint32_t loc = h0 + h1;
+    uint32_t inc = loc;  // inclusive suffix within the wave
 #pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-          const uint32_t y = __shfl_down(inc, o, 64);
-          if (lane + o < 64) inc += y;
-        }
-        if (lane == 0) sh.wred[w][0] = inc;
-        __syncthreads();
-        uint32_t later = 0;
-        for (int i = w + 1; i < kSelWaves; ++i) later += sh.wred[i][0];
-        const uint32_t sfx = later + inc - loc;  // count in bins above 2t+1
-        if (sfx < krem && krem <= sfx + loc) {
-          if (sfx + h1 >= krem) { sh.bcast[0] = 2 * tid + 1; sh.bcast[1] = sfx; }
-          else { sh.bcast[0] = 2 * tid; sh.bcast[1] = sfx + h1; }
-        }
-        __syncthreads();
-      }
-      const uint32_t b = sh.bcast[0], above = sh.bcast[1];
-      krem -= above;
-      prefix |= b << lo;
-      pmask |= (nb - 1) << lo;
-      __syncthreads();
-      if (lo == 0) break;
-      hb = lo - 1;
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t y = __shfl_down(inc, o, 64);
+      if (lane + o < 64) inc += y;
     }
+    if (lane == 0) sh.wred[w][0] = inc;
+    __syncthreads();
+    uint32_t later = 0;
+    for (int i = w + 1; i < kSelWaves; ++i) later += sh.wred[i][0];
+    const uint32_t sfx = later + inc - loc;  // count in bins above 2t+1
+    if (sfx < krem && krem <= sfx + loc) {
+      if (sfx + h1 >= krem) { sh.bcast[0] = 2 * tid + 1; sh.bcast[1] = sfx; sh.bcast[2] = h1; }
+      else { sh.bcast[0] = 2 * tid; sh.bcast[1] = sfx + h1; sh.bcast[2] = h0; }
+    }
+    __syncthreads();
   }
-  T_out = prefix;
-  need_eq = krem;
+  const uint32_t b = sh.bcast[0], above = sh.bcast[1];
+  *inbin = sh.bcast[2];
+  krem -= above;
+  prefix |= b << lo;
+  pmask |= (nb - 1) << lo;
+  __syncthreads();
+  return lo;
 }
 
 // Register-resident selector for n = P - s <= 1024 * KPT candidates: wave w
 // holds pages s + w*64*KPT + i*64 + lane (i < KPT) as keys; the radix passes
-// and the ordered write read only registers.  Same contract as
-// select_column.
+// and the ordered write read only registers.  Slots past the last page hold
+// key 0, which is below every real key (ukey >= 0x007fffff), so it is never
+// selected, never equal to the threshold and never in the threshold's radix
+// bin: no pass needs a validity test.  Same contract as select_column.
 template <int KPT, typename Col>
 HKV_DEV void select_column_regs(const Col& col, int64_t P, int64_t s, int64_t keff, int64_t* out,
                                 int64_t ostride, SelShared& sh) {
@@ -468,38 +553,75 @@ HKV_DEV void select_column_regs(const Col& col, int64_t P, int64_t s, int64_t ke
   for (int64_t i = tid; i < s; i += kSelThreads) out[i * ostride] = i;
   if (keff <= 0) return;
   const int64_t c0 = s + (int64_t)w * (64 * KPT) + lane;  // page of key[0]
-  // key[i] is a candidate iff i*64 < lim
-  const int64_t lim = P - c0;
+  const int64_t lim = P - c0;                              // key[i] is a page iff i*64 < lim
   uint32_t key[KPT];
-  uint32_t kmn = 0xffffffffu, kmx = 0;
 #pragma unroll
   for (int i = 0; i < KPT; ++i) key[i] = (int64_t)i * 64 < lim ? col.key(c0 + (int64_t)i * 64) : 0u;
+  // min over real keys: the sentinel 0 wraps to the largest value under "- 1"
+  uint32_t kmn = 0xffffffffu, kmx = 0;
 #pragma unroll
   for (int i = 0; i < KPT; ++i) {
-    if ((int64_t)i * 64 < lim) {
-      kmn = key[i] < kmn ? key[i] : kmn;
-      kmx = key[i] > kmx ? key[i] : kmx;
-    }
+    const uint32_t m1 = key[i] - 1u;
+    kmn = m1 < kmn ? m1 : kmn;
+    kmx = key[i] > kmx ? key[i] : kmx;
   }
-  kmn = block_min_u32(kmn, sh);
+  kmn = block_min_u32(kmn, sh) + 1u;
   kmx = block_max_u32(kmx, sh);
-  uint32_t T, need_eq;
-  radix_threshold(kmn, kmx, keff, sh,
-                  [&](uint32_t pmask, uint32_t prefix, int lo, uint32_t nb) {
+  auto count_regs = [&](uint32_t pmask, uint32_t prefix, int lo, uint32_t nb) {
 #pragma unroll
-                    for (int i = 0; i < KPT; ++i)
-                      if ((int64_t)i * 64 < lim && (key[i] & pmask) == prefix)
-                        atomicAdd(&sh.hist[(key[i] >> lo) & (nb - 1)], 1u);
-                  },
-                  T, need_eq);
+    for (int i = 0; i < KPT; ++i)
+      atomicAdd(&sh.hist[(key[i] >> lo) & (nb - 1)], (key[i] & pmask) == prefix ? 1u : 0u);
+  };
+  // First digit over the registers; then, when the chosen bin is small, its
+  // keys are compacted into LDS and the remaining digits run over them only.
+  uint32_t T = kmx, need_eq = (uint32_t)keff;
+  if (kmn != kmx) {
+    int hb = 31 - __builtin_clz(kmn ^ kmx);
+    uint32_t pmask = hb == 31 ? 0u : ~((2u << hb) - 1u);
+    uint32_t prefix = kmx & pmask, krem = (uint32_t)keff, inbin;
+    int lo = radix_digit(hb, prefix, pmask, krem, sh, count_regs, &inbin);
+    if (lo > 0 && inbin <= (uint32_t)kCand) {
+      if (tid == 0) sh.ncand = 0;
+      __syncthreads();
+      const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+#pragma unroll
+      for (int i = 0; i < KPT; ++i) {
+        const bool in = (key[i] & pmask) == prefix;
+        const uint64_t m = __ballot(in);
+        if (m) {
+          const int leader = __builtin_ctzll(m);
+          uint32_t base = 0;
+          if (lane == leader) base = atomicAdd(&sh.ncand, (uint32_t)__builtin_popcountll(m));
+          base = __shfl(base, leader, 64);
+          if (in) sh.cand[base + __builtin_popcountll(m & lt)] = key[i];
+        }
+      }
+      __syncthreads();
+      const uint32_t nc = sh.ncand;
+      auto count_cand = [&](uint32_t pm, uint32_t pf, int l, uint32_t nbins) {
+        for (uint32_t j = tid; j < nc; j += kSelThreads) {
+          const uint32_t k = sh.cand[j];
+          atomicAdd(&sh.hist[(k >> l) & (nbins - 1)], (k & pm) == pf ? 1u : 0u);
+        }
+      };
+      while (lo > 0) lo = radix_digit(lo - 1, prefix, pmask, krem, sh, count_cand, &inbin);
+    } else {
+      while (lo > 0) lo = radix_digit(lo - 1, prefix, pmask, krem, sh, count_regs, &inbin);
+    }
+    T = prefix;
+    need_eq = krem;
+  }
 
   uint32_t cgt = 0, ceq = 0;
 #pragma unroll
   for (int i = 0; i < KPT; ++i) {
-    const bool v = (int64_t)i * 64 < lim;
-    cgt += v && key[i] > T;
-    ceq += v && key[i] == T;
+    cgt += key[i] > T ? 1u : 0u;
+    ceq += key[i] == T ? 1u : 0u;
   }
+  // A fresh copy of T for the ordered write: otherwise the compiler keeps the
+  // 64 compare masks of the count pass alive (in SGPRs, then spilled) to reuse.
+  uint32_t Tw;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(Tw) : "v"(T));
   for (int o = 32; o >= 1; o >>= 1) {
     cgt += __shfl_xor(cgt, o, 64);
     ceq += __shfl_xor(ceq, o, 64);
@@ -518,11 +640,10 @@ HKV_DEV void select_column_regs(const Col& col, int64_t P, int64_t s, int64_t ke
   const uint64_t lanemask_lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
 #pragma unroll
   for (int i = 0; i < KPT; ++i) {
-    const bool v = (int64_t)i * 64 < lim;
-    const bool is_eq = v && key[i] == T;
+    const bool is_eq = key[i] == Tw;
     const uint64_t eqm = __ballot(is_eq);
     const uint32_t eq_rank = eq_before + run_eq + __builtin_popcountll(eqm & lanemask_lt);
-    const bool sel = v && (key[i] > T || (is_eq && eq_rank < need_eq));
+    const bool sel = key[i] > Tw || (is_eq && eq_rank < need_eq);
     const uint64_t selm = __ballot(sel);
     if (sel) {
       const uint32_t pos = out_before + run_out + __builtin_popcountll(selm & lanemask_lt);
@@ -555,72 +676,7 @@ topk_kernel(Col col0, int64_t P, int H, int64_t s, int64_t keff, int64_t* out) {
   __shared__ SelShared sh;
   const int h = blockIdx.x;
   Col col = col0;
-  col.base += h;
-  select_any<KPT>(col, P, s, keff, out + h, H, sh);
-}
-
-// ----------------------------------------------- fused score + select (cfg3)
-
-struct SelectWs {
-  uint32_t done[64];  // per-head block completion counters
-};
-
-constexpr int kScoreUnroll = 4;
-
-// grid (page blocks, H); 1024 threads; rows are pages of head h.  Scores go to
-// scores[h*P + p] (head-major).  The last block of head h selects for head h.
-template <int KPT, typename KT>
-__global__ void __launch_bounds__(kSelThreads)
-select_fused_kernel(const void* q, int qdt, int group, const KT* __restrict__ kmin,
-                    const KT* __restrict__ kmax, int64_t P, int H, int D, int64_t pages_per_block,
-                    float* __restrict__ scores, int64_t s, int64_t keff, int64_t* out,
-                    SelectWs* ws) {
-  __shared__ SelShared sh;
-  __shared__ uint32_t s_last;
-  const int h = blockIdx.y;
-  const int n = lanes_for(D);
-  const int c = threadIdx.x % n;
-  const int rows = kSelThreads / n;
-  float qp[8], qn[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int d = 8 * c + i;
-    if (d < D) group_q(q, qdt, h, group, D, d, qp[i], qn[i]);
-    else { qp[i] = 0.0f; qn[i] = 0.0f; }
-  }
-  const int64_t pb0 = (int64_t)blockIdx.x * pages_per_block;
-  const int64_t pb1 = pb0 + pages_per_block < P ? pb0 + pages_per_block : P;
-  for (int64_t p0 = pb0; p0 < pb1; p0 += (int64_t)rows * kScoreUnroll) {
-    float ps[kScoreUnroll], ns[kScoreUnroll];
-#pragma unroll
-    for (int u = 0; u < kScoreUnroll; ++u) {
-      const int64_t p = p0 + (int64_t)u * rows + threadIdx.x / n;
-      ps[u] = 0.0f;
-      ns[u] = 0.0f;
-      if (p < pb1) {
-        const int64_t row = p * H + h;
-        chunk_sums<KT>(kmin + row * D, kmax + row * D, D, c, qp, qn, ps[u], ns[u]);
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < kScoreUnroll; ++u) {
-      const int64_t p = p0 + (int64_t)u * rows + threadIdx.x / n;
-      const float a = row_reduce(ps[u], n);
-      const float b = row_reduce(ns[u], n);
-      if (p < pb1 && c == 0) scores[(int64_t)h * P + p] = __fadd_rn(__fadd_rn(a, b), 0.0f);
-    }
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const uint32_t prev = atomicAdd(&ws->done[h], 1u);
-    s_last = prev == gridDim.x - 1;
-    if (s_last) ws->done[h] = 0;
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-  ColumnF32 col{scores + (int64_t)h * P, 1};
+  col.base += h * col.hstride;
   select_any<KPT>(col, P, s, keff, out + h, H, sh);
 }
 
@@ -663,45 +719,75 @@ extern "C" int hkv_quest_page_stats(const void* k_pages, int dtype, int64_t P, i
   return HKV_OK;
 }
 
-extern "C" int hkv_quest_page_bound(const void* q, int q_dtype, int Hq, const void* kmin,
-                                    const void* kmax, int k_dtype, int64_t P, int H, int D,
-                                    void* out, int out_dtype, void* stream) {
+namespace {
+
+template <int G>
+void launch_bound_f16(bool hfix, unsigned grid, size_t lds, hipStream_t s, const void* q, int qdt,
+                      int group, const uint16_t* kmin, const uint16_t* kmax, int64_t P, int H,
+                      void* out, int odt, int head_major) {
+  if (hfix)
+    hipLaunchKernelGGL((bound_f16_kernel<G, true>), dim3(grid), dim3(256), lds, s, q, qdt, group,
+                       kmin, kmax, P, H, out, odt, head_major);
+  else
+    hipLaunchKernelGGL((bound_f16_kernel<G, false>), dim3(grid), dim3(256), lds, s, q, qdt, group,
+                       kmin, kmax, P, H, out, odt, head_major);
+}
+
+// Bound into out, (P,H) or head-major (H,P).
+int page_bound(const void* q, int q_dtype, int Hq, const void* kmin, const void* kmax, int k_dtype,
+               int64_t P, int H, int D, void* out, int out_dtype, int head_major,
+               hipStream_t s) {
   if (!fdt(q_dtype) && q_dtype != HKV_DT_BF16) return HKV_ERR_DTYPE;
   if (!fdt(k_dtype) || !fdt(out_dtype)) return HKV_ERR_DTYPE;
   if (P < 0 || H < 1 || D < 1 || D > 512 || Hq < H || Hq % H) return HKV_ERR_SHAPE;
   if (P == 0) return HKV_OK;
   if (!q || !kmin || !kmax || !out) return HKV_ERR_ARG;
-  const int esz = k_dtype == HKV_DT_F16 ? 2 : 4;
   if (D % 8 == 0 && (((uintptr_t)kmin | (uintptr_t)kmax) & 15u)) return HKV_ERR_ARG;
-  (void)esz;
-  hipStream_t s = (hipStream_t)stream;
   const int64_t rows = P * H;
+  const size_t lds = sizeof(float) * 2 * H * D;
+  if (lds > 64 * 1024) return HKV_ERR_SHAPE;
+  const int G = D / 8;
+  if (k_dtype == HKV_DT_F16 && D % 8 == 0 && (G & (G - 1)) == 0 && G <= 64) {
+    const int64_t span = (int64_t)(256 / G) * kBoundUnrollF16;
+    const unsigned grid =
+        (unsigned)std::min<int64_t>((rows + span - 1) / span, (int64_t)num_cus() * 8);
+    const bool hfix = (64 / G) % H == 0;
+    auto mn = (const uint16_t*)kmin;
+    auto mx = (const uint16_t*)kmax;
+    const int group = Hq / H;
+    switch (G) {
+      case 1: launch_bound_f16<1>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major); break;
+      case 2: launch_bound_f16<2>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major); break;
+      case 4: launch_bound_f16<4>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major); break;
+      case 8: launch_bound_f16<8>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major); break;
+      case 16: launch_bound_f16<16>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major); break;
+      case 32: launch_bound_f16<32>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major); break;
+      default: launch_bound_f16<64>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major); break;
+    }
+    HKV_CHECK_LAUNCH();
+    return HKV_OK;
+  }
   int n = 1;
   while (n < (D + 7) / 8) n <<= 1;
   const int rpb = 256 / n;
   const int64_t span = (int64_t)rpb * kBoundUnroll;
   const unsigned grid = (unsigned)std::min<int64_t>((rows + span - 1) / span, (int64_t)num_cus() * 8);
-  const size_t lds = sizeof(float) * 2 * H * D;
-  if (lds > 64 * 1024) return HKV_ERR_SHAPE;
   if (k_dtype == HKV_DT_F16)
     hipLaunchKernelGGL(bound_kernel<uint16_t>, dim3(grid), dim3(256), lds, s, q, q_dtype, Hq / H,
-                       (const uint16_t*)kmin, (const uint16_t*)kmax, P, H, D, out, out_dtype);
+                       (const uint16_t*)kmin, (const uint16_t*)kmax, P, H, D, out, out_dtype,
+                       head_major);
   else
     hipLaunchKernelGGL(bound_kernel<float>, dim3(grid), dim3(256), lds, s, q, q_dtype, Hq / H,
-                       (const float*)kmin, (const float*)kmax, P, H, D, out, out_dtype);
+                       (const float*)kmin, (const float*)kmax, P, H, D, out, out_dtype,
+                       head_major);
   HKV_CHECK_LAUNCH();
   return HKV_OK;
 }
 
-extern "C" size_t hkv_quest_topk_workspace_bytes(int64_t P, int H) {
-  (void)P;
-  (void)H;
-  return sizeof(SelectWs);
-}
-
-extern "C" int hkv_quest_topk(const void* bound, int b_dtype, int64_t P, int H, int64_t k,
-                              int64_t sink_pages, int64_t* out, int64_t* n_out, void* workspace,
-                              size_t workspace_bytes, void* stream) {
+// Top-K over columns of a score matrix with page stride `ps` and head stride
+// `hs` (elements).
+int topk(const void* bound, int b_dtype, int64_t P, int H, int64_t ps, int64_t hs, int64_t k,
+         int64_t sink_pages, int64_t* out, int64_t* n_out, hipStream_t st) {
   if (!fdt(b_dtype)) return HKV_ERR_DTYPE;
   if (P < 0 || H < 1) return HKV_ERR_SHAPE;
   const int64_t s = sink_pages < 0 ? 0 : (sink_pages > P ? P : sink_pages);
@@ -709,17 +795,14 @@ extern "C" int hkv_quest_topk(const void* bound, int b_dtype, int64_t P, int H, 
   if (n_out) *n_out = s + keff;
   if (s + keff == 0) return HKV_OK;
   if (!bound || !out) return HKV_ERR_ARG;
-  (void)workspace;
-  (void)workspace_bytes;
-  hipStream_t st = (hipStream_t)stream;
   const int kpt = kpt_for(P - s);
 #define HKV_TOPK(K)                                                                        \
   if (b_dtype == HKV_DT_F32)                                                               \
     hipLaunchKernelGGL((topk_kernel<K, ColumnF32>), dim3(H), dim3(kSelThreads), 0, st,     \
-                       ColumnF32{(const float*)bound, H}, P, H, s, keff, out);            \
+                       ColumnF32{(const float*)bound, ps, hs}, P, H, s, keff, out);       \
   else                                                                                     \
     hipLaunchKernelGGL((topk_kernel<K, ColumnF16>), dim3(H), dim3(kSelThreads), 0, st,     \
-                       ColumnF16{(const uint16_t*)bound, H}, P, H, s, keff, out);
+                       ColumnF16{(const uint16_t*)bound, ps, hs}, P, H, s, keff, out);
   switch (kpt) {
     case 4: HKV_TOPK(4) break;
     case 16: HKV_TOPK(16) break;
@@ -731,46 +814,47 @@ extern "C" int hkv_quest_topk(const void* bound, int b_dtype, int64_t P, int H, 
   return HKV_OK;
 }
 
+}  // namespace
+
+extern "C" int hkv_quest_page_bound(const void* q, int q_dtype, int Hq, const void* kmin,
+                                    const void* kmax, int k_dtype, int64_t P, int H, int D,
+                                    void* out, int out_dtype, void* stream) {
+  return page_bound(q, q_dtype, Hq, kmin, kmax, k_dtype, P, H, D, out, out_dtype, 0,
+                    (hipStream_t)stream);
+}
+
+// The selectors keep all state in LDS and registers; a nominal size is
+// returned so callers that always pass a workspace keep working.
+extern "C" size_t hkv_quest_topk_workspace_bytes(int64_t P, int H) {
+  (void)P;
+  (void)H;
+  return 256;
+}
+
+extern "C" int hkv_quest_topk(const void* bound, int b_dtype, int64_t P, int H, int64_t k,
+                              int64_t sink_pages, int64_t* out, int64_t* n_out, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  (void)workspace;
+  (void)workspace_bytes;
+  return topk(bound, b_dtype, P, H, H, 1, k, sink_pages, out, n_out, (hipStream_t)stream);
+}
+
 extern "C" int hkv_quest_select(const void* q, int q_dtype, int Hq, const void* kmin,
                                 const void* kmax, int k_dtype, int64_t P, int H, int D, int64_t k,
                                 int64_t sink_pages, float* scores, int64_t* out, int64_t* n_out,
                                 void* workspace, size_t workspace_bytes, void* stream) {
+  (void)workspace;
+  (void)workspace_bytes;
   if (!fdt(q_dtype) && q_dtype != HKV_DT_BF16) return HKV_ERR_DTYPE;
   if (!fdt(k_dtype)) return HKV_ERR_DTYPE;
-  if (P < 0 || H < 1 || H > 64 || D < 1 || D > 512 || Hq < H || Hq % H) return HKV_ERR_SHAPE;
+  if (P < 0 || H < 1 || D < 1 || D > 512 || Hq < H || Hq % H) return HKV_ERR_SHAPE;
   const int64_t s = sink_pages < 0 ? 0 : (sink_pages > P ? P : sink_pages);
   const int64_t keff = k < 0 ? 0 : (k > P - s ? P - s : k);
   if (n_out) *n_out = s + keff;
   if (P == 0) return HKV_OK;
   if (!q || !kmin || !kmax || !scores || !out) return HKV_ERR_ARG;
-  if (!workspace || workspace_bytes < sizeof(SelectWs)) return HKV_ERR_WORKSPACE;
-  if (D % 8 == 0 && (((uintptr_t)kmin | (uintptr_t)kmax) & 15u)) return HKV_ERR_ARG;
-  hipStream_t st = (hipStream_t)stream;
-  int n = 1;
-  while (n < (D + 7) / 8) n <<= 1;
-  const int64_t rows = kSelThreads / n;
-  // enough blocks to fill the chip, each a multiple of the block's row count
-  int64_t target = std::max<int64_t>(1, (int64_t)num_cus() * 2 / H);
-  int64_t ppb = (P + target - 1) / target;
-  ppb = std::max<int64_t>(rows, (ppb + rows - 1) / rows * rows);
-  const unsigned gx = (unsigned)((P + ppb - 1) / ppb);
-  const int kpt = kpt_for(P - s);
-#define HKV_SEL(K)                                                                             \
-  if (k_dtype == HKV_DT_F16)                                                                   \
-    hipLaunchKernelGGL((select_fused_kernel<K, uint16_t>), dim3(gx, H), dim3(kSelThreads), 0,  \
-                       st, q, q_dtype, Hq / H, (const uint16_t*)kmin, (const uint16_t*)kmax, P, \
-                       H, D, ppb, scores, s, keff, out, (SelectWs*)workspace);                 \
-  else                                                                                         \
-    hipLaunchKernelGGL((select_fused_kernel<K, float>), dim3(gx, H), dim3(kSelThreads), 0, st, \
-                       q, q_dtype, Hq / H, (const float*)kmin, (const float*)kmax, P, H, D,    \
-                       ppb, scores, s, keff, out, (SelectWs*)workspace);
-  switch (kpt) {
-    case 4: HKV_SEL(4) break;
-    case 16: HKV_SEL(16) break;
-    case 64: HKV_SEL(64) break;
-    default: HKV_SEL(0) break;
-  }
-#undef HKV_SEL
-  HKV_CHECK_LAUNCH();
-  return HKV_OK;
+  const int st = page_bound(q, q_dtype, Hq, kmin, kmax, k_dtype, P, H, D, scores, HKV_DT_F32, 1,
+                            (hipStream_t)stream);
+  if (st != HKV_OK) return st;
+  return topk(scores, HKV_DT_F32, P, H, 1, P, k, sink_pages, out, nullptr, (hipStream_t)stream);
 }

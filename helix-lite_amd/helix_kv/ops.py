@@ -338,10 +338,11 @@ def quest_topk(bound: torch.Tensor, k: int, sink_pages: int = 1) -> torch.Tensor
 def quest_select(query: torch.Tensor, K_min: torch.Tensor, K_max: torch.Tensor, k: int,
                  sink_pages: int, *, scores: torch.Tensor | None = None,
                  out: torch.Tensor | None = None):
-    """Fused bound + top-K for one decode step.
+    """Bound + top-K for one decode step.
 
     query (Hq,D) with Hq a multiple of H; stats (P,H,D) fp16/fp32.  Returns
-    (indices (sinks + k_eff, H) int64, scores (H,P) fp32 head-major).
+    (indices (sinks + k_eff, H) int64, scores (H,P) fp32 head-major -- the
+    group-summed bound of every page).
     """
     N.require_gpu(query, K_min, K_max)
     if K_min.dim() != 3 or K_min.shape != K_max.shape:
@@ -359,10 +360,11 @@ def quest_select(query: torch.Tensor, K_min: torch.Tensor, K_max: torch.Tensor, 
         out = torch.empty((s + keff, H), dtype=torch.int64, device=kmin.device)
     if scores is None:
         scores = torch.empty((H, P), dtype=torch.float32, device=kmin.device)
-    ws = N.workspace("quest_select", 256, kmin.device)
+    if tuple(out.shape) != (s + keff, H) or tuple(scores.shape) != (H, P):
+        raise ValueError("out must be (sinks + k_eff, H) and scores (H, P)")
     n_out = N._i64(0)
     st = N.lib().hkv_quest_select(N.ptr(q), N.dtype_code(q), Hq, N.ptr(kmin), N.ptr(kmax),
                                   _fdt(kmin), P, H, D, int(k), int(sink_pages), N.ptr(scores),
-                                  N.ptr(out), n_out, N.ptr(ws), ws.numel(), N.stream_of(q))
+                                  N.ptr(out), n_out, None, 0, N.stream_of(q))
     N.check(st, "hkv_quest_select", ValueError)
     return out, scores

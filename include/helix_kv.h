@@ -201,7 +201,8 @@ int hkv_quest_page_bound(const void *q, int q_dtype, int Hq, const void *kmin,
  * (sinks + k_eff, H) int64, per head the sinks then the k_eff highest-bound
  * non-sink pages, ascending; ties go to the lower page index; NaN ranks highest.
  * src/quest/reference.py:96-133.  Returns sinks + k_eff through *n_out.
- * workspace: hkv_quest_topk_workspace_bytes(P, H) bytes, zero-filled once.
+ * workspace: unused (may be NULL); hkv_quest_topk_workspace_bytes is kept for
+ * callers that size one.
  */
 size_t hkv_quest_topk_workspace_bytes(int64_t P, int H);
 int hkv_quest_topk(const void *bound, int b_dtype, int64_t P, int H, int64_t k,
@@ -209,10 +210,12 @@ int hkv_quest_topk(const void *bound, int b_dtype, int64_t P, int H, int64_t k,
                    size_t workspace_bytes, void *stream);
 
 /*
- * Fused Quest selection for one decode step: bound (as hkv_quest_page_bound,
- * f32) + top-K with sinks (as hkv_quest_topk) in one launch.  scores (P,H) f32
- * receives the bounds.  The per-layer path of src/kvquant/quest_selector.py:
- * 64-78 without the union.
+ * Quest selection for one decode step: the bound (as hkv_quest_page_bound,
+ * f32, written head-major to scores (H,P)) then the top-K with sinks (as
+ * hkv_quest_topk),
+ * two launches on `stream`.  The per-layer path of src/kvquant/quest_selector.py:
+ * 64-78 without the union.  workspace / workspace_bytes are unused (may be
+ * NULL / 0).
  */
 int hkv_quest_select(const void *q, int q_dtype, int Hq, const void *kmin, const void *kmax,
                      int k_dtype, int64_t P, int H, int D, int64_t k, int64_t sink_pages,

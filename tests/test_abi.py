@@ -36,13 +36,15 @@ def test_host_only_entry_points():
     assert b"gfx950" in L.hkv_version()
     assert L.hkv_status_string(0) == b"ok"
     assert L.hkv_status_string(4) == b"output capacity too small"
-    # 256-byte header, one u32 count per tile of 128 rows (D = 128), then the
-    # staging columns (1 B) and values (2 B) of every element, 256-aligned
-    ntiles = 131072 * 4 // 128
+    # 256-byte header, one u32 count and one u32 base per wave tile of 32 rows
+    # (D = 128; plus the final base), then a 4-byte staging entry per element,
+    # each region 256-aligned
+    ntiles = 131072 * 4 // 32
     assert L.hkv_nuq_pack_compact_workspace_bytes(131072, 4, 128) == \
-        256 + 4 * ntiles + 131072 * 4 * 128 * 3
-    # one partial tile: header, count (padded to 256), staging for 128 x 128
-    assert L.hkv_nuq_pack_compact_workspace_bytes(10, 4, 128) == 256 + 256 + 16384 * 3
+        256 + 4 * ntiles + (4 * ntiles + 256) + 131072 * 4 * 128 * 4
+    # 40 rows = 2 wave tiles: header, counts and bases (each padded to 256),
+    # staging for 64 x 128
+    assert L.hkv_nuq_pack_compact_workspace_bytes(10, 4, 128) == 256 + 256 + 256 + 64 * 128 * 4
     assert L.hkv_nuq_pack_compact_workspace_bytes(10, 4, 100) == 0  # unsupported D
     assert L.hkv_quest_topk_workspace_bytes(65536, 4) >= 64
 

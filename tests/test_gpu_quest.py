@@ -44,6 +44,7 @@ def test_page_stats_vs_oracle(dev, dt, P, S, H, D):
 
 @pytest.mark.parametrize("kdt", [np.float16, np.float32])
 @pytest.mark.parametrize("P,H,D,g", [(512, 4, 128, 1), (300, 4, 128, 7), (77, 2, 32, 1),
+                                     (50, 3, 128, 2), (33, 5, 64, 1),
                                      (40, 1, 20, 3), (16, 2, 8, 1)])
 def test_bound_bit_exact_vs_oracle(dev, kdt, P, H, D, g):
     from helix_kv.ops import quest_page_bound
