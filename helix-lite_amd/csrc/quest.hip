@@ -179,7 +179,7 @@ template <typename KT>
 __global__ void __launch_bounds__(256)
 bound_kernel(const void* q, int qdt, int group, const KT* __restrict__ kmin,
              const KT* __restrict__ kmax, int64_t P, int H, int D, void* out, int odt,
-             int head_major) {
+             int head_major, const int64_t* __restrict__ page_ids, int64_t nstat) {
   extern __shared__ float qs[];  // [2][H][D]
   for (int i = threadIdx.x; i < H * D; i += 256) {
     float a, b;
@@ -209,7 +209,14 @@ bound_kernel(const void* q, int qdt, int group, const KT* __restrict__ kmin,
           qp[i] = d < D ? qs[h * D + d] : 0.0f;
           qn[i] = d < D ? qs[H * D + h * D + d] : 0.0f;
         }
-        chunk_sums<KT>(kmin + r * D, kmax + r * D, D, c, qp, qn, ps[u], ns[u]);
+        int64_t src = r;
+        if (page_ids) {
+          const int64_t id = page_ids[r / H];
+          // a page id outside the statistics gets bound -inf (never preferred)
+          src = (id >= 0 && id < nstat) ? id * H + h : -1;
+        }
+        if (src >= 0) chunk_sums<KT>(kmin + src * D, kmax + src * D, D, c, qp, qn, ps[u], ns[u]);
+        else { ps[u] = -__builtin_inff(); ns[u] = 0.0f; }
       }
     }
 #pragma unroll
@@ -736,7 +743,7 @@ void launch_bound_f16(bool hfix, unsigned grid, size_t lds, hipStream_t s, const
 // Bound into out, (P,H) or head-major (H,P).
 int page_bound(const void* q, int q_dtype, int Hq, const void* kmin, const void* kmax, int k_dtype,
                int64_t P, int H, int D, void* out, int out_dtype, int head_major,
-               hipStream_t s) {
+               hipStream_t s, const int64_t* page_ids = nullptr, int64_t nstat = 0) {
   if (!fdt(q_dtype) && q_dtype != HKV_DT_BF16) return HKV_ERR_DTYPE;
   if (!fdt(k_dtype) || !fdt(out_dtype)) return HKV_ERR_DTYPE;
   if (P < 0 || H < 1 || D < 1 || D > 512 || Hq < H || Hq % H) return HKV_ERR_SHAPE;
@@ -747,7 +754,7 @@ int page_bound(const void* q, int q_dtype, int Hq, const void* kmin, const void*
   const size_t lds = sizeof(float) * 2 * H * D;
   if (lds > 64 * 1024) return HKV_ERR_SHAPE;
   const int G = D / 8;
-  if (k_dtype == HKV_DT_F16 && D % 8 == 0 && (G & (G - 1)) == 0 && G <= 64) {
+  if (!page_ids && k_dtype == HKV_DT_F16 && D % 8 == 0 && (G & (G - 1)) == 0 && G <= 64) {
     const int64_t span = (int64_t)(256 / G) * kBoundUnrollF16;
     const unsigned grid =
         (unsigned)std::min<int64_t>((rows + span - 1) / span, (int64_t)num_cus() * 8);
@@ -775,11 +782,11 @@ int page_bound(const void* q, int q_dtype, int Hq, const void* kmin, const void*
   if (k_dtype == HKV_DT_F16)
     hipLaunchKernelGGL(bound_kernel<uint16_t>, dim3(grid), dim3(256), lds, s, q, q_dtype, Hq / H,
                        (const uint16_t*)kmin, (const uint16_t*)kmax, P, H, D, out, out_dtype,
-                       head_major);
+                       head_major, page_ids, nstat);
   else
     hipLaunchKernelGGL(bound_kernel<float>, dim3(grid), dim3(256), lds, s, q, q_dtype, Hq / H,
                        (const float*)kmin, (const float*)kmax, P, H, D, out, out_dtype,
-                       head_major);
+                       head_major, page_ids, nstat);
   HKV_CHECK_LAUNCH();
   return HKV_OK;
 }
@@ -812,6 +819,77 @@ int topk(const void* bound, int b_dtype, int64_t P, int H, int64_t ps, int64_t h
 #undef HKV_TOPK
   HKV_CHECK_LAUNCH();
   return HKV_OK;
+}
+
+// Union of the per-head selections as flags over pool block ids.
+__global__ void __launch_bounds__(256)
+mark_blocks_kernel(const int64_t* __restrict__ sel, int64_t nsel,
+                   const int64_t* __restrict__ used, int64_t NU, uint8_t* __restrict__ flags,
+                   int64_t nblocks) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= nsel) return;
+  const int64_t j = sel[i];
+  if (j < 0 || j >= NU) return;
+  const int64_t id = used[j];
+  if (id >= 0 && id < nblocks) flags[id] = 1;
+}
+
+// One block: flagged ids in ascending order, their first positions, the
+// count; the flags are cleared on the way (left all zero for the next call).
+// Windows of 16 flags per thread (one 128-bit load; flags 16-byte aligned).
+__global__ void __launch_bounds__(kSelThreads)
+compact_blocks_kernel(uint8_t* __restrict__ flags, int64_t nblocks, int64_t block_size,
+                      int64_t* __restrict__ out_ids, int64_t* __restrict__ out_first,
+                      int64_t* __restrict__ n_out) {
+  __shared__ uint32_t s_w[kSelWaves];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  uint32_t carry = 0;
+  for (int64_t w0 = 0; w0 < nblocks; w0 += 16 * kSelThreads) {
+    const int64_t i0 = w0 + (int64_t)tid * 16;
+    uint32_t f[4] = {0u, 0u, 0u, 0u};
+    const bool full = i0 + 16 <= nblocks;
+    if (full) {
+      const uint4 v = *reinterpret_cast<const uint4*>(flags + i0);
+      f[0] = v.x; f[1] = v.y; f[2] = v.z; f[3] = v.w;
+    } else {
+      for (int k = 0; k < 16; ++k)
+        if (i0 + k < nblocks && flags[i0 + k]) f[k >> 2] |= 1u << (8 * (k & 3));
+    }
+    uint32_t bits = 0;  // bit k: flag k set
+#pragma unroll
+    for (int k = 0; k < 16; ++k) bits |= ((f[k >> 2] >> (8 * (k & 3))) & 0xffu) ? (1u << k) : 0u;
+    const uint32_t cnt = __builtin_popcount(bits);
+    uint32_t inc = cnt;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t y = __shfl_up(inc, o, 64);
+      if (lane >= o) inc += y;
+    }
+    if (lane == 63) s_w[w] = inc;
+    __syncthreads();
+    uint32_t pos = carry + inc - cnt, total = 0;
+    for (int i = 0; i < kSelWaves; ++i) {
+      if (i < w) pos += s_w[i];
+      total += s_w[i];
+    }
+    while (bits) {
+      const int k = __builtin_ctz(bits);
+      bits &= bits - 1u;
+      out_ids[pos] = i0 + k;
+      out_first[pos] = (i0 + k) * block_size;
+      ++pos;
+    }
+    if (full) {
+      if (f[0] | f[1] | f[2] | f[3])
+        *reinterpret_cast<uint4*>(flags + i0) = make_uint4(0u, 0u, 0u, 0u);
+    } else {
+      for (int k = 0; k < 16; ++k)
+        if (i0 + k < nblocks) flags[i0 + k] = 0;
+    }
+    carry += total;
+    __syncthreads();  // s_w is reused by the next window
+  }
+  if (tid == 0) *n_out = carry;
 }
 
 }  // namespace
@@ -857,4 +935,40 @@ extern "C" int hkv_quest_select(const void* q, int q_dtype, int Hq, const void* 
                             (hipStream_t)stream);
   if (st != HKV_OK) return st;
   return topk(scores, HKV_DT_F32, P, H, 1, P, k, sink_pages, out, nullptr, (hipStream_t)stream);
+}
+
+extern "C" int hkv_quest_select_blocks(const void* q, int q_dtype, int H, const void* kmin,
+                                       const void* kmax, int k_dtype, int64_t num_blocks, int D,
+                                       const int64_t* used_block_ids, int64_t NU, int64_t top_k,
+                                       int64_t sink_blocks, int64_t block_size, float* scores,
+                                       int64_t* sel, uint8_t* flags, int64_t* out_ids,
+                                       int64_t* out_first_pos, int64_t* n_selected,
+                                       void* stream) {
+  if (NU < 0 || num_blocks < 0 || H < 1 || H > 64 || block_size < 1) return HKV_ERR_SHAPE;
+  if (!n_selected) return HKV_ERR_ARG;
+  hipStream_t st = (hipStream_t)stream;
+  if (NU == 0 || num_blocks == 0) {
+    hipLaunchKernelGGL(compact_blocks_kernel, dim3(1), dim3(kSelThreads), 0, st, flags,
+                       (int64_t)0, block_size, out_ids, out_first_pos, n_selected);
+    HKV_CHECK_LAUNCH();
+    return HKV_OK;
+  }
+  if (!q || !kmin || !kmax || !used_block_ids || !scores || !sel || !flags || !out_ids ||
+      !out_first_pos)
+    return HKV_ERR_ARG;
+  if ((uintptr_t)flags & 15u) return HKV_ERR_ARG;
+  int rc = page_bound(q, q_dtype, H, kmin, kmax, k_dtype, NU, H, D, scores, HKV_DT_F32, 1, st,
+                      used_block_ids, num_blocks);
+  if (rc != HKV_OK) return rc;
+  int64_t n = 0;
+  rc = topk(scores, HKV_DT_F32, NU, H, 1, NU, top_k, sink_blocks, sel, &n, st);
+  if (rc != HKV_OK) return rc;
+  const int64_t nsel = n * H;
+  if (nsel > 0)
+    hipLaunchKernelGGL(mark_blocks_kernel, dim3((unsigned)((nsel + 255) / 256)), dim3(256), 0, st,
+                       sel, nsel, used_block_ids, NU, flags, num_blocks);
+  hipLaunchKernelGGL(compact_blocks_kernel, dim3(1), dim3(kSelThreads), 0, st, flags, num_blocks,
+                     block_size, out_ids, out_first_pos, n_selected);
+  HKV_CHECK_LAUNCH();
+  return HKV_OK;
 }

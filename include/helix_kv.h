@@ -175,6 +175,36 @@ int hkv_nuq_dequantize_generic(int ndim, const int64_t *shape, const hkv_tensor_
                                void *out, int out_dtype, int32_t *err, void *stream);
 
 /*
+ * Compact KV pool write (one layer, K or V): token t of values (T,H,D) fp16
+ * is quantised into slot slot_mapping[t] of the layer's pool tensors codes u8,
+ * outlier_v fp16 (0 where not an outlier) and outlier_m u8, each
+ * (num_blocks, block_size, H, D); slot < 0 (padding) and slot >=
+ * num_blocks * block_size are skipped.  For V pass per-token scales with
+ * scales->positions = the tokens' absolute positions (row min(pos, rows-1)).
+ * For K, k_min / k_max (num_blocks, H, D) fp32 (or both NULL) receive the
+ * running min / max of the reconstructed values (input for outliers, fp32
+ * pole otherwise), -0 below +0; initialise them to +inf / -inf.  Requires
+ * scales->tables; D/8 a power of two <= 32.  Replaces CompactKVPool.write_kv
+ * (src/kvquant/compact_pool.py:447-489; kernels :160-287).
+ */
+int hkv_pool_write(const void *values, int64_t T, int H, int D, const hkv_nuq_scales *scales,
+                   const int64_t *slot_mapping, int64_t num_blocks, int block_size, void *codes,
+                   void *outlier_v, void *outlier_m, float *k_min, float *k_max, void *stream);
+
+/*
+ * Compact KV pool gather-dequant (one layer, K or V): staging (NK,
+ * block_size, H, D) fp16 row k = dequantised pool block block_ids[k]; for V
+ * (per-token scales) position p of kept block k uses scale row
+ * min(first_pos[k] + p, rows - 1).  Block ids outside [0, num_blocks) give
+ * zero rows.  Replaces CompactKVPool.unpack_to_staging
+ * (src/kvquant/compact_pool.py:492-537; kernels :292-395).
+ */
+int hkv_pool_gather(const void *codes, const void *outlier_v, const void *outlier_m,
+                    int64_t num_blocks, int block_size, int H, int D,
+                    const hkv_nuq_scales *scales, const int64_t *block_ids,
+                    const int64_t *first_pos, int64_t NK, void *staging, void *stream);
+
+/*
  * Quest page statistics: K_pages (P,S,H,D) -> kmin, kmax (P,H,D), same dtype
  * (f16 or f32).  -0 orders below +0; a NaN in a page-channel gives NaN.
  * src/quest/reference.py:38-56.
@@ -221,6 +251,27 @@ int hkv_quest_select(const void *q, int q_dtype, int Hq, const void *kmin, const
                      int k_dtype, int64_t P, int H, int D, int64_t k, int64_t sink_pages,
                      float *scores, int64_t *out, int64_t *n_out, void *workspace,
                      size_t workspace_bytes, void *stream);
+
+/*
+ * Quest block selection over a compact pool layer
+ * (src/kvquant/quest_selector.py:38-90): q (H,D) (one query per KV head),
+ * pool statistics kmin/kmax (num_blocks,H,D) (f32 or f16), the sequence's
+ * used blocks used_block_ids (NU,) int64.  Bound of every used block (as
+ * hkv_quest_page_bound with page p -> statistics row used_block_ids[p]; an id
+ * outside [0, num_blocks) gets bound -inf), per-head top-K with the first
+ * min(sink_blocks, NU) used blocks as sinks (as hkv_quest_topk), union over
+ * heads.  Writes the selected block ids ascending to out_ids, id * block_size
+ * to out_first_pos, and their number to *n_selected (device int64).
+ * Workspaces: scores H*NU f32, sel (min(sink,NU) + min(top_k, NU - sinks))*H
+ * int64, flags num_blocks bytes (16-byte aligned), zero-filled before the first
+ * call (the call leaves them zero).  out_ids / out_first_pos need min(num_blocks, NU)
+ * entries.
+ */
+int hkv_quest_select_blocks(const void *q, int q_dtype, int H, const void *kmin, const void *kmax,
+                            int k_dtype, int64_t num_blocks, int D, const int64_t *used_block_ids,
+                            int64_t NU, int64_t top_k, int64_t sink_blocks, int64_t block_size,
+                            float *scores, int64_t *sel, uint8_t *flags, int64_t *out_ids,
+                            int64_t *out_first_pos, int64_t *n_selected, void *stream);
 
 #ifdef __cplusplus
 }

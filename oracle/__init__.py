@@ -352,6 +352,70 @@ def selected_attention(query, K_pages, V_pages, page_indices, kv_of_head):
     return out
 
 
+def ordered_min_max(vals, axis):
+    """min / max of fp32 values along ``axis`` with -0 ordered below +0 (the
+    pool statistics' order), via the monotone integer key of each value."""
+    v = np.ascontiguousarray(vals, np.float32)
+    b = v.view(np.int32).astype(np.int64)
+    key = np.where(b >= 0, b, -(b & 0x7FFFFFFF) - 1)
+    lo = np.take_along_axis(v, np.expand_dims(key.argmin(axis), axis), axis).squeeze(axis)
+    hi = np.take_along_axis(v, np.expand_dims(key.argmax(axis), axis), axis).squeeze(axis)
+    return lo, hi
+
+
+def pool_write(pool: dict, key, value, slot_mapping, abs_positions, kscale, vscale,
+               block_size: int) -> None:
+    """CompactKVPool.write_kv for one layer (src/kvquant/compact_pool.py:447-489,
+    kernels :160-287), in place on ``pool``: numpy arrays k_codes, k_outv
+    (fp16 bits), k_outm, v_codes, v_outv, v_outm (NB,BS,H,D) and k_min, k_max
+    (NB,H,D) fp32.  kscale / vscale = (poles, upper, lower) as fp32 arrays
+    holding the scales' values.  Slots < 0 (or past the pool) are skipped; V
+    uses scale row min(abs_position, T_cal-1); the K statistics fold in the
+    reconstructed value (input for outliers, fp32 pole otherwise) of each
+    written token, -0 below +0."""
+    key = np.asarray(key, np.float16)
+    value = np.asarray(value, np.float16)
+    slots = np.asarray(slot_mapping, np.int64)
+    pos = np.asarray(abs_positions, np.int64)
+    NB, BS, H, D = pool["k_codes"].shape
+    keep = (slots >= 0) & (slots < NB * BS)
+    if not keep.any():
+        return
+    k, v, sl, ps = key[keep], value[keep], slots[keep], pos[keep]
+    kc, kv, km = pack_k(k, *kscale)
+    vc, vv, vm = pack_v(v, *vscale, positions=ps)
+    blk, off = sl // BS, sl % BS
+    for name, arr in (("k_codes", kc), ("k_outv", kv), ("k_outm", km),
+                      ("v_codes", vc), ("v_outv", vv), ("v_outm", vm)):
+        pool[name][blk, off] = arr
+    kp = _f32(kscale[0])
+    hh, dd = np.meshgrid(np.arange(H), np.arange(D), indexing="ij")
+    recon = np.where(km.astype(bool), h2f(kv), kp[hh[None], dd[None], kc.astype(np.int64)])
+    for b in np.unique(blk):
+        rows = recon[blk == b]
+        lo, _ = ordered_min_max(np.concatenate([rows, pool["k_min"][b][None]]), axis=0)
+        _, hi = ordered_min_max(np.concatenate([rows, pool["k_max"][b][None]]), axis=0)
+        pool["k_min"][b], pool["k_max"][b] = lo, hi
+
+
+def pool_gather(pool: dict, block_ids, first_pos, kscale, vscale):
+    """CompactKVPool.unpack_to_staging (src/kvquant/compact_pool.py:492-537,
+    kernels :292-395) -> (staging_k, staging_v) fp16 bits (NK,BS,H,D); V row of
+    position p in kept block k is min(first_pos[k] + p, T_cal - 1)."""
+    ids = np.asarray(block_ids, np.int64)
+    fp = np.asarray(first_pos, np.int64)
+    NB, BS, H, D = pool["k_codes"].shape
+    NK = ids.shape[0]
+    c = pool["k_codes"][ids].reshape(NK * BS, H, D)
+    sk = unpack(c, pool["k_outv"][ids].reshape(NK * BS, H, D),
+                pool["k_outm"][ids].reshape(NK * BS, H, D), kscale[0], "k")
+    positions = (fp[:, None] + np.arange(BS)[None, :]).reshape(-1)
+    sv = unpack(pool["v_codes"][ids].reshape(NK * BS, H, D),
+                pool["v_outv"][ids].reshape(NK * BS, H, D),
+                pool["v_outm"][ids].reshape(NK * BS, H, D), vscale[0], "v", positions=positions)
+    return sk.reshape(NK, BS, H, D), sv.reshape(NK, BS, H, D)
+
+
 def h2f(bits) -> np.ndarray:
     return np.asarray(bits, np.uint16).view(np.float16).astype(np.float32)
 
