@@ -107,20 +107,21 @@ def per_launch_ms(launches) -> list[float]:
     return [a.elapsed_time(b) for a, b in evs]
 
 
-def cpu_baseline(tokens: int) -> dict:
-    """The CPU oracle (single thread) on a bounded slice of the same workload:
-    `tokens` tokens of one nuq2 layer and one nuq4 layer, K and V, including
-    bit packing and CSR."""
+def cpu_baseline(layers: list[int], dev) -> dict:
+    """The CPU oracle (one thread) on a bounded sample of the same workload:
+    every token of the given layers, K and V, quantised, bit-packed and
+    CSR-encoded (about 3.5 s of CPU work per layer)."""
     import oracle as O
 
     total_bytes, total_s = 0.0, 0.0
-    for layer in (0, CUT):
-        K, V, ks, vs, L = make_layer(layer, torch.device("cuda:0"))
+    for layer in layers:
+        K, V, ks, vs, L = make_layer(layer, dev)
         bits = 2 if L <= 4 else 4
-        k = K[:tokens].cpu().numpy()
-        v = V[:tokens].cpu().numpy()
+        k = K.cpu().numpy()
+        v = V.cpu().numpy()
         kp, ku, kl = (x.float().cpu().numpy() for x in ks)
         vp, vu, vl = (x.float().cpu().numpy() for x in vs)
+        sb = scale_bytes(ks) + scale_bytes(vs)
         del K, V
         t0 = time.perf_counter()
         c, ov, om = O.pack_k(k, kp, ku, kl)
@@ -129,10 +130,16 @@ def cpu_baseline(tokens: int) -> dict:
         pv = O.pack_compact(c2, ov2, om2, bits)
         total_s += time.perf_counter() - t0
         n = k.size
-        total_bytes += 2 * (n * 2 + n * bits / 8 + (tokens * H + 1) * 4) + 3 * (len(pk[2]) + len(pv[2]))
-    return {"value": total_bytes / total_s / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"oracle C pack + numpy bit-pack/CSR, {tokens} tokens x 4 heads x 128 of "
-                      f"layer 0 (nuq2) and layer {CUT} (nuq4), K and V; {total_s:.1f} s",
+        tokens = k.shape[0]
+        total_bytes += (2 * (n * 2 + n * bits // 8 + (tokens * H + 1) * 4) + sb
+                        + 3 * (len(pk[2]) + len(pv[2])))
+        log(f"[bench] cpu baseline: layer {layer} done ({total_s:.1f} s so far)")
+    names = ", ".join(f"{l} (nuq{2 if l < CUT else 4})" for l in layers)
+    return {"value": round(total_bytes / total_s / 1e9, 4), "unit": "GB/s", "cores": 1,
+            "kind": "port",
+            "sample": f"oracle C quant+pack + numpy bit-pack/CSR over all {T_TOK} tokens x {H} heads "
+                      f"x {D} of layers {names}, K and V ({len(layers)} of the {LAYERS} layers); "
+                      f"{total_s:.1f} s",
             "cpu": platform.processor() or platform.machine(), "host_cores": os.cpu_count()}
 
 
@@ -278,7 +285,8 @@ def main() -> None:
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--only", choices=["all", "nuq", "quest"], default="all")
-    ap.add_argument("--cpu-tokens", type=int, default=16384)
+    ap.add_argument("--cpu-layers", default="0,1,16,17",
+                    help="layers timed on the CPU oracle for the baseline")
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -296,7 +304,7 @@ def main() -> None:
         res.update(bench_quest(args, dev))
     cpu = None
     if not args.no_cpu and args.only in ("all", "nuq"):
-        cpu = cpu_baseline(args.cpu_tokens)
+        cpu = cpu_baseline([int(x) for x in args.cpu_layers.split(",")], dev)
         log(f"[bench] cpu baseline {cpu['value']:.3f} GB/s")
     line = {
         "metric": METRIC,

@@ -82,6 +82,11 @@ _SIGS = {
                           ctypes.POINTER(_i64), _p, _sz, _p], _i32),
     "hkv_quest_select_blocks": ([_p, _i32, _i32, _p, _p, _i32, _i64, _i32, _p, _i64, _i64, _i64,
                                  _i64, _p, _p, _p, _p, _p, _p, _p], _i32),
+    "hkv_decode_workspace_bytes": ([_i64, _i32, _i32], _sz),
+    "hkv_decode_attn": ([_p, _i32, _i32, _i32, _i64,
+                         _p, _p, _p, _p, _i64, _i32, _p,
+                         _p, _p, _p, _p, _i64, _i32, _p, _i64,
+                         _p, _i64, _i32, ctypes.c_float, _p, _i32, _p, _sz, _p], _i32),
 }
 
 _lib = None
@@ -173,3 +178,15 @@ def desc(t: torch.Tensor, ndim: int) -> TensorDesc:
     for i in range(6):
         d.strides[i] = st[i] if i < ndim else 0
     return d
+
+
+_cus: dict[int, int] = {}
+
+
+def num_cus(device=None) -> int:
+    """Compute units of the (current) device, cached."""
+    dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    if idx not in _cus:
+        _cus[idx] = int(torch.cuda.get_device_properties(idx).multi_processor_count)
+    return _cus[idx]

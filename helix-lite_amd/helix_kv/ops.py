@@ -368,3 +368,61 @@ def quest_select(query: torch.Tensor, K_min: torch.Tensor, K_max: torch.Tensor, 
                                   N.ptr(out), n_out, None, 0, N.stream_of(q))
     N.check(st, "hkv_quest_select", ValueError)
     return out, scores
+
+
+# ------------------------------------------------------------ decode attention
+
+def decode_pages_per_split(nsel: int, H: int) -> int:
+    """Pages per split of the decode kernel: about 3 blocks of 4 waves per CU
+    over the (split, KV head) grid, a multiple of the block's 4 waves."""
+    cus = N.num_cus()
+    want = max(1, -(-nsel * H // (3 * cus)))
+    return max(4, -(-want // 4) * 4)
+
+
+def decode_attention(query: torch.Tensor, k: CompactCodes, kt: NuqLayerTables, v: CompactCodes,
+                     vt: NuqLayerTables, sel: torch.Tensor, *, scale: float | None = None,
+                     pages_per_split: int | None = None, out: torch.Tensor | None = None,
+                     out_dtype: torch.dtype = torch.float16) -> torch.Tensor:
+    """softmax(q.K^T * scale).V per query head over its KV head's selected
+    pages, read straight from the compact format (hkv_decode_attn).
+
+    query (Hq, 128) fp16; k / v the CompactCodes of (T, H, 128) with their
+    scales' tables (K per-channel, V per-token, token t at V row
+    min(t, rows - 1)); sel (n, H) int64 page ids of 16 tokens (quest_topk's
+    output).  Query head hq uses KV head hq // (Hq // H).  Returns (Hq, 128).
+    """
+    N.require_gpu(query, k.packed, v.packed, sel)
+    T, H, D = k.shape
+    if v.shape != (T, H, D):
+        raise AssertionError("K and V must have the same (T, H, D)")
+    if query.dim() != 2 or int(query.shape[1]) != D or int(query.shape[0]) % H:
+        raise ValueError(f"query {tuple(query.shape)} incompatible with (T, H, D) = {(T, H, D)}")
+    if query.dtype != torch.float16:
+        raise AssertionError("query must be fp16")
+    if kt.per_token or not vt.per_token:
+        raise AssertionError("K scales are per-channel, V scales per-token")
+    Hq = int(query.shape[0])
+    if sel.dim() != 2 or int(sel.shape[1]) != H:
+        raise ValueError(f"sel should be (n, {H}), got {tuple(sel.shape)}")
+    s = sel.to(torch.int64).contiguous()
+    nsel = int(s.shape[0])
+    pps = int(pages_per_split) if pages_per_split else decode_pages_per_split(nsel, H)
+    q = query.contiguous()
+    if out is None:
+        out = torch.empty((Hq, D), dtype=out_dtype, device=q.device)
+    if tuple(out.shape) != (Hq, D) or out.dtype not in (torch.float16, torch.float32):
+        raise AssertionError("out must be (Hq, D) fp16 or fp32")
+    nb = int(N.lib().hkv_decode_workspace_bytes(nsel, Hq, pps))
+    ws = N.workspace("decode", nb, q.device)
+    sc = float(scale) if scale is not None else D ** -0.5
+    st = N.lib().hkv_decode_attn(
+        N.ptr(q), Hq, H, D, T,
+        N.ptr(k.packed), N.ptr(k.row_ptr), N.ptr(k.col), N.ptr(k.val),
+        min(int(k.col.numel()), int(k.val.numel())), k.bits, N.ptr(kt.ensure_tables()),
+        N.ptr(v.packed), N.ptr(v.row_ptr), N.ptr(v.col), N.ptr(v.val),
+        min(int(v.col.numel()), int(v.val.numel())), v.bits, N.ptr(vt.ensure_tables()), vt.rows,
+        N.ptr(s), nsel, pps, sc, N.ptr(out), N.dtype_code(out), N.ptr(ws), ws.numel(),
+        N.stream_of(q))
+    N.check(st, "hkv_decode_attn", AssertionError)
+    return out

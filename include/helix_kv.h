@@ -273,6 +273,32 @@ int hkv_quest_select_blocks(const void *q, int q_dtype, int H, const void *kmin,
                             float *scores, int64_t *sel, uint8_t *flags, int64_t *out_ids,
                             int64_t *out_first_pos, int64_t *n_selected, void *stream);
 
+/*
+ * Fused dequant + Quest-sparse decode attention, batch 1, head_dim 128, page
+ * size 16.  Replaces unpack_to_staging + flash_attn_varlen_func over the fp16
+ * staging copy (src/kvquant/compact_backend.py:233-299) and restates
+ * selected_attention (src/quest/reference.py:136-168) with the standard GQA
+ * map: query head hq attends with KV head hq / (Hq / H), over the tokens of
+ * pages sel[0..nsel)[hq / (Hq / H)] (sel (nsel, H) int64, as hkv_quest_topk
+ * returns; page p = tokens [16p, 16p+16), tokens >= T masked, page ids outside
+ * [0, ceil(T/16)) skipped), softmax(q.K^T * scale) in fp32.
+ * K and V are in the compact format of hkv_nuq_pack_compact over (T, H, 128)
+ * (packed 16-byte aligned); tables are the decision tables of the K scales
+ * (H*128 per-channel) and of the V scales (H*v_rows per-token, row
+ * min(t, v_rows - 1)).  q (Hq, 128) fp16, 8-byte aligned; out (Hq, 128) fp16
+ * or fp32.  Hq / H <= 16.  The workspace holds per-split partials (m, l, o):
+ * hkv_decode_workspace_bytes(nsel, Hq, pages_per_split) bytes, no zeroing.
+ */
+size_t hkv_decode_workspace_bytes(int64_t nsel, int Hq, int pages_per_split);
+int hkv_decode_attn(const void *q, int Hq, int H, int D, int64_t T,
+                    const void *k_packed, const int32_t *k_row_ptr, const uint8_t *k_col,
+                    const uint16_t *k_val, int64_t k_cap, int k_bits, const void *k_tables,
+                    const void *v_packed, const int32_t *v_row_ptr, const uint8_t *v_col,
+                    const uint16_t *v_val, int64_t v_cap, int v_bits, const void *v_tables,
+                    int64_t v_rows, const int64_t *sel, int64_t nsel, int pages_per_split,
+                    float scale, void *out, int out_dtype, void *workspace,
+                    size_t workspace_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

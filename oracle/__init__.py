@@ -326,12 +326,15 @@ def select_union(bound, used_block_ids, top_k: int, sink_blocks: int, block_size
     return ids, ids * block_size
 
 
-def selected_attention(query, K_pages, V_pages, page_indices, kv_of_head):
-    """softmax(q.K^T/sqrt(D)).V over each head's selected pages, in float64.
+def selected_attention(query, K_pages, V_pages, page_indices, kv_of_head, num_tokens=None,
+                       scale=None):
+    """softmax(q.K^T * scale).V over each head's selected pages, in float64.
 
     query (Hq,D); K_pages/V_pages (P,S,Hkv,D); page_indices (n,Hsel) where
     column j selects pages for KV head j (Hsel == Hkv) or for query head j
-    (Hsel == Hq); kv_of_head(h) maps a query head to its KV head.
+    (Hsel == Hq); kv_of_head(h) maps a query head to its KV head.  Slots of
+    token index >= num_tokens (page * S + slot) are masked out, and so are page
+    ids outside [0, P); scale defaults to 1/sqrt(D).
     src/quest/reference.py:136-168 (fp32 softmax there; float64 here, compared
     with a tolerance).
     """
@@ -340,13 +343,21 @@ def selected_attention(query, K_pages, V_pages, page_indices, kv_of_head):
     V = np.asarray(V_pages, np.float64)
     idx = np.asarray(page_indices, np.int64)
     Hq, D = q.shape
+    P, S = K.shape[0], K.shape[1]
+    sc = 1.0 / np.sqrt(D) if scale is None else float(scale)
+    ntok = P * S if num_tokens is None else int(num_tokens)
     out = np.zeros((Hq, V.shape[-1]))
     for h in range(Hq):
         g = kv_of_head(h)
         col = idx[:, h] if idx.shape[1] == Hq else idx[:, g]
-        Kh = K[col, :, g, :].reshape(-1, D)
-        Vh = V[col, :, g, :].reshape(-1, V.shape[-1])
-        s = Kh @ q[h] / np.sqrt(D)
+        col = col[(col >= 0) & (col < P)]
+        tok = (col[:, None] * S + np.arange(S)[None, :]).reshape(-1)
+        keep = tok < ntok
+        Kh = K[col, :, g, :].reshape(-1, D)[keep]
+        Vh = V[col, :, g, :].reshape(-1, V.shape[-1])[keep]
+        if Kh.shape[0] == 0:
+            continue
+        s = Kh @ q[h] * sc
         s = np.exp(s - s.max())
         out[h] = (s / s.sum()) @ Vh
     return out

@@ -1,0 +1,160 @@
+"""GPU parity of the fused dequant + Quest-sparse decode attention.
+
+The kernel reads K/V in the compact format written by the GPU pack; the
+expected output is the oracle's float64 attention (selected_attention, the
+restatement of src/quest/reference.py:136-168 with the h // group GQA map)
+over K/V that the oracle itself decodes from the same compact bytes
+(bitunpack + csr_decode + unpack).  Tolerance, written per test: the
+per-head relative L2 error and the per-head max abs error over max |ref| are
+both <= 1e-3 (P is rounded to fp16 for the PV product: relative error about
+2^-12 per term).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+RNG = np.random.default_rng(55)
+PS = 16
+TOL = 1e-3
+
+
+def _t(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _scales(H, n, L, thr):
+    poles = np.sort(RNG.standard_normal((H, n, L)), axis=-1).astype(np.float16)
+    up = np.full((H, n), thr, np.float16)
+    return poles, up, (-up).astype(np.float16)
+
+
+def _side(dev, x, poles, up, lo, per_token, bits):
+    """GPU compact pack, then the oracle's decode of the packed bytes."""
+    from helix_kv.ops import NuqLayerTables, nuq_pack_compact
+
+    T, H, D = x.shape
+    lt = NuqLayerTables(_t(poles, dev), _t(up, dev), _t(lo, dev), per_token=per_token)
+    cc = nuq_pack_compact(_t(x, dev), lt, bits)
+    codes = O.bitunpack(cc.packed.cpu().numpy(), bits, D)
+    m, v = O.csr_decode(cc.row_ptr.cpu().numpy(), cc.col.cpu().numpy(),
+                        cc.val.cpu().numpy().view(np.uint16), T * H, D)
+    deq = O.unpack(codes, v.reshape(T, H, D), m.reshape(T, H, D), poles.astype(np.float32),
+                   "v" if per_token else "k")
+    return cc, lt, O.h2f(deq)
+
+
+def _problem(dev, T, H, Lk, Lv, rows, thr=1.2):
+    D = 128
+    k = (RNG.standard_t(3, (T, H, D)) * 0.7).astype(np.float16)
+    v = (RNG.standard_t(3, (T, H, D)) * 0.7).astype(np.float16)
+    kp, ku, kl = _scales(H, D, Lk, thr)
+    vp, vu, vl = _scales(H, rows, Lv, thr)
+    kc, kt, kd = _side(dev, k, kp, ku, kl, False, 4 if Lk > 4 else 2)
+    vc, vt, vd = _side(dev, v, vp, vu, vl, True, 4 if Lv > 4 else 2)
+    P = -(-T // PS)
+    pad = P * PS - T
+    kd = np.concatenate([kd, np.zeros((pad, H, D))]).reshape(P, PS, H, D)
+    vd = np.concatenate([vd, np.zeros((pad, H, D))]).reshape(P, PS, H, D)
+    return kc, kt, kd, vc, vt, vd
+
+
+def _select(P, H, n, sinks=4):
+    cols = []
+    for _ in range(H):
+        rest = RNG.permutation(np.arange(sinks, P))[: n - sinks]
+        cols.append(np.sort(np.concatenate([np.arange(sinks), rest])))
+    return np.stack(cols, 1).astype(np.int64)
+
+
+def _check(got, want):
+    got = got.float().cpu().numpy().astype(np.float64)
+    for h in range(want.shape[0]):
+        ref = want[h]
+        err = got[h] - ref
+        assert np.linalg.norm(err) <= TOL * np.linalg.norm(ref), h
+        assert np.abs(err).max() <= TOL * np.abs(ref).max(), h
+
+
+@pytest.mark.parametrize("T,H,group,Lk,Lv,rows,frac,pps", [
+    (1000, 2, 7, 16, 4, 512, 0.5, 4),     # partial last page, V row clamp
+    (4096, 4, 7, 16, 16, 4096, 0.25, 8),  # nuq4 both, cfg5 GQA 7:1
+    (4096, 4, 7, 4, 4, 4096, 0.25, 88),   # nuq2 both, one split per head
+    (257, 1, 1, 4, 16, 300, 1.0, 1),      # group 1, idle waves in each split
+    (2048, 2, 16, 16, 4, 64, 0.3, 12),    # group 16, split not a multiple of 4
+])
+def test_decode_vs_oracle(dev, T, H, group, Lk, Lv, rows, frac, pps):
+    from helix_kv.ops import decode_attention
+
+    kc, kt, kd, vc, vt, vd = _problem(dev, T, H, Lk, Lv, rows)
+    P = kd.shape[0]
+    n = max(min(P, 4) + 1, int(frac * P)) if frac < 1 else P
+    sel = _select(P, H, min(n, P), sinks=min(4, P))
+    q = RNG.standard_normal((H * group, 128)).astype(np.float16)
+    want = O.selected_attention(q.astype(np.float64), kd, vd, sel, lambda h: h // group,
+                                num_tokens=T)
+    out = decode_attention(_t(q, dev), kc, kt, vc, vt, _t(sel, dev), pages_per_split=pps,
+                           out_dtype=torch.float32)
+    _check(out, want)
+    out16 = decode_attention(_t(q, dev), kc, kt, vc, vt, _t(sel, dev), out_dtype=torch.float16)
+    assert out16.dtype == torch.float16
+    _check(out16, want)
+
+
+def test_decode_invalid_ids_and_scale(dev):
+    from helix_kv.ops import decode_attention
+
+    T, H, group = 700, 2, 3
+    kc, kt, kd, vc, vt, vd = _problem(dev, T, H, 16, 16, 1024)
+    P = kd.shape[0]
+    sel = _select(P, H, 12)
+    bad = np.concatenate([sel, [[-1, P], [P + 5, -7]]]).astype(np.int64)
+    q = RNG.standard_normal((H * group, 128)).astype(np.float16)
+    want = O.selected_attention(q.astype(np.float64), kd, vd, sel, lambda h: h // group,
+                                num_tokens=T, scale=0.05)
+    out = decode_attention(_t(q, dev), kc, kt, vc, vt, _t(bad, dev), scale=0.05,
+                           pages_per_split=4, out_dtype=torch.float32)
+    _check(out, want)
+
+
+def test_decode_all_pages_equals_dense_sdpa(dev):
+    """Every page selected == dense attention over all T tokens (torch's fp32
+    scaled_dot_product_attention on the CPU over the oracle-decoded K/V);
+    src/quest/tests/test_reference.py:95-117."""
+    from helix_kv.ops import decode_attention
+
+    T, H, group = 1500, 2, 7
+    kc, kt, kd, vc, vt, vd = _problem(dev, T, H, 16, 4, 2048)
+    P = kd.shape[0]
+    sel = np.stack([np.arange(P)] * H, 1).astype(np.int64)
+    q = RNG.standard_normal((H * group, 128)).astype(np.float16)
+    out = decode_attention(_t(q, dev), kc, kt, vc, vt, _t(sel, dev), out_dtype=torch.float32)
+    K = torch.tensor(kd.reshape(-1, H, 128)[:T], dtype=torch.float32).permute(1, 0, 2)
+    V = torch.tensor(vd.reshape(-1, H, 128)[:T], dtype=torch.float32).permute(1, 0, 2)
+    Q = torch.tensor(q, dtype=torch.float32).reshape(H, group, 128)
+    want = torch.nn.functional.scaled_dot_product_attention(Q, K, V).reshape(H * group, 128)
+    _check(out, want.double().numpy())
+
+
+def test_decode_errors(dev):
+    from helix_kv.ops import decode_attention
+
+    kc, kt, kd, vc, vt, vd = _problem(dev, 64, 2, 16, 16, 64)
+    sel = torch.zeros((2, 2), dtype=torch.int64, device=dev)
+    q = torch.zeros((6, 128), dtype=torch.float16, device=dev)
+    with pytest.raises(ValueError):
+        decode_attention(q[:5], kc, kt, vc, vt, sel)         # Hq not a multiple of H
+    with pytest.raises(ValueError):
+        decode_attention(q, kc, kt, vc, vt, sel[:, :1])      # sel columns != H
+    with pytest.raises(AssertionError):
+        decode_attention(q.float(), kc, kt, vc, vt, sel)     # query dtype
+    with pytest.raises(AssertionError):
+        decode_attention(q, kc, vt, vc, vt, sel)             # K tables must be per-channel
+    q34 = torch.zeros((34, 128), dtype=torch.float16, device=dev)
+    with pytest.raises(AssertionError):
+        decode_attention(q34, kc, kt, vc, vt, sel)           # group 17 > 16

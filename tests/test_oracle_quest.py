@@ -159,3 +159,42 @@ def test_attention_all_pages_equals_dense():
     for h in range(H):
         a = torch.softmax(Kf[:, h] @ torch.tensor(q[h]) / np.sqrt(D), 0)
         assert np.allclose(out[h], (a @ Vf[:, h]).numpy(), atol=1e-9)
+
+
+def test_attention_gqa_mask_matches_sdpa():
+    """GQA (query head h -> KV head h // group), partial last page and page
+    subsets against torch's own scaled_dot_product_attention in float64 over
+    the gathered keys (a library routine, independent of the oracle's loop)."""
+    P, S, H, group, D = 6, 16, 2, 7, 32
+    T = 5 * S + 3  # last valid page holds 3 tokens, page 5 none
+    K = RNG.standard_normal((P, S, H, D))
+    V = RNG.standard_normal((P, S, H, D))
+    q = RNG.standard_normal((H * group, D))
+    sel = np.array([[0, 1], [4, 2], [5, 4], [2, 0]])  # page 5 is past T: masked
+    out = O.selected_attention(q, K, V, sel, lambda h: h // group, num_tokens=T, scale=0.3)
+    for hq in range(H * group):
+        g = hq // group
+        toks = [p * S + s for p in sel[:, g] for s in range(S) if p * S + s < T]
+        Kg = torch.tensor(K.reshape(P * S, H, D)[toks, g])
+        Vg = torch.tensor(V.reshape(P * S, H, D)[toks, g])
+        want = torch.nn.functional.scaled_dot_product_attention(
+            torch.tensor(q[hq])[None, None, None], Kg[None, None], Vg[None, None], scale=0.3)
+        assert np.allclose(out[hq], want.reshape(-1).numpy(), rtol=1e-12, atol=1e-12)
+
+
+def test_attention_exclusion_and_invalid_ids():
+    # src/quest/tests/test_reference.py:120-139: an unselected page cannot move
+    # the output, however large its keys; ids outside [0, P) select nothing.
+    P, S, H, D = 5, 4, 1, 8
+    K = RNG.standard_normal((P, S, H, D))
+    V = RNG.standard_normal((P, S, H, D))
+    q = RNG.standard_normal((H, D))
+    sel = np.array([[0], [2], [4]])
+    a = O.selected_attention(q, K, V, sel, lambda h: 0)
+    K2, V2 = K.copy(), V.copy()
+    K2[1], V2[1], K2[3] = 1e3 * q[0], 1e3, -1e3 * q[0]
+    assert np.array_equal(a, O.selected_attention(q, K2, V2, sel, lambda h: 0))
+    b = O.selected_attention(q, K, V, np.array([[0], [-1], [2], [P], [4], [99]]), lambda h: 0)
+    assert np.array_equal(a, b)
+    # a selection with no valid token leaves the head at zero
+    assert not O.selected_attention(q, K, V, np.array([[3]]), lambda h: 0, num_tokens=12).any()
