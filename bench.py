@@ -38,6 +38,22 @@ METRIC = "nuq quant+pack / unpack GB/s (% HBM peak); Quest top-K µs/step at 1M 
 T_TOK, H, D, LAYERS, CUT, T_CAL = 131072, 4, 128, 28, 16, 4096
 
 
+PACK_PROFILE = "profiles/pack_unpack_compact_mixed_prefill_28L.md"
+
+
+def profiled_traffic(rel: str):
+    """HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
+    (calibrated against a copy of known size), as recorded in the profile
+    summary; None when the summary is absent."""
+    import re
+
+    path = ROOT / rel
+    if not path.exists():
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*(\d+)", path.read_text())
+    return int(m.group(1)) if m else None
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -54,18 +70,21 @@ def student_t3(shape, g, dev):
     return z / chi.sqrt()
 
 
-def make_layer(layer: int, dev, T: int = T_TOK):
-    """Synthetic K, V (T,H,D) fp16 and their calibrated scales (fp16)."""
-    g = torch.Generator(device=dev).manual_seed(1000 + layer)
+def make_layer(layer: int, dev, T: int = T_TOK, seed_base: int = 1000):
+    """Synthetic K, V (T,H,D) fp16 and their calibrated scales (fp16).  The K
+    thresholds and poles are calibrated on the first min(T, 131072) tokens,
+    the V scales on the first 4096 positions."""
+    g = torch.Generator(device=dev).manual_seed(seed_base + layer)
     L = 4 if layer < CUT else 16
     c = torch.exp(0.5 * torch.randn((H, D), generator=g, device=dev))
     K = (student_t3((T, H, D), g, dev) * c).half()
     V = (student_t3((T, H, D), g, dev) * c).half()
     lv = lut(L).to(dev)
     # K: per (h, d) over tokens
-    kf = K.float()
-    k_lo = torch.kthvalue(K.view(T, H * D).float(), max(1, int(0.025 * T)), dim=0).values.view(H, D)
-    k_hi = torch.kthvalue(K.view(T, H * D).float(), int(0.975 * T), dim=0).values.view(H, D)
+    Tc = min(T, T_TOK)
+    kf = K[:Tc].float()
+    k_lo = torch.kthvalue(kf.view(Tc, H * D), max(1, int(0.025 * Tc)), dim=0).values.view(H, D)
+    k_hi = torch.kthvalue(kf.view(Tc, H * D), int(0.975 * Tc), dim=0).values.view(H, D)
     k_poles = (kf.mean(0)[..., None] + kf.std(0)[..., None] * lv).half()
     # V: per (h, t) over channels, first T_CAL positions
     vc = V[:T_CAL].float().permute(1, 0, 2)  # (H, T_CAL, D)
@@ -279,12 +298,189 @@ def bench_quest(args, dev):
                 stats_bytes=P * page * H * D * 2 + 2 * P * H * D * 2)
 
 
+DEC_TOK, HQ = 1 << 20, 28
+
+
+def build_decode_layers(dev, layers):
+    """The decode workload's compact pool: for each layer, K and V of
+    1,048,576 tokens packed to the compact format (nuq2 below layer 16, nuq4
+    from it), the fp16 page min / max of the reconstructed K (the statistics
+    the pool keeps), and the layer's decode query (28, 128) fp16."""
+    from helix_kv.ops import NuqLayerTables, nuq_pack_compact, nuq_unpack_compact, quest_page_stats
+
+    P = DEC_TOK // 16
+    gq = torch.Generator(device=dev).manual_seed(5)
+    out = []
+    for l in layers:
+        K, V, ks, vs, L = make_layer(l, dev, T=DEC_TOK, seed_base=5000)
+        kt = NuqLayerTables(*ks, per_token=False)
+        vt = NuqLayerTables(*vs, per_token=True)
+        bits = 2 if L <= 4 else 4
+        cap = DEC_TOK * H * D // 10
+        ck = nuq_pack_compact(K, kt, bits, capacity=cap)
+        cv = nuq_pack_compact(V, vt, bits, capacity=cap)
+        del K, V
+        kr = nuq_unpack_compact(ck, kt)
+        kmin, kmax = quest_page_stats(kr.view(P, 16, H, D))
+        del kr
+        q = torch.randn((HQ, D), generator=gq, device=dev).half()
+        out.append(dict(layer=l, ck=ck, cv=cv, kt=kt, vt=vt, bits=bits, kmin=kmin, kmax=kmax, q=q))
+    torch.cuda.synchronize()
+    return out
+
+
+def graph_us(fn, stream, iters: int) -> float:
+    """Capture fn() in a HIP graph on `stream` and time `iters` replays (us each)."""
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        fn()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(gr, stream=stream):
+            fn()
+    torch.cuda.synchronize()
+    for _ in range(3):
+        gr.replay()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    a.record()
+    for _ in range(iters):
+        gr.replay()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / iters * 1e3
+
+
+def bench_decode(args, dev):
+    """Fused dequant + Quest-sparse decode at 1M tokens, batch 1, 28 layers:
+    per layer Quest selection (group-sum bound, top 16384 + 4 sink pages per
+    KV head) and the fused decode attention over the selected pages, read from
+    the mixed nuq2/nuq4 compact pool.  The 28-layer step is one HIP graph."""
+    from helix_kv.ops import decode_attention, decode_pages_per_split, nuq_unpack_compact, quest_select
+
+    P = DEC_TOK // 16
+    k, s = P // 4, 4
+    nsel = k + s
+    log(f"[bench] decode: building the {LAYERS}-layer compact pool at {DEC_TOK} tokens")
+    layers = build_decode_layers(dev, range(LAYERS))
+    log(f"[bench] decode pool ready, {torch.cuda.memory_allocated() / 2**30:.1f} GiB allocated")
+    pps = decode_pages_per_split(nsel, H)
+    scores = torch.empty((H, P), dtype=torch.float32, device=dev)
+    for Ld in layers:
+        Ld["sel"] = torch.empty((nsel, H), dtype=torch.int64, device=dev)
+        Ld["out"] = torch.empty((HQ, D), dtype=torch.float16, device=dev)
+
+    def select_all():
+        for Ld in layers:
+            quest_select(Ld["q"], Ld["kmin"], Ld["kmax"], k, s, scores=scores, out=Ld["sel"])
+
+    def decode_all():
+        for Ld in layers:
+            decode_attention(Ld["q"], Ld["ck"], Ld["kt"], Ld["cv"], Ld["vt"], Ld["sel"],
+                             pages_per_split=pps, out=Ld["out"])
+
+    def step():
+        select_all()
+        decode_all()
+
+    stream = torch.cuda.Stream()
+    iters = max(10, 4 * args.steps)
+    step_us = graph_us(step, stream, iters)
+    sel_us = graph_us(select_all, stream, iters)
+    dec_us = graph_us(decode_all, stream, iters)
+    # full-size check of two layers (nuq2, nuq4) against torch fp32 attention
+    # over the fp16 dequantised pool (the staging + dense-attention path)
+    worst = 0.0
+    for Ld in (layers[0], layers[-1]):
+        Kf = nuq_unpack_compact(Ld["ck"], Ld["kt"])
+        Vf = nuq_unpack_compact(Ld["cv"], Ld["vt"])
+        grp = HQ // H
+        for g in range(H):
+            tok = (Ld["sel"][:, g, None] * 16 + torch.arange(16, device=dev)).reshape(-1)
+            Kg, Vg = Kf[tok, g].float(), Vf[tok, g].float()
+            qs = Ld["q"][g * grp:(g + 1) * grp].float()
+            a = torch.softmax((qs @ Kg.T) * D ** -0.5, dim=-1)
+            ref = a @ Vg
+            got = Ld["out"][g * grp:(g + 1) * grp].float()
+            rel = ((got - ref).norm(dim=-1) / ref.norm(dim=-1)).max().item()
+            worst = max(worst, rel)
+        del Kf, Vf
+    if worst > 1e-3:
+        raise RuntimeError(f"decode attention differs from fp32 attention: rel {worst:.2e}")
+    # algorithmic bytes
+    sel_bytes = LAYERS * (2 * P * H * D * 2 + HQ * D * 2 + nsel * H * 8)
+    dec_bytes = 0
+    sel_out = 0
+    for Ld in layers:
+        b = Ld["bits"]
+        rows = H * nsel * 16
+        dec_bytes += nsel * H * 8 + HQ * D * 2 * 2 + 2 * rows * (D * b // 8 + 4)
+        for cc in (Ld["ck"], Ld["cv"]):
+            rp = cc.row_ptr.long()
+            cnt = (rp[1:] - rp[:-1]).view(P, 16, H).sum(1)  # outliers per (page, head)
+            sel_out += int(torch.gather(cnt, 0, Ld["sel"]).sum().item())
+    dec_bytes += 3 * sel_out
+    log(f"[bench] decode step: {step_us:.1f} us ({LAYERS} layers; select {sel_us:.1f} us, "
+        f"decode {dec_us:.1f} us); check rel err {worst:.2e}")
+    del layers
+    torch.cuda.empty_cache()
+    return dict(dec_step_us=step_us, dec_select_us=sel_us, dec_attn_us=dec_us,
+                dec_sel_bytes=sel_bytes, dec_attn_bytes=dec_bytes, dec_rel_err=worst,
+                dec_pps=pps, dec_sel_outliers=sel_out)
+
+
+def profile_pass(what: str, dev) -> None:
+    """A short, fixed sequence of launches for counter collection: three
+    copies of 1 GiB (the calibration kernel: 1 GiB read + 1 GiB written each),
+    then three calls of the named op on one nuq2 and one nuq4 layer."""
+    from helix_kv.ops import (CompactCodes, NuqLayerTables, decode_attention, nuq_pack_compact,
+                              nuq_unpack_compact, quest_page_stats, quest_select)
+
+    src = torch.ones(1 << 29, dtype=torch.float16, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    if what in ("pack", "unpack"):
+        for layer in (0, CUT):
+            K, V, ks, vs, L = make_layer(layer, dev)
+            bits = 2 if L <= 4 else 4
+            for X, sc, pt in ((K, ks, False), (V, vs, True)):
+                tb = NuqLayerTables(*sc, per_token=pt)
+                tb.ensure_tables()
+                cc = CompactCodes.empty(*X.shape, bits, X.numel() // 8, dev)
+                nuq_pack_compact(X, tb, bits, out=cc, sync=False)
+                out = torch.empty_like(X)
+                for _ in range(3):
+                    if what == "pack":
+                        nuq_pack_compact(X, tb, bits, out=cc, sync=False)
+                    else:
+                        nuq_unpack_compact(cc, tb, out=out)
+    elif what == "quest":
+        P = 65536
+        g = torch.Generator(device=dev).manual_seed(3)
+        q = torch.randn((HQ, D), generator=g, device=dev).half()
+        mn, mx = quest_page_stats(torch.randn((P, 16, H, D), generator=g, device=dev).half())
+        for _ in range(3):
+            quest_select(q, mn, mx, P // 4, 4)
+    elif what == "decode":
+        P = DEC_TOK // 16
+        for Ld in build_decode_layers(dev, (0, CUT)):
+            sel, _ = quest_select(Ld["q"], Ld["kmin"], Ld["kmax"], P // 4, 4)
+            for _ in range(3):
+                decode_attention(Ld["q"], Ld["ck"], Ld["kt"], Ld["cv"], Ld["vt"], sel)
+    torch.cuda.synchronize()
+    log(f"[bench] profile pass {what} done")
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--only", choices=["all", "nuq", "quest"], default="all")
+    ap.add_argument("--only", choices=["all", "nuq", "quest", "decode"], default="all")
+    ap.add_argument("--profile", choices=["pack", "unpack", "quest", "decode"], default=None,
+                    help="run a short fixed launch sequence for rocprofv3 counters and exit")
     ap.add_argument("--cpu-layers", default="0,1,16,17",
                     help="layers timed on the CPU oracle for the baseline")
     ap.add_argument("--no-cpu", action="store_true")
@@ -297,11 +493,16 @@ def main() -> None:
     from helix_kv import _native
 
     _native.lib()
+    if args.profile:
+        profile_pass(args.profile, dev)
+        return
     res = {}
     if args.only in ("all", "nuq"):
         res.update(bench_nuq(args, dev))
     if args.only in ("all", "quest"):
         res.update(bench_quest(args, dev))
+    if args.only in ("all", "decode"):
+        res.update(bench_decode(args, dev))
     cpu = None
     if not args.no_cpu and args.only in ("all", "nuq"):
         cpu = cpu_baseline([int(x) for x in args.cpu_layers.split(",")], dev)
@@ -326,12 +527,16 @@ def main() -> None:
                    "nuq2_layers": CUT, "t_cal": T_CAL},
     }
     if "pack_gbs" in res:
+        n_l = res["launches"]
         ach = res["algo_bytes"] / (res["pack_kernel_ms"] * 1e-3)
         line["roofline"] = {"bound": "hbm", "achieved": round(ach / 1e9, 1), "peak": HBM_PEAK / 1e9,
-                            "unit": "GB/s", "frac": round(ach / HBM_PEAK, 4), "traffic": None,
-                            "kernel": "pack_compact_kernel (all 56 launches, bytes-weighted)",
-                            "algorithmic_bytes_per_step": res["algo_bytes"],
-                            "kernel_ms_per_step": round(res["pack_kernel_ms"], 4)}
+                            "unit": "GB/s", "frac": round(ach / HBM_PEAK, 4),
+                            "traffic": profiled_traffic(PACK_PROFILE),
+                            "kernel": "hkv_nuq_pack_compact call (stage + scan + copy kernels), "
+                                      f"{n_l} calls per step, event-timed one by one",
+                            "algorithmic_bytes_per_launch": round(res["algo_bytes"] / n_l),
+                            "launch_us": round(res["pack_kernel_ms"] * 1e3 / n_l, 2),
+                            "traffic_source": PACK_PROFILE}
         uach = res["algo_bytes"] / (res["unpack_kernel_ms"] * 1e-3)
         line["unpack"] = {"GBps": round(res["unpack_gbs"], 2), "ms_per_step": round(res["unpack_ms"], 4),
                           "kernel_GBps": round(uach / 1e9, 1), "frac": round(uach / HBM_PEAK, 4)}
@@ -345,6 +550,23 @@ def main() -> None:
                                    "replays over 3 metadata sets (HBM-resident)",
                          "page_stats_build_us": round(res["stats_ms"] * 1e3, 1),
                          "page_stats_build_GBps": round(res["stats_bytes"] / (res["stats_ms"] * 1e-3) / 1e9, 1)}
+    if "dec_step_us" in res:
+        dsel = res["dec_sel_bytes"] / (res["dec_select_us"] * 1e-6)
+        datt = res["dec_attn_bytes"] / (res["dec_attn_us"] * 1e-6)
+        tot = (res["dec_sel_bytes"] + res["dec_attn_bytes"]) / (res["dec_step_us"] * 1e-6)
+        line["decode"] = {
+            "us_per_step": round(res["dec_step_us"], 1),
+            "achieved_GBps": round(tot / 1e9, 1), "frac": round(tot / HBM_PEAK, 4),
+            "select_us": round(res["dec_select_us"], 1), "select_GBps": round(dsel / 1e9, 1),
+            "attn_us": round(res["dec_attn_us"], 1), "attn_GBps": round(datt / 1e9, 1),
+            "attn_frac": round(datt / HBM_PEAK, 4),
+            "algorithmic_bytes": res["dec_sel_bytes"] + res["dec_attn_bytes"],
+            "selected_outliers": res["dec_sel_outliers"], "pages_per_split": res["dec_pps"],
+            "check_rel_err": float(f"{res['dec_rel_err']:.3g}"),
+            "config": f"Qwen2.5-7B shapes: {LAYERS} layers, 28 q heads, 4 KV heads, 128; "
+                      f"{DEC_TOK} tokens in the mixed nuq2/nuq4 compact pool (~5% CSR "
+                      "outliers); per layer Quest top 16384 + 4 sink pages per KV head, then "
+                      "fused dequant + attention; batch 1; one HIP graph per step"}
     if cpu is not None:
         line["cpu_baseline"] = cpu
     print(json.dumps(line), flush=True)
