@@ -1,29 +1,40 @@
-// decode.hip -- fused dequant + Quest-sparse decode attention (batch 1).
+// decode.hip -- decode attention over Quest-selected pages (batch 1).
 //
-// Replaces the reference's decode path unpack_to_staging + flash_attn_varlen_
-// func over an fp16 staging copy (src/kvquant/compact_backend.py:233-299):
-// the selected pages are read straight from the compact format (bit-packed
-// nuq2/nuq4 codes + CSR outliers, as written by hkv_nuq_pack_compact over
-// rows t*H + h), dequantised in LDS and fed to MFMA.  Semantics: for query
-// head hq (KV head g = hq / group), softmax(q . K^T * scale) . V over the
-// tokens of the pages sel[0..nsel)[g] (page p = tokens [16p, 16p+16), tokens
-// >= T masked), with an fp32 softmax -- the dense restatement
-// src/quest/reference.py:136-168 with the standard GQA head map.
+// 1. hkv_decode_attn: fused dequant + sparse attention from the compact format.
+//    Replaces the reference's decode path unpack_to_staging +
+//    flash_attn_varlen_func over an fp16 staging copy
+//    (src/kvquant/compact_backend.py:233-299): the selected pages are read
+//    straight from the compact format (bit-packed nuq2/nuq4 codes + CSR
+//    outliers over rows t*H + h, as written by hkv_nuq_pack_compact),
+//    dequantised in LDS and fed to MFMA.  For query head hq (KV head
+//    g = hq / group): softmax(q . K^T * scale) . V over the tokens of the pages
+//    sel[0..nsel)[g] (page p = tokens [16p, 16p+16), tokens >= T masked), fp32
+//    softmax -- the restatement of src/quest/reference.py:136-168 with the
+//    standard GQA head map.
 //
-// Work: grid (splits, H); a split is a run of pps consecutive selected pages
-// of one KV head; each of the block's 4 waves takes every 4th page.  Per page
-// a wave:
-//   1. loads the 16 rows' packed K and V codes (16 B per lane),
-//   2. dequantises them through LUTs in LDS (K: per-channel poles of head g,
-//      staged once per block; V: the rows' per-token poles, row
-//      min(t, rows-1)), into padded fp16 tiles [16 keys][136],
-//   3. patches the rows' CSR outliers into the tiles,
-//   4. S^T = K Q^T with 8 v_mfma_f32_16x16x16f16 (lane l: query head l%16 of
-//      the group, keys 4*(l/16)..+3), online softmax per query head (lanes
-//      l, l^16, l^32, l^48 share a head),
-//   5. O^T += V^T P^T with 8 more MFMAs; P comes straight from S's registers.
-// The 4 waves' (m, l, O) are merged through LDS into one partial per split;
-// merge_kernel combines the splits (flash-decoding) and normalises.
+//    Work: grid (splits, H); a split is a run of pps consecutive selected
+//    pages of one KV head; wave w of the block takes pages w, w+4, ... of the
+//    split (at most 64, one page id per lane).  Per page a wave
+//      - dequantises the 16 rows' K and V codes through LUTs in LDS (K: the
+//        per-channel poles of head g, staged once per block in a bank-swizzled
+//        [channel][level] layout; V: the rows' per-token poles, row
+//        min(t, rows-1)) into padded fp16 tiles [16 keys][136],
+//      - writes the rows' CSR outliers over the tiles,
+//      - S^T = K Q^T with 8 v_mfma_f32_16x16x16f16 (lane l: query head l%16
+//        of the group, keys 4*(l/16)..+3), online softmax per query head,
+//      - O^T += V^T P^T with 8 more MFMAs, P straight from S's registers.
+//    Global loads run three pages ahead of the math in a software pipeline:
+//    while page i is computed, the CSR entries of page i+1 (whose row_ptr
+//    arrived during page i-1) and the codes, pole rows and row_ptr of page
+//    i+2 are in flight, so no global latency sits between two pages.
+//    The 4 waves' (m, l, O) are merged through LDS into one partial per split.
+//
+// 2. hkv_selected_attention: the same attention over dense K/V pages
+//    (P, page, H, D) in fp16/fp32/bf16 -- the drop-in for selected_attention
+//    (src/quest/reference.py:136-168), any page size, head dims <= 512.
+//
+// merge_kernel combines the splits of either kernel (flash-decoding):
+// out = sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s, m in log2 units.
 #include "hkv_common.h"
 
 namespace {
@@ -31,11 +42,21 @@ namespace {
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kDT = 256;       // threads per block
-constexpr int kW = kDT / 64;   // waves per block
-constexpr int kHD = 128;       // head dim
-constexpr int kPS = 16;        // tokens per page
-constexpr int kTS = kHD + 8;   // padded tile row (halves): conflict-free MFMA operand reads
+constexpr int kDT = 256;        // threads per block
+constexpr int kW = kDT / 64;    // waves per block
+constexpr int kHD = 128;        // head dim of the fused kernel
+constexpr int kPS = 16;         // tokens per page
+constexpr int kTS = kHD + 8;    // padded tile row (halves)
+constexpr int kMaxPPS = 256;    // pages per split: at most 64 per wave
+constexpr int kSlots = 4;       // CSR entries per lane per side kept in registers
+constexpr int kKLut = kHD * 16 + 16 * 4;  // halves of the swizzled K LUT
+constexpr float kLog2e = 1.4426950408889634f;
+
+// K LUT index of (channel, level).  A lane dequantises channels
+// [32q, 32q+32) of one row (q = lane % 4); for a fixed channel offset the
+// 16 lanes of one q read one channel's 8 words, and the 16-half skew per
+// q puts the four q groups on disjoint banks (32 or 64 banks).
+HKV_DEV int klut_index(int ch, int c) { return ch * 16 + 16 * (ch >> 5) + c; }
 
 struct Side {  // one of K / V in the compact format
   const uint8_t* packed;   // (T, H, D*bits/8)
@@ -45,14 +66,13 @@ struct Side {  // one of K / V in the compact format
   int64_t cap;
   const hkv_table_t* tabs; // decision tables: pf16 are the dequantised poles
   int64_t rows;            // per-token scale rows (V); unused for K
-  int bits;
 };
 
 struct DecodeArgs {
   const uint16_t* q;  // (Hq, D) fp16
   Side k, v;
   int H, group;
-  int64_t T;
+  int64_t T, npages;
   const int64_t* sel;  // (nsel, H)
   int64_t nsel;
   int pps;             // pages per split
@@ -68,24 +88,81 @@ HKV_DEV void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Dequantise one side of a page into tile[16][kTS]: lane l owns row l/4 and
-// channels [32*(l%4), +32).  lut(row, ch, code) gives the fp16 bits.
-template <typename Lut>
-HKV_DEV void dequant_page(const Side& sd, int64_t t0, int64_t T, int H, int g, int lane,
-                          uint16_t* tile, Lut lut) {
-  const int row = lane >> 2, c0 = 32 * (lane & 3);
-  const int64_t t = t0 + row;
-  uint32_t w[4] = {0u, 0u, 0u, 0u};
-  if (t < T) {
-    const int64_t r = t * H + g;
-    if (sd.bits == 4) {
-      const uint4 v = *reinterpret_cast<const uint4*>(sd.packed + r * (kHD / 2) + c0 / 2);
-      w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
-    } else {
-      const uint2 v = *reinterpret_cast<const uint2*>(sd.packed + r * (kHD / 4) + c0 / 4);
-      w[0] = v.x; w[1] = v.y;
+// Loads of one page that depend only on its id.  Lane l covers row l/4 and
+// channels [32(l%4), +32): NB dwords of codes per side (nuq4: 4, nuq2: 2),
+// row_ptr[r] and row_ptr[r+1] of its row, and levels 4(l%4)..+3 of its row's
+// V poles.  Every load is unconditional from an in-bounds address (row 0 for
+// rows past the context, whose data the math ignores), so no load result is
+// moved or combined before it is used: the loads stay in flight across the
+// pipeline stages.  Offsets fit in 32 bits (T*H*D < 2^31 is checked).
+template <int KB, int VB>
+struct PageLoad {
+  uint32_t kc[KB], vc[VB];
+  uint2 vtab;
+  int2 kr, vr;
+};
+
+// The page's CSR entries: lane l holds entries a + l%4 + 4s (s < kSlots) of
+// its row (index clamped into [0, cap); whether an entry belongs to the row is
+// decided from row_ptr when it is used).
+struct PageOutl {
+  uint32_t kval[kSlots], kcol[kSlots], vval[kSlots], vcol[kSlots];
+};
+
+template <int NB>
+HKV_DEV void load_codes(const uint8_t* packed, int r, int q, uint32_t (&w)[NB]) {
+  const uint8_t* base = packed + (uint32_t)(r * (kHD * NB / 8) + q * (32 * NB / 8));
+  if constexpr (NB == 4) {
+    const uint4 v = *reinterpret_cast<const uint4*>(base);
+    w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+  } else {
+    const uint2 v = *reinterpret_cast<const uint2*>(base);
+    w[0] = v.x; w[1] = v.y;
+  }
+}
+
+template <int KB, int VB>
+HKV_DEV void load_page(const DecodeArgs& A, int p, int g, int lane, PageLoad<KB, VB>& L) {
+  const int row = lane >> 2, q = lane & 3;
+  const int t = p < 0 ? 0 : p * kPS + row;
+  const int tc = t < (int)A.T ? t : 0;
+  const int r = tc * A.H + g;
+  L.kr = *reinterpret_cast<const int2*>(A.k.row_ptr + (uint32_t)r);
+  L.vr = *reinterpret_cast<const int2*>(A.v.row_ptr + (uint32_t)r);
+  load_codes<KB>(A.k.packed, r, q, L.kc);
+  load_codes<VB>(A.v.packed, r, q, L.vc);
+  const int vrow = t < (int)A.v.rows ? t : (int)A.v.rows - 1;
+  L.vtab = *reinterpret_cast<const uint2*>(A.v.tabs[(uint32_t)(g * (int)A.v.rows + vrow)].pf16 + 4 * q);
+}
+
+HKV_DEV int csr_slot(int a, int sub, int s, int cap) {
+  const int i = (a < 0 ? 0 : a) + sub + 4 * s;
+  return i < cap ? i : cap - 1;
+}
+
+template <int KB, int VB>
+HKV_DEV void load_outl(const DecodeArgs& A, const PageLoad<KB, VB>& L, int lane, PageOutl& O) {
+  const int sub = lane & 3;
+  const int kcap = (int)A.k.cap, vcap = (int)A.v.cap;
+#pragma unroll
+  for (int s = 0; s < kSlots; ++s) {
+    if (kcap > 0) {
+      const uint32_t i = (uint32_t)csr_slot(L.kr.x, sub, s, kcap);
+      O.kval[s] = A.k.val[i];
+      O.kcol[s] = A.k.col[i];
+    }
+    if (vcap > 0) {
+      const uint32_t i = (uint32_t)csr_slot(L.vr.x, sub, s, vcap);
+      O.vval[s] = A.v.val[i];
+      O.vcol[s] = A.v.col[i];
     }
   }
+}
+
+// Dequantise the lane's 32 codes into tile row l/4, channels [32(l%4), +32).
+template <int NB, typename Lut>
+HKV_DEV void dequant_rows(const uint32_t (&w)[NB], bool valid, int lane, uint16_t* tile, Lut lut) {
+  const int row = lane >> 2, c0 = 32 * (lane & 3);
 #pragma unroll
   for (int k = 0; k < 4; ++k) {  // 8 channels per 128-bit LDS store
     uint32_t h[4];
@@ -96,37 +173,33 @@ HKV_DEV void dequant_page(const Side& sd, int64_t t0, int64_t T, int H, int g, i
       for (int e2 = 0; e2 < 2; ++e2) {
         const int e = 8 * k + 2 * j + e2;  // channel c0 + e
         uint32_t code;
-        if (sd.bits == 4) code = (w[e >> 3] >> (4 * (e & 7))) & 15u;
+        if constexpr (NB == 4) code = (w[e >> 3] >> (4 * (e & 7))) & 15u;
         else code = (w[e >> 4] >> (2 * (e & 15))) & 3u;
-        pr |= (uint32_t)lut(row, c0 + e, code) << (16 * e2);
+        pr |= (uint32_t)lut(c0 + e, code) << (16 * e2);
       }
-      h[j] = t < T ? pr : 0u;  // rows past the context read as zeros
+      h[j] = valid ? pr : 0u;  // rows past the context read as zeros
     }
     *reinterpret_cast<uint4*>(tile + row * kTS + c0 + 8 * k) = make_uint4(h[0], h[1], h[2], h[3]);
   }
 }
 
-// The page's CSR outliers over the tile (after dequant_page, before use):
-// lane l handles row l/4, entries (l%4), +4, ...
-HKV_DEV void patch_page(const Side& sd, int64_t t0, int64_t T, int H, int g, int lane,
-                        uint16_t* tile) {
+// CSR entries beyond the kSlots held in registers (rows with > 4*kSlots
+// outliers): read directly.
+HKV_DEV void patch_rest(const Side& sd, int2 rb, int lane, uint16_t* tile) {
   const int row = lane >> 2;
-  const int64_t t = t0 + row;
-  if (t >= T) return;
-  const int64_t r = t * H + g;
-  int32_t a = sd.row_ptr[r], b = sd.row_ptr[r + 1];
-  if (a < 0) a = 0;
-  if ((int64_t)b > sd.cap) b = (int32_t)sd.cap;
-  for (int32_t i = a + (lane & 3); i < b; i += 4) {
+  int64_t i = (int64_t)(rb.x < 0 ? 0 : rb.x) + 4 * kSlots + (lane & 3);
+  const int64_t e = rb.y < sd.cap ? rb.y : sd.cap;
+  for (; i < e; i += 4) {
     const uint32_t d = sd.col[i];
     if (d < (uint32_t)kHD) tile[row * kTS + d] = sd.val[i];
   }
 }
 
-__global__ void __launch_bounds__(kDT)
+template <int KB, int VB>
+__global__ void __launch_bounds__(kDT) __attribute__((amdgpu_waves_per_eu(3, 3)))
 decode_kernel(DecodeArgs A) {
-  __shared__ uint16_t s_klut[16 * kHD];           // [level][channel] of head g
-  __shared__ __align__(16) uint16_t s_vlut[kW][kPS * 16];  // [row][level] of the wave's page
+  __shared__ __align__(16) uint16_t s_klut[kKLut];
+  __shared__ __align__(16) uint16_t s_vlut[kW][kPS * 16];   // [row][level] of the wave's page
   __shared__ __align__(16) uint16_t s_tiles[kW][2][kPS * kTS];
   __shared__ float s_m[kW][16], s_l[kW][16];
 
@@ -135,11 +208,20 @@ decode_kernel(DecodeArgs A) {
   const int64_t j0 = (int64_t)blockIdx.x * A.pps;
   const int64_t j1 = j0 + A.pps < A.nsel ? j0 + A.pps : A.nsel;
 
-  for (int i = tid; i < 16 * kHD; i += kDT) {
-    const int l = i / kHD, d = i % kHD;
-    s_klut[i] = A.k.tabs[(int64_t)g * kHD + d].pf16[l];
+  for (int i = tid; i < kHD * 16; i += kDT) {
+    const int d = i >> 4, l = i & 15;
+    s_klut[klut_index(d, l)] = A.k.tabs[(int64_t)g * kHD + d].pf16[l];
   }
-  __syncthreads();
+
+  // the wave's page ids, one per lane (-1: none / out of range)
+  const int64_t nw64 = j1 - j0 > wv ? (j1 - j0 - wv + kW - 1) / kW : 0;
+  const int nw = (int)nw64;  // <= kMaxPPS / kW = 64
+  int my_p = -1;
+  if (lane < nw) {
+    const int64_t s = A.sel[(j0 + wv + (int64_t)kW * lane) * H + g];
+    my_p = (s >= 0 && s < A.npages) ? (int)s : -1;
+  }
+  auto page_at = [&](int i) -> int { return i < nw ? __builtin_amdgcn_readlane(my_p, i) : -1; };
 
   // B operand of S^T = K Q^T: lane l holds q[qh = l%16][16i + 4(l/16) .. +3]
   const int qh = lane & 15, kg = lane >> 4;
@@ -158,31 +240,39 @@ decode_kernel(DecodeArgs A) {
 #pragma unroll
   for (int t = 0; t < 8; ++t) o[t] = (float4_t){0.f, 0.f, 0.f, 0.f};
   float m = -__builtin_inff(), lsum = 0.0f;
-  const float sl2 = A.scale * 1.4426950408889634f;  // scale * log2(e)
+  const float sl2 = A.scale * kLog2e;
+  __syncthreads();  // K LUT
 
   uint16_t* kt = s_tiles[wv][0];
   uint16_t* vt = s_tiles[wv][1];
   uint16_t* vl = s_vlut[wv];
-  for (int64_t j = j0 + wv; j < j1; j += kW) {
-    const int64_t p = A.sel[j * H + g];
-    if (p < 0 || p >= (A.T + kPS - 1) / kPS) continue;  // no such page: nothing to attend
-    const int64_t t0 = p * kPS;
-    // V row tables: lanes 0..15 stage row `lane`'s 16 poles
-    if (lane < kPS) {
-      const int64_t t = t0 + lane;
-      const int64_t row = t < A.v.rows ? t : A.v.rows - 1;
-      const uint4* src = reinterpret_cast<const uint4*>(A.v.tabs[(int64_t)g * A.v.rows + row].pf16);
-      reinterpret_cast<uint4*>(vl + lane * 16)[0] = src[0];
-      reinterpret_cast<uint4*>(vl + lane * 16)[1] = src[1];
+
+  auto compute = [&](const PageLoad<KB, VB>& L, const PageOutl& Ob, int p) {
+    const int64_t t0 = (int64_t)p * kPS;
+    const int row = lane >> 2;
+    const bool valid = t0 + row < A.T;
+    *reinterpret_cast<uint2*>(vl + row * 16 + 4 * (lane & 3)) = L.vtab;
+    wave_sync();
+    dequant_rows<KB>(L.kc, valid, lane, kt,
+                     [&](int ch, uint32_t c) { return s_klut[klut_index(ch, (int)c)]; });
+    dequant_rows<VB>(L.vc, valid, lane, vt,
+                     [&](int, uint32_t c) { return vl[row * 16 + (int)c]; });
+    wave_sync();
+    if (valid) {
+      const int sub = lane & 3;
+      const int ka = L.kr.x < 0 ? 0 : L.kr.x, va = L.vr.x < 0 ? 0 : L.vr.x;
+      const int ke = L.kr.y < (int)A.k.cap ? L.kr.y : (int)A.k.cap;
+      const int ve = L.vr.y < (int)A.v.cap ? L.vr.y : (int)A.v.cap;
+#pragma unroll
+      for (int s = 0; s < kSlots; ++s) {
+        if (ka + sub + 4 * s < ke && Ob.kcol[s] < (uint32_t)kHD)
+          kt[row * kTS + Ob.kcol[s]] = (uint16_t)Ob.kval[s];
+        if (va + sub + 4 * s < ve && Ob.vcol[s] < (uint32_t)kHD)
+          vt[row * kTS + Ob.vcol[s]] = (uint16_t)Ob.vval[s];
+      }
+      if (ke - ka > 4 * kSlots) patch_rest(A.k, L.kr, lane, kt);
+      if (ve - va > 4 * kSlots) patch_rest(A.v, L.vr, lane, vt);
     }
-    wave_sync();
-    dequant_page(A.k, t0, A.T, H, g, lane, kt,
-                 [&](int, int ch, uint32_t c) { return s_klut[c * kHD + ch]; });
-    dequant_page(A.v, t0, A.T, H, g, lane, vt,
-                 [&](int row, int, uint32_t c) { return vl[row * 16 + c]; });
-    wave_sync();
-    patch_page(A.k, t0, A.T, H, g, lane, kt);
-    patch_page(A.v, t0, A.T, H, g, lane, vt);
     wave_sync();
 
     // S^T (16 keys x 16 query heads)
@@ -204,7 +294,7 @@ decode_kernel(DecodeArgs A) {
     }
     mp = fmaxf(mp, __shfl_xor(mp, 16, 64));
     mp = fmaxf(mp, __shfl_xor(mp, 32, 64));
-    const float mn = fmaxf(m, mp);  // finite: every selected page holds a token < T
+    const float mn = fmaxf(m, mp);  // finite: a valid page holds a token < T
     const float alpha = exp2f(m - mn);
     m = mn;
     half4_t pb;
@@ -227,7 +317,29 @@ decode_kernel(DecodeArgs A) {
         a[r] = __builtin_bit_cast(_Float16, vt[(4 * kg + r) * kTS + 16 * t + qh]);
       o[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, pb, o[t], 0, 0, 0);
     }
-    wave_sync();  // the tiles are rewritten by the wave's next page
+    wave_sync();  // the tiles and the V LUT are rewritten by the next page
+  };
+
+  // three-stage pipeline over the wave's pages, unrolled by 3 so that every
+  // in-flight load keeps its registers (no copies of pending loads)
+  PageLoad<KB, VB> L0, L1, L2;
+  PageOutl O0, O1, O2;
+  load_page(A, page_at(0), g, lane, L0);
+  load_page(A, page_at(1), g, lane, L1);
+  load_outl(A, L0, lane, O0);
+  auto step = [&](int i, const PageLoad<KB, VB>& Lc, const PageOutl& Oc, const PageLoad<KB, VB>& Ln,
+                  PageOutl& On, PageLoad<KB, VB>& Lw) {
+    load_page(A, page_at(i + 2), g, lane, Lw);
+    if (i + 1 < nw) load_outl(A, Ln, lane, On);
+    const int p = page_at(i);
+    if (p >= 0) compute(Lc, Oc, p);
+  };
+  for (int i = 0; i < nw; i += 3) {
+    step(i, L0, O0, L1, O1, L2);
+    if (i + 1 >= nw) break;
+    step(i + 1, L1, O1, L2, O2, L0);
+    if (i + 2 >= nw) break;
+    step(i + 2, L2, O2, L0, O0, L1);
   }
 
   // wave partials: m (replicated over the 4 lane groups), l summed over them
@@ -265,39 +377,174 @@ decode_kernel(DecodeArgs A) {
   }
 }
 
-// out[hq] = sum_s exp2(m_s - M) o_s / sum_s exp2(m_s - M) l_s  (m in log2 units)
-__global__ void __launch_bounds__(kHD)
+// ------------------------------------------------ dense pages (any dtype)
+
+constexpr int kDenseKeys = 1024;  // keys per split of the dense kernel
+constexpr int kDenseMaxD = 512;
+
+struct DenseArgs {
+  const void* q;       // (Hq, D)
+  const void* k;       // (P, S, Hk, D)
+  const void* v;       // (P, S, Hv, Dv)
+  int q_dt, kv_dt;
+  int64_t P;
+  int S, Hk, Hv, D, Dv, Hq, head_map;  // head_map 0: K head h, V head h % Hv; 1: h / (Hq/Hk)
+  const int64_t* sel;  // (nsel, ncols)
+  int64_t nsel;
+  int ncols;           // Hq (column per query head) or Hk (column per KV head)
+  int pps;
+  float scale;
+  float *part_m, *part_l, *part_o;
+};
+
+__global__ void __launch_bounds__(kDT)
+dense_attn_kernel(DenseArgs A) {
+  __shared__ float s_q[kDenseMaxD];
+  __shared__ float s_s[kDenseKeys];
+  __shared__ float s_red[kW];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int h = blockIdx.y;
+  const int kh = A.head_map == 0 ? h : h / (A.Hq / A.Hk);
+  const int vh = A.head_map == 0 ? h % A.Hv : kh;
+  const int col = A.ncols == A.Hq ? h : kh;
+  const int64_t j0 = (int64_t)blockIdx.x * A.pps;
+  const int64_t j1 = j0 + A.pps < A.nsel ? j0 + A.pps : A.nsel;
+  const int nk = (int)(j1 - j0) * A.S;  // <= kDenseKeys
+  for (int d = tid; d < A.D; d += kDT) s_q[d] = load_scale(A.q, A.q_dt, (int64_t)h * A.D + d);
+  __syncthreads();
+  // scores: one wave per key, lanes over channels
+  const float sl2 = A.scale * kLog2e;
+  for (int kk = wv; kk < nk; kk += kW) {
+    const int64_t p = A.sel[(j0 + kk / A.S) * A.ncols + col];
+    float sc = -__builtin_inff();
+    if (p >= 0 && p < A.P) {  // uniform per wave
+      const int64_t base = ((p * A.S + kk % A.S) * A.Hk + kh) * A.D;
+      float acc = 0.0f;
+      for (int d = lane; d < A.D; d += 64) acc += s_q[d] * load_scale(A.k, A.kv_dt, base + d);
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+      sc = acc * sl2;
+    }
+    if (lane == 0) s_s[kk] = sc;
+  }
+  __syncthreads();
+  float mx = -__builtin_inff();
+  for (int kk = tid; kk < nk; kk += kDT) mx = fmaxf(mx, s_s[kk]);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  if (lane == 0) s_red[wv] = mx;
+  __syncthreads();
+  float M = s_red[0];
+  for (int w = 1; w < kW; ++w) M = fmaxf(M, s_red[w]);
+  __syncthreads();
+  float ls = 0.0f;
+  for (int kk = tid; kk < nk; kk += kDT) {
+    const float e = M == -__builtin_inff() ? 0.0f : exp2f(s_s[kk] - M);
+    s_s[kk] = e;
+    ls += e;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) ls += __shfl_xor(ls, off, 64);
+  if (lane == 0) s_red[wv] = ls;
+  __syncthreads();
+  float L = 0.0f;
+  for (int w = 0; w < kW; ++w) L += s_red[w];
+  for (int d = tid; d < A.Dv; d += kDT) {
+    float acc = 0.0f;
+    for (int kk = 0; kk < nk; ++kk) {
+      const float pk = s_s[kk];
+      if (pk == 0.0f) continue;
+      const int64_t p = A.sel[(j0 + kk / A.S) * A.ncols + col];
+      const int64_t base = ((p * A.S + kk % A.S) * A.Hv + vh) * A.Dv;
+      acc += pk * load_scale(A.v, A.kv_dt, base + d);
+    }
+    A.part_o[((int64_t)blockIdx.x * A.Hq + h) * A.Dv + d] = acc;
+  }
+  if (tid == 0) {
+    A.part_m[(int64_t)blockIdx.x * A.Hq + h] = M;
+    A.part_l[(int64_t)blockIdx.x * A.Hq + h] = L;
+  }
+}
+
+// ------------------------------------------------------------------ merge
+
+// Block (query head, 16-channel slice); thread (d, sub) sums the splits
+// s = sub (mod 16) of channel d, then the 16 partial sums are added in LDS.
+// Every block first reduces M = max_s m_s and L = sum_s 2^(m_s - M) l_s.
+constexpr int kMergeCh = 16;
+constexpr int kMergeSub = kDT / kMergeCh;
+
+__global__ void __launch_bounds__(kDT)
 merge_kernel(const float* __restrict__ pm, const float* __restrict__ pl,
-             const float* __restrict__ po, int64_t splits, int Hq, int H, int group,
-             int64_t pps, int64_t nsel, void* out, int odt) {
-  const int hq = blockIdx.x, d = threadIdx.x;
-  (void)H;
-  (void)group;
-  (void)pps;
-  (void)nsel;
-  float M = -__builtin_inff();
-  for (int64_t s = 0; s < splits; ++s) M = fmaxf(M, pm[s * Hq + hq]);
-  float acc = 0.0f, L = 0.0f;
-  if (M != -__builtin_inff()) {
-    for (int64_t s = 0; s < splits; ++s) {
+             const float* __restrict__ po, int64_t splits, int Hq, int Dv, void* out, int odt) {
+  __shared__ float s_red[kW];
+  __shared__ float s_acc[kDT];
+  const int hq = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  float mx = -__builtin_inff();
+  for (int64_t s = tid; s < splits; s += kDT) mx = fmaxf(mx, pm[s * Hq + hq]);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  if (lane == 0) s_red[wv] = mx;
+  __syncthreads();
+  float M = s_red[0];
+  for (int w = 1; w < kW; ++w) M = fmaxf(M, s_red[w]);
+  __syncthreads();
+  float ls = 0.0f;
+  if (M != -__builtin_inff())
+    for (int64_t s = tid; s < splits; s += kDT) {
       const float ms = pm[s * Hq + hq];
-      if (ms == -__builtin_inff()) continue;
-      const float f = exp2f(ms - M);
-      acc += f * po[(s * Hq + hq) * kHD + d];
-      L += f * pl[s * Hq + hq];
+      if (ms != -__builtin_inff()) ls += exp2f(ms - M) * pl[s * Hq + hq];
+    }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) ls += __shfl_xor(ls, off, 64);
+  if (lane == 0) s_red[wv] = ls;
+  __syncthreads();
+  float L = 0.0f;
+  for (int w = 0; w < kW; ++w) L += s_red[w];
+  const int d = blockIdx.y * kMergeCh + (tid % kMergeCh), sub = tid / kMergeCh;
+  float acc = 0.0f;
+  if (d < Dv && M != -__builtin_inff()) {
+#pragma unroll 4
+    for (int64_t s = sub; s < splits; s += kMergeSub) {
+      const float ms = pm[s * Hq + hq];
+      const float w = ms == -__builtin_inff() ? 0.0f : exp2f(ms - M);
+      acc += w * po[(s * Hq + hq) * Dv + d];
     }
   }
-  const float r = L > 0.0f ? acc / L : 0.0f;
-  if (odt == HKV_DT_F32) ((float*)out)[(int64_t)hq * kHD + d] = r;
-  else ((uint16_t*)out)[(int64_t)hq * kHD + d] = f2h(r);
+  s_acc[tid] = acc;
+  __syncthreads();
+  if (sub == 0 && d < Dv) {
+    float a = 0.0f;
+    for (int u = 0; u < kMergeSub; ++u) a += s_acc[tid + u * kMergeCh];
+    const float r = L > 0.0f ? a / L : 0.0f;
+    if (odt == HKV_DT_F32) ((float*)out)[(int64_t)hq * Dv + d] = r;
+    else if (odt == HKV_DT_BF16) {
+      const uint32_t b = __builtin_bit_cast(uint32_t, r);
+      const uint32_t rb = (b + 0x7fffu + ((b >> 16) & 1u)) >> 16;  // nearest even
+      ((uint16_t*)out)[(int64_t)hq * Dv + d] = (r != r) ? (uint16_t)0x7fc0u : (uint16_t)rb;
+    } else ((uint16_t*)out)[(int64_t)hq * Dv + d] = f2h(r);
+  }
+}
+
+void launch_merge(const float* pm, const float* pl, const float* po, int64_t splits, int Hq, int Dv,
+                  void* out, int odt, hipStream_t s) {
+  hipLaunchKernelGGL(merge_kernel, dim3((unsigned)Hq, (unsigned)((Dv + kMergeCh - 1) / kMergeCh)),
+                     dim3(kDT), 0, s, pm, pl, po, splits, Hq, Dv, out, odt);
+}
+
+int64_t n_splits(int64_t nsel, int pps) { return nsel == 0 ? 1 : (nsel + pps - 1) / pps; }
+
+template <int KB, int VB>
+void launch_decode(const DecodeArgs& a, int64_t splits, hipStream_t s) {
+  hipLaunchKernelGGL((decode_kernel<KB, VB>), dim3((unsigned)splits, (unsigned)a.H), dim3(kDT), 0,
+                     s, a);
 }
 
 }  // namespace
 
 extern "C" size_t hkv_decode_workspace_bytes(int64_t nsel, int Hq, int pages_per_split) {
   if (nsel < 0 || Hq < 1 || pages_per_split < 1) return 0;
-  const int64_t splits = nsel == 0 ? 1 : (nsel + pages_per_split - 1) / pages_per_split;
-  return sizeof(float) * (size_t)splits * Hq * (2 + kHD);
+  return sizeof(float) * (size_t)n_splits(nsel, pages_per_split) * Hq * (2 + kHD);
 }
 
 extern "C" int hkv_decode_attn(const void* q, int Hq, int H, int D, int64_t T,
@@ -311,13 +558,14 @@ extern "C" int hkv_decode_attn(const void* q, int Hq, int H, int D, int64_t T,
                                void* out, int out_dtype, void* workspace, size_t workspace_bytes,
                                void* stream) {
   if (D != kHD) return HKV_ERR_SHAPE;
-  if (H < 1 || H > 65535 || Hq < H || Hq % H || Hq / H > 16 || T < 1 || nsel < 0 ||
-      pages_per_split < 1)
+  if (H < 1 || H > 65535 || Hq < H || Hq % H || Hq / H > 16 || T < 1 || nsel < 0)
     return HKV_ERR_SHAPE;
+  if (pages_per_split < 1 || pages_per_split > kMaxPPS) return HKV_ERR_ARG;
   if ((k_bits != 2 && k_bits != 4) || (v_bits != 2 && v_bits != 4)) return HKV_ERR_ARG;
   if (out_dtype != HKV_DT_F16 && out_dtype != HKV_DT_F32) return HKV_ERR_DTYPE;
   if (v_rows < 1 || k_cap < 0 || v_cap < 0) return HKV_ERR_ARG;
-  if (T * H * D >= ((int64_t)1 << 31)) return HKV_ERR_SHAPE;
+  if (T * H * D >= ((int64_t)1 << 31) || (int64_t)H * v_rows >= ((int64_t)1 << 31))
+    return HKV_ERR_SHAPE;
   if (!q || !k_packed || !k_row_ptr || !k_tables || !v_packed || !v_row_ptr || !v_tables || !out)
     return HKV_ERR_ARG;
   if ((k_cap > 0 && (!k_col || !k_val)) || (v_cap > 0 && (!v_col || !v_val))) return HKV_ERR_ARG;
@@ -326,7 +574,7 @@ extern "C" int hkv_decode_attn(const void* q, int Hq, int H, int D, int64_t T,
     return HKV_ERR_ARG;
   const size_t need = hkv_decode_workspace_bytes(nsel, Hq, pages_per_split);
   if (!workspace || workspace_bytes < need) return HKV_ERR_WORKSPACE;
-  const int64_t splits = nsel == 0 ? 1 : (nsel + pages_per_split - 1) / pages_per_split;
+  const int64_t splits = n_splits(nsel, pages_per_split);
   if (splits > 0x7fffffff) return HKV_ERR_SHAPE;
   hipStream_t s = (hipStream_t)stream;
   float* pm = (float*)workspace;
@@ -334,13 +582,13 @@ extern "C" int hkv_decode_attn(const void* q, int Hq, int H, int D, int64_t T,
   float* po = pl + splits * Hq;
   DecodeArgs a;
   a.q = (const uint16_t*)q;
-  a.k = Side{(const uint8_t*)k_packed, k_row_ptr, k_col, k_val, k_cap,
-             (const hkv_table_t*)k_tables, 0, k_bits};
-  a.v = Side{(const uint8_t*)v_packed, v_row_ptr, v_col, v_val, v_cap,
-             (const hkv_table_t*)v_tables, v_rows, v_bits};
+  a.k = Side{(const uint8_t*)k_packed, k_row_ptr, k_col, k_val, k_cap, (const hkv_table_t*)k_tables, 0};
+  a.v = Side{(const uint8_t*)v_packed, v_row_ptr, v_col, v_val, v_cap, (const hkv_table_t*)v_tables,
+             v_rows};
   a.H = H;
   a.group = Hq / H;
   a.T = T;
+  a.npages = (T + kPS - 1) / kPS;
   a.sel = sel;
   a.nsel = nsel;
   a.pps = pages_per_split;
@@ -348,10 +596,74 @@ extern "C" int hkv_decode_attn(const void* q, int Hq, int H, int D, int64_t T,
   a.part_m = pm;
   a.part_l = pl;
   a.part_o = po;
-  hipLaunchKernelGGL(decode_kernel, dim3((unsigned)splits, (unsigned)H), dim3(kDT), 0, s, a);
+  if (k_bits == 4 && v_bits == 4) launch_decode<4, 4>(a, splits, s);
+  else if (k_bits == 4) launch_decode<4, 2>(a, splits, s);
+  else if (v_bits == 4) launch_decode<2, 4>(a, splits, s);
+  else launch_decode<2, 2>(a, splits, s);
   HKV_CHECK_LAUNCH();
-  hipLaunchKernelGGL(merge_kernel, dim3((unsigned)Hq), dim3(kHD), 0, s, pm, pl, po, splits, Hq, H,
-                     a.group, (int64_t)pages_per_split, nsel, out, out_dtype);
+  launch_merge(pm, pl, po, splits, Hq, kHD, out, out_dtype, s);
+  HKV_CHECK_LAUNCH();
+  return HKV_OK;
+}
+
+extern "C" size_t hkv_selected_attention_workspace_bytes(int64_t nsel, int page_size, int Hq,
+                                                         int Dv) {
+  if (nsel < 0 || page_size < 1 || page_size > kDenseKeys || Hq < 1 || Dv < 1) return 0;
+  const int pps = kDenseKeys / page_size;
+  return sizeof(float) * (size_t)n_splits(nsel, pps) * Hq * (2 + (size_t)Dv);
+}
+
+extern "C" int hkv_selected_attention(const void* q, int q_dtype, int Hq, int D, const void* k_pages,
+                                      const void* v_pages, int kv_dtype, int64_t P, int page_size,
+                                      int Hk, int Hv, int Dv, const int64_t* sel, int64_t nsel,
+                                      int sel_cols, int head_map, float scale, void* out,
+                                      int out_dtype, void* workspace, size_t workspace_bytes,
+                                      void* stream) {
+  auto okdt = [](int d) { return d == HKV_DT_F16 || d == HKV_DT_F32 || d == HKV_DT_BF16; };
+  if (!okdt(q_dtype) || !okdt(kv_dtype) || !okdt(out_dtype)) return HKV_ERR_DTYPE;
+  if (Hq < 1 || Hk < 1 || Hv < 1 || D < 1 || Dv < 1 || D > kDenseMaxD || Dv > kDenseMaxD ||
+      P < 0 || nsel < 0 || page_size < 1 || page_size > kDenseKeys || Hq > 65535)
+    return HKV_ERR_SHAPE;
+  if (head_map == 0) {
+    if (Hk != Hq) return HKV_ERR_SHAPE;
+  } else if (head_map == 1) {
+    if (Hq % Hk || Hv != Hk) return HKV_ERR_SHAPE;
+  } else {
+    return HKV_ERR_ARG;
+  }
+  if (sel_cols != Hq && sel_cols != Hk) return HKV_ERR_SHAPE;
+  if (!q || !out || (nsel > 0 && (!sel || !k_pages || !v_pages))) return HKV_ERR_ARG;
+  const size_t need = hkv_selected_attention_workspace_bytes(nsel, page_size, Hq, Dv);
+  if (!workspace || workspace_bytes < need) return HKV_ERR_WORKSPACE;
+  const int pps = kDenseKeys / page_size;
+  const int64_t splits = n_splits(nsel, pps);
+  if (splits > 0x7fffffff) return HKV_ERR_SHAPE;
+  hipStream_t s = (hipStream_t)stream;
+  DenseArgs a;
+  a.q = q;
+  a.k = k_pages;
+  a.v = v_pages;
+  a.q_dt = q_dtype;
+  a.kv_dt = kv_dtype;
+  a.P = P;
+  a.S = page_size;
+  a.Hk = Hk;
+  a.Hv = Hv;
+  a.D = D;
+  a.Dv = Dv;
+  a.Hq = Hq;
+  a.head_map = head_map;
+  a.sel = sel;
+  a.nsel = nsel;
+  a.ncols = sel_cols;
+  a.pps = pps;
+  a.scale = scale;
+  a.part_m = (float*)workspace;
+  a.part_l = a.part_m + splits * Hq;
+  a.part_o = a.part_l + splits * Hq;
+  hipLaunchKernelGGL(dense_attn_kernel, dim3((unsigned)splits, (unsigned)Hq), dim3(kDT), 0, s, a);
+  HKV_CHECK_LAUNCH();
+  launch_merge(a.part_m, a.part_l, a.part_o, splits, Hq, Dv, out, out_dtype, s);
   HKV_CHECK_LAUNCH();
   return HKV_OK;
 }

@@ -87,6 +87,9 @@ _SIGS = {
                          _p, _p, _p, _p, _i64, _i32, _p,
                          _p, _p, _p, _p, _i64, _i32, _p, _i64,
                          _p, _i64, _i32, ctypes.c_float, _p, _i32, _p, _sz, _p], _i32),
+    "hkv_selected_attention_workspace_bytes": ([_i64, _i32, _i32, _i32], _sz),
+    "hkv_selected_attention": ([_p, _i32, _i32, _i32, _p, _p, _i32, _i64, _i32, _i32, _i32, _i32,
+                                _p, _i64, _i32, _i32, ctypes.c_float, _p, _i32, _p, _sz, _p], _i32),
 }
 
 _lib = None

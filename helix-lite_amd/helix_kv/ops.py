@@ -377,7 +377,7 @@ def decode_pages_per_split(nsel: int, H: int) -> int:
     over the (split, KV head) grid, a multiple of the block's 4 waves."""
     cus = N.num_cus()
     want = max(1, -(-nsel * H // (3 * cus)))
-    return max(4, -(-want // 4) * 4)
+    return min(256, max(4, -(-want // 4) * 4))
 
 
 def decode_attention(query: torch.Tensor, k: CompactCodes, kt: NuqLayerTables, v: CompactCodes,
@@ -425,4 +425,42 @@ def decode_attention(query: torch.Tensor, k: CompactCodes, kt: NuqLayerTables, v
         N.ptr(s), nsel, pps, sc, N.ptr(out), N.dtype_code(out), N.ptr(ws), ws.numel(),
         N.stream_of(q))
     N.check(st, "hkv_decode_attn", AssertionError)
+    return out
+
+
+def selected_attention(query: torch.Tensor, K_pages: torch.Tensor, V_pages: torch.Tensor,
+                       page_indices: torch.Tensor, *, gqa: bool = False,
+                       scale: float | None = None) -> torch.Tensor:
+    """Attention of each query head over its selected dense pages
+    (hkv_selected_attention).
+
+    query (Hq, D); K_pages (P, page, Hk, D); V_pages (P, page, Hv, Dv);
+    page_indices (n, Hq) or (n, Hk) int64.  gqa=False is the reference's head
+    map (src/quest/reference.py:136-168: K head h, V head h % Hv, Hk == Hq);
+    gqa=True maps query head h to KV head h // (Hq // Hk).  Returns (Hq, Dv) in
+    query's dtype (fp16 / fp32 / bf16)."""
+    N.require_gpu(query, K_pages, V_pages, page_indices)
+    if query.dim() != 2 or K_pages.dim() != 4 or V_pages.dim() != 4 or page_indices.dim() != 2:
+        raise ValueError("expected query (H, D), pages (P, page, H, D), page_indices (n, H)")
+    Hq, D = (int(x) for x in query.shape)
+    P, S, Hk, Dk = (int(x) for x in K_pages.shape)
+    Pv, Sv, Hv, Dv = (int(x) for x in V_pages.shape)
+    if Dk != D or Pv != P or Sv != S:
+        raise ValueError(f"K_pages {tuple(K_pages.shape)} / V_pages {tuple(V_pages.shape)} do not "
+                         f"match query {tuple(query.shape)}")
+    kv_dt = K_pages.dtype
+    k = K_pages.contiguous()
+    v = V_pages.to(kv_dt).contiguous()
+    q = query.contiguous()
+    idx = page_indices.to(torch.int64).contiguous()
+    nsel, cols = (int(x) for x in idx.shape)
+    out = torch.empty((Hq, Dv), dtype=query.dtype, device=query.device)
+    nb = int(N.lib().hkv_selected_attention_workspace_bytes(nsel, S, Hq, Dv))
+    ws = N.workspace("selected_attention", nb, q.device)
+    sc = float(scale) if scale is not None else D ** -0.5
+    st = N.lib().hkv_selected_attention(
+        N.ptr(q), N.dtype_code(q), Hq, D, N.ptr(k), N.ptr(v), N.dtype_code(k), P, S, Hk, Hv, Dv,
+        N.ptr(idx), nsel, cols, 1 if gqa else 0, sc, N.ptr(out), N.dtype_code(out), N.ptr(ws),
+        ws.numel(), N.stream_of(q))
+    N.check(st, "hkv_selected_attention", ValueError)
     return out

@@ -20,6 +20,7 @@ from __future__ import annotations
 import torch
 
 from helix_kv.ops import quest_page_bound, quest_page_stats, quest_topk
+from helix_kv.ops import selected_attention as _selected_attention
 
 
 def compute_page_stats(K_pages: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
@@ -58,9 +59,10 @@ def topk_pages_with_sinks(bound: torch.Tensor, k: int, sink_pages: int = 1) -> t
 
 def selected_attention(query: torch.Tensor, K_pages: torch.Tensor, V_pages: torch.Tensor,
                        page_indices: torch.Tensor) -> torch.Tensor:
-    """Attention of each head over its selected pages (src/quest/reference.py:136-168)."""
-    from helix_kv.attention import selected_attention as _sa
-    return _sa(query, K_pages, V_pages, page_indices)
+    """Attention of each head over its selected pages (src/quest/reference.py:136-168):
+    head h attends with K head h and V head h % H_v over the pages
+    page_indices[:, h]; fp32 softmax, (H, D_v) output in query's dtype."""
+    return _selected_attention(query, K_pages, V_pages, page_indices)
 
 
 __all__ = ["compute_page_stats", "page_upper_bound", "topk_pages_with_sinks",

@@ -123,19 +123,21 @@ int hkv_nuq_unpack_dense(const void *codes, const void *outlier_v, const void *o
  * hkv_nuq_pack_compact_status).  bits = 2 or 4 (levels <= 2^bits).  Requires
  * scales->tables, D % 8 == 0, D <= 256.  The planned format of
  * src/kvquant/triton_kernels.py:7-18 and src/kvquant/compact_pool.py:11-12
- * (the reference never implemented it).  Single pass: the CSR offsets come
- * from a decoupled look-back over tiles, so `workspace` (zero-filled once
- * before first use, then reused as-is) must hold
- * hkv_nuq_pack_compact_workspace_bytes(T, H, D) bytes and must not be shared by
- * calls that may overlap.
+ * (the reference never implemented it).  Three kernels on `stream`: a stage
+ * kernel (codes, per-tile outlier counts, outliers staged per tile), a scan of
+ * the tile counts and a copy into col/val.  `workspace` (256-byte aligned, no
+ * initialisation needed) holds the counts, bases and staged outliers:
+ * hkv_nuq_pack_compact_workspace_bytes(T, H, D) bytes; calls that may overlap
+ * must not share it.
  */
 size_t hkv_nuq_pack_compact_workspace_bytes(int64_t T, int H, int D);
 int hkv_nuq_pack_compact(const void *values, int64_t T, int H, int D, int bits,
                          const hkv_nuq_scales *scales, void *packed, int32_t *row_ptr,
                          uint8_t *col, uint16_t *val, int64_t capacity, void *workspace,
                          size_t workspace_bytes, void *stream);
-/* Device-side error word of a pack workspace (0 = fine; bit 0: look-back
- * wait exceeded its limit).  Reads device memory: synchronises `stream`. */
+/* Device-side error word of a pack workspace.  The three-kernel pack has no
+ * device-side failure mode, so this returns 0 for any workspace (kept for
+ * callers of the status protocol); HKV_ERR_ARG for NULL. */
 int hkv_nuq_pack_compact_status(const void *workspace, void *stream);
 
 /*
@@ -290,6 +292,7 @@ int hkv_quest_select_blocks(const void *q, int q_dtype, int H, const void *kmin,
  * hkv_decode_workspace_bytes(nsel, Hq, pages_per_split) bytes, no zeroing.
  */
 size_t hkv_decode_workspace_bytes(int64_t nsel, int Hq, int pages_per_split);
+/* pages_per_split in [1, 256]. */
 int hkv_decode_attn(const void *q, int Hq, int H, int D, int64_t T,
                     const void *k_packed, const int32_t *k_row_ptr, const uint8_t *k_col,
                     const uint16_t *k_val, int64_t k_cap, int k_bits, const void *k_tables,
@@ -298,6 +301,25 @@ int hkv_decode_attn(const void *q, int Hq, int H, int D, int64_t T,
                     int64_t v_rows, const int64_t *sel, int64_t nsel, int pages_per_split,
                     float scale, void *out, int out_dtype, void *workspace,
                     size_t workspace_bytes, void *stream);
+
+/*
+ * Attention of each query head over its selected dense pages: the drop-in for
+ * selected_attention (src/quest/reference.py:136-168).  q (Hq, D); k_pages
+ * (P, page_size, Hk, D) and v_pages (P, page_size, Hv, Dv) in kv_dtype; sel
+ * (nsel, sel_cols) int64 with sel_cols = Hq (a column per query head, the
+ * reference's layout) or Hk (a column per KV head).  head_map 0: the
+ * reference's map (K head h, V head h % Hv; needs Hk == Hq); 1: GQA (K and V
+ * head h / (Hq / Hk)).  softmax(q.K^T * scale) in fp32, result rounded once to
+ * out_dtype; page ids outside [0, P) are skipped.  D, Dv <= 512, page_size <=
+ * 1024; dtypes fp16 / fp32 / bf16.  Workspace:
+ * hkv_selected_attention_workspace_bytes(nsel, page_size, Hq, Dv).
+ */
+size_t hkv_selected_attention_workspace_bytes(int64_t nsel, int page_size, int Hq, int Dv);
+int hkv_selected_attention(const void *q, int q_dtype, int Hq, int D, const void *k_pages,
+                           const void *v_pages, int kv_dtype, int64_t P, int page_size, int Hk,
+                           int Hv, int Dv, const int64_t *sel, int64_t nsel, int sel_cols,
+                           int head_map, float scale, void *out, int out_dtype, void *workspace,
+                           size_t workspace_bytes, void *stream);
 
 #ifdef __cplusplus
 }

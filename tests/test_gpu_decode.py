@@ -158,3 +158,34 @@ def test_decode_errors(dev):
     q34 = torch.zeros((34, 128), dtype=torch.float16, device=dev)
     with pytest.raises(AssertionError):
         decode_attention(q34, kc, kt, vc, vt, sel)           # group 17 > 16
+
+
+@pytest.mark.parametrize("dt,S,H,D,gqa", [(torch.float32, 8, 4, 64, False),
+                                          (torch.float16, 16, 3, 128, False),
+                                          (torch.bfloat16, 4, 2, 32, False),
+                                          (torch.float16, 16, 4, 128, True)])
+def test_dense_selected_attention_vs_oracle(dev, dt, S, H, D, gqa):
+    """quest.selected_attention (src/quest/reference.py:136-168) on dense
+    pages; with gqa the query heads map to KV head h // group."""
+    from helix_kv.ops import selected_attention
+    from quest import selected_attention as ref_api
+
+    P, n = 50, 9
+    Hq = H * 7 if gqa else H
+    K = torch.randn((P, S, H, D), dtype=torch.float32).to(dt)
+    V = torch.randn((P, S, H, D), dtype=torch.float32).to(dt)
+    q = torch.randn((Hq, D), dtype=torch.float32).to(dt)
+    cols = H if gqa else Hq
+    sel = torch.stack([torch.randperm(P)[:n].sort().values for _ in range(cols)], 1)
+    kv = (lambda h: h // 7) if gqa else (lambda h: h)
+    want = O.selected_attention(q.double().numpy(), K.double().numpy(), V.double().numpy(),
+                                sel.numpy(), kv)
+    if gqa:
+        got = selected_attention(q.to(dev), K.to(dev), V.to(dev), sel.to(dev), gqa=True)
+    else:
+        got = ref_api(q.to(dev), K.to(dev), V.to(dev), sel.to(dev))
+    assert got.dtype == dt and tuple(got.shape) == (Hq, D)
+    tol = {torch.float32: 1e-5, torch.float16: 1e-3, torch.bfloat16: 8e-3}[dt]
+    g = got.double().cpu().numpy()
+    for h in range(Hq):
+        assert np.linalg.norm(g[h] - want[h]) <= tol * np.linalg.norm(want[h]), h
