@@ -241,11 +241,13 @@ constexpr int kBoundUnrollF16 = 8;  // row groups of loads in flight per thread
 // the rows of one wave (64/G) are a multiple of H, so a lane's head is fixed
 // and its clamped query sums live in registers.  Same summation order as
 // bound_kernel.
+// out_p / out_off: head-major output goes to out[h * out_p + out_off + p]
+// (out_p = P, out_off = 0 for one sequence; the ragged kernel writes each
+// sequence's pages at its offset within the concatenated page axis).
 template <int G, bool HFIX>
-__global__ void __launch_bounds__(256)
-bound_f16_kernel(const void* q, int qdt, int group, const uint16_t* __restrict__ kmin,
-                 const uint16_t* __restrict__ kmax, int64_t P, int H, void* out, int odt,
-                 int head_major) {
+HKV_DEV void bound_f16_rows(const void* q, int qdt, int group, const uint16_t* __restrict__ kmin,
+                            const uint16_t* __restrict__ kmax, int64_t P, int H, void* out, int odt,
+                            int head_major, int64_t out_p, int64_t out_off) {
   constexpr int D = 8 * G;
   constexpr int RB = 256 / G;  // rows per block per step
   extern __shared__ float qs[];  // [2][H][D]
@@ -311,12 +313,42 @@ bound_f16_kernel(const void* q, int qdt, int group, const uint16_t* __restrict__
       ns = row_reduce(ns, G);
       if (r < nrows && c == 0) {
         const float v = __fadd_rn(__fadd_rn(ps, ns), 0.0f);
-        const int64_t o = head_major ? (int64_t)h * P + p : r;
+        const int64_t o = head_major ? (int64_t)h * out_p + out_off + p : out_off * H + r;
         if (odt == HKV_DT_F16) ((uint16_t*)out)[o] = f2h(v);
         else ((float*)out)[o] = v;
       }
     }
   }
+}
+
+template <int G, bool HFIX>
+__global__ void __launch_bounds__(256)
+bound_f16_kernel(const void* q, int qdt, int group, const uint16_t* __restrict__ kmin,
+                 const uint16_t* __restrict__ kmax, int64_t P, int H, void* out, int odt,
+                 int head_major) {
+  bound_f16_rows<G, HFIX>(q, qdt, group, kmin, kmax, P, H, out, odt, head_major, P, 0);
+}
+
+// Ragged batch: sequence s = blockIdx.y owns pages [off[s], off[s+1]) of the
+// concatenated statistics and query q + s * q_bytes; scores head-major over
+// the concatenated page axis, (H, off[nseg]).
+constexpr int kMaxSeqs = 64;
+struct Segs {
+  int64_t off[kMaxSeqs + 1];
+  int64_t k[kMaxSeqs];
+  int64_t out_off[kMaxSeqs + 1];
+  int nseg;
+};
+
+template <int G, bool HFIX>
+__global__ void __launch_bounds__(256)
+bound_f16_ragged_kernel(const char* q, int64_t q_bytes, int qdt, int group,
+                        const uint16_t* __restrict__ kmin, const uint16_t* __restrict__ kmax, int H,
+                        float* out, const Segs segs) {
+  const int sq = blockIdx.y;
+  const int64_t o0 = segs.off[sq], P = segs.off[sq + 1] - o0;
+  bound_f16_rows<G, HFIX>(q + sq * q_bytes, qdt, group, kmin + o0 * H * (8 * G),
+                          kmax + o0 * H * (8 * G), P, H, out, HKV_DT_F32, 1, segs.off[segs.nseg], o0);
 }
 
 // --------------------------------------------------------- a10: top-K
@@ -687,6 +719,22 @@ topk_kernel(Col col0, int64_t P, int H, int64_t s, int64_t keff, int64_t* out) {
   select_any<KPT>(col, P, s, keff, out + h, H, sh);
 }
 
+// Ragged batch: block (h, s) selects over pages [off[s], off[s+1]) of column h
+// of the head-major scores (H, off[nseg]) with sinks and k[s]; the indices
+// (local to the sequence) go to rows out_off[s] .. of out (rows, H).
+template <int KPT>
+__global__ void __launch_bounds__(kSelThreads)
+topk_ragged_kernel(const float* scores, int H, int64_t sinks, int64_t* out, const Segs segs) {
+  __shared__ SelShared sh;
+  const int h = blockIdx.x, sq = blockIdx.y;
+  const int64_t o0 = segs.off[sq], P = segs.off[sq + 1] - o0;
+  const int64_t s = sinks < 0 ? 0 : (sinks > P ? P : sinks);
+  const int64_t k = segs.k[sq];
+  const int64_t keff = k < 0 ? 0 : (k > P - s ? P - s : k);
+  ColumnF32 col{scores + (int64_t)h * segs.off[segs.nseg] + o0, 1, 0};
+  select_any<KPT>(col, P, s, keff, out + segs.out_off[sq] * H + h, H, sh);
+}
+
 int num_cus() {
   static int n = 0;
   if (!n) {
@@ -969,6 +1017,83 @@ extern "C" int hkv_quest_select_blocks(const void* q, int q_dtype, int H, const 
                        sel, nsel, used_block_ids, NU, flags, num_blocks);
   hipLaunchKernelGGL(compact_blocks_kernel, dim3(1), dim3(kSelThreads), 0, st, flags, num_blocks,
                      block_size, out_ids, out_first_pos, n_selected);
+  HKV_CHECK_LAUNCH();
+  return HKV_OK;
+}
+
+extern "C" int hkv_quest_select_ragged(const void* q, int q_dtype, int B, int Hq, const void* kmin,
+                                       const void* kmax, int k_dtype, int H, int D,
+                                       const int64_t* page_offsets, const int64_t* top_k,
+                                       int64_t sink_pages, float* scores, int64_t* out,
+                                       int64_t* out_offsets, void* stream) {
+  if (B < 1 || B > kMaxSeqs) return HKV_ERR_SHAPE;
+  if (!page_offsets || !top_k || !out_offsets) return HKV_ERR_ARG;
+  if (q_dtype != HKV_DT_F16 && q_dtype != HKV_DT_F32 && q_dtype != HKV_DT_BF16) return HKV_ERR_DTYPE;
+  if (k_dtype != HKV_DT_F16) return HKV_ERR_DTYPE;
+  if (H < 1 || Hq < H || Hq % H || D < 8 || D % 8 || D > 512) return HKV_ERR_SHAPE;
+  const int G = D / 8;
+  if (G & (G - 1)) return HKV_ERR_SHAPE;
+  Segs sg;
+  sg.nseg = B;
+  int64_t maxn = 0;
+  if (page_offsets[0] != 0) return HKV_ERR_ARG;
+  out_offsets[0] = 0;
+  for (int b = 0; b < B; ++b) {
+    const int64_t P = page_offsets[b + 1] - page_offsets[b];
+    if (P < 0) return HKV_ERR_ARG;
+    sg.off[b] = page_offsets[b];
+    sg.k[b] = top_k[b];
+    const int64_t s = sink_pages < 0 ? 0 : (sink_pages > P ? P : sink_pages);
+    const int64_t keff = top_k[b] < 0 ? 0 : (top_k[b] > P - s ? P - s : top_k[b]);
+    out_offsets[b + 1] = out_offsets[b] + s + keff;
+    maxn = std::max<int64_t>(maxn, P - s);
+  }
+  sg.off[B] = page_offsets[B];
+  for (int b = 0; b <= B; ++b) sg.out_off[b] = out_offsets[b];
+  const int64_t Ptot = page_offsets[B];
+  if (Ptot == 0) return HKV_OK;
+  if (!q || !kmin || !kmax || !scores || (out_offsets[B] > 0 && !out)) return HKV_ERR_ARG;
+  if (((uintptr_t)kmin | (uintptr_t)kmax) & 15u) return HKV_ERR_ARG;
+  hipStream_t st = (hipStream_t)stream;
+  const size_t lds = sizeof(float) * 2 * H * D;
+  if (lds > 64 * 1024) return HKV_ERR_SHAPE;
+  // blocks per sequence: enough for the longest one to fill the chip with B sequences
+  int64_t maxP = 0;
+  for (int b = 0; b < B; ++b) maxP = std::max<int64_t>(maxP, page_offsets[b + 1] - page_offsets[b]);
+  const int64_t span = (int64_t)(256 / G) * kBoundUnrollF16;
+  const int64_t want = std::max<int64_t>(1, ((int64_t)num_cus() * 8 + B - 1) / B);
+  const unsigned gx = (unsigned)std::max<int64_t>(1, std::min<int64_t>((maxP * H + span - 1) / span, want));
+  const int64_t q_bytes = (int64_t)Hq * D * (q_dtype == HKV_DT_F32 ? 4 : 2);
+  const bool hfix = (64 / G) % H == 0;
+  auto mn = (const uint16_t*)kmin;
+  auto mx = (const uint16_t*)kmax;
+  const int group = Hq / H;
+#define HKV_RB(GG)                                                                                \
+  if (hfix)                                                                                       \
+    hipLaunchKernelGGL((bound_f16_ragged_kernel<GG, true>), dim3(gx, B), dim3(256), lds, st,      \
+                       (const char*)q, q_bytes, q_dtype, group, mn, mx, H, scores, sg);           \
+  else                                                                                            \
+    hipLaunchKernelGGL((bound_f16_ragged_kernel<GG, false>), dim3(gx, B), dim3(256), lds, st,     \
+                       (const char*)q, q_bytes, q_dtype, group, mn, mx, H, scores, sg);
+  switch (G) {
+    case 1: HKV_RB(1) break;
+    case 2: HKV_RB(2) break;
+    case 4: HKV_RB(4) break;
+    case 8: HKV_RB(8) break;
+    case 16: HKV_RB(16) break;
+    case 32: HKV_RB(32) break;
+    default: HKV_RB(64) break;
+  }
+#undef HKV_RB
+  HKV_CHECK_LAUNCH();
+  if (out_offsets[B] == 0) return HKV_OK;
+  const int kpt = kpt_for(maxn);
+  switch (kpt) {
+    case 4: hipLaunchKernelGGL((topk_ragged_kernel<4>), dim3(H, B), dim3(kSelThreads), 0, st, scores, H, sink_pages, out, sg); break;
+    case 16: hipLaunchKernelGGL((topk_ragged_kernel<16>), dim3(H, B), dim3(kSelThreads), 0, st, scores, H, sink_pages, out, sg); break;
+    case 64: hipLaunchKernelGGL((topk_ragged_kernel<64>), dim3(H, B), dim3(kSelThreads), 0, st, scores, H, sink_pages, out, sg); break;
+    default: hipLaunchKernelGGL((topk_ragged_kernel<0>), dim3(H, B), dim3(kSelThreads), 0, st, scores, H, sink_pages, out, sg); break;
+  }
   HKV_CHECK_LAUNCH();
   return HKV_OK;
 }

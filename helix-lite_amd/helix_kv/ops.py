@@ -464,3 +464,85 @@ def selected_attention(query: torch.Tensor, K_pages: torch.Tensor, V_pages: torc
         ws.numel(), N.stream_of(q))
     N.check(st, "hkv_selected_attention", ValueError)
     return out
+
+
+# ------------------------------------------------------------ ragged batches
+
+def _ragged_rows(page_offsets, top_k, sink_pages: int) -> list[int]:
+    out = [0]
+    for b in range(len(page_offsets) - 1):
+        P = int(page_offsets[b + 1]) - int(page_offsets[b])
+        s = max(0, min(int(sink_pages), P))
+        keff = max(0, min(int(top_k[b]), P - s))
+        out.append(out[-1] + s + keff)
+    return out
+
+
+def quest_select_ragged(query: torch.Tensor, K_min: torch.Tensor, K_max: torch.Tensor,
+                        page_offsets, top_k, sink_pages: int, *,
+                        scores: torch.Tensor | None = None):
+    """Quest selection for a ragged batch of B decode queries (hkv_quest_select_ragged).
+
+    query (B, Hq, D); K_min / K_max (P_total, H, D) fp16, sequence b owning
+    pages page_offsets[b] .. page_offsets[b+1]-1; top_k an int or one per
+    sequence.  Returns (sel (rows, H) int64 local page indices, ascending per
+    sequence and head; out_offsets (B+1 ints): rows of sequence b are
+    out_offsets[b] .. out_offsets[b+1]-1; scores (H, P_total) fp32)."""
+    import ctypes
+
+    N.require_gpu(query, K_min, K_max)
+    if query.dim() != 3 or K_min.dim() != 3 or K_min.shape != K_max.shape:
+        raise ValueError("query should be (B, Hq, D) and K_min/K_max (P_total, H, D)")
+    B, Hq, D = (int(x) for x in query.shape)
+    Ptot, H, Dk = (int(x) for x in K_min.shape)
+    offs = [int(x) for x in page_offsets]
+    if len(offs) != B + 1 or offs[0] != 0 or offs[-1] != Ptot or Dk != D or Hq % H:
+        raise ValueError("page_offsets must be (B+1,) from 0 to P_total; shapes must agree")
+    ks = [int(top_k)] * B if isinstance(top_k, int) else [int(x) for x in top_k]
+    if len(ks) != B:
+        raise ValueError("one top_k per sequence")
+    rows = _ragged_rows(offs, ks, sink_pages)
+    kmin = K_min.contiguous()
+    kmax = K_max.to(kmin.dtype).contiguous()
+    q = query.contiguous()
+    out = torch.empty((max(rows[-1], 1), H), dtype=torch.int64, device=q.device)
+    if scores is None:
+        scores = torch.empty((H, max(Ptot, 1)), dtype=torch.float32, device=q.device)
+    c_off = (ctypes.c_int64 * (B + 1))(*offs)
+    c_k = (ctypes.c_int64 * B)(*ks)
+    c_out = (ctypes.c_int64 * (B + 1))()
+    st = N.lib().hkv_quest_select_ragged(N.ptr(q), N.dtype_code(q), B, Hq, N.ptr(kmin), N.ptr(kmax),
+                                         N.dtype_code(kmin), H, D, c_off, c_k, int(sink_pages),
+                                         N.ptr(scores), N.ptr(out), c_out, N.stream_of(q))
+    N.check(st, "hkv_quest_select_ragged", ValueError)
+    assert list(c_out) == rows
+    return out[: rows[-1]], rows, scores[:, :Ptot]
+
+
+def nuq_gather_pages(cc: CompactCodes, t: NuqLayerTables, sel: torch.Tensor, page_offsets,
+                     out_offsets, *, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Gather + dequantise the selected (page, head) pairs of a compact K or V
+    of B concatenated sequences into (rows, 16, H, 128) fp16
+    (hkv_nuq_gather_pages); sel (rows, H) holds pages local to each sequence,
+    as quest_select_ragged returns them with out_offsets."""
+    import ctypes
+
+    N.require_gpu(cc.packed, sel)
+    T, H, D = cc.shape
+    B = len(page_offsets) - 1
+    rows = int(out_offsets[-1])
+    if sel.dim() != 2 or int(sel.shape[1]) != H or int(sel.shape[0]) < rows:
+        raise ValueError(f"sel should be ({rows}, {H})")
+    if out is None:
+        out = torch.empty((rows, 16, H, D), dtype=torch.float16, device=cc.packed.device)
+    if tuple(out.shape) != (rows, 16, H, D) or out.dtype != torch.float16 or not out.is_contiguous():
+        raise AssertionError(f"out must be contiguous ({rows}, 16, {H}, {D}) fp16")
+    s = sel.to(torch.int64).contiguous()
+    c_off = (ctypes.c_int64 * (B + 1))(*[int(x) for x in page_offsets])
+    c_out = (ctypes.c_int64 * (B + 1))(*[int(x) for x in out_offsets])
+    st = N.lib().hkv_nuq_gather_pages(
+        N.ptr(cc.packed), N.ptr(cc.row_ptr), N.ptr(cc.col), N.ptr(cc.val),
+        min(int(cc.col.numel()), int(cc.val.numel())), T, H, D, cc.bits, t.struct(), 16, B, c_off,
+        c_out, N.ptr(s), N.ptr(out), N.stream_of(out))
+    N.check(st, "hkv_nuq_gather_pages", AssertionError)
+    return out

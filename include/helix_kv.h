@@ -303,6 +303,45 @@ int hkv_decode_attn(const void *q, int Hq, int H, int D, int64_t T,
                     size_t workspace_bytes, void *stream);
 
 /*
+ * Ragged batched Quest selection: B <= 64 sequences, sequence b owning pages
+ * [page_offsets[b], page_offsets[b+1]) of the concatenated statistics kmin /
+ * kmax (P_total, H, D) fp16 (D % 8 == 0, D/8 a power of two), with its own
+ * decode query q[b] (Hq, D).  Per sequence and KV head: the group-summed bound
+ * (as hkv_quest_select) and topk_pages_with_sinks (src/quest/reference.py:
+ * 96-133) with the first sink_pages pages as sinks and top_k[b] more, indices
+ * local to the sequence, ascending.  page_offsets (B+1, page_offsets[0] == 0)
+ * and top_k (B) are HOST arrays; out_offsets (B+1, host) receives the row
+ * offsets of each sequence's selection in out (rows, H) int64.  scores (H,
+ * P_total) fp32 receives the bounds.  One bound launch over every sequence and
+ * one top-K launch of H x B blocks.  (The reference selects per sequence,
+ * src/kvquant/quest_selector.py:38-90; this is the batched form.)
+ */
+int hkv_quest_select_ragged(const void *q, int q_dtype, int B, int Hq, const void *kmin,
+                            const void *kmax, int k_dtype, int H, int D,
+                            const int64_t *page_offsets, const int64_t *top_k, int64_t sink_pages,
+                            float *scores, int64_t *out, int64_t *out_offsets, void *stream);
+
+/*
+ * Gather + dequantise the selected pages of a compact-format K or V (as
+ * hkv_nuq_pack_compact writes it over the concatenated tokens of B <= 64
+ * sequences; page p = tokens [16p, 16p+16)) into staging (rows, 16, H, 128)
+ * fp16, per KV head: staging[i, j, h] = token (page_offsets[b] + sel[i][h])*16
+ * + j of head h, for row i of sequence b (rows out_offsets[b] ..
+ * out_offsets[b+1]-1).  Per-token (V) scales use row min(sel[i][h]*16 + j,
+ * rows - 1), the position within the sequence (scales->positions and
+ * pos_offset are not used); pages outside the sequence give zero rows.  The
+ * compact-format, per-head counterpart of unpack_to_staging
+ * (src/kvquant/compact_pool.py:492-537).  page_offsets / out_offsets are HOST
+ * arrays (out_offsets as hkv_quest_select_ragged returns them); sel (rows, H)
+ * int64 device.  D = 128, page_size = 16; packed and out 16-byte aligned.
+ */
+int hkv_nuq_gather_pages(const void *packed, const int32_t *row_ptr, const uint8_t *col,
+                         const uint16_t *val, int64_t capacity, int64_t T, int H, int D, int bits,
+                         const hkv_nuq_scales *scales, int page_size, int B,
+                         const int64_t *page_offsets, const int64_t *out_offsets,
+                         const int64_t *sel, void *out, void *stream);
+
+/*
  * Attention of each query head over its selected dense pages: the drop-in for
  * selected_attention (src/quest/reference.py:136-168).  q (Hq, D); k_pages
  * (P, page_size, Hk, D) and v_pages (P, page_size, Hv, Dv) in kv_dtype; sel

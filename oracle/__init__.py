@@ -363,6 +363,52 @@ def selected_attention(query, K_pages, V_pages, page_indices, kv_of_head, num_to
     return out
 
 
+def select_ragged(query, kmin, kmax, page_offsets, top_k, sink_pages: int):
+    """Per-sequence Quest selection over a ragged batch: sequence b owns pages
+    [page_offsets[b], page_offsets[b+1]) of the statistics and query query[b]
+    (Hq, D); group-summed bound + topk_sinks per sequence (the per-sequence
+    restatement of src/quest/reference.py:59-133, src/kvquant/quest_selector.py:
+    64-78).  Returns (sel (rows, H) local indices, out_offsets (B+1,),
+    scores (H, P_total))."""
+    q = _f32(query)
+    mn, mx = _f32(kmin), _f32(kmax)
+    B, Hq, D = q.shape
+    Ptot, H, _ = mn.shape
+    sels, outs, scores = [], [0], np.zeros((H, Ptot), np.float32)
+    for b in range(B):
+        o0, o1 = int(page_offsets[b]), int(page_offsets[b + 1])
+        if o1 > o0:
+            bound = page_bound_group(q[b], mn[o0:o1], mx[o0:o1], Hq // H)
+            scores[:, o0:o1] = bound.T
+            sel = topk_sinks(bound, int(top_k[b]), sink_pages)
+        else:
+            sel = np.zeros((0, H), np.int64)
+        sels.append(sel)
+        outs.append(outs[-1] + sel.shape[0])
+    return np.concatenate(sels), np.array(outs, np.int64), scores
+
+
+def gather_pages(deq, sel, page_offsets, out_offsets, page_size: int = 16):
+    """staging[i, j, h] = deq[(page_offsets[b] + sel[i, h]) * page_size + j, h]
+    for row i of sequence b, zero rows for pages outside the sequence: the
+    per-head, compact-format counterpart of unpack_to_staging
+    (src/kvquant/compact_pool.py:492-537).  deq (T, H, D) fp16 bits."""
+    d = np.asarray(deq, np.uint16)
+    T, H, D = d.shape
+    sel = np.asarray(sel, np.int64)
+    rows = int(out_offsets[-1])
+    out = np.zeros((rows, page_size, H, D), np.uint16)
+    for b in range(len(page_offsets) - 1):
+        P = int(page_offsets[b + 1]) - int(page_offsets[b])
+        for i in range(int(out_offsets[b]), int(out_offsets[b + 1])):
+            for h in range(H):
+                lp = sel[i, h]
+                if 0 <= lp < P:
+                    t0 = (int(page_offsets[b]) + lp) * page_size
+                    out[i, :, h] = d[t0:t0 + page_size, h]
+    return out
+
+
 def ordered_min_max(vals, axis):
     """min / max of fp32 values along ``axis`` with -0 ordered below +0 (the
     pool statistics' order), via the monotone integer key of each value."""

@@ -198,3 +198,56 @@ def test_attention_exclusion_and_invalid_ids():
     assert np.array_equal(a, b)
     # a selection with no valid token leaves the head at zero
     assert not O.selected_attention(q, K, V, np.array([[3]]), lambda h: 0, num_tokens=12).any()
+
+
+def test_select_ragged_known_answers():
+    """Each sequence of a ragged batch selects from its own pages only, with
+    local indices: a page planted with large keys in each sequence is chosen
+    there and nowhere else; sinks are each sequence's first pages; an empty
+    sequence contributes no rows."""
+    H, D, group = 2, 16, 3
+    lens = [6, 0, 9, 4]
+    offs = np.concatenate([[0], np.cumsum(lens)])
+    Ptot = offs[-1]
+    mn = np.zeros((Ptot, H, D), np.float32)
+    mx = np.zeros((Ptot, H, D), np.float32)
+    planted = [4, None, 7, 2]
+    for b, p in enumerate(planted):
+        if p is not None:
+            mx[offs[b] + p] = 5.0
+            mn[offs[b] + p] = 4.0
+    q = np.ones((len(lens), H * group, D), np.float32)
+    sel, outs, scores = O.select_ragged(q, mn, mx, offs, [1, 1, 1, 1], 2)
+    assert outs.tolist() == [0, 3, 3, 6, 9]
+    assert sel[0:3, 0].tolist() == [0, 1, 4] and sel[3:6, 1].tolist() == [0, 1, 7]
+    assert sel[6:9, 0].tolist() == [0, 1, 2]
+    assert scores.shape == (H, Ptot) and scores[0, offs[2] + 7] == 5.0 * D * group
+
+
+def test_select_ragged_single_sequence_is_plain_select():
+    P, H, D, group = 300, 4, 32, 7
+    mn = RNG.standard_normal((P, H, D)).astype(np.float16).astype(np.float32)
+    mx = mn + np.abs(RNG.standard_normal((P, H, D))).astype(np.float16).astype(np.float32)
+    q = RNG.standard_normal((1, H * group, D)).astype(np.float32)
+    sel, outs, scores = O.select_ragged(q, mn, mx, [0, P], [70], 4)
+    b = O.page_bound_group(q[0], mn, mx, group)
+    assert np.array_equal(scores, b.T) and np.array_equal(sel, O.topk_sinks(b, 70, 4))
+
+
+def test_gather_pages_known_answer():
+    """Tokens carry their own index, so the gathered staging spells out which
+    token of which head landed where; ids outside a sequence give zeros."""
+    H, D, S = 2, 8, 16
+    lens = [3, 2]
+    offs = [0, 3, 5]
+    T = 5 * S
+    deq = np.zeros((T, H, D), np.uint16)
+    for t in range(T):
+        for h in range(H):
+            deq[t, h] = t * 10 + h
+    sel = np.array([[0, 2], [2, -1], [1, 0], [5, 1]], np.int64)  # seq 0: rows 0-1, seq 1: rows 2-3
+    st = O.gather_pages(deq, sel, offs, [0, 2, 4], S)
+    assert st[0, 3, 1, 0] == (2 * S + 3) * 10 + 1          # seq 0, page 2, slot 3, head 1
+    assert not st[1, :, 1].any()                            # id -1
+    assert st[2, 0, 0, 0] == ((3 + 1) * S) * 10             # seq 1 page 1 = global page 4
+    assert not st[3, :, 0].any() and st[3, 5, 1, 0] == ((3 + 1) * S + 5) * 10 + 1
