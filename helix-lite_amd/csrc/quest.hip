@@ -103,6 +103,14 @@ page_stats_generic(const T* __restrict__ K, int64_t P, int S, int H, int D, T* _
 
 // --------------------------------------------------------------- a9: bound
 
+// Ordered key: NaN above +inf, -0 == +0.
+HKV_DEV uint32_t ukey(float f) {
+  if (__builtin_isnan(f)) return 0xffffffffu;
+  if (f == 0.0f) f = 0.0f;
+  const uint32_t b = __builtin_bit_cast(uint32_t, f);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
 HKV_DEV float clamp_pos(float q) { return q < 0.0f ? 0.0f : q; }
 HKV_DEV float clamp_neg(float q) { return q > 0.0f ? 0.0f : q; }
 
@@ -149,6 +157,24 @@ HKV_DEV void chunk_sums(const KT* __restrict__ mn_row, const KT* __restrict__ mx
 // Butterfly over n lanes (n | 64, lanes of a row contiguous and aligned).
 HKV_DEV float row_reduce(float v, int n) {
   for (int off = n >> 1; off >= 1; off >>= 1) v = __fadd_rn(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// The same butterfly as row_reduce(v, 16) on DPP moves instead of LDS
+// permutes: row_ror:8 is xor 8; after it the values are symmetric under xor 8,
+// so row_ror:4 reads the xor-4 partner's value; quad_perm gives xor 2 and
+// xor 1.  Each step adds the same two operands as the xor butterfly (IEEE
+// addition is commutative), so the sum is bit-identical.
+template <int CTRL>
+HKV_DEV float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                               0xf, 0xf, false));
+}
+HKV_DEV float row16_reduce(float v) {
+  v = __fadd_rn(v, dpp_f<0x128>(v));  // row_ror:8
+  v = __fadd_rn(v, dpp_f<0x124>(v));  // row_ror:4
+  v = __fadd_rn(v, dpp_f<0x4e>(v));   // quad_perm [2,3,0,1]
+  v = __fadd_rn(v, dpp_f<0xb1>(v));   // quad_perm [1,0,3,2]
   return v;
 }
 
@@ -234,7 +260,8 @@ bound_kernel(const void* q, int qdt, int group, const KT* __restrict__ kmin,
   }
 }
 
-constexpr int kBoundUnrollF16 = 8;  // row groups of loads in flight per thread
+constexpr int kMaxMMHeads = 64;  // heads with per-block key ranges (multi-block top-K)
+constexpr int kBoundUnrollF16 = 4;  // row groups per step (two steps of loads in flight)
 
 // fp16 stats with D = 8*G (G a power of two, G <= 64): lane c of a row owns
 // channels [8c, 8c+8) and loads them with one 128-bit load per array.  HFIX:
@@ -247,18 +274,44 @@ constexpr int kBoundUnrollF16 = 8;  // row groups of loads in flight per thread
 template <int G, bool HFIX>
 HKV_DEV void bound_f16_rows(const void* q, int qdt, int group, const uint16_t* __restrict__ kmin,
                             const uint16_t* __restrict__ kmax, int64_t P, int H, void* out, int odt,
-                            int head_major, int64_t out_p, int64_t out_off) {
+                            int head_major, int64_t out_p, int64_t out_off,
+                            uint2* __restrict__ mm = nullptr) {
   constexpr int D = 8 * G;
-  constexpr int RB = 256 / G;  // rows per block per step
+  constexpr int RB = 256 / G;  // rows per block per row group
+  constexpr int U = kBoundUnrollF16;
+  constexpr int span = RB * U;  // rows per block per step
   extern __shared__ float qs[];  // [2][H][D]
   const int c = threadIdx.x % G, rl = threadIdx.x / G;
-  const int64_t nrows = P * H;
+  // 32-bit row arithmetic (P * H < 2^31 is checked by the host); with HFIX
+  // the page of a row advances by a constant per step (H divides RB), so no
+  // division is needed in the loop.
+  const int nr = (int)(P * H);
+  // No rows (an empty sequence of a ragged batch): nothing to load.  The loads
+  // below clamp to row nr - 1, which must exist.  Uniform over the block.
+  if (nr <= 0) return;
+  const int step = gridDim.x * span;
+  uint4 a0[U], b0[U], a1[U], b1[U];
+  // Loads are unconditional, rows past the end clamped to the last row (their
+  // results are not written): a fixed number of loads per step lets the
+  // compiler wait for exactly one step's loads while the next step's are in
+  // flight.
+  auto load = [&](int r0, uint4 (&a)[U], uint4 (&b)[U]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      int r = r0 + u * RB + rl;
+      r = r < nr ? r : nr - 1;
+      a[u] = reinterpret_cast<const uint4*>(kmin + (uint32_t)r * D)[c];
+      b[u] = reinterpret_cast<const uint4*>(kmax + (uint32_t)r * D)[c];
+    }
+  };
+  int r0 = blockIdx.x * span;
+  load(r0, a0, b0);  // in flight while the query is staged
   // the block's clamped, group-summed query, [2][H][D] in LDS
   for (int i = threadIdx.x; i < H * D; i += 256) {
-    float a, b;
-    group_q(q, qdt, i / D, group, D, i % D, a, b);
-    qs[i] = a;
-    qs[H * D + i] = b;
+    float qa, qb;
+    group_q(q, qdt, i / D, group, D, i % D, qa, qb);
+    qs[i] = qa;
+    qs[H * D + i] = qb;
   }
   __syncthreads();
   float qp[8], qn[8];
@@ -270,29 +323,18 @@ HKV_DEV void bound_f16_rows(const void* q, int qdt, int group, const uint16_t* _
       qn[i] = qs[H * D + h * D + 8 * c + i];
     }
   }
-  const int64_t span = (int64_t)RB * kBoundUnrollF16;
-  for (int64_t r0 = (int64_t)blockIdx.x * span; r0 < nrows; r0 += (int64_t)gridDim.x * span) {
-    uint4 a[kBoundUnrollF16], b[kBoundUnrollF16];
+  uint32_t kmn_t = 0xffffffffu, kmx_t = 0u;  // key range of this thread's rows (HFIX: one head)
+  auto compute = [&](int rs, int pb, const uint4 (&a)[U], const uint4 (&b)[U]) {
 #pragma unroll
-    for (int u = 0; u < kBoundUnrollF16; ++u) {
-      const int64_t r = r0 + (int64_t)u * RB + rl;
-      a[u] = b[u] = make_uint4(0u, 0u, 0u, 0u);
-      if (r < nrows) {
-        a[u] = reinterpret_cast<const uint4*>(kmin + r * D)[c];
-        b[u] = reinterpret_cast<const uint4*>(kmax + r * D)[c];
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < kBoundUnrollF16; ++u) {
-      const int64_t r = r0 + (int64_t)u * RB + rl;
-      int h;
-      int64_t p;
+    for (int u = 0; u < U; ++u) {
+      const int r = rs + u * RB + rl;
+      int h, p;
       if constexpr (HFIX) {
         h = rl % H;
-        p = (r0 + (int64_t)u * RB) / H + rl / H;
+        p = pb + u * (RB / H) + rl / H;
       } else {
         p = r / H;
-        h = (int)(r - p * H);
+        h = r - p * H;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           qp[i] = qs[h * D + 8 * c + i];
@@ -309,14 +351,55 @@ HKV_DEV void bound_f16_rows(const void* q, int qdt, int group, const uint16_t* _
         ps = __fadd_rn(ps, __fmul_rn(qp[i], kmx));
         ns = __fadd_rn(ns, __fmul_rn(qn[i], kmn));
       }
-      ps = row_reduce(ps, G);
-      ns = row_reduce(ns, G);
-      if (r < nrows && c == 0) {
+      if constexpr (G == 16) {
+        ps = row16_reduce(ps);
+        ns = row16_reduce(ns);
+      } else {
+        ps = row_reduce(ps, G);
+        ns = row_reduce(ns, G);
+      }
+      if (r < nr && c == 0) {
         const float v = __fadd_rn(__fadd_rn(ps, ns), 0.0f);
         const int64_t o = head_major ? (int64_t)h * out_p + out_off + p : out_off * H + r;
         if (odt == HKV_DT_F16) ((uint16_t*)out)[o] = f2h(v);
         else ((float*)out)[o] = v;
+        if constexpr (HFIX) {
+          const uint32_t kk = ukey(v);
+          kmn_t = kk < kmn_t ? kk : kmn_t;
+          kmx_t = kk > kmx_t ? kk : kmx_t;
+        }
       }
+    }
+  };
+  // two register buffers: the loads of the next step are in flight while the
+  // current one is computed (unrolled by 2 so no pending load is copied)
+  int pb = HFIX ? r0 / H : 0;
+  const int pstep = HFIX ? step / H : 0;
+  while (r0 < nr) {
+    int r1 = r0 + step;
+    load(r1, a1, b1);  // past the end: clamped, harmless
+    compute(r0, pb, a0, b0);
+    r0 = r1;
+    pb += pstep;
+    if (r0 >= nr) break;
+    r1 = r0 + step;
+    load(r1, a0, b0);
+    compute(r0, pb, a1, b1);
+    r0 = r1;
+    pb += pstep;
+  }
+  if constexpr (HFIX) {
+    // per-block key range of each head for the multi-block top-K
+    if (mm) {
+      __shared__ uint32_t s_mn[kMaxMMHeads], s_mx[kMaxMMHeads];
+      for (int i = threadIdx.x; i < H; i += 256) { s_mn[i] = 0xffffffffu; s_mx[i] = 0u; }
+      __syncthreads();
+      if (c == 0) {
+        atomicMin(&s_mn[rl % H], kmn_t);
+        atomicMax(&s_mx[rl % H], kmx_t);
+      }
+      __syncthreads();
+      for (int i = threadIdx.x; i < H; i += 256) mm[(int64_t)blockIdx.x * H + i] = make_uint2(s_mn[i], s_mx[i]);
     }
   }
 }
@@ -325,8 +408,8 @@ template <int G, bool HFIX>
 __global__ void __launch_bounds__(256)
 bound_f16_kernel(const void* q, int qdt, int group, const uint16_t* __restrict__ kmin,
                  const uint16_t* __restrict__ kmax, int64_t P, int H, void* out, int odt,
-                 int head_major) {
-  bound_f16_rows<G, HFIX>(q, qdt, group, kmin, kmax, P, H, out, odt, head_major, P, 0);
+                 int head_major, uint2* mm) {
+  bound_f16_rows<G, HFIX>(q, qdt, group, kmin, kmax, P, H, out, odt, head_major, P, 0, mm);
 }
 
 // Ragged batch: sequence s = blockIdx.y owns pages [off[s], off[s+1]) of the
@@ -357,13 +440,6 @@ constexpr int kSelThreads = 1024;
 constexpr int kSelWaves = kSelThreads / 64;
 constexpr int kBins = 2048;
 
-// Ordered key: NaN above +inf, -0 == +0.
-HKV_DEV uint32_t ukey(float f) {
-  if (__builtin_isnan(f)) return 0xffffffffu;
-  if (f == 0.0f) f = 0.0f;
-  const uint32_t b = __builtin_bit_cast(uint32_t, f);
-  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-}
 
 constexpr int kCand = 4096;  // keys of the first digit's bin kept in LDS
 
@@ -735,6 +811,351 @@ topk_ragged_kernel(const float* scores, int H, int64_t sinks, int64_t* out, cons
   select_any<KPT>(col, P, s, keff, out + segs.out_off[sq] * H + h, H, sh);
 }
 
+// ------------------------------------------ multi-block top-K (large columns)
+//
+// One head's candidates [s, P) are split into NB slices of kMBThreads*KPT
+// consecutive pages, one block each, in two kernels (no block ever waits):
+//  topk_mb_hist: a block histograms its slice into 4096 bins of
+//    (key - kmn) >> sh, where kmn / kmx come from the bound kernel's per-block
+//    key ranges and sh makes the range fit; it stores the histogram and
+//    arrives at the head's counter.  The last block to arrive sums the
+//    histograms, finds the bin of the keff-th largest key, re-reads the head's
+//    keys, sorts that bin's keys (bitonic; ties to the lower page) and writes
+//    the threshold key T, how many keys equal to T are taken, and for every
+//    slice the output row of its first selected page and the number of
+//    T-equal keys before it.  It leaves the counter at zero for the next call.
+//    A bin of more than kMBCand keys falls back to the single-block selector.
+//  topk_mb_write: each block writes its slice's selected pages in page order.
+// Same result as select_column_regs: sinks, then the keff highest keys with
+// ties to the lower page, ascending.
+constexpr int kMBThreads = 1024;
+constexpr int kMBWaves = kMBThreads / 64;
+constexpr int kMBBins = 4096;
+constexpr int kMBCand = 4096;
+constexpr int kMBMaxSlices = 64;
+
+struct MBWork {
+  uint32_t* ctr;     // [H] arrival counters (zero between calls)
+  const uint2* mm;   // [nmm][H] (min key, max key) of the bound kernel's blocks
+  int nmm;
+  uint32_t* hist;    // [H][NB][kMBBins]
+  int* meta;         // [H][NB][2] (out row of the slice's first selected page, T-equal keys before it)
+  uint32_t* thr;     // [H][4] (T, T-equal keys taken, 1 = selection already written)
+};
+
+struct MBShared {
+  uint32_t hist[kMBBins];
+  unsigned long long cand[kMBCand];
+  uint32_t ncand;
+  uint32_t red[kMBWaves];
+  uint32_t bc[8];
+  int sl_gt[kMBMaxSlices], sl_eq[kMBMaxSlices];
+};
+
+HKV_DEV uint32_t mb_reduce(uint32_t v, int op, uint32_t* red) {  // op 0 min, 1 max, 2 sum
+  for (int o = 32; o >= 1; o >>= 1) {
+    const uint32_t y = __shfl_xor(v, o, 64);
+    v = op == 0 ? (y < v ? y : v) : op == 1 ? (y > v ? y : v) : v + y;
+  }
+  const int w = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  uint32_t r = red[0];
+  for (int i = 1; i < kMBWaves; ++i) {
+    const uint32_t y = red[i];
+    r = op == 0 ? (y < r ? y : r) : op == 1 ? (y > r ? y : r) : r + y;
+  }
+  return r;
+}
+
+// Exclusive prefix sum over the block in thread order; total in `total`.
+HKV_DEV uint32_t mb_excl_scan(uint32_t v, uint32_t* red, uint32_t& total) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  uint32_t x = v;
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  __syncthreads();
+  if (lane == 63) red[w] = x;
+  __syncthreads();
+  uint32_t before = 0, tot = 0;
+  for (int i = 0; i < kMBWaves; ++i) {
+    const uint32_t r = red[i];
+    before += i < w ? r : 0u;
+    tot += r;
+  }
+  total = tot;
+  return before + x - v;
+}
+
+template <int KPT>
+__global__ void __launch_bounds__(kMBThreads)
+topk_mb_hist(const float* scores, int64_t P, int64_t s, int64_t keff, int64_t* out, int H,
+             MBWork w) {
+  __shared__ MBShared sh;
+  __shared__ int s_last;
+  const int j = blockIdx.x, h = blockIdx.y, NB = gridDim.x, tid = threadIdx.x;
+  const int n = (int)(P - s);
+  const float* col = scores + (int64_t)h * P + s;  // candidate i is page s + i
+  constexpr int slice = kMBThreads * KPT;
+  // key range of the head (all pages, sinks included: a superset of the candidates')
+  uint32_t mn = 0xffffffffu, mx = 0u;
+  for (int b = tid; b < w.nmm; b += kMBThreads) {
+    const uint2 v = w.mm[(int64_t)b * H + h];
+    mn = v.x < mn ? v.x : mn;
+    mx = v.y > mx ? v.y : mx;
+  }
+  mn = mb_reduce(mn, 0, sh.red);
+  mx = mb_reduce(mx, 1, sh.red);
+  const uint32_t range = mx - mn;
+  const int wbits = range ? 32 - __builtin_clz(range) : 0;
+  const int sh1 = wbits > 12 ? wbits - 12 : 0;
+  for (int b = tid; b < kMBBins; b += kMBThreads) sh.hist[b] = 0u;
+  __syncthreads();
+  const int c0 = j * slice + tid * KPT;
+  // loads are unconditional (clamped index) so that all KPT are in flight at once
+  float kv[KPT];
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) kv[i] = col[c0 + i < n ? c0 + i : n - 1];
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) {
+    if (c0 + i < n) {
+      const uint32_t k = ukey(kv[i]);
+      const uint32_t b = k < mn ? 0u : (k - mn) >> sh1;
+      atomicAdd(&sh.hist[b < (uint32_t)kMBBins ? b : (uint32_t)(kMBBins - 1)], 1u);
+    }
+  }
+  __syncthreads();
+  uint32_t* gh = w.hist + ((int64_t)h * NB + j) * kMBBins;
+  for (int b = tid; b < kMBBins; b += kMBThreads) gh[b] = sh.hist[b];
+  __syncthreads();
+  if (tid == 0) {
+    __threadfence();  // release this slice's histogram
+    s_last = atomicAdd(&w.ctr[h], 1u) == (uint32_t)(NB - 1);
+  }
+  __syncthreads();
+  if (!s_last) return;
+  if (tid == 0) {
+    __threadfence();  // acquire every slice's histogram (one cache invalidation for the block)
+    atomicExch(&w.ctr[h], 0u);  // every slice has arrived: ready for the next call
+  }
+  __syncthreads();
+
+  // ---- last block of head h: the threshold
+  // Thread t sums bins t + 1024 k4 over the slices, keeping each slice's value
+  // (per-slice counts above the threshold bin come from them).
+  constexpr int KB = kMBBins / kMBThreads;  // bins per thread
+  const int NBc = NB < kMBMaxSlices ? NB : kMBMaxSlices;
+  uint32_t hv[KB][8];  // slices j0..j0+7 of the thread's bins (the last group kept)
+  for (int k4 = 0; k4 < KB; ++k4) sh.hist[k4 * kMBThreads + tid] = 0u;
+  for (int j0 = 0; j0 < NBc; j0 += 8) {
+#pragma unroll
+    for (int k4 = 0; k4 < KB; ++k4)
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int jj = j0 + u < NBc ? j0 + u : NBc - 1;
+        hv[k4][u] = w.hist[((int64_t)h * NB + jj) * kMBBins + k4 * kMBThreads + tid];
+      }
+#pragma unroll
+    for (int k4 = 0; k4 < KB; ++k4) {
+      uint32_t t = 0;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) t += j0 + u < NBc ? hv[k4][u] : 0u;
+      sh.hist[k4 * kMBThreads + tid] += t;
+    }
+  }
+  __syncthreads();
+  // bins high to low: thread t owns bins [4095 - 4t - 3, 4095 - 4t]
+  const uint32_t need = (uint32_t)keff;
+  uint32_t mine = 0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) mine += sh.hist[kMBBins - 1 - 4 * tid - k];
+  uint32_t tot;
+  uint32_t above = mb_excl_scan(mine, sh.red, tot);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int b = kMBBins - 1 - 4 * tid - k;
+    const uint32_t c = sh.hist[b];
+    if (above < need && above + c >= need) {
+      sh.bc[0] = (uint32_t)b;
+      sh.bc[1] = above;
+    }
+    above += c;
+  }
+  __syncthreads();
+  const uint32_t b1 = sh.bc[0], above1 = sh.bc[1], cnt1 = sh.hist[b1];
+  const uint32_t r = need - above1;  // 1 <= r <= cnt1
+  const uint32_t lo1 = mn + (b1 << sh1);
+  const uint32_t hi1 = lo1 + ((sh1 >= 32 ? 0xffffffffu : (1u << sh1)) - 1u);
+  if (cnt1 > (uint32_t)kMBCand) {
+    // a huge bin: the single-block selector over the whole column
+    __shared__ SelShared ssh;
+    ColumnF32 cc{scores + (int64_t)h * P, 1, 0};
+    select_column(cc, P, s, keff, out + h, H, ssh);
+    if (tid == 0) w.thr[h * 4 + 2] = 1u;
+    return;
+  }
+  for (int k = tid; k < kMBMaxSlices; k += kMBThreads) { sh.sl_gt[k] = 0; sh.sl_eq[k] = 0; }
+  if (tid == 0) sh.ncand = 0u;
+  __syncthreads();
+  // per-slice counts of keys in bins above b1
+  for (int j0 = 0; j0 < NBc; j0 += 8) {
+    if (j0 + 8 < NBc || j0 > 0) {  // more than 8 slices: reload this group
+#pragma unroll
+      for (int k4 = 0; k4 < KB; ++k4)
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int jj = j0 + u < NBc ? j0 + u : NBc - 1;
+          hv[k4][u] = w.hist[((int64_t)h * NB + jj) * kMBBins + k4 * kMBThreads + tid];
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      uint32_t c = 0;
+#pragma unroll
+      for (int k4 = 0; k4 < KB; ++k4) c += (uint32_t)(k4 * kMBThreads + tid) > b1 ? hv[k4][u] : 0u;
+      c = mb_reduce(c, 2, sh.red);
+      if (tid == 0 && j0 + u < NBc) sh.sl_gt[j0 + u] = (int)c;
+    }
+  }
+  // candidates: the keys of bin b1 (re-read, the next 16 in flight while 16 are checked)
+  const int per = (n + kMBThreads - 1) / kMBThreads;
+  constexpr int RU = 16;
+  uint32_t ka[RU], kb[RU];
+  auto load_keys = [&](int i0, uint32_t (&kk)[RU]) {
+#pragma unroll
+    for (int u = 0; u < RU; ++u) {
+      const int idx = (i0 + u) * kMBThreads + tid;
+      kk[u] = ukey(col[idx < n ? idx : n - 1]);  // validity is checked where kk is used
+    }
+  };
+  auto scan_keys = [&](int i0, const uint32_t (&kk)[RU]) {
+#pragma unroll
+    for (int u = 0; u < RU; ++u) {
+      const int idx = (i0 + u) * kMBThreads + tid;
+      const uint32_t k = kk[u];
+      if (idx < n && k >= lo1 && k <= hi1) {
+        const uint32_t slot = atomicAdd(&sh.ncand, 1u);
+        if (slot < (uint32_t)kMBCand)
+          sh.cand[slot] = ((unsigned long long)k << 32) | (uint32_t)~(uint32_t)idx;
+      }
+    }
+  };
+  load_keys(0, ka);
+  for (int i0 = 0; i0 < per; i0 += 2 * RU) {
+    load_keys(i0 + RU, kb);
+    scan_keys(i0, ka);
+    if (i0 + RU >= per) break;
+    load_keys(i0 + 2 * RU, ka);
+    scan_keys(i0 + RU, kb);
+  }
+  __syncthreads();
+  const uint32_t nc = sh.ncand < (uint32_t)kMBCand ? sh.ncand : (uint32_t)kMBCand;  // == cnt1
+  if (nc <= (uint32_t)kMBThreads) {
+    // few candidates: each finds its rank (key descending, page ascending) directly
+    const unsigned long long mine_c = tid < (int)nc ? sh.cand[tid] : 0ull;
+    uint32_t rank = 0;
+    for (uint32_t u = 0; u < nc; ++u) rank += sh.cand[u] > mine_c ? 1u : 0u;
+    __syncthreads();
+    if (tid < (int)nc) sh.cand[rank] = mine_c;  // ranks are distinct: a permutation
+    __syncthreads();
+  } else {
+  uint32_t np2 = 1;
+  while (np2 < nc) np2 <<= 1;
+  for (uint32_t i = nc + tid; i < np2; i += kMBThreads) sh.cand[i] = 0ull;
+  __syncthreads();
+  for (uint32_t k = 2; k <= np2; k <<= 1) {
+    for (uint32_t jj = k >> 1; jj > 0; jj >>= 1) {
+      for (uint32_t i = tid; i < np2; i += kMBThreads) {
+        const uint32_t ixj = i ^ jj;
+        if (ixj > i) {
+          const unsigned long long a = sh.cand[i], b = sh.cand[ixj];
+          const bool desc = (i & k) == 0;
+          if (desc ? (a < b) : (a > b)) {
+            sh.cand[i] = b;
+            sh.cand[ixj] = a;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+  }
+  const uint32_t rr = r < 1u ? 1u : (r > nc ? nc : r);  // r is in [1, nc]; clamped for safety
+  const uint32_t T = nc ? (uint32_t)(sh.cand[rr - 1] >> 32) : 0xffffffffu;
+  uint32_t gtc = 0;
+  for (uint32_t i = tid; i < nc; i += kMBThreads) {
+    const unsigned long long v = sh.cand[i];
+    const uint32_t k = (uint32_t)(v >> 32);
+    const int idx = (int)~(uint32_t)v;
+    gtc += k > T ? 1u : 0u;
+    if (k > T) atomicAdd(&sh.sl_gt[idx / slice], 1);
+    else if (k == T) atomicAdd(&sh.sl_eq[idx / slice], 1);
+  }
+  const uint32_t ngt = mb_reduce(gtc, 2, sh.red);  // candidates above T
+  __syncthreads();
+  if (tid == 0) {
+    const int need_eq = (int)(rr - ngt);
+    int outp = (int)s, eqb = 0;
+    for (int jj = 0; jj < NB; ++jj) {
+      w.meta[((int64_t)h * NB + jj) * 2] = outp;
+      w.meta[((int64_t)h * NB + jj) * 2 + 1] = eqb;
+      const int e = sh.sl_eq[jj];
+      const int take = eqb >= need_eq ? 0 : (need_eq - eqb < e ? need_eq - eqb : e);
+      outp += sh.sl_gt[jj] + take;
+      eqb += e;
+    }
+    w.thr[h * 4] = T;
+    w.thr[h * 4 + 1] = (uint32_t)need_eq;
+    w.thr[h * 4 + 2] = 0u;
+  }
+}
+
+template <int KPT>
+__global__ void __launch_bounds__(kMBThreads)
+topk_mb_write(const float* scores, int64_t P, int64_t s, int64_t* out, int H, MBWork w) {
+  __shared__ uint32_t red[kMBWaves];
+  const int j = blockIdx.x, h = blockIdx.y, NB = gridDim.x, tid = threadIdx.x;
+  if (j == 0)
+    for (int64_t i = tid; i < s; i += kMBThreads) out[i * H + h] = i;
+  if (w.thr[h * 4 + 2]) return;  // written by the fallback
+  const int n = (int)(P - s);
+  const float* col = scores + (int64_t)h * P + s;
+  const uint32_t T = w.thr[h * 4];
+  const int need_eq = (int)w.thr[h * 4 + 1];
+  const int outp0 = w.meta[((int64_t)h * NB + j) * 2];
+  const int eqb0 = w.meta[((int64_t)h * NB + j) * 2 + 1];
+  const int c0 = j * (kMBThreads * KPT) + tid * KPT;
+  uint32_t key[KPT];
+  uint32_t gt = 0, eq = 0;
+  float kv[KPT];
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) kv[i] = col[c0 + i < n ? c0 + i : n - 1];  // all in flight
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) {
+    const int idx = c0 + i;
+    key[i] = idx < n ? ukey(kv[i]) : 0u;  // 0: below every real key
+    gt += key[i] > T ? 1u : 0u;
+    eq += (idx < n && key[i] == T) ? 1u : 0u;
+  }
+  uint32_t tot;
+  const int eq_rank0 = eqb0 + (int)mb_excl_scan(eq, red, tot);
+  int take = need_eq - eq_rank0;
+  take = take < 0 ? 0 : (take > (int)eq ? (int)eq : take);
+  int pos = outp0 + (int)mb_excl_scan(gt + (uint32_t)take, red, tot);
+  int eqr = eq_rank0;
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) {
+    const int idx = c0 + i;
+    const bool is_eq = idx < n && key[i] == T;
+    const bool sel = key[i] > T || (is_eq && eqr < need_eq);
+    eqr += is_eq ? 1 : 0;
+    if (sel) out[(int64_t)(pos++) * H + h] = s + idx;
+  }
+}
+
 int num_cus() {
   static int n = 0;
   if (!n) {
@@ -779,22 +1200,25 @@ namespace {
 template <int G>
 void launch_bound_f16(bool hfix, unsigned grid, size_t lds, hipStream_t s, const void* q, int qdt,
                       int group, const uint16_t* kmin, const uint16_t* kmax, int64_t P, int H,
-                      void* out, int odt, int head_major) {
+                      void* out, int odt, int head_major, uint2* mm) {
   if (hfix)
     hipLaunchKernelGGL((bound_f16_kernel<G, true>), dim3(grid), dim3(256), lds, s, q, qdt, group,
-                       kmin, kmax, P, H, out, odt, head_major);
+                       kmin, kmax, P, H, out, odt, head_major, mm);
   else
     hipLaunchKernelGGL((bound_f16_kernel<G, false>), dim3(grid), dim3(256), lds, s, q, qdt, group,
-                       kmin, kmax, P, H, out, odt, head_major);
+                       kmin, kmax, P, H, out, odt, head_major, nullptr);
 }
 
 // Bound into out, (P,H) or head-major (H,P).
 int page_bound(const void* q, int q_dtype, int Hq, const void* kmin, const void* kmax, int k_dtype,
                int64_t P, int H, int D, void* out, int out_dtype, int head_major,
-               hipStream_t s, const int64_t* page_ids = nullptr, int64_t nstat = 0) {
+               hipStream_t s, const int64_t* page_ids = nullptr, int64_t nstat = 0,
+               uint2* mm = nullptr, int* nmm = nullptr) {
+  if (nmm) *nmm = 0;
   if (!fdt(q_dtype) && q_dtype != HKV_DT_BF16) return HKV_ERR_DTYPE;
   if (!fdt(k_dtype) || !fdt(out_dtype)) return HKV_ERR_DTYPE;
   if (P < 0 || H < 1 || D < 1 || D > 512 || Hq < H || Hq % H) return HKV_ERR_SHAPE;
+  if (P * H >= ((int64_t)1 << 31)) return HKV_ERR_SHAPE;
   if (P == 0) return HKV_OK;
   if (!q || !kmin || !kmax || !out) return HKV_ERR_ARG;
   if (D % 8 == 0 && (((uintptr_t)kmin | (uintptr_t)kmax) & 15u)) return HKV_ERR_ARG;
@@ -805,21 +1229,24 @@ int page_bound(const void* q, int q_dtype, int Hq, const void* kmin, const void*
   if (!page_ids && k_dtype == HKV_DT_F16 && D % 8 == 0 && (G & (G - 1)) == 0 && G <= 64) {
     const int64_t span = (int64_t)(256 / G) * kBoundUnrollF16;
     const unsigned grid =
-        (unsigned)std::min<int64_t>((rows + span - 1) / span, (int64_t)num_cus() * 8);
+        (unsigned)std::min<int64_t>((rows + span - 1) / span, (int64_t)num_cus() * 4);
     const bool hfix = (64 / G) % H == 0;
     auto mn = (const uint16_t*)kmin;
     auto mx = (const uint16_t*)kmax;
     const int group = Hq / H;
+    // key ranges per block only where a head is fixed per lane and scores are fp32
+    uint2* mmp = (mm && hfix && H <= kMaxMMHeads && out_dtype == HKV_DT_F32) ? mm : nullptr;
     switch (G) {
-      case 1: launch_bound_f16<1>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major); break;
-      case 2: launch_bound_f16<2>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major); break;
-      case 4: launch_bound_f16<4>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major); break;
-      case 8: launch_bound_f16<8>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major); break;
-      case 16: launch_bound_f16<16>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major); break;
-      case 32: launch_bound_f16<32>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major); break;
-      default: launch_bound_f16<64>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major); break;
+      case 1: launch_bound_f16<1>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major, mmp); break;
+      case 2: launch_bound_f16<2>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major, mmp); break;
+      case 4: launch_bound_f16<4>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major, mmp); break;
+      case 8: launch_bound_f16<8>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major, mmp); break;
+      case 16: launch_bound_f16<16>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major, mmp); break;
+      case 32: launch_bound_f16<32>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major, mmp); break;
+      default: launch_bound_f16<64>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major, mmp); break;
     }
     HKV_CHECK_LAUNCH();
+    if (nmm && mmp) *nmm = (int)grid;
     return HKV_OK;
   }
   int n = 1;
@@ -942,6 +1369,44 @@ compact_blocks_kernel(uint8_t* __restrict__ flags, int64_t nblocks, int64_t bloc
 
 }  // namespace
 
+namespace {
+
+// Workspace of hkv_quest_select's multi-block top-K (NB = 0: not used).
+struct SelectWs {
+  int NB, kpt;
+  size_t ctr_off, thr_off, mm_off, hist_off, meta_off, bytes;
+};
+
+SelectWs select_ws_layout(int64_t P, int H) {
+  SelectWs l{};
+  const int64_t n = P;  // candidates are at most P
+  if (H < 1 || H > kMaxMMHeads || n < 4 * (int64_t)kMBThreads * 8) return l;  // small: one block per head
+  int kpt = 8;
+  int64_t nb = (n + kMBThreads * 8 - 1) / (kMBThreads * 8);
+  if (nb > kMBMaxSlices) {
+    kpt = 32;
+    nb = (n + kMBThreads * 32 - 1) / (kMBThreads * 32);
+    if (nb > kMBMaxSlices) return l;
+  }
+  auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
+  l.NB = (int)nb;
+  l.kpt = kpt;
+  l.ctr_off = 0;
+  l.thr_off = al(sizeof(uint32_t) * H);
+  l.mm_off = l.thr_off + al(sizeof(uint32_t) * 4 * H);
+  l.hist_off = l.mm_off + al(sizeof(uint2) * (size_t)num_cus() * 4 * H);
+  l.meta_off = l.hist_off + al(sizeof(uint32_t) * (size_t)H * nb * kMBBins);
+  l.bytes = l.meta_off + al(sizeof(int) * 2 * (size_t)H * nb);
+  return l;
+}
+
+}  // namespace
+
+extern "C" size_t hkv_quest_select_workspace_bytes(int64_t P, int H) {
+  const SelectWs l = select_ws_layout(P, H);
+  return l.NB ? l.bytes : 256;
+}
+
 extern "C" int hkv_quest_page_bound(const void* q, int q_dtype, int Hq, const void* kmin,
                                     const void* kmax, int k_dtype, int64_t P, int H, int D,
                                     void* out, int out_dtype, void* stream) {
@@ -979,10 +1444,35 @@ extern "C" int hkv_quest_select(const void* q, int q_dtype, int Hq, const void* 
   if (n_out) *n_out = s + keff;
   if (P == 0) return HKV_OK;
   if (!q || !kmin || !kmax || !scores || !out) return HKV_ERR_ARG;
-  const int st = page_bound(q, q_dtype, Hq, kmin, kmax, k_dtype, P, H, D, scores, HKV_DT_F32, 1,
-                            (hipStream_t)stream);
-  if (st != HKV_OK) return st;
-  return topk(scores, HKV_DT_F32, P, H, 1, P, k, sink_pages, out, nullptr, (hipStream_t)stream);
+  hipStream_t st = (hipStream_t)stream;
+  const SelectWs lay = select_ws_layout(P, H);
+  const bool mb = workspace && workspace_bytes >= lay.bytes && lay.NB > 0 && keff > 0 &&
+                  ((uintptr_t)workspace & 255u) == 0;
+  char* ws = (char*)workspace;
+  int nmm = 0;
+  const int rc = page_bound(q, q_dtype, Hq, kmin, kmax, k_dtype, P, H, D, scores, HKV_DT_F32, 1, st,
+                            nullptr, 0, mb ? (uint2*)(ws + lay.mm_off) : nullptr, &nmm);
+  if (rc != HKV_OK) return rc;
+  if (!mb || nmm == 0) return topk(scores, HKV_DT_F32, P, H, 1, P, k, sink_pages, out, nullptr, st);
+  MBWork w;
+  w.ctr = (uint32_t*)(ws + lay.ctr_off);
+  w.mm = (const uint2*)(ws + lay.mm_off);
+  w.nmm = nmm;
+  w.hist = (uint32_t*)(ws + lay.hist_off);
+  w.meta = (int*)(ws + lay.meta_off);
+  w.thr = (uint32_t*)(ws + lay.thr_off);
+  const dim3 grid((unsigned)lay.NB, (unsigned)H);
+  if (lay.kpt == 8) {
+    hipLaunchKernelGGL((topk_mb_hist<8>), grid, dim3(kMBThreads), 0, st, scores, P, s, keff, out, H, w);
+    HKV_CHECK_LAUNCH();
+    hipLaunchKernelGGL((topk_mb_write<8>), grid, dim3(kMBThreads), 0, st, scores, P, s, out, H, w);
+  } else {
+    hipLaunchKernelGGL((topk_mb_hist<32>), grid, dim3(kMBThreads), 0, st, scores, P, s, keff, out, H, w);
+    HKV_CHECK_LAUNCH();
+    hipLaunchKernelGGL((topk_mb_write<32>), grid, dim3(kMBThreads), 0, st, scores, P, s, out, H, w);
+  }
+  HKV_CHECK_LAUNCH();
+  return HKV_OK;
 }
 
 extern "C" int hkv_quest_select_blocks(const void* q, int q_dtype, int H, const void* kmin,
@@ -1051,6 +1541,7 @@ extern "C" int hkv_quest_select_ragged(const void* q, int q_dtype, int B, int Hq
   sg.off[B] = page_offsets[B];
   for (int b = 0; b <= B; ++b) sg.out_off[b] = out_offsets[b];
   const int64_t Ptot = page_offsets[B];
+  if (Ptot * H >= ((int64_t)1 << 31)) return HKV_ERR_SHAPE;
   if (Ptot == 0) return HKV_OK;
   if (!q || !kmin || !kmax || !scores || (out_offsets[B] > 0 && !out)) return HKV_ERR_ARG;
   if (((uintptr_t)kmin | (uintptr_t)kmax) & 15u) return HKV_ERR_ARG;
@@ -1061,7 +1552,7 @@ extern "C" int hkv_quest_select_ragged(const void* q, int q_dtype, int B, int Hq
   int64_t maxP = 0;
   for (int b = 0; b < B; ++b) maxP = std::max<int64_t>(maxP, page_offsets[b + 1] - page_offsets[b]);
   const int64_t span = (int64_t)(256 / G) * kBoundUnrollF16;
-  const int64_t want = std::max<int64_t>(1, ((int64_t)num_cus() * 8 + B - 1) / B);
+  const int64_t want = std::max<int64_t>(1, ((int64_t)num_cus() * 4 + B - 1) / B);
   const unsigned gx = (unsigned)std::max<int64_t>(1, std::min<int64_t>((maxP * H + span - 1) / span, want));
   const int64_t q_bytes = (int64_t)Hq * D * (q_dtype == HKV_DT_F32 ? 4 : 2);
   const bool hfix = (64 / G) % H == 0;

@@ -363,9 +363,10 @@ def quest_select(query: torch.Tensor, K_min: torch.Tensor, K_max: torch.Tensor, 
     if tuple(out.shape) != (s + keff, H) or tuple(scores.shape) != (H, P):
         raise ValueError("out must be (sinks + k_eff, H) and scores (H, P)")
     n_out = N._i64(0)
+    ws = N.workspace("quest_select", int(N.lib().hkv_quest_select_workspace_bytes(P, H)), q.device)
     st = N.lib().hkv_quest_select(N.ptr(q), N.dtype_code(q), Hq, N.ptr(kmin), N.ptr(kmax),
                                   _fdt(kmin), P, H, D, int(k), int(sink_pages), N.ptr(scores),
-                                  N.ptr(out), n_out, None, 0, N.stream_of(q))
+                                  N.ptr(out), n_out, N.ptr(ws), ws.numel(), N.stream_of(q))
     N.check(st, "hkv_quest_select", ValueError)
     return out, scores
 

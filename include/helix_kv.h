@@ -244,11 +244,17 @@ int hkv_quest_topk(const void *bound, int b_dtype, int64_t P, int H, int64_t k,
 /*
  * Quest selection for one decode step: the bound (as hkv_quest_page_bound,
  * f32, written head-major to scores (H,P)) then the top-K with sinks (as
- * hkv_quest_topk),
- * two launches on `stream`.  The per-layer path of src/kvquant/quest_selector.py:
- * 64-78 without the union.  workspace / workspace_bytes are unused (may be
- * NULL / 0).
+ * hkv_quest_topk).  The per-layer path of src/kvquant/quest_selector.py:64-78
+ * without the union.  With a workspace of hkv_quest_select_workspace_bytes(P,
+ * H) bytes (256-byte aligned, zero-filled once before its first use; every
+ * call leaves it reusable; calls that may overlap must not share it), large
+ * fp16 columns take the multi-block top-K (the bound kernel also records the
+ * key range of its blocks; a histogram kernel over slices of each column whose
+ * last block resolves the threshold; a write kernel): three launches.
+ * Without one (NULL / too small), the single-block top-K: two launches.  Both
+ * give identical results.
  */
+size_t hkv_quest_select_workspace_bytes(int64_t P, int H);
 int hkv_quest_select(const void *q, int q_dtype, int Hq, const void *kmin, const void *kmax,
                      int k_dtype, int64_t P, int H, int D, int64_t k, int64_t sink_pages,
                      float *scores, int64_t *out, int64_t *n_out, void *workspace,

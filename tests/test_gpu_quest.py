@@ -142,3 +142,36 @@ def test_fused_select_small_and_per_kv_head(dev):
         wb = O.page_bound_group(q, mn, mx, g) if g > 1 else O.page_bound(q, mn, mx)
         assert np.array_equal(sc.cpu().numpy().T, wb)
         assert np.array_equal(idx.cpu().numpy(), O.topk_sinks(wb, k, s))
+
+
+@pytest.mark.parametrize("P,H,g,k,s,mode", [
+    (40000, 4, 7, 10000, 4, "normal"),     # five slices, the last one partial
+    (65536, 2, 7, 1, 0, "normal"),         # a single page besides no sinks
+    (65536, 4, 1, 65532, 4, "normal"),     # every candidate
+    (50000, 1, 3, 12345, 7, "ties"),       # few distinct scores: big equal runs
+    (70000, 4, 7, 17500, 4, "equal"),      # all scores equal: the huge-bin fallback
+    (600000, 2, 7, 150000, 4, "normal"),   # many slices (KPT 32)
+])
+def test_multiblock_select_vs_oracle(dev, P, H, g, k, s, mode):
+    """The multi-block top-K (fp16 statistics, large columns) against the
+    oracle, including repeated calls on the same workspace."""
+    from helix_kv.ops import quest_select
+
+    D = 128
+    if mode == "equal":
+        mn = np.zeros((P, H, D), np.float16)
+        mx = np.ones((P, H, D), np.float16)
+    elif mode == "ties":
+        levels = RNG.integers(0, 5, size=(P, 1, 1)).astype(np.float16)
+        mn = np.broadcast_to(levels - 1, (P, H, D)).astype(np.float16)
+        mx = np.broadcast_to(levels, (P, H, D)).astype(np.float16)
+    else:
+        mn = RNG.standard_normal((P, H, D)).astype(np.float16)
+        mx = (mn + np.abs(RNG.standard_normal((P, H, D))).astype(np.float16)).astype(np.float16)
+    q = RNG.standard_normal((H * g, D)).astype(np.float16)
+    want_b = O.page_bound_group(q, mn.astype(np.float32), mx.astype(np.float32), g)
+    want = O.topk_sinks(want_b, k, s)
+    for _ in range(2):
+        idx, scores = quest_select(_t(q, dev), _t(mn, dev), _t(mx, dev), k, s)
+        assert np.array_equal(scores.cpu().numpy().T.view(np.uint32), want_b.view(np.uint32))
+        assert np.array_equal(idx.cpu().numpy(), want)
