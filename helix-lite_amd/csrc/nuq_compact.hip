@@ -303,33 +303,63 @@ unpack_compact_kernel(const uint8_t* __restrict__ packed, const int32_t* __restr
     __syncthreads();
   }
 
-  const int64_t nwaves = (int64_t)gridDim.x * NW;
-  for (int64_t wt = (int64_t)blockIdx.x * NW + wv; wt < nwtiles; wt += nwaves) {
-    const int64_t r0 = wt * WR;
+  // Three-stage pipeline over the wave's tiles: codes, row_ptr and (PT) pole
+  // rows are loaded two tiles ahead, each row's first CSR entries one tile
+  // ahead, so no global load is waited on right after it is issued.  Loads
+  // are unconditional from clamped in-bounds rows (row nrows - 1 for rows past
+  // the end, whose results are not stored).
+  struct TileLoad {
     uint32_t cw[kUPasses];
-    int32_t ra[kUPasses], rb[kUPasses];
+    int2 rp[kUPasses];
+    uint32_t pv[kUPasses];  // PT: pole cg of the row's 16 (G >= 16), or poles cg, cg+G, ...
+  };
+  struct TileCsr {
+    uint32_t c[kUPasses], v[kUPasses];  // entry ra + cg of each pass's row
+  };
+  const int64_t nwaves = (int64_t)gridDim.x * NW;
+  auto load_tile = [&](int64_t wt, TileLoad& L) {
 #pragma unroll
     for (int p = 0; p < kUPasses; ++p) {
-      const int64_t r = r0 + p * RW + rw;
-      cw[p] = 0;
-      ra[p] = rb[p] = 0;
-      if (r < nrows) {
-        if constexpr (BITS == 4) cw[p] = *reinterpret_cast<const uint32_t*>(packed + r * RB + 4 * cg);
-        else cw[p] = *reinterpret_cast<const uint16_t*>(packed + r * RB + 2 * cg);
-        ra[p] = row_ptr[r];
-        rb[p] = row_ptr[r + 1];
+      int64_t r = wt * WR + p * RW + rw;
+      r = r < nrows ? r : nrows - 1;
+      if constexpr (BITS == 4) L.cw[p] = *reinterpret_cast<const uint32_t*>(packed + r * RB + 4 * cg);
+      else L.cw[p] = *reinterpret_cast<const uint16_t*>(packed + r * RB + 2 * cg);
+      L.rp[p] = *reinterpret_cast<const int2*>(row_ptr + r);
+      if constexpr (PT) {
+        const int ri = (int)r;  // rows < 2^31
+        const int t = ri / H;
+        const int h = ri - t * H;
+        const int64_t tab = (int64_t)h * sc.rows + clamp_row(token_pos(sc, t), sc.rows);
+        L.pv[p] = tabs[tab].pf16[cg & 15];
       }
     }
+  };
+  auto load_csr = [&](const TileLoad& L, TileCsr& C) {
+    if (cap <= 0) return;
+#pragma unroll
+    for (int p = 0; p < kUPasses; ++p) {
+      int64_t i = (int64_t)(L.rp[p].x > 0 ? L.rp[p].x : 0) + cg;
+      i = i < cap ? i : cap - 1;
+      C.c[p] = col[i];
+      C.v[p] = val[i];
+    }
+  };
+  auto process = [&](int64_t wt, const TileLoad& L, const TileCsr& C) {
+    const int64_t r0 = wt * WR;
     if constexpr (PT) {
 #pragma unroll
-      for (int p = 0; p < kUPasses; ++p) {
-        const int64_t r = r0 + p * RW + rw;
-        if (r < nrows && cg < 2) {
-          const int64_t t = r / H;
-          const int h = (int)(r - t * H);
+      for (int p = 0; p < kUPasses; ++p)
+        if (cg < 16) prow[(p * RW + rw) * 16 + cg] = (uint16_t)L.pv[p];
+      if constexpr (G < 16) {  // fewer lanes than poles per row: the rest directly
+#pragma unroll
+        for (int p = 0; p < kUPasses; ++p) {
+          int64_t r = r0 + p * RW + rw;
+          r = r < nrows ? r : nrows - 1;
+          const int ri = (int)r;
+          const int t = ri / H;
+          const int h = ri - t * H;
           const int64_t tab = (int64_t)h * sc.rows + clamp_row(token_pos(sc, t), sc.rows);
-          const uint4 v = reinterpret_cast<const uint4*>(tabs[tab].pf16)[cg];
-          *reinterpret_cast<uint4*>(prow + (p * RW + rw) * 16 + 8 * cg) = v;
+          for (int l = cg + G; l < 16; l += G) prow[(p * RW + rw) * 16 + l] = tabs[tab].pf16[l];
         }
       }
       wave_sync();
@@ -338,7 +368,6 @@ unpack_compact_kernel(const uint8_t* __restrict__ packed, const int32_t* __restr
     for (int p = 0; p < kUPasses; ++p) {
       const int rr = p * RW + rw;
       const int64_t r = r0 + rr;
-      if (r >= nrows) continue;
       const int h = (int)(r % H);
       uint32_t res[4];
 #pragma unroll
@@ -347,7 +376,7 @@ unpack_compact_kernel(const uint8_t* __restrict__ packed, const int32_t* __restr
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
           const int e = 2 * j + k;
-          const uint32_t c = (cw[p] >> (BITS * e)) & ((1u << BITS) - 1u);
+          const uint32_t c = (L.cw[p] >> (BITS * e)) & ((1u << BITS) - 1u);
           uint16_t v;
           if constexpr (PT) v = prow[rr * 16 + c];
           else if constexpr (KLDS) v = kp[(h * 16 + c) * D + 8 * cg + e];
@@ -362,9 +391,10 @@ unpack_compact_kernel(const uint8_t* __restrict__ packed, const int32_t* __restr
 #pragma unroll
     for (int p = 0; p < kUPasses; ++p) {
       const int rr = p * RW + rw;
-      const int32_t lo = ra[p] > 0 ? ra[p] : 0;
-      const int32_t hi = (int64_t)rb[p] < cap ? rb[p] : (int32_t)cap;
-      for (int32_t i = lo + cg; i < hi; i += G) {
+      const int32_t lo = L.rp[p].x > 0 ? L.rp[p].x : 0;
+      const int32_t hi = (int64_t)L.rp[p].y < cap ? L.rp[p].y : (int32_t)cap;
+      if (lo + cg < hi && C.c[p] < (uint32_t)D) seg[rr * D + C.c[p]] = (uint16_t)C.v[p];
+      for (int32_t i = lo + cg + G; i < hi; i += G) {  // rows with more than G outliers
         const uint32_t d = col[i];
         if (d < (uint32_t)D) seg[rr * D + d] = val[i];
       }
@@ -379,6 +409,26 @@ unpack_compact_kernel(const uint8_t* __restrict__ packed, const int32_t* __restr
           *reinterpret_cast<const uint4*>(seg + rr * D + 8 * cg);
     }
     wave_sync();
+  };
+  const int64_t wt0 = (int64_t)blockIdx.x * NW + wv;
+  if (wt0 >= nwtiles) return;
+  TileLoad L0, L1, L2;
+  TileCsr C0, C1, C2;
+  load_tile(wt0, L0);
+  load_tile(wt0 + nwaves, L1);
+  load_csr(L0, C0);
+  auto step = [&](int64_t wt, const TileLoad& Lc, const TileCsr& Cc, const TileLoad& Ln, TileCsr& Cn,
+                  TileLoad& Lw) {
+    load_tile(wt + 2 * nwaves, Lw);
+    load_csr(Ln, Cn);
+    process(wt, Lc, Cc);
+  };
+  for (int64_t wt = wt0; wt < nwtiles; wt += 3 * nwaves) {
+    step(wt, L0, C0, L1, C1, L2);
+    if (wt + nwaves >= nwtiles) break;
+    step(wt + nwaves, L1, C1, L2, C2, L0);
+    if (wt + 2 * nwaves >= nwtiles) break;
+    step(wt + 2 * nwaves, L2, C2, L0, C0, L1);
   }
 }
 
