@@ -531,6 +531,8 @@ def profile_pass(what: str, dev) -> None:
         mn, mx = quest_page_stats(torch.randn((P, 16, H, D), generator=g, device=dev).half())
         for _ in range(3):
             quest_select(q, mn, mx, P // 4, 4)
+    elif what == "ragged":
+        bench_ragged(argparse.Namespace(steps=1), dev)
     elif what == "decode":
         P = DEC_TOK // 16
         for Ld in build_decode_layers(dev, (0, CUT)):
@@ -547,7 +549,7 @@ def main() -> None:
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--only", choices=["all", "nuq", "quest", "ragged", "decode"], default="all")
-    ap.add_argument("--profile", choices=["pack", "unpack", "quest", "decode"], default=None,
+    ap.add_argument("--profile", choices=["pack", "unpack", "quest", "ragged", "decode"], default=None,
                     help="run a short fixed launch sequence for rocprofv3 counters and exit")
     ap.add_argument("--cpu-layers", default="0,1,16,17",
                     help="layers timed on the CPU oracle for the baseline")
