@@ -833,6 +833,8 @@ constexpr int kMBWaves = kMBThreads / 64;
 constexpr int kMBBins = 4096;
 constexpr int kMBCand = 4096;
 constexpr int kMBMaxSlices = 64;
+constexpr int kMBWinBins = 24;  // window half-width around a slice's own threshold-bin estimate
+constexpr int kMBWin = 1024;    // window keys stored per slice
 
 struct MBWork {
   uint32_t* ctr;     // [H] arrival counters (zero between calls)
@@ -841,6 +843,8 @@ struct MBWork {
   uint32_t* hist;    // [H][NB][kMBBins]
   int* meta;         // [H][NB][2] (out row of the slice's first selected page, T-equal keys before it)
   uint32_t* thr;     // [H][4] (T, T-equal keys taken, 1 = selection already written)
+  unsigned long long* wcand;  // [H][NB][kMBWin] keys of the slice's window bins (key << 32 | ~page)
+  int* wmeta;        // [H][NB][4] (first window bin, last window bin, keys stored, overflowed)
 };
 
 struct MBShared {
@@ -850,6 +854,8 @@ struct MBShared {
   uint32_t red[kMBWaves];
   uint32_t bc[8];
   int sl_gt[kMBMaxSlices], sl_eq[kMBMaxSlices];
+  int wm[kMBMaxSlices][4];
+  uint32_t sl_b1[kMBMaxSlices];
 };
 
 HKV_DEV uint32_t mb_reduce(uint32_t v, int op, uint32_t* red) {  // op 0 min, 1 max, 2 sum
@@ -930,9 +936,57 @@ topk_mb_hist(const float* scores, int64_t P, int64_t s, int64_t keff, int64_t* o
   __syncthreads();
   uint32_t* gh = w.hist + ((int64_t)h * NB + j) * kMBBins;
   for (int b = tid; b < kMBBins; b += kMBThreads) gh[b] = sh.hist[b];
+  {
+    // This slice's own estimate of the threshold bin (the bin of its
+    // proportional share of keff), and the keys of the bins around it: if the
+    // true threshold bin lies in every slice's window, the last block finds
+    // its candidates here instead of re-reading the column.
+    const int nj = n - j * slice < slice ? n - j * slice : slice;
+    uint64_t kj = ((uint64_t)keff * (uint64_t)nj + (uint64_t)n - 1) / (uint64_t)n;
+    kj = kj < 1 ? 1 : (kj > (uint64_t)nj ? (uint64_t)nj : kj);
+    uint32_t mine_l = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) mine_l += sh.hist[kMBBins - 1 - 4 * tid - k];
+    if (tid == 0) sh.bc[2] = 0u;  // ordered before the writes below by the scan's barriers
+    uint32_t tot_l;
+    uint32_t above_l = mb_excl_scan(mine_l, sh.red, tot_l);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int b = kMBBins - 1 - 4 * tid - k;
+      const uint32_t c = sh.hist[b];
+      if (above_l < (uint32_t)kj && above_l + c >= (uint32_t)kj) sh.bc[2] = (uint32_t)b;
+      above_l += c;
+    }
+    if (tid == 0) sh.ncand = 0u;
+    __syncthreads();
+    const int bj = (int)sh.bc[2];
+    const int wlo = bj - kMBWinBins > 0 ? bj - kMBWinBins : 0;
+    const int whi = bj + kMBWinBins < kMBBins - 1 ? bj + kMBWinBins : kMBBins - 1;
+    unsigned long long* wc = w.wcand + ((int64_t)h * NB + j) * kMBWin;
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      if (c0 + i < n) {
+        const uint32_t k = ukey(kv[i]);
+        const uint32_t b0 = k < mn ? 0u : (k - mn) >> sh1;
+        const int b = b0 < (uint32_t)kMBBins ? (int)b0 : kMBBins - 1;
+        if (b >= wlo && b <= whi) {
+          const uint32_t slot = atomicAdd(&sh.ncand, 1u);
+          if (slot < (uint32_t)kMBWin) wc[slot] = ((unsigned long long)k << 32) | (uint32_t)~(uint32_t)(c0 + i);
+        }
+      }
+    }
+    __syncthreads();
+    if (tid == 0) {
+      int* wm = w.wmeta + ((int64_t)h * NB + j) * 4;
+      wm[0] = wlo;
+      wm[1] = whi;
+      wm[2] = sh.ncand < (uint32_t)kMBWin ? (int)sh.ncand : kMBWin;
+      wm[3] = sh.ncand > (uint32_t)kMBWin ? 1 : 0;
+    }
+  }
   __syncthreads();
   if (tid == 0) {
-    __threadfence();  // release this slice's histogram
+    __threadfence();  // release this slice's histogram and window
     s_last = atomicAdd(&w.ctr[h], 1u) == (uint32_t)(NB - 1);
   }
   __syncthreads();
@@ -945,9 +999,22 @@ topk_mb_hist(const float* scores, int64_t P, int64_t s, int64_t keff, int64_t* o
 
   // ---- last block of head h: the threshold
   // Thread t sums bins t + 1024 k4 over the slices, keeping each slice's value
-  // (per-slice counts above the threshold bin come from them).
+  // (per-slice counts above the threshold bin come from them).  The slices'
+  // windows are requested in the same round trip (up to 8 slices).
   constexpr int KB = kMBBins / kMBThreads;  // bins per thread
   const int NBc = NB < kMBMaxSlices ? NB : kMBMaxSlices;
+  const bool win_regs = NBc * kMBWin <= 8 * kMBThreads;
+  unsigned long long wcr[8];
+  if (win_regs) {
+    const int nwin = NBc * kMBWin;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      int f = u * kMBThreads + tid;
+      f = f < nwin ? f : nwin - 1;
+      wcr[u] = w.wcand[(int64_t)h * NB * kMBWin + f];  // slices are consecutive: [NB][kMBWin]
+    }
+  }
+  for (int i = tid; i < NBc * 4; i += kMBThreads) sh.wm[i >> 2][i & 3] = w.wmeta[((int64_t)h * NB) * 4 + i];
   uint32_t hv[KB][8];  // slices j0..j0+7 of the thread's bins (the last group kept)
   for (int k4 = 0; k4 < KB; ++k4) sh.hist[k4 * kMBThreads + tid] = 0u;
   for (int j0 = 0; j0 < NBc; j0 += 8) {
@@ -1020,6 +1087,40 @@ topk_mb_hist(const float* scores, int64_t P, int64_t s, int64_t keff, int64_t* o
       if (tid == 0 && j0 + u < NBc) sh.sl_gt[j0 + u] = (int)c;
     }
   }
+  // the slices' counts in bin b1 (known for up to 8 slices: the last group in hv)
+  if (NBc <= 8 && tid == (int)(b1 % kMBThreads)) {
+    const int k4 = (int)(b1 / kMBThreads);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      uint32_t v = 0;
+#pragma unroll
+      for (int kk = 0; kk < KB; ++kk) v = kk == k4 ? hv[kk][u] : v;
+      if (u < NBc) sh.sl_b1[u] = v;
+    }
+  }
+  __syncthreads();
+  // the windows hold every key of bin b1 if b1 lies in every window of a slice
+  // with keys there (and no window overflowed)
+  bool use_win = win_regs;
+  for (int jj = 0; jj < NBc && use_win; ++jj) {
+    const bool covers = (int)b1 >= sh.wm[jj][0] && (int)b1 <= sh.wm[jj][1];
+    const bool empty = NBc <= 8 && sh.sl_b1[jj] == 0u;
+    if (sh.wm[jj][3] || !(covers || empty)) use_win = false;
+  }
+  if (use_win) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int f = u * kMBThreads + tid;
+      const int jj = f / kMBWin, e = f - jj * kMBWin;
+      if (jj < NBc && e < sh.wm[jj][2]) {
+        const uint32_t k = (uint32_t)(wcr[u] >> 32);
+        if (k >= lo1 && k <= hi1) {
+          const uint32_t slot = atomicAdd(&sh.ncand, 1u);
+          if (slot < (uint32_t)kMBCand) sh.cand[slot] = wcr[u];
+        }
+      }
+    }
+  } else {
   // candidates: the keys of bin b1 (re-read, the next 16 in flight while 16 are checked)
   const int per = (n + kMBThreads - 1) / kMBThreads;
   constexpr int RU = 16;
@@ -1050,6 +1151,7 @@ topk_mb_hist(const float* scores, int64_t P, int64_t s, int64_t keff, int64_t* o
     if (i0 + RU >= per) break;
     load_keys(i0 + 2 * RU, ka);
     scan_keys(i0 + RU, kb);
+  }
   }
   __syncthreads();
   const uint32_t nc = sh.ncand < (uint32_t)kMBCand ? sh.ncand : (uint32_t)kMBCand;  // == cnt1
@@ -1374,7 +1476,7 @@ namespace {
 // Workspace of hkv_quest_select's multi-block top-K (NB = 0: not used).
 struct SelectWs {
   int NB, kpt;
-  size_t ctr_off, thr_off, mm_off, hist_off, meta_off, bytes;
+  size_t ctr_off, thr_off, mm_off, hist_off, meta_off, wcand_off, wmeta_off, bytes;
 };
 
 SelectWs select_ws_layout(int64_t P, int H) {
@@ -1396,7 +1498,9 @@ SelectWs select_ws_layout(int64_t P, int H) {
   l.mm_off = l.thr_off + al(sizeof(uint32_t) * 4 * H);
   l.hist_off = l.mm_off + al(sizeof(uint2) * (size_t)num_cus() * 4 * H);
   l.meta_off = l.hist_off + al(sizeof(uint32_t) * (size_t)H * nb * kMBBins);
-  l.bytes = l.meta_off + al(sizeof(int) * 2 * (size_t)H * nb);
+  l.wcand_off = l.meta_off + al(sizeof(int) * 2 * (size_t)H * nb);
+  l.wmeta_off = l.wcand_off + al(sizeof(unsigned long long) * (size_t)H * nb * kMBWin);
+  l.bytes = l.wmeta_off + al(sizeof(int) * 4 * (size_t)H * nb);
   return l;
 }
 
@@ -1461,6 +1565,8 @@ extern "C" int hkv_quest_select(const void* q, int q_dtype, int Hq, const void* 
   w.hist = (uint32_t*)(ws + lay.hist_off);
   w.meta = (int*)(ws + lay.meta_off);
   w.thr = (uint32_t*)(ws + lay.thr_off);
+  w.wcand = (unsigned long long*)(ws + lay.wcand_off);
+  w.wmeta = (int*)(ws + lay.wmeta_off);
   const dim3 grid((unsigned)lay.NB, (unsigned)H);
   if (lay.kpt == 8) {
     hipLaunchKernelGGL((topk_mb_hist<8>), grid, dim3(kMBThreads), 0, st, scores, P, s, keff, out, H, w);
