@@ -114,6 +114,19 @@ HKV_DEV uint32_t ukey(float f) {
 HKV_DEV float clamp_pos(float q) { return q < 0.0f ? 0.0f : q; }
 HKV_DEV float clamp_neg(float q) { return q > 0.0f ? 0.0f : q; }
 
+// The fp32 product of q and the fp16 half HI of w, rounded once: one
+// v_fma_mix_f32 with addend -0 (x + -0 == x for every x, +0 included), instead
+// of a conversion and a multiply.
+template <int HI>
+HKV_DEV float mul_f16(uint32_t w, float q) {
+  float r;
+  if constexpr (HI)
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(w), "v"(q), "v"(-0.0f));
+  else
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(w), "v"(q), "v"(-0.0f));
+  return r;
+}
+
 template <typename KT> HKV_DEV float kval(KT v);
 template <> HKV_DEV float kval<uint16_t>(uint16_t v) { return h2f(v); }
 template <> HKV_DEV float kval<float>(float v) { return v; }
@@ -176,6 +189,48 @@ HKV_DEV float row16_reduce(float v) {
   v = __fadd_rn(v, dpp_f<0x4e>(v));   // quad_perm [2,3,0,1]
   v = __fadd_rn(v, dpp_f<0xb1>(v));   // quad_perm [1,0,3,2]
   return v;
+}
+
+// Integer wave reductions and scans on DPP moves (no LDS permutes): rows of
+// 16 lanes by row_ror / quad_perm (every lane ends with its row's value) or
+// by row_shr (a lane reads the lane n below it, 0 past the row start), then
+// the four rows combined through readlane.
+template <int CTRL>
+HKV_DEV uint32_t dpp_u(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
+}
+HKV_DEV uint32_t rl_u(uint32_t v, int lane) { return (uint32_t)__builtin_amdgcn_readlane((int)v, lane); }
+HKV_DEV uint32_t wave_sum_u(uint32_t v) {  // same value in every lane
+  v += dpp_u<0x128>(v);
+  v += dpp_u<0x124>(v);
+  v += dpp_u<0x4e>(v);
+  v += dpp_u<0xb1>(v);
+  return rl_u(v, 0) + rl_u(v, 16) + rl_u(v, 32) + rl_u(v, 48);
+}
+HKV_DEV uint32_t min_u(uint32_t a, uint32_t b) { return a < b ? a : b; }
+HKV_DEV uint32_t max_u(uint32_t a, uint32_t b) { return a > b ? a : b; }
+HKV_DEV uint32_t wave_min_u(uint32_t v) {
+  v = min_u(v, dpp_u<0x128>(v));
+  v = min_u(v, dpp_u<0x124>(v));
+  v = min_u(v, dpp_u<0x4e>(v));
+  v = min_u(v, dpp_u<0xb1>(v));
+  return min_u(min_u(rl_u(v, 0), rl_u(v, 16)), min_u(rl_u(v, 32), rl_u(v, 48)));
+}
+HKV_DEV uint32_t wave_max_u(uint32_t v) {
+  v = max_u(v, dpp_u<0x128>(v));
+  v = max_u(v, dpp_u<0x124>(v));
+  v = max_u(v, dpp_u<0x4e>(v));
+  v = max_u(v, dpp_u<0xb1>(v));
+  return max_u(max_u(rl_u(v, 0), rl_u(v, 16)), max_u(rl_u(v, 32), rl_u(v, 48)));
+}
+HKV_DEV uint32_t wave_incl_scan_u(uint32_t x) {  // lane order
+  x += dpp_u<0x111>(x);  // row_shr:1
+  x += dpp_u<0x112>(x);  // row_shr:2
+  x += dpp_u<0x114>(x);  // row_shr:4
+  x += dpp_u<0x118>(x);  // row_shr:8: x = sum of the row's lanes up to this one
+  const uint32_t t0 = rl_u(x, 15), t1 = rl_u(x, 31), t2 = rl_u(x, 47);
+  const int row = (threadIdx.x & 63) >> 4;
+  return x + (row >= 1 ? t0 : 0u) + (row >= 2 ? t1 : 0u) + (row >= 3 ? t2 : 0u);
 }
 
 HKV_DEV int lanes_for(int D) {
@@ -346,10 +401,10 @@ HKV_DEV void bound_f16_rows(const void* q, int qdt, int group, const uint16_t* _
       float ps = 0.0f, ns = 0.0f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const float kmx = h2f((uint16_t)(wb[i >> 1] >> (16 * (i & 1))));
-        const float kmn = h2f((uint16_t)(wa[i >> 1] >> (16 * (i & 1))));
-        ps = __fadd_rn(ps, __fmul_rn(qp[i], kmx));
-        ns = __fadd_rn(ns, __fmul_rn(qn[i], kmn));
+        const float px = (i & 1) ? mul_f16<1>(wb[i >> 1], qp[i]) : mul_f16<0>(wb[i >> 1], qp[i]);
+        const float pn = (i & 1) ? mul_f16<1>(wa[i >> 1], qn[i]) : mul_f16<0>(wa[i >> 1], qn[i]);
+        ps = __fadd_rn(ps, px);
+        ns = __fadd_rn(ns, pn);
       }
       if constexpr (G == 16) {
         ps = row16_reduce(ps);
@@ -815,16 +870,19 @@ topk_ragged_kernel(const float* scores, int H, int64_t sinks, int64_t* out, cons
 //
 // One head's candidates [s, P) are split into NB slices of kMBThreads*KPT
 // consecutive pages, one block each, in two kernels (no block ever waits):
-//  topk_mb_hist: a block histograms its slice into 4096 bins of
+//  topk_mb_hist: every block histograms its slice into 4096 bins of
 //    (key - kmn) >> sh, where kmn / kmx come from the bound kernel's per-block
-//    key ranges and sh makes the range fit; it stores the histogram and
-//    arrives at the head's counter.  The last block to arrive sums the
-//    histograms, finds the bin of the keff-th largest key, re-reads the head's
-//    keys, sorts that bin's keys (bitonic; ties to the lower page) and writes
-//    the threshold key T, how many keys equal to T are taken, and for every
-//    slice the output row of its first selected page and the number of
-//    T-equal keys before it.  It leaves the counter at zero for the next call.
-//    A bin of more than kMBCand keys falls back to the single-block selector.
+//    key ranges and sh makes the range fit; it stores the histogram and the
+//    keys of the bins around its own estimate of the threshold bin (the bin
+//    of its proportional share of keff), then arrives at the head's counter.
+//    The last block to arrive sums the histograms, finds the bin b1 of the
+//    keff-th largest key, gathers that bin's keys (from the slices' windows
+//    when b1 lies in every window that can hold keys of b1, else by re-reading
+//    the column), ranks them (key descending, page ascending) and writes the
+//    threshold key T, how many keys equal to T are taken, and for every slice
+//    the output row of its first selected page and the number of T-equal keys
+//    before it.  It leaves the counter at zero for the next call.  A bin of
+//    more than kMBCand keys falls back to the single-block selector.
 //  topk_mb_write: each block writes its slice's selected pages in page order.
 // Same result as select_column_regs: sinks, then the keff highest keys with
 // ties to the lower page, ascending.
@@ -833,8 +891,8 @@ constexpr int kMBWaves = kMBThreads / 64;
 constexpr int kMBBins = 4096;
 constexpr int kMBCand = 4096;
 constexpr int kMBMaxSlices = 64;
-constexpr int kMBWinBins = 24;  // window half-width around a slice's own threshold-bin estimate
-constexpr int kMBWin = 1024;    // window keys stored per slice
+constexpr int kMBWinBins = 24;   // window half-width around a slice's own threshold-bin estimate
+constexpr int kMBWin = 1024;     // window keys stored per slice
 
 struct MBWork {
   uint32_t* ctr;     // [H] arrival counters (zero between calls)
@@ -842,7 +900,7 @@ struct MBWork {
   int nmm;
   uint32_t* hist;    // [H][NB][kMBBins]
   int* meta;         // [H][NB][2] (out row of the slice's first selected page, T-equal keys before it)
-  uint32_t* thr;     // [H][4] (T, T-equal keys taken, 1 = selection already written)
+  uint32_t* thr;     // [H][4] (T, T-equal keys taken, 1 = selection already written, s + keff)
   unsigned long long* wcand;  // [H][NB][kMBWin] keys of the slice's window bins (key << 32 | ~page)
   int* wmeta;        // [H][NB][4] (first window bin, last window bin, keys stored, overflowed)
 };
@@ -851,38 +909,37 @@ struct MBShared {
   uint32_t hist[kMBBins];
   unsigned long long cand[kMBCand];
   uint32_t ncand;
-  uint32_t red[kMBWaves];
+  uint32_t red[2][kMBWaves];
   uint32_t bc[8];
-  int sl_gt[kMBMaxSlices], sl_eq[kMBMaxSlices];
   int wm[kMBMaxSlices][4];
   uint32_t sl_b1[kMBMaxSlices];
+  uint32_t slw[kMBWaves][8];
+  int sl_gt[kMBMaxSlices], sl_eq[kMBMaxSlices];
 };
 
-HKV_DEV uint32_t mb_reduce(uint32_t v, int op, uint32_t* red) {  // op 0 min, 1 max, 2 sum
-  for (int o = 32; o >= 1; o >>= 1) {
-    const uint32_t y = __shfl_xor(v, o, 64);
-    v = op == 0 ? (y < v ? y : v) : op == 1 ? (y > v ? y : v) : v + y;
-  }
+// Block-wide minimum of a and maximum of b (one pair of barriers).
+HKV_DEV void mb_minmax(uint32_t& a, uint32_t& b, uint32_t (*red)[kMBWaves]) {
+  a = wave_min_u(a);
+  b = wave_max_u(b);
   const int w = threadIdx.x >> 6;
   __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[w] = v;
-  __syncthreads();
-  uint32_t r = red[0];
-  for (int i = 1; i < kMBWaves; ++i) {
-    const uint32_t y = red[i];
-    r = op == 0 ? (y < r ? y : r) : op == 1 ? (y > r ? y : r) : r + y;
+  if ((threadIdx.x & 63) == 0) {
+    red[0][w] = a;
+    red[1][w] = b;
   }
-  return r;
+  __syncthreads();
+  a = red[0][0];
+  b = red[1][0];
+  for (int i = 1; i < kMBWaves; ++i) {
+    a = red[0][i] < a ? red[0][i] : a;
+    b = red[1][i] > b ? red[1][i] : b;
+  }
 }
 
 // Exclusive prefix sum over the block in thread order; total in `total`.
 HKV_DEV uint32_t mb_excl_scan(uint32_t v, uint32_t* red, uint32_t& total) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  uint32_t x = v;
-  for (int o = 1; o < 64; o <<= 1) {
-    const uint32_t y = __shfl_up(x, o, 64);
-    if (lane >= o) x += y;
-  }
+  const uint32_t x = wave_incl_scan_u(v);
   __syncthreads();
   if (lane == 63) red[w] = x;
   __syncthreads();
@@ -896,16 +953,27 @@ HKV_DEV uint32_t mb_excl_scan(uint32_t v, uint32_t* red, uint32_t& total) {
   return before + x - v;
 }
 
+// Waits until this wave's global stores are complete (s_waitcnt vmcnt(0);
+// the export and LDS counters are left alone).  __syncthreads() does not wait
+// for them, so without this another wave's agent-scope release could write L2
+// back to memory before this wave's stores have reached L2.
+HKV_DEV void wait_stores() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 template <int KPT>
 __global__ void __launch_bounds__(kMBThreads)
 topk_mb_hist(const float* scores, int64_t P, int64_t s, int64_t keff, int64_t* out, int H,
-             MBWork w) {
+               MBWork w) {
   __shared__ MBShared sh;
   __shared__ int s_last;
   const int j = blockIdx.x, h = blockIdx.y, NB = gridDim.x, tid = threadIdx.x;
   const int n = (int)(P - s);
   const float* col = scores + (int64_t)h * P + s;  // candidate i is page s + i
   constexpr int slice = kMBThreads * KPT;
+  const int c0 = j * slice + tid * KPT;
+  // loads are unconditional (clamped index) so that all KPT are in flight at once
+  float kv[KPT];
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) kv[i] = col[c0 + i < n ? c0 + i : n - 1];
   // key range of the head (all pages, sinks included: a superset of the candidates')
   uint32_t mn = 0xffffffffu, mx = 0u;
   for (int b = tid; b < w.nmm; b += kMBThreads) {
@@ -913,26 +981,18 @@ topk_mb_hist(const float* scores, int64_t P, int64_t s, int64_t keff, int64_t* o
     mn = v.x < mn ? v.x : mn;
     mx = v.y > mx ? v.y : mx;
   }
-  mn = mb_reduce(mn, 0, sh.red);
-  mx = mb_reduce(mx, 1, sh.red);
+  for (int b = tid; b < kMBBins; b += kMBThreads) sh.hist[b] = 0u;  // ordered by mb_minmax's barriers
+  mb_minmax(mn, mx, sh.red);
   const uint32_t range = mx - mn;
   const int wbits = range ? 32 - __builtin_clz(range) : 0;
   const int sh1 = wbits > 12 ? wbits - 12 : 0;
-  for (int b = tid; b < kMBBins; b += kMBThreads) sh.hist[b] = 0u;
-  __syncthreads();
-  const int c0 = j * slice + tid * KPT;
-  // loads are unconditional (clamped index) so that all KPT are in flight at once
-  float kv[KPT];
+  auto bin_of = [&](uint32_t k) {
+    const uint32_t b0 = k < mn ? 0u : (k - mn) >> sh1;
+    return b0 < (uint32_t)kMBBins ? (int)b0 : kMBBins - 1;
+  };
 #pragma unroll
-  for (int i = 0; i < KPT; ++i) kv[i] = col[c0 + i < n ? c0 + i : n - 1];
-#pragma unroll
-  for (int i = 0; i < KPT; ++i) {
-    if (c0 + i < n) {
-      const uint32_t k = ukey(kv[i]);
-      const uint32_t b = k < mn ? 0u : (k - mn) >> sh1;
-      atomicAdd(&sh.hist[b < (uint32_t)kMBBins ? b : (uint32_t)(kMBBins - 1)], 1u);
-    }
-  }
+  for (int i = 0; i < KPT; ++i)
+    if (c0 + i < n) atomicAdd(&sh.hist[bin_of(ukey(kv[i]))], 1u);
   __syncthreads();
   uint32_t* gh = w.hist + ((int64_t)h * NB + j) * kMBBins;
   for (int b = tid; b < kMBBins; b += kMBThreads) gh[b] = sh.hist[b];
@@ -949,7 +1009,7 @@ topk_mb_hist(const float* scores, int64_t P, int64_t s, int64_t keff, int64_t* o
     for (int k = 0; k < 4; ++k) mine_l += sh.hist[kMBBins - 1 - 4 * tid - k];
     if (tid == 0) sh.bc[2] = 0u;  // ordered before the writes below by the scan's barriers
     uint32_t tot_l;
-    uint32_t above_l = mb_excl_scan(mine_l, sh.red, tot_l);
+    uint32_t above_l = mb_excl_scan(mine_l, sh.red[0], tot_l);
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const int b = kMBBins - 1 - 4 * tid - k;
@@ -967,8 +1027,7 @@ topk_mb_hist(const float* scores, int64_t P, int64_t s, int64_t keff, int64_t* o
     for (int i = 0; i < KPT; ++i) {
       if (c0 + i < n) {
         const uint32_t k = ukey(kv[i]);
-        const uint32_t b0 = k < mn ? 0u : (k - mn) >> sh1;
-        const int b = b0 < (uint32_t)kMBBins ? (int)b0 : kMBBins - 1;
+        const int b = bin_of(k);
         if (b >= wlo && b <= whi) {
           const uint32_t slot = atomicAdd(&sh.ncand, 1u);
           if (slot < (uint32_t)kMBWin) wc[slot] = ((unsigned long long)k << 32) | (uint32_t)~(uint32_t)(c0 + i);
@@ -984,6 +1043,7 @@ topk_mb_hist(const float* scores, int64_t P, int64_t s, int64_t keff, int64_t* o
       wm[3] = sh.ncand > (uint32_t)kMBWin ? 1 : 0;
     }
   }
+  wait_stores();
   __syncthreads();
   if (tid == 0) {
     __threadfence();  // release this slice's histogram and window
@@ -999,7 +1059,7 @@ topk_mb_hist(const float* scores, int64_t P, int64_t s, int64_t keff, int64_t* o
 
   // ---- last block of head h: the threshold
   // Thread t sums bins t + 1024 k4 over the slices, keeping each slice's value
-  // (per-slice counts above the threshold bin come from them).  The slices'
+  // (the slices' counts in the threshold bin come from them).  The slices'
   // windows are requested in the same round trip (up to 8 slices).
   constexpr int KB = kMBBins / kMBThreads;  // bins per thread
   const int NBc = NB < kMBMaxSlices ? NB : kMBMaxSlices;
@@ -1017,6 +1077,10 @@ topk_mb_hist(const float* scores, int64_t P, int64_t s, int64_t keff, int64_t* o
   for (int i = tid; i < NBc * 4; i += kMBThreads) sh.wm[i >> 2][i & 3] = w.wmeta[((int64_t)h * NB) * 4 + i];
   uint32_t hv[KB][8];  // slices j0..j0+7 of the thread's bins (the last group kept)
   for (int k4 = 0; k4 < KB; ++k4) sh.hist[k4 * kMBThreads + tid] = 0u;
+  if (tid == 0) {  // found below (defaults for safety)
+    sh.bc[0] = 0u;
+    sh.bc[1] = 0u;
+  }
   for (int j0 = 0; j0 < NBc; j0 += 8) {
 #pragma unroll
     for (int k4 = 0; k4 < KB; ++k4)
@@ -1040,7 +1104,7 @@ topk_mb_hist(const float* scores, int64_t P, int64_t s, int64_t keff, int64_t* o
 #pragma unroll
   for (int k = 0; k < 4; ++k) mine += sh.hist[kMBBins - 1 - 4 * tid - k];
   uint32_t tot;
-  uint32_t above = mb_excl_scan(mine, sh.red, tot);
+  uint32_t above = mb_excl_scan(mine, sh.red[0], tot);
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const int b = kMBBins - 1 - 4 * tid - k;
@@ -1055,7 +1119,9 @@ topk_mb_hist(const float* scores, int64_t P, int64_t s, int64_t keff, int64_t* o
   const uint32_t b1 = sh.bc[0], above1 = sh.bc[1], cnt1 = sh.hist[b1];
   const uint32_t r = need - above1;  // 1 <= r <= cnt1
   const uint32_t lo1 = mn + (b1 << sh1);
-  const uint32_t hi1 = lo1 + ((sh1 >= 32 ? 0xffffffffu : (1u << sh1)) - 1u);
+  // last key of bin b1, saturated (the top bin can end past 2^32 - 1)
+  const uint64_t hi1w = (uint64_t)lo1 + ((1ull << sh1) - 1ull);
+  const uint32_t hi1 = hi1w > 0xffffffffull ? 0xffffffffu : (uint32_t)hi1w;
   if (cnt1 > (uint32_t)kMBCand) {
     // a huge bin: the single-block selector over the whole column
     __shared__ SelShared ssh;
@@ -1064,10 +1130,25 @@ topk_mb_hist(const float* scores, int64_t P, int64_t s, int64_t keff, int64_t* o
     if (tid == 0) w.thr[h * 4 + 2] = 1u;
     return;
   }
-  for (int k = tid; k < kMBMaxSlices; k += kMBThreads) { sh.sl_gt[k] = 0; sh.sl_eq[k] = 0; }
-  if (tid == 0) sh.ncand = 0u;
-  __syncthreads();
-  // per-slice counts of keys in bins above b1
+  // the slices' counts in bin b1 (known for up to 8 slices: the last group in hv)
+  if (NBc <= 8 && tid == (int)(b1 % kMBThreads)) {
+    const int k4 = (int)(b1 / kMBThreads);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      uint32_t v = 0;
+#pragma unroll
+      for (int kk = 0; kk < KB; ++kk) v = kk == k4 ? hv[kk][u] : v;
+      if (u < NBc) sh.sl_b1[u] = v;
+    }
+  }
+  if (tid == 0) {
+    sh.ncand = 0u;
+    sh.bc[3] = 0u;
+    sh.bc[4] = 0xffffffffu;
+  }
+  if (tid < kMBMaxSlices) sh.sl_eq[tid] = 0;
+  // per-slice counts of keys in bins above b1: thread sums, wave sums, one
+  // exchange through LDS per group of 8 slices
   for (int j0 = 0; j0 < NBc; j0 += 8) {
     if (j0 + 8 < NBc || j0 > 0) {  // more than 8 slices: reload this group
 #pragma unroll
@@ -1083,22 +1164,18 @@ topk_mb_hist(const float* scores, int64_t P, int64_t s, int64_t keff, int64_t* o
       uint32_t c = 0;
 #pragma unroll
       for (int k4 = 0; k4 < KB; ++k4) c += (uint32_t)(k4 * kMBThreads + tid) > b1 ? hv[k4][u] : 0u;
-      c = mb_reduce(c, 2, sh.red);
-      if (tid == 0 && j0 + u < NBc) sh.sl_gt[j0 + u] = (int)c;
+      c = wave_sum_u(c);
+      if ((tid & 63) == 0) sh.slw[tid >> 6][u] = c;
     }
-  }
-  // the slices' counts in bin b1 (known for up to 8 slices: the last group in hv)
-  if (NBc <= 8 && tid == (int)(b1 % kMBThreads)) {
-    const int k4 = (int)(b1 / kMBThreads);
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      uint32_t v = 0;
-#pragma unroll
-      for (int kk = 0; kk < KB; ++kk) v = kk == k4 ? hv[kk][u] : v;
-      if (u < NBc) sh.sl_b1[u] = v;
+    __syncthreads();
+    if (tid < 8 && j0 + tid < NBc) {
+      uint32_t t = 0;
+      for (int i = 0; i < kMBWaves; ++i) t += sh.slw[i][tid];
+      sh.sl_gt[j0 + tid] = (int)t;
     }
+    __syncthreads();
   }
-  __syncthreads();
+
   // the windows hold every key of bin b1 if b1 lies in every window of a slice
   // with keys there (and no window overflowed)
   bool use_win = win_regs;
@@ -1121,140 +1198,184 @@ topk_mb_hist(const float* scores, int64_t P, int64_t s, int64_t keff, int64_t* o
       }
     }
   } else {
-  // candidates: the keys of bin b1 (re-read, the next 16 in flight while 16 are checked)
-  const int per = (n + kMBThreads - 1) / kMBThreads;
-  constexpr int RU = 16;
-  uint32_t ka[RU], kb[RU];
-  auto load_keys = [&](int i0, uint32_t (&kk)[RU]) {
+    // candidates: the keys of bin b1 (re-read, the next 16 in flight while 16 are checked)
+    const int per = (n + kMBThreads - 1) / kMBThreads;
+    constexpr int RU = 16;
+    uint32_t ka[RU], kb[RU];
+    auto load_keys = [&](int i0, uint32_t (&kk)[RU]) {
 #pragma unroll
-    for (int u = 0; u < RU; ++u) {
-      const int idx = (i0 + u) * kMBThreads + tid;
-      kk[u] = ukey(col[idx < n ? idx : n - 1]);  // validity is checked where kk is used
-    }
-  };
-  auto scan_keys = [&](int i0, const uint32_t (&kk)[RU]) {
-#pragma unroll
-    for (int u = 0; u < RU; ++u) {
-      const int idx = (i0 + u) * kMBThreads + tid;
-      const uint32_t k = kk[u];
-      if (idx < n && k >= lo1 && k <= hi1) {
-        const uint32_t slot = atomicAdd(&sh.ncand, 1u);
-        if (slot < (uint32_t)kMBCand)
-          sh.cand[slot] = ((unsigned long long)k << 32) | (uint32_t)~(uint32_t)idx;
+      for (int u = 0; u < RU; ++u) {
+        const int idx = (i0 + u) * kMBThreads + tid;
+        kk[u] = ukey(col[idx < n ? idx : n - 1]);  // validity is checked where kk is used
       }
+    };
+    auto scan_keys = [&](int i0, const uint32_t (&kk)[RU]) {
+#pragma unroll
+      for (int u = 0; u < RU; ++u) {
+        const int idx = (i0 + u) * kMBThreads + tid;
+        const uint32_t k = kk[u];
+        if (idx < n && k >= lo1 && k <= hi1) {
+          const uint32_t slot = atomicAdd(&sh.ncand, 1u);
+          if (slot < (uint32_t)kMBCand)
+            sh.cand[slot] = ((unsigned long long)k << 32) | (uint32_t)~(uint32_t)idx;
+        }
+      }
+    };
+    load_keys(0, ka);
+    for (int i0 = 0; i0 < per; i0 += 2 * RU) {
+      load_keys(i0 + RU, kb);
+      scan_keys(i0, ka);
+      if (i0 + RU >= per) break;
+      load_keys(i0 + 2 * RU, ka);
+      scan_keys(i0 + RU, kb);
     }
-  };
-  load_keys(0, ka);
-  for (int i0 = 0; i0 < per; i0 += 2 * RU) {
-    load_keys(i0 + RU, kb);
-    scan_keys(i0, ka);
-    if (i0 + RU >= per) break;
-    load_keys(i0 + 2 * RU, ka);
-    scan_keys(i0 + RU, kb);
-  }
   }
   __syncthreads();
   const uint32_t nc = sh.ncand < (uint32_t)kMBCand ? sh.ncand : (uint32_t)kMBCand;  // == cnt1
+  const uint32_t rr = r < 1u ? 1u : (r > nc ? nc : r);  // r is in [1, nc]; clamped for safety
+  // T = the rr-th largest candidate key; ngt = candidates above T
+  uint32_t T, ngt;
   if (nc <= (uint32_t)kMBThreads) {
-    // few candidates: each finds its rank (key descending, page ascending) directly
-    const unsigned long long mine_c = tid < (int)nc ? sh.cand[tid] : 0ull;
-    uint32_t rank = 0;
-    for (uint32_t u = 0; u < nc; ++u) rank += sh.cand[u] > mine_c ? 1u : 0u;
+    // few candidates: a candidate's key is T iff fewer than rr keys exceed it
+    // and at least rr keys are >= it
+    const uint32_t* ck = reinterpret_cast<const uint32_t*>(sh.cand);  // key of candidate u: ck[2u + 1]
+    const uint32_t mk = tid < (int)nc ? ck[2 * tid + 1] : 0u;
+    uint32_t gtc = 0, gec = 0, u = 0;
+    for (; u + 8 <= nc; u += 8) {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const uint32_t k = ck[2 * (u + q) + 1];
+        gtc += k > mk ? 1u : 0u;
+        gec += k >= mk ? 1u : 0u;
+      }
+    }
+    for (; u < nc; ++u) {
+      const uint32_t k = ck[2 * u + 1];
+      gtc += k > mk ? 1u : 0u;
+      gec += k >= mk ? 1u : 0u;
+    }
+    if (tid < (int)nc && gtc < rr && rr <= gec) {  // every such candidate has key T
+      sh.bc[4] = mk;
+      sh.bc[3] = gtc;
+    }
     __syncthreads();
-    if (tid < (int)nc) sh.cand[rank] = mine_c;  // ranks are distinct: a permutation
-    __syncthreads();
+    T = sh.bc[4];
+    ngt = sh.bc[3];
   } else {
-  uint32_t np2 = 1;
-  while (np2 < nc) np2 <<= 1;
-  for (uint32_t i = nc + tid; i < np2; i += kMBThreads) sh.cand[i] = 0ull;
-  __syncthreads();
-  for (uint32_t k = 2; k <= np2; k <<= 1) {
-    for (uint32_t jj = k >> 1; jj > 0; jj >>= 1) {
-      for (uint32_t i = tid; i < np2; i += kMBThreads) {
-        const uint32_t ixj = i ^ jj;
-        if (ixj > i) {
-          const unsigned long long a = sh.cand[i], b = sh.cand[ixj];
-          const bool desc = (i & k) == 0;
-          if (desc ? (a < b) : (a > b)) {
-            sh.cand[i] = b;
-            sh.cand[ixj] = a;
+    // bitonic sort, key descending, page ascending
+    uint32_t np2 = 1;
+    while (np2 < nc) np2 <<= 1;
+    for (uint32_t i = nc + tid; i < np2; i += kMBThreads) sh.cand[i] = 0ull;
+    __syncthreads();
+    for (uint32_t k = 2; k <= np2; k <<= 1) {
+      for (uint32_t jj = k >> 1; jj > 0; jj >>= 1) {
+        for (uint32_t i = tid; i < np2; i += kMBThreads) {
+          const uint32_t ixj = i ^ jj;
+          if (ixj > i) {
+            const unsigned long long a = sh.cand[i], b = sh.cand[ixj];
+            const bool desc = (i & k) == 0;
+            if (desc ? (a < b) : (a > b)) {
+              sh.cand[i] = b;
+              sh.cand[ixj] = a;
+            }
           }
         }
+        __syncthreads();
       }
-      __syncthreads();
     }
+    T = (uint32_t)(sh.cand[rr - 1] >> 32);
+    for (uint32_t i = tid; i < nc; i += kMBThreads) {  // the first T-equal candidate in rank order
+      const uint32_t k = (uint32_t)(sh.cand[i] >> 32);
+      if (k == T && (i == 0 || (uint32_t)(sh.cand[i - 1] >> 32) > T)) sh.bc[3] = i;
+    }
+    __syncthreads();
+    ngt = sh.bc[3];
   }
-  }
-  const uint32_t rr = r < 1u ? 1u : (r > nc ? nc : r);  // r is in [1, nc]; clamped for safety
-  const uint32_t T = nc ? (uint32_t)(sh.cand[rr - 1] >> 32) : 0xffffffffu;
-  uint32_t gtc = 0;
+  const uint32_t need_eq = rr - ngt;  // T-equal keys taken, lowest pages first
+  // the slices' candidates above and equal to T
   for (uint32_t i = tid; i < nc; i += kMBThreads) {
     const unsigned long long v = sh.cand[i];
     const uint32_t k = (uint32_t)(v >> 32);
     const int idx = (int)~(uint32_t)v;
-    gtc += k > T ? 1u : 0u;
     if (k > T) atomicAdd(&sh.sl_gt[idx / slice], 1);
     else if (k == T) atomicAdd(&sh.sl_eq[idx / slice], 1);
   }
-  const uint32_t ngt = mb_reduce(gtc, 2, sh.red);  // candidates above T
   __syncthreads();
   if (tid == 0) {
-    const int need_eq = (int)(rr - ngt);
     int outp = (int)s, eqb = 0;
     for (int jj = 0; jj < NB; ++jj) {
       w.meta[((int64_t)h * NB + jj) * 2] = outp;
       w.meta[((int64_t)h * NB + jj) * 2 + 1] = eqb;
       const int e = sh.sl_eq[jj];
-      const int take = eqb >= need_eq ? 0 : (need_eq - eqb < e ? need_eq - eqb : e);
+      const int take = eqb >= (int)need_eq ? 0 : ((int)need_eq - eqb < e ? (int)need_eq - eqb : e);
       outp += sh.sl_gt[jj] + take;
       eqb += e;
     }
     w.thr[h * 4] = T;
-    w.thr[h * 4 + 1] = (uint32_t)need_eq;
+    w.thr[h * 4 + 1] = need_eq;
     w.thr[h * 4 + 2] = 0u;
+    w.thr[h * 4 + 3] = (uint32_t)(s + keff);
   }
 }
 
+// Block j writes the selected pages of slice j: every key > T and, of the
+// keys == T, those whose rank among the head's T-equal keys is below the
+// number taken.  Positions come from one block scan of the per-thread counts,
+// (== T) << 16 | (> T) (at most kMBThreads * KPT each).  The pages are staged
+// in LDS in output order and written by consecutive threads: the column of
+// head h is strided by H, so each 128-byte line is written with one request
+// instead of one per page.
 template <int KPT>
 __global__ void __launch_bounds__(kMBThreads)
 topk_mb_write(const float* scores, int64_t P, int64_t s, int64_t* out, int H, MBWork w) {
+  constexpr uint32_t kStage = 8192;
   __shared__ uint32_t red[kMBWaves];
+  __shared__ uint32_t stage[kStage];
   const int j = blockIdx.x, h = blockIdx.y, NB = gridDim.x, tid = threadIdx.x;
-  if (j == 0)
-    for (int64_t i = tid; i < s; i += kMBThreads) out[i * H + h] = i;
-  if (w.thr[h * 4 + 2]) return;  // written by the fallback
   const int n = (int)(P - s);
   const float* col = scores + (int64_t)h * P + s;
-  const uint32_t T = w.thr[h * 4];
-  const int need_eq = (int)w.thr[h * 4 + 1];
-  const int outp0 = w.meta[((int64_t)h * NB + j) * 2];
-  const int eqb0 = w.meta[((int64_t)h * NB + j) * 2 + 1];
   const int c0 = j * (kMBThreads * KPT) + tid * KPT;
-  uint32_t key[KPT];
-  uint32_t gt = 0, eq = 0;
+  // the keys, the threshold and the slice's offsets are requested together
   float kv[KPT];
 #pragma unroll
-  for (int i = 0; i < KPT; ++i) kv[i] = col[c0 + i < n ? c0 + i : n - 1];  // all in flight
+  for (int i = 0; i < KPT; ++i) kv[i] = col[c0 + i < n ? c0 + i : n - 1];
+  const uint4 th = *reinterpret_cast<const uint4*>(w.thr + h * 4);
+  const int2 me = *reinterpret_cast<const int2*>(w.meta + ((int64_t)h * NB + j) * 2);
+  if (j == 0)
+    for (int64_t i = tid; i < s; i += kMBThreads) out[i * H + h] = i;
+  if (th.z) return;  // written by the fallback
+  const uint32_t T = th.x, need_eq = th.y, row_end = th.w;
+  auto taken = [&](uint32_t eqs) { return eqs < need_eq ? eqs : need_eq; };
+  uint32_t key[KPT];
+  uint32_t gt = 0, eq = 0;
 #pragma unroll
   for (int i = 0; i < KPT; ++i) {
-    const int idx = c0 + i;
-    key[i] = idx < n ? ukey(kv[i]) : 0u;  // 0: below every real key
+    key[i] = c0 + i < n ? ukey(kv[i]) : 0u;  // 0: below every real key
     gt += key[i] > T ? 1u : 0u;
-    eq += (idx < n && key[i] == T) ? 1u : 0u;
+    eq += (c0 + i < n && key[i] == T) ? 1u : 0u;
   }
   uint32_t tot;
-  const int eq_rank0 = eqb0 + (int)mb_excl_scan(eq, red, tot);
-  int take = need_eq - eq_rank0;
-  take = take < 0 ? 0 : (take > (int)eq ? (int)eq : take);
-  int pos = outp0 + (int)mb_excl_scan(gt + (uint32_t)take, red, tot);
-  int eqr = eq_rank0;
+  const uint32_t pre = mb_excl_scan(gt | (eq << 16), red, tot);
+  const uint32_t eqb0 = (uint32_t)me.y;
+  const uint32_t nsel = (tot & 0xffffu) + taken(eqb0 + (tot >> 16)) - taken(eqb0);
+  const uint32_t rel0 = (pre & 0xffffu) + taken(eqb0 + (pre >> 16)) - taken(eqb0);
+  for (uint32_t sub = 0; sub < nsel; sub += kStage) {
+    uint32_t rel = rel0, eqr = eqb0 + (pre >> 16);
 #pragma unroll
-  for (int i = 0; i < KPT; ++i) {
-    const int idx = c0 + i;
-    const bool is_eq = idx < n && key[i] == T;
-    const bool sel = key[i] > T || (is_eq && eqr < need_eq);
-    eqr += is_eq ? 1 : 0;
-    if (sel) out[(int64_t)(pos++) * H + h] = s + idx;
+    for (int i = 0; i < KPT; ++i) {
+      const bool is_eq = c0 + i < n && key[i] == T;
+      const bool sel = key[i] > T || (is_eq && eqr < need_eq);
+      eqr += is_eq ? 1u : 0u;
+      if (sel && rel - sub < kStage) stage[rel - sub] = (uint32_t)(s + c0 + i);
+      rel += sel ? 1u : 0u;
+    }
+    __syncthreads();
+    const uint32_t cnt = nsel - sub < kStage ? nsel - sub : kStage;
+    for (uint32_t i = tid; i < cnt; i += kMBThreads) {
+      const uint32_t r = (uint32_t)me.x + sub + i;
+      if (r < row_end) out[(int64_t)r * H + h] = (int64_t)stage[i];
+    }
+    __syncthreads();
   }
 }
 
@@ -1328,7 +1449,9 @@ int page_bound(const void* q, int q_dtype, int Hq, const void* kmin, const void*
   const size_t lds = sizeof(float) * 2 * H * D;
   if (lds > 64 * 1024) return HKV_ERR_SHAPE;
   const int G = D / 8;
-  if (!page_ids && k_dtype == HKV_DT_F16 && D % 8 == 0 && (G & (G - 1)) == 0 && G <= 64) {
+  // (the fp16 kernel indexes elements r * D in 32 bits)
+  if (!page_ids && k_dtype == HKV_DT_F16 && D % 8 == 0 && (G & (G - 1)) == 0 && G <= 64 &&
+      rows * D < ((int64_t)1 << 32)) {
     const int64_t span = (int64_t)(256 / G) * kBoundUnrollF16;
     const unsigned grid =
         (unsigned)std::min<int64_t>((rows + span - 1) / span, (int64_t)num_cus() * 4);
@@ -1647,7 +1770,7 @@ extern "C" int hkv_quest_select_ragged(const void* q, int q_dtype, int B, int Hq
   sg.off[B] = page_offsets[B];
   for (int b = 0; b <= B; ++b) sg.out_off[b] = out_offsets[b];
   const int64_t Ptot = page_offsets[B];
-  if (Ptot * H >= ((int64_t)1 << 31)) return HKV_ERR_SHAPE;
+  if (Ptot * H >= ((int64_t)1 << 31) || Ptot * H * D >= ((int64_t)1 << 32)) return HKV_ERR_SHAPE;
   if (Ptot == 0) return HKV_OK;
   if (!q || !kmin || !kmax || !scores || (out_offsets[B] > 0 && !out)) return HKV_ERR_ARG;
   if (((uintptr_t)kmin | (uintptr_t)kmax) & 15u) return HKV_ERR_ARG;

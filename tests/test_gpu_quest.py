@@ -151,6 +151,8 @@ def test_fused_select_small_and_per_kv_head(dev):
     (50000, 1, 3, 12345, 7, "ties"),       # few distinct scores: big equal runs
     (70000, 4, 7, 17500, 4, "equal"),      # all scores equal: the huge-bin fallback
     (600000, 2, 7, 150000, 4, "normal"),   # many slices (KPT 32)
+    (65536, 2, 7, 100, 4, "nan"),          # NaN ranks highest: the threshold in the top bin
+    (65536, 2, 7, 5000, 1, "nan"),         # NaN present (coarse bins), one sink: unaligned column
 ])
 def test_multiblock_select_vs_oracle(dev, P, H, g, k, s, mode):
     """The multi-block top-K (fp16 statistics, large columns) against the
@@ -168,10 +170,17 @@ def test_multiblock_select_vs_oracle(dev, P, H, g, k, s, mode):
     else:
         mn = RNG.standard_normal((P, H, D)).astype(np.float16)
         mx = (mn + np.abs(RNG.standard_normal((P, H, D))).astype(np.float16)).astype(np.float16)
+    if mode == "nan":  # 300 pages whose bound is NaN
+        bad = RNG.choice(P, 300, replace=False)
+        mn[bad, :, 5] = np.nan
+        mx[bad, :, 5] = np.nan
     q = RNG.standard_normal((H * g, D)).astype(np.float16)
     want_b = O.page_bound_group(q, mn.astype(np.float32), mx.astype(np.float32), g)
     want = O.topk_sinks(want_b, k, s)
+    nan = np.isnan(want_b)
     for _ in range(2):
         idx, scores = quest_select(_t(q, dev), _t(mn, dev), _t(mx, dev), k, s)
-        assert np.array_equal(scores.cpu().numpy().T.view(np.uint32), want_b.view(np.uint32))
+        got_b = scores.cpu().numpy().T
+        assert np.array_equal(np.isnan(got_b), nan)  # NaN payloads are not compared
+        assert np.array_equal(got_b[~nan].view(np.uint32), want_b[~nan].view(np.uint32))
         assert np.array_equal(idx.cpu().numpy(), want)
