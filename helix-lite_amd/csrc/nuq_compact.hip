@@ -432,6 +432,181 @@ unpack_compact_kernel(const uint8_t* __restrict__ packed, const int32_t* __restr
   }
 }
 
+// Unpack for D = 128 (16 lanes per row) when H is a power of two dividing the
+// 16 rows of a wave tile, with the same three-stage load pipeline as
+// unpack_compact_kernel.  A lane's head and token follow from its row by a
+// mask and a shift, the tile's rows are addressed from a uniform base row
+// (clamped at the end), codes are bit fields of one word, and the K poles sit
+// in LDS as [h][level][d] with padded rows (kU128SC, kU128SH halfwords) so
+// that the heads of a pass and the two halves of a row use different banks.
+constexpr int kU128SC = 130;               // halfwords per (head, level) row of the K poles
+constexpr int kU128SH = 16 * kU128SC + 2;  // halfwords per head
+
+template <bool PT, int BITS>
+__global__ void __launch_bounds__(kThreads)
+unpack_d128_kernel(const uint8_t* __restrict__ packed, const int32_t* __restrict__ row_ptr,
+                   const uint8_t* __restrict__ col, const uint16_t* __restrict__ val, int64_t cap,
+                   int64_t nrows, int lgH, hkv_nuq_scales sc, uint16_t* __restrict__ out,
+                   int64_t nwtiles) {
+  constexpr int D = 128, RW = 4, WR = RW * kUPasses, RB = D * BITS / 8, NW = kThreads / 64;
+  const int H = 1 << lgH;
+  extern __shared__ uint16_t dyn[];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int cg = lane & 15, rw = lane >> 4;
+  uint16_t* seg = dyn + wv * (WR * D);
+  uint16_t* prow = dyn + NW * WR * D + wv * (WR * 16);  // PT: poles of each row
+  uint16_t* kp = dyn + NW * WR * D;                     // K: poles [h][level][d], padded
+  const hkv_table_t* tabs = (const hkv_table_t*)sc.tables;
+  if constexpr (!PT) {
+    for (int i = tid; i < H * D; i += kThreads) {
+      const uint4* src = reinterpret_cast<const uint4*>(tabs[i].pf16);
+      const uint4 a = src[0], b = src[1];
+      const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+      const int h = i >> 7, d = i & (D - 1);
+#pragma unroll
+      for (int l = 0; l < 16; ++l)
+        kp[h * kU128SH + l * kU128SC + d] = (uint16_t)(w[l >> 1] >> (16 * (l & 1)));
+    }
+    __syncthreads();
+  }
+  // The tile's base row (clamped to the last row past the end) and the last
+  // valid row offset within it.
+  auto tile_base = [&](int64_t wt, int64_t& rbase, int& lim) {
+    const int64_t r0 = wt * WR;
+    rbase = r0 < nrows ? r0 : nrows - 1;
+    const int64_t rest = nrows - 1 - rbase;
+    lim = rest < WR - 1 ? (int)rest : WR - 1;
+  };
+  struct TileLoad {
+    uint32_t cw[kUPasses];
+    int2 rp[kUPasses];
+    uint32_t pv[kUPasses];  // PT: pole cg of the row
+  };
+  struct TileCsr {
+    uint32_t c[kUPasses], v[kUPasses];  // entry ra + cg of each pass's row
+  };
+  const int64_t nwaves = (int64_t)gridDim.x * NW;
+  const int rows32 = (int)sc.rows;  // the host checks H * rows * 80 < 2^31 for this kernel
+  auto load_tile = [&](int64_t wt, TileLoad& L) {
+    int64_t rbase;
+    int lim;
+    tile_base(wt, rbase, lim);
+    const uint8_t* pk = packed + rbase * RB;
+    const int32_t* rp = row_ptr + rbase;
+    // PT: token of row o is t0 + (o >> lgH) and its head o & (H - 1) (rbase
+    // is a multiple of H for a tile in range; past the end, o = 0 and the
+    // loads stay at the last row)
+    const int64_t t0 = rbase >> lgH;
+    const int64_t p0 = sc.pos_offset + t0;  // position of token t0 without a position array
+    const int p0c = p0 < -(int64_t)WR ? -WR : (p0 > (int64_t)rows32 ? rows32 : (int)p0);
+#pragma unroll
+    for (int p = 0; p < kUPasses; ++p) {
+      const int o = p * RW + rw < lim ? p * RW + rw : lim;
+      if constexpr (BITS == 4) L.cw[p] = *reinterpret_cast<const uint32_t*>(pk + o * RB + 4 * cg);
+      else L.cw[p] = *reinterpret_cast<const uint16_t*>(pk + o * RB + 2 * cg);
+      L.rp[p] = *reinterpret_cast<const int2*>(rp + o);
+      if constexpr (PT) {
+        const int k = o >> lgH, h = o & (H - 1);
+        int pos;
+        if (sc.positions) {
+          const int64_t ap = sc.positions[t0 + k];
+          pos = ap < 0 ? 0 : (ap > rows32 - 1 ? rows32 - 1 : (int)ap);
+        } else {
+          pos = p0c + k;
+          pos = pos < 0 ? 0 : (pos > rows32 - 1 ? rows32 - 1 : pos);
+        }
+        const uint32_t off = (uint32_t)(h * rows32 + pos) * (uint32_t)sizeof(hkv_table_t) + 32u + 2u * cg;
+        L.pv[p] = *reinterpret_cast<const uint16_t*>(reinterpret_cast<const char*>(tabs) + off);
+      }
+    }
+  };
+  auto load_csr = [&](const TileLoad& L, TileCsr& C) {
+    if (cap <= 0) return;
+#pragma unroll
+    for (int p = 0; p < kUPasses; ++p) {
+      int64_t i = (int64_t)(L.rp[p].x > 0 ? L.rp[p].x : 0) + cg;
+      i = i < cap ? i : cap - 1;
+      C.c[p] = col[i];
+      C.v[p] = val[i];
+    }
+  };
+  auto process = [&](int64_t wt, const TileLoad& L, const TileCsr& C) {
+    int64_t rbase;
+    int lim;
+    tile_base(wt, rbase, lim);  // rbase = wt * WR: the tile is in range
+    if constexpr (PT) {
+#pragma unroll
+      for (int p = 0; p < kUPasses; ++p) prow[(p * RW + rw) * 16 + cg] = (uint16_t)L.pv[p];
+      wave_sync();
+    }
+#pragma unroll
+    for (int p = 0; p < kUPasses; ++p) {
+      const int rr = p * RW + rw;
+      const uint16_t* lb;
+      if constexpr (PT) {
+        lb = prow + rr * 16;
+      } else {
+        lb = kp + (rr & (H - 1)) * kU128SH + 8 * cg;  // rbase is a multiple of H
+      }
+      uint32_t res[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uint32_t pr = 0;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          const int e = 2 * j + k;
+          const uint32_t c = (L.cw[p] >> (BITS * e)) & ((1u << BITS) - 1u);
+          const uint16_t v = PT ? lb[c] : lb[c * kU128SC + e];
+          pr |= (uint32_t)v << (16 * k);
+        }
+        res[j] = pr;
+      }
+      *reinterpret_cast<uint4*>(seg + rr * D + 8 * cg) = make_uint4(res[0], res[1], res[2], res[3]);
+    }
+    wave_sync();
+#pragma unroll
+    for (int p = 0; p < kUPasses; ++p) {
+      const int rr = p * RW + rw;
+      const int32_t lo = L.rp[p].x > 0 ? L.rp[p].x : 0;
+      const int32_t hi = (int64_t)L.rp[p].y < cap ? L.rp[p].y : (int32_t)cap;
+      if (lo + cg < hi && C.c[p] < (uint32_t)D) seg[rr * D + C.c[p]] = (uint16_t)C.v[p];
+      for (int32_t i = lo + cg + 16; i < hi; i += 16) {  // rows with more than 16 outliers
+        const uint32_t d = col[i];
+        if (d < (uint32_t)D) seg[rr * D + d] = val[i];
+      }
+    }
+    wave_sync();
+    uint16_t* ob = out + rbase * D;
+#pragma unroll
+    for (int p = 0; p < kUPasses; ++p) {
+      const int rr = p * RW + rw;
+      if (rr > lim) continue;
+      *reinterpret_cast<uint4*>(ob + rr * D + 8 * cg) = *reinterpret_cast<const uint4*>(seg + rr * D + 8 * cg);
+    }
+    wave_sync();
+  };
+  const int64_t wt0 = (int64_t)blockIdx.x * NW + wv;
+  if (wt0 >= nwtiles) return;
+  TileLoad L0, L1, L2;
+  TileCsr C0, C1, C2;
+  load_tile(wt0, L0);
+  load_tile(wt0 + nwaves, L1);
+  load_csr(L0, C0);
+  auto step = [&](int64_t wt, const TileLoad& Lc, const TileCsr& Cc, const TileLoad& Ln, TileCsr& Cn,
+                  TileLoad& Lw) {
+    load_tile(wt + 2 * nwaves, Lw);
+    load_csr(Ln, Cn);
+    process(wt, Lc, Cc);
+  };
+  for (int64_t wt = wt0; wt < nwtiles; wt += 3 * nwaves) {
+    step(wt, L0, C0, L1, C1, L2);
+    if (wt + nwaves >= nwtiles) break;
+    step(wt + nwaves, L1, C1, L2, C2, L0);
+    if (wt + 2 * nwaves >= nwtiles) break;
+    step(wt + 2 * nwaves, L2, C2, L0, C0, L1);
+  }
+}
+
 __global__ void write_zero_rowptr(int32_t* row_ptr) { row_ptr[0] = 0; }
 
 bool pow2_G(int D) { return D % 8 == 0 && D >= 8 && D <= 256 && ((D / 8) & (D / 8 - 1)) == 0; }
@@ -635,6 +810,26 @@ extern "C" int hkv_nuq_unpack_compact(const void* packed, const int32_t* row_ptr
   const size_t kpole_bytes = (size_t)H * 16 * D * 2;
   auto pk = (const uint8_t*)packed;
   auto o = (uint16_t*)out;
+  const int lgH = __builtin_ctz((unsigned)H);
+  const bool h_pow2 = (H & (H - 1)) == 0 && H <= 16;
+  if (D == 128 && h_pow2 && (sc.per_token || H <= 8) &&
+      (!sc.per_token || (int64_t)H * sc.rows * (int64_t)sizeof(hkv_table_t) < ((int64_t)1 << 31))) {
+    // the specialised kernel (the tile's 16 rows hold whole tokens)
+    const size_t lds = seg_bytes + (sc.per_token ? (size_t)NW * WR * 16 * 2 : (size_t)H * kU128SH * 2);
+#define HKV_D128(PT_, B_)                                                                          \
+  hipLaunchKernelGGL((unpack_d128_kernel<PT_, B_>), dim3(grid), dim3(kThreads), lds, s, pk, row_ptr, \
+                     col, val, capacity, nrows, lgH, sc, o, nwtiles)
+    if (sc.per_token) {
+      if (bits == 4) HKV_D128(true, 4);
+      else HKV_D128(true, 2);
+    } else {
+      if (bits == 4) HKV_D128(false, 4);
+      else HKV_D128(false, 2);
+    }
+#undef HKV_D128
+    HKV_CHECK_LAUNCH();
+    return HKV_OK;
+  }
 #define HKV_UARGS G, grid, lds, s, pk, row_ptr, col, val, capacity, nrows, H, sc, o, nwtiles
   if (sc.per_token) {
     const size_t lds = seg_bytes + (size_t)NW * WR * 16 * 2;

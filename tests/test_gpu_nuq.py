@@ -280,6 +280,44 @@ def test_compact_many_tiles_vs_oracle(dev, per_token, L):
     assert np.array_equal(_bits(out), want)
 
 
+@pytest.mark.parametrize("H,per_token,L,T", [(1, False, 16, 257), (2, False, 4, 129), (8, False, 16, 333),
+                                          (8, True, 16, 333), (16, True, 4, 77), (2, True, 16, 5)])
+def test_compact_unpack_heads_and_positions(dev, H, per_token, L, T):
+    """D = 128 unpack for every power-of-two head count, partial last tiles,
+    and per-token rows from explicit positions, some outside the calibrated
+    rows (clamped), and from a negative offset."""
+    from helix_kv.ops import NuqLayerTables, nuq_pack_compact, nuq_unpack_compact
+
+    D = 128
+    bits = 2 if L <= 4 else 4
+    x = RNG.standard_t(3, (T, H, D)).astype(np.float16)
+    rows = D if not per_token else 40
+    poles = np.sort(RNG.standard_normal((H, rows, L)), axis=-1).astype(np.float16)
+    up = RNG.uniform(1.0, 2.5, (H, rows)).astype(np.float16)
+    t = NuqLayerTables(_t(poles, dev), _t(up, dev), _t(-up, dev), per_token=per_token)
+    f32 = [a.astype(np.float32) for a in (poles, up, -up)]
+    cases = [("none", None)]
+    if per_token:
+        cases = [("array", RNG.integers(-20, rows + 20, T)), ("offset", np.arange(T) - 7)]
+    for kind, pos in cases:
+        if per_token:
+            wc, wv, wm = O.pack_v(x, *f32, positions=pos)
+        else:
+            wc, wv, wm = O.pack_k(x, *f32)
+        want = O.unpack(wc, wv, wm, f32[0], "v" if per_token else "k", positions=pos)
+        if kind == "offset":  # the same rows from an offset
+            cc = nuq_pack_compact(_t(x, dev), t, bits, pos_offset=-7)
+            got = nuq_unpack_compact(cc, t, pos_offset=-7)
+        else:
+            kw = {} if pos is None else dict(positions=torch.from_numpy(pos))
+            cc = nuq_pack_compact(_t(x, dev), t, bits, **kw)
+            got = nuq_unpack_compact(cc, t, **kw)
+        pk, rp, col, val = O.pack_compact(wc, wv, wm, bits)
+        assert np.array_equal(cc.packed.cpu().numpy(), pk)
+        assert np.array_equal(cc.row_ptr.cpu().numpy(), rp)
+        assert np.array_equal(_bits(got), want)
+
+
 def test_compact_unpack_respects_capacity(dev):
     """CSR entries beyond the col/val capacity are never read: those outliers
     decode as their poles, everything else is unchanged."""
