@@ -433,14 +433,16 @@ unpack_compact_kernel(const uint8_t* __restrict__ packed, const int32_t* __restr
 }
 
 // Unpack for D = 128 (16 lanes per row) when H is a power of two dividing the
-// 16 rows of a wave tile, with the same three-stage load pipeline as
+// rows of a wave tile, with the same three-stage load pipeline as
 // unpack_compact_kernel.  A lane's head and token follow from its row by a
 // mask and a shift, the tile's rows are addressed from a uniform base row
 // (clamped at the end), codes are bit fields of one word, and the K poles sit
-// in LDS as [h][level][d] with padded rows (kU128SC, kU128SH halfwords) so
+// in LDS as [h][level][d] with padded rows (kU128SC, u128_head halfwords) so
 // that the heads of a pass and the two halves of a row use different banks.
-constexpr int kU128SC = 130;               // halfwords per (head, level) row of the K poles
-constexpr int kU128SH = 16 * kU128SC + 2;  // halfwords per head
+constexpr int kU128Passes = 2;             // passes of 4 rows per wave tile
+constexpr int kU128SC = 130;  // halfwords per (head, level) row of the K poles
+// halfwords per head of the K poles (levels rows of kU128SC, skewed by 2)
+__host__ __device__ constexpr int u128_head(int levels) { return levels * kU128SC + 2; }
 
 template <bool PT, int BITS>
 __global__ void __launch_bounds__(kThreads)
@@ -448,10 +450,13 @@ unpack_d128_kernel(const uint8_t* __restrict__ packed, const int32_t* __restrict
                    const uint8_t* __restrict__ col, const uint16_t* __restrict__ val, int64_t cap,
                    int64_t nrows, int lgH, hkv_nuq_scales sc, uint16_t* __restrict__ out,
                    int64_t nwtiles) {
-  constexpr int D = 128, RW = 4, WR = RW * kUPasses, RB = D * BITS / 8, NW = kThreads / 64;
+  constexpr int D = 128, RW = 4, WR = RW * kU128Passes, RB = D * BITS / 8, NW = kThreads / 64;
+  constexpr int NL = 1 << BITS, SH = u128_head(NL);  // pole levels per channel, halfwords per head
   const int H = 1 << lgH;
   extern __shared__ uint16_t dyn[];
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  // the wave index through readfirstlane: tile bases are then known to be
+  // uniform and stay in scalar registers (loads take a 32-bit lane offset)
+  const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int cg = lane & 15, rw = lane >> 4;
   uint16_t* seg = dyn + wv * (WR * D);
   uint16_t* prow = dyn + NW * WR * D + wv * (WR * 16);  // PT: poles of each row
@@ -464,8 +469,7 @@ unpack_d128_kernel(const uint8_t* __restrict__ packed, const int32_t* __restrict
       const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
       const int h = i >> 7, d = i & (D - 1);
 #pragma unroll
-      for (int l = 0; l < 16; ++l)
-        kp[h * kU128SH + l * kU128SC + d] = (uint16_t)(w[l >> 1] >> (16 * (l & 1)));
+      for (int l = 0; l < NL; ++l) kp[h * SH + l * kU128SC + d] = (uint16_t)(w[l >> 1] >> (16 * (l & 1)));
     }
     __syncthreads();
   }
@@ -478,14 +482,15 @@ unpack_d128_kernel(const uint8_t* __restrict__ packed, const int32_t* __restrict
     lim = rest < WR - 1 ? (int)rest : WR - 1;
   };
   struct TileLoad {
-    uint32_t cw[kUPasses];
-    int2 rp[kUPasses];
-    uint32_t pv[kUPasses];  // PT: pole cg of the row
+    uint32_t cw[kU128Passes];
+    int2 rp[kU128Passes];
+    uint32_t pv[kU128Passes];  // PT: pole cg of the row
   };
   struct TileCsr {
-    uint32_t c[kUPasses], v[kUPasses];  // entry ra + cg of each pass's row
+    uint32_t c[kU128Passes], v[kU128Passes];  // entry ra + cg of each pass's row
   };
   const int64_t nwaves = (int64_t)gridDim.x * NW;
+  const uint32_t cap32 = (uint32_t)(cap < 0x7fffffff ? cap : 0x7fffffff);  // row_ptr entries are int32
   const int rows32 = (int)sc.rows;  // the host checks H * rows * 80 < 2^31 for this kernel
   auto load_tile = [&](int64_t wt, TileLoad& L) {
     int64_t rbase;
@@ -500,13 +505,14 @@ unpack_d128_kernel(const uint8_t* __restrict__ packed, const int32_t* __restrict
     const int64_t p0 = sc.pos_offset + t0;  // position of token t0 without a position array
     const int p0c = p0 < -(int64_t)WR ? -WR : (p0 > (int64_t)rows32 ? rows32 : (int)p0);
 #pragma unroll
-    for (int p = 0; p < kUPasses; ++p) {
-      const int o = p * RW + rw < lim ? p * RW + rw : lim;
-      if constexpr (BITS == 4) L.cw[p] = *reinterpret_cast<const uint32_t*>(pk + o * RB + 4 * cg);
-      else L.cw[p] = *reinterpret_cast<const uint16_t*>(pk + o * RB + 2 * cg);
-      L.rp[p] = *reinterpret_cast<const int2*>(rp + o);
+    for (int p = 0; p < kU128Passes; ++p) {
+      // unsigned 32-bit lane offsets from the uniform bases (scalar-base addressing)
+      const uint32_t o = (uint32_t)(p * RW + rw < lim ? p * RW + rw : lim);
+      if constexpr (BITS == 4) L.cw[p] = *reinterpret_cast<const uint32_t*>(pk + (o * RB + 4u * cg));
+      else L.cw[p] = *reinterpret_cast<const uint16_t*>(pk + (o * RB + 2u * cg));
+      L.rp[p] = *reinterpret_cast<const int2*>(reinterpret_cast<const char*>(rp) + 4u * o);
       if constexpr (PT) {
-        const int k = o >> lgH, h = o & (H - 1);
+        const int k = (int)(o >> lgH), h = (int)(o & (H - 1));
         int pos;
         if (sc.positions) {
           const int64_t ap = sc.positions[t0 + k];
@@ -523,11 +529,11 @@ unpack_d128_kernel(const uint8_t* __restrict__ packed, const int32_t* __restrict
   auto load_csr = [&](const TileLoad& L, TileCsr& C) {
     if (cap <= 0) return;
 #pragma unroll
-    for (int p = 0; p < kUPasses; ++p) {
-      int64_t i = (int64_t)(L.rp[p].x > 0 ? L.rp[p].x : 0) + cg;
-      i = i < cap ? i : cap - 1;
+    for (int p = 0; p < kU128Passes; ++p) {
+      uint32_t i = (uint32_t)(L.rp[p].x > 0 ? L.rp[p].x : 0) + (uint32_t)cg;
+      i = i < cap32 ? i : cap32 - 1u;
       C.c[p] = col[i];
-      C.v[p] = val[i];
+      C.v[p] = *reinterpret_cast<const uint16_t*>(reinterpret_cast<const char*>(val) + 2u * i);
     }
   };
   auto process = [&](int64_t wt, const TileLoad& L, const TileCsr& C) {
@@ -536,17 +542,17 @@ unpack_d128_kernel(const uint8_t* __restrict__ packed, const int32_t* __restrict
     tile_base(wt, rbase, lim);  // rbase = wt * WR: the tile is in range
     if constexpr (PT) {
 #pragma unroll
-      for (int p = 0; p < kUPasses; ++p) prow[(p * RW + rw) * 16 + cg] = (uint16_t)L.pv[p];
+      for (int p = 0; p < kU128Passes; ++p) prow[(p * RW + rw) * 16 + cg] = (uint16_t)L.pv[p];
       wave_sync();
     }
 #pragma unroll
-    for (int p = 0; p < kUPasses; ++p) {
+    for (int p = 0; p < kU128Passes; ++p) {
       const int rr = p * RW + rw;
       const uint16_t* lb;
       if constexpr (PT) {
         lb = prow + rr * 16;
       } else {
-        lb = kp + (rr & (H - 1)) * kU128SH + 8 * cg;  // rbase is a multiple of H
+        lb = kp + (rr & (H - 1)) * SH + 8 * cg;  // rbase is a multiple of H
       }
       uint32_t res[4];
 #pragma unroll
@@ -565,7 +571,7 @@ unpack_d128_kernel(const uint8_t* __restrict__ packed, const int32_t* __restrict
     }
     wave_sync();
 #pragma unroll
-    for (int p = 0; p < kUPasses; ++p) {
+    for (int p = 0; p < kU128Passes; ++p) {
       const int rr = p * RW + rw;
       const int32_t lo = L.rp[p].x > 0 ? L.rp[p].x : 0;
       const int32_t hi = (int64_t)L.rp[p].y < cap ? L.rp[p].y : (int32_t)cap;
@@ -578,10 +584,11 @@ unpack_d128_kernel(const uint8_t* __restrict__ packed, const int32_t* __restrict
     wave_sync();
     uint16_t* ob = out + rbase * D;
 #pragma unroll
-    for (int p = 0; p < kUPasses; ++p) {
+    for (int p = 0; p < kU128Passes; ++p) {
       const int rr = p * RW + rw;
       if (rr > lim) continue;
-      *reinterpret_cast<uint4*>(ob + rr * D + 8 * cg) = *reinterpret_cast<const uint4*>(seg + rr * D + 8 * cg);
+      *reinterpret_cast<uint4*>(ob + (uint32_t)(rr * D + 8 * cg)) =
+          *reinterpret_cast<const uint4*>(seg + rr * D + 8 * cg);
     }
     wave_sync();
   };
@@ -811,14 +818,19 @@ extern "C" int hkv_nuq_unpack_compact(const void* packed, const int32_t* row_ptr
   auto pk = (const uint8_t*)packed;
   auto o = (uint16_t*)out;
   const int lgH = __builtin_ctz((unsigned)H);
-  const bool h_pow2 = (H & (H - 1)) == 0 && H <= 16;
-  if (D == 128 && h_pow2 && (sc.per_token || H <= 8) &&
+  // H a power of two dividing the rows of a wave tile (4 * kU128Passes)
+  const bool h_pow2 = (H & (H - 1)) == 0 && (4 * kU128Passes) % H == 0;
+  if (D == 128 && h_pow2 &&
       (!sc.per_token || (int64_t)H * sc.rows * (int64_t)sizeof(hkv_table_t) < ((int64_t)1 << 31))) {
-    // the specialised kernel (the tile's 16 rows hold whole tokens)
-    const size_t lds = seg_bytes + (sc.per_token ? (size_t)NW * WR * 16 * 2 : (size_t)H * kU128SH * 2);
+    // the specialised kernel (a tile's rows hold whole tokens)
+    const int64_t WR1 = 4 * kU128Passes;
+    const int64_t nwt1 = (nrows + WR1 - 1) / WR1;
+    const size_t seg1 = (size_t)NW * WR1 * D * 2;
+    const size_t lds = seg1 + (sc.per_token ? (size_t)NW * WR1 * 16 * 2 : (size_t)H * u128_head(1 << bits) * 2);
 #define HKV_D128(PT_, B_)                                                                          \
-  hipLaunchKernelGGL((unpack_d128_kernel<PT_, B_>), dim3(grid), dim3(kThreads), lds, s, pk, row_ptr, \
-                     col, val, capacity, nrows, lgH, sc, o, nwtiles)
+  hipLaunchKernelGGL((unpack_d128_kernel<PT_, B_>), dim3(resident_grid(unpack_d128_kernel<PT_, B_>, \
+                     (nwt1 + NW - 1) / NW, lds)), dim3(kThreads), lds, s, pk, row_ptr,                \
+                     col, val, capacity, nrows, lgH, sc, o, nwt1)
     if (sc.per_token) {
       if (bits == 4) HKV_D128(true, 4);
       else HKV_D128(true, 2);
