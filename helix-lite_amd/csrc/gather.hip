@@ -133,6 +133,8 @@ gather_pages_kernel(GArgs A, const GSegs sg) {
     }
     uint4* dst = reinterpret_cast<uint4*>(A.out + ((i * kGPS + row) * H + h) * kGD + 32 * q);
 #pragma unroll
+    // plain stores: a store instruction covers 16-byte pieces of several
+    // lines, which L2 merges (streaming stores would write them out partial)
     for (int k = 0; k < 4; ++k) dst[k] = make_uint4(o[4 * k], o[4 * k + 1], o[4 * k + 2], o[4 * k + 3]);
     if constexpr (PT) {  // the V LUT is rewritten by the wave's next item
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");

@@ -86,6 +86,17 @@ HKV_DEV uint32_t bsel(uint32_t m, uint32_t a, uint32_t b) {
   return r;
 }
 
+// Streaming (non-temporal) stores for outputs that are not re-read by the
+// same kernel: the lines are written through L2 without displacing the
+// kernel's input working set.
+typedef unsigned int hkv_v4u __attribute__((ext_vector_type(4)));
+HKV_DEV void store_stream(void* p, uint4 v) {
+  const hkv_v4u x = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(x, reinterpret_cast<hkv_v4u*>(p));
+}
+HKV_DEV void store_stream(uint32_t* p, uint32_t v) { __builtin_nontemporal_store(v, p); }
+HKV_DEV void store_stream(uint16_t* p, uint16_t v) { __builtin_nontemporal_store(v, p); }
+
 // Pack the low halves of a and b into one register (a -> lane 0, b -> lane 1).
 HKV_DEV uint32_t pack_lo(uint32_t a, uint32_t b) { return (a & 0xffffu) | (b << 16); }
 

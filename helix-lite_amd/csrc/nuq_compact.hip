@@ -133,9 +133,9 @@ pack_stage_kernel(const uint16_t* __restrict__ x, int64_t nrows, int H, hkv_nuq_
           quant8<NB, PT, ChanTab, true>(xv, S, si, ChanTab{tab0}, c, om);
         }
         if constexpr (BITS == 4) {
-          *reinterpret_cast<uint32_t*>(packed + r * RB + 4 * cg) = pack_nibbles(c);
+          store_stream(reinterpret_cast<uint32_t*>(packed + r * RB + 4 * cg), pack_nibbles(c));
         } else {
-          *reinterpret_cast<uint16_t*>(packed + r * RB + 2 * cg) = (uint16_t)pack_crumbs(c);
+          store_stream(reinterpret_cast<uint16_t*>(packed + r * RB + 2 * cg), (uint16_t)pack_crumbs(c));
         }
         m = mask_bits_sign(om);
       }
@@ -405,8 +405,7 @@ unpack_compact_kernel(const uint8_t* __restrict__ packed, const int32_t* __restr
       const int rr = p * RW + rw;
       const int64_t r = r0 + rr;
       if (r >= nrows) continue;
-      *reinterpret_cast<uint4*>(out + r * D + 8 * cg) =
-          *reinterpret_cast<const uint4*>(seg + rr * D + 8 * cg);
+      store_stream(out + r * D + 8 * cg, *reinterpret_cast<const uint4*>(seg + rr * D + 8 * cg));
     }
     wave_sync();
   };
@@ -587,8 +586,7 @@ unpack_d128_kernel(const uint8_t* __restrict__ packed, const int32_t* __restrict
     for (int p = 0; p < kU128Passes; ++p) {
       const int rr = p * RW + rw;
       if (rr > lim) continue;
-      *reinterpret_cast<uint4*>(ob + (uint32_t)(rr * D + 8 * cg)) =
-          *reinterpret_cast<const uint4*>(seg + rr * D + 8 * cg);
+      store_stream(ob + (uint32_t)(rr * D + 8 * cg), *reinterpret_cast<const uint4*>(seg + rr * D + 8 * cg));
     }
     wave_sync();
   };

@@ -136,7 +136,7 @@ unpack_dense_kernel(const uint8_t* __restrict__ codes, const uint16_t* __restric
       }
       res[j] = half2;
     }
-    *reinterpret_cast<uint4*>(out + off) = make_uint4(res[0], res[1], res[2], res[3]);
+    store_stream(out + off, make_uint4(res[0], res[1], res[2], res[3]));
   }
 }
 

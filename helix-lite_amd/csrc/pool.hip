@@ -183,7 +183,7 @@ pool_gather_kernel(const uint8_t* __restrict__ codes, const uint16_t* __restrict
       }
       res[j] = pr;
     }
-    *reinterpret_cast<uint4*>(staging + dst) = make_uint4(res[0], res[1], res[2], res[3]);
+    store_stream(staging + dst, make_uint4(res[0], res[1], res[2], res[3]));
   }
 }
 
