@@ -124,6 +124,11 @@ struct Search2 {
 
 // Code of two fp16 lanes by binary search over sorted breakpoints.  Returns the
 // two codes in the low bits of each 16-bit lane.
+//
+// The code bits are the complements of the comparison masks.  v_bitop3 merges
+// two masks at once: bitop3(A, B, K, 0x1B) is, per bit, K ? ~A : ~B.
+HKV_DEV uint32_t not_sel(uint32_t a, uint32_t b, uint32_t k) { return __builtin_amdgcn_bitop3_b32(a, b, k, 0x1B); }
+
 template <int NB>
 HKV_DEV uint32_t search2(uint32_t x, const Search2<NB>& s) {
   if constexpr (NB == 0) {
@@ -135,7 +140,7 @@ HKV_DEV uint32_t search2(uint32_t x, const Search2<NB>& s) {
     uint32_t m1 = lt2(x, s.bp[1]);
     uint32_t t = bsel(m1, s.bp[0], s.bp[2]);
     uint32_t m0 = lt2(x, t);
-    return ~((m1 & 0x00020002u) | (m0 & 0x00010001u)) & 0x00030003u;
+    return not_sel(m1, m0, 0x00020002u) & 0x00030003u;
   } else if constexpr (NB == 3) {
     uint32_t m2 = lt2(x, s.bp[3]);
     uint32_t t1 = bsel(m2, s.bp[1], s.bp[5]);
@@ -162,8 +167,7 @@ HKV_DEV uint32_t search2(uint32_t x, const Search2<NB>& s) {
     uint32_t m1 = lt2(x, t1);
     uint32_t t0 = bsel(m1, r0, r1);
     uint32_t m0 = lt2(x, t0);
-    return ~((m3 & 0x00080008u) | (m2 & 0x00040004u) | (m1 & 0x00020002u) |
-             (m0 & 0x00010001u)) & 0x000f000fu;
+    return (not_sel(m3, m2, 0x00080008u) & 0x000c000cu) | (not_sel(m1, m0, 0x00020002u) & 0x00030003u);
   }
 }
 

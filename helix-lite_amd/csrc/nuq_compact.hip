@@ -9,7 +9,7 @@
 //   val fp16 = the original value; (row, col) ascending.
 //
 // Pack runs as three kernels.  pack_stage_kernel streams the fp16 input once;
-// its unit of work is a wave tile (kPasses passes of 64/G rows, G = D/8 lanes
+// its unit of work is a wave tile (PASSES passes of 64/G rows, G = D/8 lanes
 // per row), handled by one wave on its own: no block-level barrier.  A wave
 // writes the packed codes, each row's outlier offset within its wave tile
 // (into row_ptr), the tile's outliers into the tile's own staging region, and
@@ -23,7 +23,9 @@
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kPasses = 8;  // passes of kThreads*8 elements per tile
+// Passes of 64/G rows per wave tile: 8, or 4 for per-channel 16-level tables
+// (their search state takes 72 registers; smaller tiles keep 3 waves a SIMD).
+__host__ __device__ inline int pack_passes(bool per_token, int nb) { return (!per_token && nb == 4) ? 4 : 8; }
 
 // Workspace: header, per-wave-tile counts and bases, then the staged entries
 // (u32: value | column << 16), each region 256-byte aligned.  Staging holds a
@@ -43,25 +45,30 @@ HKV_DEV void wave_sync() {
 
 // KFIX: the rows of one pass of a wave (RW = 64/G) are a multiple of H, so a
 // lane's head is fixed (rw % H) and its token advances by RW / H per pass.
-template <int NB, bool PT, int G, int BITS, bool KFIX>
+template <int NB, bool PT, int G, int BITS, bool KFIX, int PASSES>
 __global__ void __launch_bounds__(kThreads)
 pack_stage_kernel(const uint16_t* __restrict__ x, int64_t nrows, int H, hkv_nuq_scales sc,
                   uint8_t* __restrict__ packed, int32_t* __restrict__ row_ptr,
                   uint32_t* __restrict__ sent, uint32_t* __restrict__ wt_cnt, int64_t nwt) {
   constexpr int RW = 64 / G;        // rows per wave per pass
-  constexpr int WT = RW * kPasses;  // rows per wave tile
+  constexpr int WT = RW * PASSES;  // rows per wave tile
   constexpr int D = 8 * G;
   constexpr int RB = D * BITS / 8;  // packed bytes per row
   constexpr int NW = kThreads / 64;
   // Per-token tables of a wave tile's rows are staged in the wave's LDS slice
-  // when they fit in 4 KiB (D >= 128); otherwise each row reads its table
-  // through L1.
+  // when they fit in 4 KiB (D >= 128), already in search form (each
+  // breakpoint and threshold duplicated into both 16-bit halves: words 0..14
+  // breakpoints, 15 lower, 16 upper, 17 fast-path bound), so a row's lanes
+  // read them without unpacking; otherwise each row reads its table through L1.
   constexpr bool STAGE = PT && WT * 80 <= 4096;
-  __shared__ uint4 s_tab[STAGE ? NW * WT * 5 : 1];
+  constexpr int TW = 20;  // staged words per row (80 bytes, 16-byte aligned)
+  __shared__ __align__(16) uint32_t s_tab[STAGE ? NW * WT * TW : 1];
 
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  // the wave index through readfirstlane: tile bases are then uniform and
+  // stay in scalar registers, addressed with 32-bit lane offsets
+  const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int cg = lane % G, rw = lane / G;
-  uint4* wtab = s_tab + (STAGE ? wv * WT * 5 : 0);
+  uint32_t* wtab = s_tab + (STAGE ? wv * WT * TW : 0);
   const hkv_table_t* tabs = (const hkv_table_t*)sc.tables;
   const SlowInfo si = slow_info(sc);
   const int hfix = KFIX ? rw % H : 0;
@@ -73,40 +80,63 @@ pack_stage_kernel(const uint16_t* __restrict__ x, int64_t nrows, int H, hkv_nuq_
     for (int j = 0; j < 4; ++j)
       load_search_pair<NB>(tabs + tab0 + 2 * j, tabs + tab0 + 2 * j + 1, S[j]);
   }
+  uint32_t xmin = 0;  // KFIX: the lane's smallest fast-path bound
+  if constexpr (!PT && KFIX) xmin = xsafe_min<NB>(S);
 
   for (int64_t wt = (int64_t)blockIdx.x * NW + wv; wt < nwt; wt += (int64_t)gridDim.x * NW) {
     const int64_t r0 = wt * WT;
     const int64_t t0 = KFIX ? r0 / H : 0;  // token of row r0 (H divides r0)
-    uint32_t xs[kPasses][4];
+    const int nv = nrows - r0 < WT ? (int)(nrows - r0) : WT;  // rows of this tile
+    const uint16_t* xt = x + r0 * D;
+    uint8_t* pt = packed + r0 * RB;
+    int32_t* rpt = row_ptr + r0;
+    uint32_t xs[PASSES][4];
 #pragma unroll
-    for (int p = 0; p < kPasses; ++p) {
-      const int64_t r = r0 + p * RW + rw;
+    for (int p = 0; p < PASSES; ++p) {
+      const int rr = p * RW + rw;
       uint4 v = make_uint4(0u, 0u, 0u, 0u);
-      if (r < nrows) v = *reinterpret_cast<const uint4*>(x + r * D + 8 * cg);
+      if (rr < nv) v = *reinterpret_cast<const uint4*>(xt + (uint32_t)(rr * D + 8 * cg));
       xs[p][0] = v.x; xs[p][1] = v.y; xs[p][2] = v.z; xs[p][3] = v.w;
     }
     if constexpr (STAGE) {
-      for (int i = lane; i < WT * 5; i += 64) {
-        const int rr = i / 5, part = i - rr * 5;
-        const int64_t r = r0 + rr;
-        if (r < nrows) {
+      // three 16-byte parts of each row's record: breakpoints 0-7, 8-14, and
+      // the thresholds (the poles are not needed here)
+      for (int i = lane; i < WT * 3; i += 64) {
+        const int rr = i / 3, q = i - rr * 3;
+        if (rr < nv) {
+          const int64_t r = r0 + rr;
           const int64_t t = r / H;
           const int h = (int)(r - t * H);
           const int64_t tab = (int64_t)h * sc.rows + clamp_row(token_pos(sc, t), sc.rows);
-          wtab[i] = reinterpret_cast<const uint4*>(tabs + tab)[part];
+          const uint4 v = reinterpret_cast<const uint4*>(tabs + tab)[q == 2 ? 4 : q];
+          uint32_t* dw = wtab + rr * TW;
+          if (q < 2) {
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+              const uint32_t hh = (w[k >> 1] >> (16 * (k & 1))) & 0xffffu;
+              if (8 * q + k < 15) dw[8 * q + k] = hh | (hh << 16);
+            }
+          } else {
+            const uint32_t lo = v.x & 0xffffu, up = v.x >> 16;
+            const uint32_t xsf = ((v.y >> 16) & 1u) ? (v.y & 0xffffu) : 0xffffu;
+            dw[15] = lo | (lo << 16);
+            dw[16] = up | (up << 16);
+            dw[17] = xsf | (xsf << 16);
+          }
         }
       }
       wave_sync();
     }
 
-    const int64_t sbase = r0 * D;  // the wave tile's staging region
+    uint32_t* st = sent + r0 * D;  // the wave tile's staging region
     uint32_t run = 0;              // outliers of the tile's earlier passes
 #pragma unroll
-    for (int p = 0; p < kPasses; ++p) {
+    for (int p = 0; p < PASSES; ++p) {
       const int rr = p * RW + rw;
       const int64_t r = r0 + rr;
       uint32_t m = 0;
-      if (r < nrows) {
+      if (rr < nv) {
         int64_t t;
         int h;
         if constexpr (KFIX) {
@@ -119,10 +149,18 @@ pack_stage_kernel(const uint16_t* __restrict__ x, int64_t nrows, int H, hkv_nuq_
         const uint4 xv = make_uint4(xs[p][0], xs[p][1], xs[p][2], xs[p][3]);
         uint32_t c[4], om[4];
         if constexpr (PT) {
-          const int64_t tab = (int64_t)h * sc.rows + clamp_row(token_pos(sc, t), sc.rows);
-          if constexpr (STAGE) load_search_bcast<NB>(reinterpret_cast<const hkv_table_t*>(wtab + rr * 5), S[0]);
-          else load_search_bcast<NB>(tabs + tab, S[0]);
-          quant8<NB, PT, RowTab, true>(xv, S, si, RowTab{tab}, c, om);
+          const RowTabAt tab{sc.rows, sc.positions, sc.pos_offset, h, t};  // for the exact scan only
+          if constexpr (STAGE) {
+            const uint32_t* tw = wtab + rr * TW;
+#pragma unroll
+            for (int i = 0; i < (1 << NB) - 1; ++i) S[0].bp[i] = tw[i];
+            S[0].lo = tw[15];
+            S[0].up = tw[16];
+            S[0].xsafe = tw[17];
+          } else {
+            load_search_bcast<NB>(tabs + tab(0), S[0]);
+          }
+          quant8<NB, PT, RowTabAt, true>(xv, S, si, tab, c, om);
         } else {
           const int64_t tab0 = (int64_t)h * D + 8 * cg;
           if constexpr (!KFIX) {
@@ -130,12 +168,13 @@ pack_stage_kernel(const uint16_t* __restrict__ x, int64_t nrows, int H, hkv_nuq_
             for (int j = 0; j < 4; ++j)
               load_search_pair<NB>(tabs + tab0 + 2 * j, tabs + tab0 + 2 * j + 1, S[j]);
           }
-          quant8<NB, PT, ChanTab, true>(xv, S, si, ChanTab{tab0}, c, om);
+          if constexpr (KFIX) quant8<NB, PT, ChanTab, true, true>(xv, S, si, ChanTab{tab0}, c, om, xmin);
+          else quant8<NB, PT, ChanTab, true>(xv, S, si, ChanTab{tab0}, c, om);
         }
         if constexpr (BITS == 4) {
-          store_stream(reinterpret_cast<uint32_t*>(packed + r * RB + 4 * cg), pack_nibbles(c));
+          store_stream(reinterpret_cast<uint32_t*>(pt + (uint32_t)(rr * RB + 4 * cg)), pack_nibbles(c));
         } else {
-          store_stream(reinterpret_cast<uint16_t*>(packed + r * RB + 2 * cg), (uint16_t)pack_crumbs(c));
+          store_stream(reinterpret_cast<uint16_t*>(pt + (uint32_t)(rr * RB + 2 * cg)), (uint16_t)pack_crumbs(c));
         }
         m = mask_bits_sign(om);
       }
@@ -144,13 +183,15 @@ pack_stage_kernel(const uint16_t* __restrict__ x, int64_t nrows, int H, hkv_nuq_
       uint32_t tot;
       uint32_t pos = run + wave_excl_count(__builtin_popcount(m), &tot);
       run += tot;
-      if (r < nrows && cg == 0) row_ptr[r] = (int32_t)pos;
+      if (rr < nv && cg == 0)
+        *reinterpret_cast<int32_t*>(reinterpret_cast<char*>(rpt) + 4u * (uint32_t)rr) = (int32_t)pos;
       while (m) {
         const int e = __builtin_ctz(m);
         m &= m - 1u;
         const uint32_t w = pick4(xs[p][0], xs[p][1], xs[p][2], xs[p][3], e >> 1);
         if (pos < (uint32_t)(WT * D))  // always true; keeps the region bound explicit
-          sent[sbase + pos] = ((w >> (16 * (e & 1))) & 0xffffu) | ((uint32_t)(8 * cg + e) << 16);
+          *reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(st) + 4u * pos) =
+              ((w >> (16 * (e & 1))) & 0xffffu) | ((uint32_t)(8 * cg + e) << 16);
         ++pos;
       }
     }
@@ -616,9 +657,9 @@ __global__ void write_zero_rowptr(int32_t* row_ptr) { row_ptr[0] = 0; }
 
 bool pow2_G(int D) { return D % 8 == 0 && D >= 8 && D <= 256 && ((D / 8) & (D / 8 - 1)) == 0; }
 
-PackLayout pack_layout(int64_t nrows, int D) {
+PackLayout pack_layout(int64_t nrows, int D, int passes) {
   PackLayout L;
-  L.tile_rows = (int64_t)(64 / (D / 8)) * kPasses;
+  L.tile_rows = (int64_t)(64 / (D / 8)) * passes;
   L.ntiles = (nrows + L.tile_rows - 1) / L.tile_rows;
   L.tile_elems = L.tile_rows * D;
   L.cnt_off = 256;
@@ -665,7 +706,7 @@ struct PackArgs {
 
 template <int NB, bool PT, int G, int BITS, bool KFIX>
 void launch_stage(const PackArgs& a) {
-  auto k = pack_stage_kernel<NB, PT, G, BITS, KFIX>;
+  auto k = pack_stage_kernel<NB, PT, G, BITS, KFIX, (!PT && NB == 4) ? 4 : 8>;  // pack_passes
   const int64_t nblocks = (a.ntiles + kThreads / 64 - 1) / (kThreads / 64);
   hipLaunchKernelGGL(k, dim3(resident_grid(k, nblocks)), dim3(kThreads), 0, a.s, a.x, a.nrows,
                      a.H, a.sc, a.pk, a.rp, a.sent, a.cnt, a.ntiles);
@@ -720,7 +761,8 @@ void launch_unpack_g(int G, unsigned grid, size_t lds, hipStream_t s, const uint
 
 extern "C" size_t hkv_nuq_pack_compact_workspace_bytes(int64_t T, int H, int D) {
   if (T < 0 || H < 1 || !pow2_G(D)) return 0;
-  return pack_layout(T * H, D).bytes;
+  // the larger of the two tilings (more tiles: more counts)
+  return std::max(pack_layout(T * H, D, 4).bytes, pack_layout(T * H, D, 8).bytes);
 }
 
 extern "C" int hkv_nuq_pack_compact(const void* values, int64_t T, int H, int D, int bits,
@@ -745,7 +787,7 @@ extern "C" int hkv_nuq_pack_compact(const void* values, int64_t T, int H, int D,
   }
   if (!values || !packed || (capacity > 0 && (!col || !val))) return HKV_ERR_ARG;
   if (((uintptr_t)values & 15u) || ((uintptr_t)packed & 3u)) return HKV_ERR_ARG;
-  const PackLayout lay = pack_layout(nrows, D);
+  const PackLayout lay = pack_layout(nrows, D, pack_passes(scales->per_token != 0, nb_for_levels_host(scales->levels)));
   if (!workspace || workspace_bytes < lay.bytes || ((uintptr_t)workspace & 255u))
     return HKV_ERR_WORKSPACE;
   const int G = D / 8, RW = 64 / G;

@@ -45,13 +45,30 @@ HKV_DEV int slow_one(uint16_t xb, const SlowInfo& si, int64_t tab, int* o) {
 // for outliers.
 // SIGN: om[j] flags outliers in its sign bits only (bits 15 and 31) instead of
 // whole 0xffff lanes.
-template <int NB, bool PT, typename TabFn, bool SIGN = false>
+//
+// XMIN: the fast path is taken when the largest |x| of the 8 elements is within
+// xmin, the smallest bound of the 8 tables (both halves; see xsafe_min),
+// instead of comparing each pair with its own bounds.  Never less exact: the
+// scan decides whatever the fast path does not.
+template <int NB, bool PT, typename TabFn, bool SIGN = false, bool XMIN = false>
 HKV_DEV void quant8(const uint4 xv, const Search2<NB>* S, const SlowInfo& si, TabFn tab,
-                    uint32_t code[4], uint32_t om[4]) {
+                    uint32_t code[4], uint32_t om[4], uint32_t xmin = 0) {
   const uint32_t x[4] = {xv.x, xv.y, xv.z, xv.w};
   uint32_t uns = 0;
+  if constexpr (PT || XMIN) {  // one bound: compare the largest magnitude
+    u2_t mg = __builtin_bit_cast(u2_t, x[0] & 0x7fff7fffu);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) uns |= unsafe2<NB>(x[j], S[PT ? 0 : j]);
+    for (int j = 1; j < 4; ++j) mg = __builtin_elementwise_max(mg, __builtin_bit_cast(u2_t, x[j] & 0x7fff7fffu));
+    if constexpr (PT) {
+      uns = unsafe2<NB>(__builtin_bit_cast(uint32_t, mg), S[0]);
+    } else {
+      const s2_t d = as_s2(xmin) - as_s2(__builtin_bit_cast(uint32_t, mg));
+      uns = as_u32(d) & 0x80008000u;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) uns |= unsafe2<NB>(x[j], S[j]);
+  }
   if (__builtin_expect(uns == 0, 1)) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -71,6 +88,17 @@ HKV_DEV void quant8(const uint4 xv, const Search2<NB>* S, const SlowInfo& si, Ta
   }
 }
 
+// The smallest fast-path bound of four channel-pair tables, in both halves
+// (bounds are in [0, 0x7bff], or 0xffff = -1 when a table has no fast path).
+template <int NB>
+HKV_DEV uint32_t xsafe_min(const Search2<NB>* S) {
+  s2_t m = as_s2(S[0].xsafe);
+#pragma unroll
+  for (int j = 1; j < 4; ++j) m = __builtin_elementwise_min(m, as_s2(S[j].xsafe));
+  const short lo = m.x < m.y ? m.x : m.y;
+  return (uint32_t)(uint16_t)lo * 0x00010001u;
+}
+
 // Per-channel tables: element e of the chunk starting at table index tab0.
 struct ChanTab {
   int64_t tab0;
@@ -80,6 +108,18 @@ struct ChanTab {
 struct RowTab {
   int64_t tab;
   HKV_DEV int64_t operator()(int) const { return tab; }
+};
+// The same, computed from (head, token) where it is needed.
+struct RowTabAt {
+  int64_t rows;
+  const int64_t* positions;
+  int64_t pos_offset;
+  int h;
+  int64_t t;
+  HKV_DEV int64_t operator()(int) const {
+    const int64_t pos = positions ? positions[t] : pos_offset + t;
+    return (int64_t)h * rows + clamp_row(pos, rows);
+  }
 };
 
 // Word k (0..3) of a 4-word register group, by an explicit select tree (a
