@@ -36,10 +36,11 @@ def test_host_only_entry_points():
     assert b"gfx950" in L.hkv_version()
     assert L.hkv_status_string(0) == b"ok"
     assert L.hkv_status_string(4) == b"output capacity too small"
-    # 256-byte header, one u32 count and one u32 base per wave tile of 32 rows
-    # (D = 128; plus the final base), then a 4-byte staging entry per element,
-    # each region 256-aligned
-    ntiles = 131072 * 4 // 32
+    # 256-byte header, one u32 count and one u32 base per wave tile (D = 128:
+    # sized for the smaller, 16-row tiles of per-channel 16-level tables; plus
+    # the final base), then a 4-byte staging entry per element, each region
+    # 256-aligned
+    ntiles = 131072 * 4 // 16
     assert L.hkv_nuq_pack_compact_workspace_bytes(131072, 4, 128) == \
         256 + 4 * ntiles + (4 * ntiles + 256) + 131072 * 4 * 128 * 4
     # 40 rows = 2 wave tiles: header, counts and bases (each padded to 256),
