@@ -326,11 +326,17 @@ constexpr int kBoundUnrollF16 = 4;  // row groups per step (two steps of loads i
 // out_p / out_off: head-major output goes to out[h * out_p + out_off + p]
 // (out_p = P, out_off = 0 for one sequence; the ragged kernel writes each
 // sequence's pages at its offset within the concatenated page axis).
+// q_lds: the raw query (H*group*D elements, at most kQRawChunks*256 16-byte
+// chunks, 16-byte aligned) is staged through LDS after qs; its loads are
+// issued before the first two steps of statistics loads, so the group sums
+// wait only for them.
+constexpr int kQRawChunks = 4;
+
 template <int G, bool HFIX>
 HKV_DEV void bound_f16_rows(const void* q, int qdt, int group, const uint16_t* __restrict__ kmin,
                             const uint16_t* __restrict__ kmax, int64_t P, int H, void* out, int odt,
                             int head_major, int64_t out_p, int64_t out_off,
-                            uint2* __restrict__ mm = nullptr) {
+                            uint2* __restrict__ mm = nullptr, int q_lds = 0) {
   constexpr int D = 8 * G;
   constexpr int RB = 256 / G;  // rows per block per row group
   constexpr int U = kBoundUnrollF16;
@@ -360,13 +366,44 @@ HKV_DEV void bound_f16_rows(const void* q, int qdt, int group, const uint16_t* _
     }
   };
   int r0 = blockIdx.x * span;
-  load(r0, a0, b0);  // in flight while the query is staged
   // the block's clamped, group-summed query, [2][H][D] in LDS
-  for (int i = threadIdx.x; i < H * D; i += 256) {
-    float qa, qb;
-    group_q(q, qdt, i / D, group, D, i % D, qa, qb);
-    qs[i] = qa;
-    qs[H * D + i] = qb;
+  if (q_lds) {
+    // raw query chunks first, then two steps of statistics: waiting for the
+    // chunks (loads complete in order) does not wait for the statistics
+    const int nch = H * group * D * (qdt == HKV_DT_F32 ? 4 : 2) / 16;
+    const uint4* gq = reinterpret_cast<const uint4*>(q);
+    uint4* qraw = reinterpret_cast<uint4*>(qs + 2 * H * D);
+    uint4 qc[kQRawChunks];
+#pragma unroll
+    for (int k = 0; k < kQRawChunks; ++k) {
+      const int i = threadIdx.x + 256 * k;
+      qc[k] = gq[i < nch ? i : nch - 1];
+    }
+    load(r0, a0, b0);
+    load(r0 + step, a1, b1);
+    // unconditional stores (a clamped chunk rewrites the last one with its
+    // own value), so the chunk loads stay ahead of the statistics loads
+#pragma unroll
+    for (int k = 0; k < kQRawChunks; ++k) {
+      const int i = threadIdx.x + 256 * k;
+      qraw[i < nch ? i : nch - 1] = qc[k];
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < H * D; i += 256) {
+      float qa, qb;
+      group_q(qraw, qdt, i / D, group, D, i % D, qa, qb);
+      qs[i] = qa;
+      qs[H * D + i] = qb;
+    }
+  } else {
+    load(r0, a0, b0);
+    load(r0 + step, a1, b1);
+    for (int i = threadIdx.x; i < H * D; i += 256) {
+      float qa, qb;
+      group_q(q, qdt, i / D, group, D, i % D, qa, qb);
+      qs[i] = qa;
+      qs[H * D + i] = qb;
+    }
   }
   __syncthreads();
   float qp[8], qn[8];
@@ -426,21 +463,20 @@ HKV_DEV void bound_f16_rows(const void* q, int qdt, int group, const uint16_t* _
       }
     }
   };
-  // two register buffers: the loads of the next step are in flight while the
-  // current one is computed (unrolled by 2 so no pending load is copied)
+  // two register buffers: while a step is computed the next one is in
+  // flight; a buffer is refilled (two steps ahead) once computed (unrolled
+  // by 2 so no pending load is copied; loads past the end are clamped)
   int pb = HFIX ? r0 / H : 0;
   const int pstep = HFIX ? step / H : 0;
   while (r0 < nr) {
-    int r1 = r0 + step;
-    load(r1, a1, b1);  // past the end: clamped, harmless
     compute(r0, pb, a0, b0);
-    r0 = r1;
+    load(r0 + 2 * step, a0, b0);
+    r0 += step;
     pb += pstep;
     if (r0 >= nr) break;
-    r1 = r0 + step;
-    load(r1, a0, b0);
     compute(r0, pb, a1, b1);
-    r0 = r1;
+    load(r0 + 2 * step, a1, b1);
+    r0 += step;
     pb += pstep;
   }
   if constexpr (HFIX) {
@@ -454,7 +490,7 @@ HKV_DEV void bound_f16_rows(const void* q, int qdt, int group, const uint16_t* _
         atomicMax(&s_mx[rl % H], kmx_t);
       }
       __syncthreads();
-      for (int i = threadIdx.x; i < H; i += 256) mm[(int64_t)blockIdx.x * H + i] = make_uint2(s_mn[i], s_mx[i]);
+      for (int i = threadIdx.x; i < H; i += 256) mm[(int64_t)i * gridDim.x + blockIdx.x] = make_uint2(s_mn[i], s_mx[i]);
     }
   }
 }
@@ -463,8 +499,8 @@ template <int G, bool HFIX>
 __global__ void __launch_bounds__(256)
 bound_f16_kernel(const void* q, int qdt, int group, const uint16_t* __restrict__ kmin,
                  const uint16_t* __restrict__ kmax, int64_t P, int H, void* out, int odt,
-                 int head_major, uint2* mm) {
-  bound_f16_rows<G, HFIX>(q, qdt, group, kmin, kmax, P, H, out, odt, head_major, P, 0, mm);
+                 int head_major, uint2* mm, int q_lds) {
+  bound_f16_rows<G, HFIX>(q, qdt, group, kmin, kmax, P, H, out, odt, head_major, P, 0, mm, q_lds);
 }
 
 // Ragged batch: sequence s = blockIdx.y owns pages [off[s], off[s+1]) of the
@@ -482,11 +518,12 @@ template <int G, bool HFIX>
 __global__ void __launch_bounds__(256)
 bound_f16_ragged_kernel(const char* q, int64_t q_bytes, int qdt, int group,
                         const uint16_t* __restrict__ kmin, const uint16_t* __restrict__ kmax, int H,
-                        float* out, const Segs segs) {
+                        float* out, const Segs segs, int q_lds) {
   const int sq = blockIdx.y;
   const int64_t o0 = segs.off[sq], P = segs.off[sq + 1] - o0;
   bound_f16_rows<G, HFIX>(q + sq * q_bytes, qdt, group, kmin + o0 * H * (8 * G),
-                          kmax + o0 * H * (8 * G), P, H, out, HKV_DT_F32, 1, segs.off[segs.nseg], o0);
+                          kmax + o0 * H * (8 * G), P, H, out, HKV_DT_F32, 1, segs.off[segs.nseg], o0,
+                          nullptr, q_lds);
 }
 
 // --------------------------------------------------------- a10: top-K
@@ -896,7 +933,7 @@ constexpr int kMBWin = 1024;     // window keys stored per slice
 
 struct MBWork {
   uint32_t* ctr;     // [H] arrival counters (zero between calls)
-  const uint2* mm;   // [nmm][H] (min key, max key) of the bound kernel's blocks
+  const uint2* mm;   // [H][nmm] (min key, max key) of the bound kernel's blocks
   int nmm;
   uint32_t* hist;    // [H][NB][kMBBins]
   int* meta;         // [H][NB][2] (out row of the slice's first selected page, T-equal keys before it)
@@ -969,15 +1006,23 @@ topk_mb_hist(const float* scores, int64_t P, int64_t s, int64_t keff, int64_t* o
   const int n = (int)(P - s);
   const float* col = scores + (int64_t)h * P + s;  // candidate i is page s + i
   constexpr int slice = kMBThreads * KPT;
-  const int c0 = j * slice + tid * KPT;
-  // loads are unconditional (clamped index) so that all KPT are in flight at once
+  // key i of the thread is candidate c0 + i * kMBThreads: each load
+  // instruction reads consecutive words across the block.  Loads are
+  // unconditional (clamped index) so that all KPT are in flight at once.
+  const int c0 = j * slice + tid;
   float kv[KPT];
 #pragma unroll
-  for (int i = 0; i < KPT; ++i) kv[i] = col[c0 + i < n ? c0 + i : n - 1];
-  // key range of the head (all pages, sinks included: a superset of the candidates')
-  uint32_t mn = 0xffffffffu, mx = 0u;
-  for (int b = tid; b < w.nmm; b += kMBThreads) {
-    const uint2 v = w.mm[(int64_t)b * H + h];
+  for (int i = 0; i < KPT; ++i) {
+    const int c = c0 + i * kMBThreads;
+    kv[i] = col[c < n ? c : n - 1];
+  }
+  // key range of the head (all pages, sinks included: a superset of the
+  // candidates'); the first range is requested with the keys
+  const uint2* hmm = w.mm + (int64_t)h * w.nmm;
+  uint2 v0 = hmm[tid < w.nmm ? tid : w.nmm - 1];
+  uint32_t mn = v0.x, mx = v0.y;
+  for (int b = tid + kMBThreads; b < w.nmm; b += kMBThreads) {
+    const uint2 v = hmm[b];
     mn = v.x < mn ? v.x : mn;
     mx = v.y > mx ? v.y : mx;
   }
@@ -992,7 +1037,7 @@ topk_mb_hist(const float* scores, int64_t P, int64_t s, int64_t keff, int64_t* o
   };
 #pragma unroll
   for (int i = 0; i < KPT; ++i)
-    if (c0 + i < n) atomicAdd(&sh.hist[bin_of(ukey(kv[i]))], 1u);
+    if (c0 + i * kMBThreads < n) atomicAdd(&sh.hist[bin_of(ukey(kv[i]))], 1u);
   __syncthreads();
   uint32_t* gh = w.hist + ((int64_t)h * NB + j) * kMBBins;
   for (int b = tid; b < kMBBins; b += kMBThreads) gh[b] = sh.hist[b];
@@ -1025,12 +1070,13 @@ topk_mb_hist(const float* scores, int64_t P, int64_t s, int64_t keff, int64_t* o
     unsigned long long* wc = w.wcand + ((int64_t)h * NB + j) * kMBWin;
 #pragma unroll
     for (int i = 0; i < KPT; ++i) {
-      if (c0 + i < n) {
+      const int c = c0 + i * kMBThreads;
+      if (c < n) {
         const uint32_t k = ukey(kv[i]);
         const int b = bin_of(k);
         if (b >= wlo && b <= whi) {
           const uint32_t slot = atomicAdd(&sh.ncand, 1u);
-          if (slot < (uint32_t)kMBWin) wc[slot] = ((unsigned long long)k << 32) | (uint32_t)~(uint32_t)(c0 + i);
+          if (slot < (uint32_t)kMBWin) wc[slot] = ((unsigned long long)k << 32) | (uint32_t)~(uint32_t)c;
         }
       }
     }
@@ -1074,7 +1120,12 @@ topk_mb_hist(const float* scores, int64_t P, int64_t s, int64_t keff, int64_t* o
       wcr[u] = w.wcand[(int64_t)h * NB * kMBWin + f];  // slices are consecutive: [NB][kMBWin]
     }
   }
-  for (int i = tid; i < NBc * 4; i += kMBThreads) sh.wm[i >> 2][i & 3] = w.wmeta[((int64_t)h * NB) * 4 + i];
+  // the slices' window descriptors, one int per thread (NBc * 4 <= 256),
+  // requested before the histograms and stored to LDS after them: a load
+  // whose result is needed first would be waited for before the histograms
+  // are requested
+  const int nwm = NBc * 4;
+  const int wmv = w.wmeta[((int64_t)h * NB) * 4 + (tid < nwm ? tid : nwm - 1)];
   uint32_t hv[KB][8];  // slices j0..j0+7 of the thread's bins (the last group kept)
   for (int k4 = 0; k4 < KB; ++k4) sh.hist[k4 * kMBThreads + tid] = 0u;
   if (tid == 0) {  // found below (defaults for safety)
@@ -1096,6 +1147,12 @@ topk_mb_hist(const float* scores, int64_t P, int64_t s, int64_t keff, int64_t* o
       for (int u = 0; u < 8; ++u) t += j0 + u < NBc ? hv[k4][u] : 0u;
       sh.hist[k4 * kMBThreads + tid] += t;
     }
+  }
+  {
+    // unconditional (threads past nwm rewrite the last entry with its own
+    // value) so that the load above is not moved after the histogram loads
+    const int i = tid < nwm ? tid : nwm - 1;
+    sh.wm[i >> 2][i & 3] = wmv;
   }
   __syncthreads();
   // bins high to low: thread t owns bins [4095 - 4t - 3, 4095 - 4t]
@@ -1335,15 +1392,30 @@ topk_mb_write(const float* scores, int64_t P, int64_t s, int64_t* out, int H, MB
   const int n = (int)(P - s);
   const float* col = scores + (int64_t)h * P + s;
   const int c0 = j * (kMBThreads * KPT) + tid * KPT;
-  // the keys, the threshold and the slice's offsets are requested together
+  // the keys, the threshold and the slice's offsets are requested together.
+  // Where the stage holds the slice, load i reads candidates
+  // j * slice + i * kMBThreads + [0, kMBThreads) (consecutive words across
+  // the block) and the stage transposes them so that the thread holds
+  // candidates c0 .. c0 + KPT - 1; else the thread reads those directly.
+  constexpr bool kTranspose = kMBThreads * KPT <= kStage;
   float kv[KPT];
 #pragma unroll
-  for (int i = 0; i < KPT; ++i) kv[i] = col[c0 + i < n ? c0 + i : n - 1];
+  for (int i = 0; i < KPT; ++i) {
+    const int c = kTranspose ? j * (kMBThreads * KPT) + i * kMBThreads + tid : c0 + i;
+    kv[i] = col[c < n ? c : n - 1];
+  }
   const uint4 th = *reinterpret_cast<const uint4*>(w.thr + h * 4);
   const int2 me = *reinterpret_cast<const int2*>(w.meta + ((int64_t)h * NB + j) * 2);
   if (j == 0)
     for (int64_t i = tid; i < s; i += kMBThreads) out[i * H + h] = i;
   if (th.z) return;  // written by the fallback
+  if constexpr (kTranspose) {
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) stage[i * kMBThreads + tid] = __float_as_uint(kv[i]);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) kv[i] = __uint_as_float(stage[tid * KPT + i]);
+  }
   const uint32_t T = th.x, need_eq = th.y, row_end = th.w;
   auto taken = [&](uint32_t eqs) { return eqs < need_eq ? eqs : need_eq; };
   uint32_t key[KPT];
@@ -1423,13 +1495,21 @@ namespace {
 template <int G>
 void launch_bound_f16(bool hfix, unsigned grid, size_t lds, hipStream_t s, const void* q, int qdt,
                       int group, const uint16_t* kmin, const uint16_t* kmax, int64_t P, int H,
-                      void* out, int odt, int head_major, uint2* mm) {
+                      void* out, int odt, int head_major, uint2* mm, int q_lds) {
   if (hfix)
     hipLaunchKernelGGL((bound_f16_kernel<G, true>), dim3(grid), dim3(256), lds, s, q, qdt, group,
-                       kmin, kmax, P, H, out, odt, head_major, mm);
+                       kmin, kmax, P, H, out, odt, head_major, mm, q_lds);
   else
     hipLaunchKernelGGL((bound_f16_kernel<G, false>), dim3(grid), dim3(256), lds, s, q, qdt, group,
-                       kmin, kmax, P, H, out, odt, head_major, nullptr);
+                       kmin, kmax, P, H, out, odt, head_major, nullptr, q_lds);
+}
+
+// Bytes of LDS for the raw query of the fp16 bound kernels (0: read it from
+// global memory): whole 16-byte chunks, at most kQRawChunks per thread.
+size_t q_raw_lds(const void* q, int qdt, int Hq, int D) {
+  const size_t nb = (size_t)Hq * D * (qdt == HKV_DT_F32 ? 4 : 2);
+  if (((uintptr_t)q & 15u) || nb % 16 || nb / 16 > (size_t)kQRawChunks * 256) return 0;
+  return nb;
 }
 
 // Bound into out, (P,H) or head-major (H,P).
@@ -1446,7 +1526,7 @@ int page_bound(const void* q, int q_dtype, int Hq, const void* kmin, const void*
   if (!q || !kmin || !kmax || !out) return HKV_ERR_ARG;
   if (D % 8 == 0 && (((uintptr_t)kmin | (uintptr_t)kmax) & 15u)) return HKV_ERR_ARG;
   const int64_t rows = P * H;
-  const size_t lds = sizeof(float) * 2 * H * D;
+  size_t lds = sizeof(float) * 2 * H * D;
   if (lds > 64 * 1024) return HKV_ERR_SHAPE;
   const int G = D / 8;
   // (the fp16 kernel indexes elements r * D in 32 bits)
@@ -1461,14 +1541,18 @@ int page_bound(const void* q, int q_dtype, int Hq, const void* kmin, const void*
     const int group = Hq / H;
     // key ranges per block only where a head is fixed per lane and scores are fp32
     uint2* mmp = (mm && hfix && H <= kMaxMMHeads && out_dtype == HKV_DT_F32) ? mm : nullptr;
+    size_t qraw = q_raw_lds(q, q_dtype, Hq, D);
+    if (lds + qraw > 64 * 1024) qraw = 0;
+    const int qlds = qraw != 0;
+    lds += qraw;
     switch (G) {
-      case 1: launch_bound_f16<1>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major, mmp); break;
-      case 2: launch_bound_f16<2>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major, mmp); break;
-      case 4: launch_bound_f16<4>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major, mmp); break;
-      case 8: launch_bound_f16<8>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major, mmp); break;
-      case 16: launch_bound_f16<16>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major, mmp); break;
-      case 32: launch_bound_f16<32>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major, mmp); break;
-      default: launch_bound_f16<64>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major, mmp); break;
+      case 1: launch_bound_f16<1>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major, mmp, qlds); break;
+      case 2: launch_bound_f16<2>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major, mmp, qlds); break;
+      case 4: launch_bound_f16<4>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major, mmp, qlds); break;
+      case 8: launch_bound_f16<8>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major, mmp, qlds); break;
+      case 16: launch_bound_f16<16>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major, mmp, qlds); break;
+      case 32: launch_bound_f16<32>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major, mmp, qlds); break;
+      default: launch_bound_f16<64>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major, mmp, qlds); break;
     }
     HKV_CHECK_LAUNCH();
     if (nmm && mmp) *nmm = (int)grid;
@@ -1788,13 +1872,17 @@ extern "C" int hkv_quest_select_ragged(const void* q, int q_dtype, int B, int Hq
   auto mn = (const uint16_t*)kmin;
   auto mx = (const uint16_t*)kmax;
   const int group = Hq / H;
+  size_t qraw = q_raw_lds(q, q_dtype, Hq, D);
+  if (lds + qraw > 64 * 1024) qraw = 0;
+  const int qlds = qraw != 0;
+  const size_t ldsq = lds + qraw;
 #define HKV_RB(GG)                                                                                \
   if (hfix)                                                                                       \
-    hipLaunchKernelGGL((bound_f16_ragged_kernel<GG, true>), dim3(gx, B), dim3(256), lds, st,      \
-                       (const char*)q, q_bytes, q_dtype, group, mn, mx, H, scores, sg);           \
+    hipLaunchKernelGGL((bound_f16_ragged_kernel<GG, true>), dim3(gx, B), dim3(256), ldsq, st,     \
+                       (const char*)q, q_bytes, q_dtype, group, mn, mx, H, scores, sg, qlds);     \
   else                                                                                            \
-    hipLaunchKernelGGL((bound_f16_ragged_kernel<GG, false>), dim3(gx, B), dim3(256), lds, st,     \
-                       (const char*)q, q_bytes, q_dtype, group, mn, mx, H, scores, sg);
+    hipLaunchKernelGGL((bound_f16_ragged_kernel<GG, false>), dim3(gx, B), dim3(256), ldsq, st,    \
+                       (const char*)q, q_bytes, q_dtype, group, mn, mx, H, scores, sg, qlds);
   switch (G) {
     case 1: HKV_RB(1) break;
     case 2: HKV_RB(2) break;
