@@ -935,10 +935,10 @@ struct MBWork {
   uint32_t* ctr;     // [H] arrival counters (zero between calls)
   const uint2* mm;   // [H][nmm] (min key, max key) of the bound kernel's blocks
   int nmm;
-  uint32_t* hist;    // [H][NB][kMBBins]
+  uint32_t* hist;    // [H][NB][kMBBins / 2] u16 counts, bin 2i in the low half of word i
   int* meta;         // [H][NB][2] (out row of the slice's first selected page, T-equal keys before it)
   uint32_t* thr;     // [H][4] (T, T-equal keys taken, 1 = selection already written, s + keff)
-  unsigned long long* wcand;  // [H][NB][kMBWin] keys of the slice's window bins (key << 32 | ~page)
+  uint32_t* wcand;   // [H][NB][kMBWin] keys of the slice's window bins
   int* wmeta;        // [H][NB][4] (first window bin, last window bin, keys stored, overflowed)
 };
 
@@ -950,7 +950,7 @@ struct MBShared {
   uint32_t bc[8];
   int wm[kMBMaxSlices][4];
   uint32_t sl_b1[kMBMaxSlices];
-  uint32_t slw[kMBWaves][8];
+  uint4 red4[kMBWaves];
   int sl_gt[kMBMaxSlices], sl_eq[kMBMaxSlices];
 };
 
@@ -988,6 +988,25 @@ HKV_DEV uint32_t mb_excl_scan(uint32_t v, uint32_t* red, uint32_t& total) {
   }
   total = tot;
   return before + x - v;
+}
+
+// Exclusive prefix sums of four values over the block in thread order.
+HKV_DEV uint4 mb_excl_scan4(uint4 v, uint4* red) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const uint4 x = make_uint4(wave_incl_scan_u(v.x), wave_incl_scan_u(v.y), wave_incl_scan_u(v.z),
+                             wave_incl_scan_u(v.w));
+  __syncthreads();
+  if (lane == 63) red[w] = x;
+  __syncthreads();
+  uint4 b = make_uint4(0u, 0u, 0u, 0u);
+  for (int i = 0; i < w; ++i) {
+    const uint4 r = red[i];
+    b.x += r.x;
+    b.y += r.y;
+    b.z += r.z;
+    b.w += r.w;
+  }
+  return make_uint4(b.x + x.x - v.x, b.y + x.y - v.y, b.z + x.z - v.z, b.w + x.w - v.w);
 }
 
 // Waits until this wave's global stores are complete (s_waitcnt vmcnt(0);
@@ -1039,8 +1058,15 @@ topk_mb_hist(const float* scores, int64_t P, int64_t s, int64_t keff, int64_t* o
   for (int i = 0; i < KPT; ++i)
     if (c0 + i * kMBThreads < n) atomicAdd(&sh.hist[bin_of(ukey(kv[i]))], 1u);
   __syncthreads();
-  uint32_t* gh = w.hist + ((int64_t)h * NB + j) * kMBBins;
-  for (int b = tid; b < kMBBins; b += kMBThreads) gh[b] = sh.hist[b];
+  // the slice's histogram as u16 (a slice holds at most 2^15 keys): thread t
+  // stores bins 4t .. 4t + 3
+  static_assert(kMBBins == 4 * kMBThreads, "four bins per thread");
+  static_assert(kMBThreads * KPT <= 65535, "u16 bin counts");
+  {
+    const uint4 hb = reinterpret_cast<const uint4*>(sh.hist)[tid];
+    reinterpret_cast<uint2*>(w.hist + ((int64_t)h * NB + j) * (kMBBins / 2))[tid] =
+        make_uint2(hb.x | (hb.y << 16), hb.z | (hb.w << 16));
+  }
   {
     // This slice's own estimate of the threshold bin (the bin of its
     // proportional share of keff), and the keys of the bins around it: if the
@@ -1067,16 +1093,28 @@ topk_mb_hist(const float* scores, int64_t P, int64_t s, int64_t keff, int64_t* o
     const int bj = (int)sh.bc[2];
     const int wlo = bj - kMBWinBins > 0 ? bj - kMBWinBins : 0;
     const int whi = bj + kMBWinBins < kMBBins - 1 ? bj + kMBWinBins : kMBBins - 1;
-    unsigned long long* wc = w.wcand + ((int64_t)h * NB + j) * kMBWin;
+    uint32_t* wc = w.wcand + ((int64_t)h * NB + j) * kMBWin;
+    // the thread's window keys (a mask), their offset among the wave's by a
+    // wave scan, and one LDS atomic per wave for the wave's base
+    static_assert(KPT <= 32, "window mask");
+    uint32_t m = 0;
 #pragma unroll
     for (int i = 0; i < KPT; ++i) {
-      const int c = c0 + i * kMBThreads;
-      if (c < n) {
-        const uint32_t k = ukey(kv[i]);
-        const int b = bin_of(k);
-        if (b >= wlo && b <= whi) {
-          const uint32_t slot = atomicAdd(&sh.ncand, 1u);
-          if (slot < (uint32_t)kMBWin) wc[slot] = ((unsigned long long)k << 32) | (uint32_t)~(uint32_t)c;
+      const int b = bin_of(ukey(kv[i]));
+      m |= (c0 + i * kMBThreads < n && b >= wlo && b <= whi) ? 1u << i : 0u;
+    }
+    const uint32_t cm = (uint32_t)__builtin_popcount(m);
+    const uint32_t incl = wave_incl_scan_u(cm);
+    const uint32_t wtot = rl_u(incl, 63);
+    if (wtot) {
+      uint32_t b0 = 0;
+      if ((tid & 63) == 0) b0 = atomicAdd(&sh.ncand, wtot);
+      uint32_t slot = rl_u(b0, 0) + incl - cm;
+#pragma unroll
+      for (int i = 0; i < KPT; ++i) {
+        if ((m >> i) & 1u) {
+          if (slot < (uint32_t)kMBWin) wc[slot] = ukey(kv[i]);
+          ++slot;
         }
       }
     }
@@ -1104,20 +1142,21 @@ topk_mb_hist(const float* scores, int64_t P, int64_t s, int64_t keff, int64_t* o
   __syncthreads();
 
   // ---- last block of head h: the threshold
-  // Thread t sums bins t + 1024 k4 over the slices, keeping each slice's value
-  // (the slices' counts in the threshold bin come from them).  The slices'
-  // windows are requested in the same round trip (up to 8 slices).
-  constexpr int KB = kMBBins / kMBThreads;  // bins per thread
+  // Thread t owns bins 4 * ch .. 4 * ch + 3, ch = 1023 - t (bins high to low
+  // over the threads; its k-th bin from the top is field 3 - k), one 8-byte
+  // chunk of every slice's u16 histogram.  Per group of 8 slices a packed
+  // scan (two slices per word) of the thread's per-slice sums gives every
+  // slice's count in the bins above the thread's.  The slices' windows and
+  // window descriptors are requested in the same round trip (up to 8 slices).
+  static_assert(kMBWin == kMBThreads, "window word u of thread t is entry t of slice u");
   const int NBc = NB < kMBMaxSlices ? NB : kMBMaxSlices;
-  const bool win_regs = NBc * kMBWin <= 8 * kMBThreads;
-  unsigned long long wcr[8];
+  const bool win_regs = NBc <= 8;
+  uint32_t wcr[8];
   if (win_regs) {
-    const int nwin = NBc * kMBWin;
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      int f = u * kMBThreads + tid;
-      f = f < nwin ? f : nwin - 1;
-      wcr[u] = w.wcand[(int64_t)h * NB * kMBWin + f];  // slices are consecutive: [NB][kMBWin]
+      const int jj = u < NBc ? u : NBc - 1;
+      wcr[u] = w.wcand[((int64_t)h * NB + jj) * kMBWin + tid];
     }
   }
   // the slices' window descriptors, one int per thread (NBc * 4 <= 256),
@@ -1126,27 +1165,59 @@ topk_mb_hist(const float* scores, int64_t P, int64_t s, int64_t keff, int64_t* o
   // are requested
   const int nwm = NBc * 4;
   const int wmv = w.wmeta[((int64_t)h * NB) * 4 + (tid < nwm ? tid : nwm - 1)];
-  uint32_t hv[KB][8];  // slices j0..j0+7 of the thread's bins (the last group kept)
-  for (int k4 = 0; k4 < KB; ++k4) sh.hist[k4 * kMBThreads + tid] = 0u;
-  if (tid == 0) {  // found below (defaults for safety)
-    sh.bc[0] = 0u;
-    sh.bc[1] = 0u;
-  }
-  for (int j0 = 0; j0 < NBc; j0 += 8) {
+  const uint2* hist2 = reinterpret_cast<const uint2*>(w.hist + (int64_t)h * NB * (kMBBins / 2));
+  const int ch = kMBThreads - 1 - tid;
+  auto field = [](uint2 x, int e) {  // bin 4 * ch + e of a chunk
+    const uint32_t v = e < 2 ? x.x : x.y;
+    return (e & 1) ? v >> 16 : v & 0xffffu;
+  };
+  uint2 hv[8];                          // chunks of slices g * 8 .. g * 8 + 7
+  uint32_t binc[4] = {0u, 0u, 0u, 0u};  // the thread's bins summed over the slices
+  auto load_group = [&](int g) {
 #pragma unroll
-    for (int k4 = 0; k4 < KB; ++k4)
+    for (int u = 0; u < 8; ++u) {
+      const int jj = g * 8 + u < NBc ? g * 8 + u : NBc - 1;
+      hv[u] = hist2[(int64_t)jj * (kMBBins / 4) + ch];
+    }
+  };
+  // the group's per-slice sums of the thread's bins, packed two per word (a
+  // slice holds at most 2^15 keys), and its exclusive scan over the threads
+  auto group_scan = [&](int g) {
+    uint32_t ss[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int jj = j0 + u < NBc ? j0 + u : NBc - 1;
-        hv[k4][u] = w.hist[((int64_t)h * NB + jj) * kMBBins + k4 * kMBThreads + tid];
-      }
-#pragma unroll
-    for (int k4 = 0; k4 < KB; ++k4) {
+    for (int u = 0; u < 8; ++u) {
       uint32_t t = 0;
 #pragma unroll
-      for (int u = 0; u < 8; ++u) t += j0 + u < NBc ? hv[k4][u] : 0u;
-      sh.hist[k4 * kMBThreads + tid] += t;
+      for (int e = 0; e < 4; ++e) t += field(hv[u], e);
+      ss[u] = g * 8 + u < NBc ? t : 0u;
     }
+    return mb_excl_scan4(make_uint4(ss[0] | ss[1] << 16, ss[2] | ss[3] << 16, ss[4] | ss[5] << 16,
+                                    ss[6] | ss[7] << 16),
+                         sh.red4);
+  };
+  auto half = [](uint4 p, int u) {
+    const uint32_t v = u < 2 ? p.x : u < 4 ? p.y : u < 6 ? p.z : p.w;
+    return (u & 1) ? v >> 16 : v & 0xffffu;
+  };
+  auto add_bins = [&](int g) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) binc[e] += g * 8 + u < NBc ? field(hv[u], e) : 0u;
+  };
+  if (tid == 0) {  // found below (defaults keep every index in range)
+    sh.bc[0] = 0u;
+    sh.bc[1] = 0u;
+    sh.bc[5] = 0u;
+    sh.bc[6] = 0u;
+    sh.bc[7] = 0u;
+  }
+  if (tid < kMBMaxSlices) sh.sl_eq[tid] = 0;
+  load_group(0);
+  add_bins(0);
+  for (int g = 1; g * 8 < NBc; ++g) {  // more than 8 slices: totals first
+    load_group(g);
+    add_bins(g);
   }
   {
     // unconditional (threads past nwm rewrite the last entry with its own
@@ -1154,26 +1225,78 @@ topk_mb_hist(const float* scores, int64_t P, int64_t s, int64_t keff, int64_t* o
     const int i = tid < nwm ? tid : nwm - 1;
     sh.wm[i >> 2][i & 3] = wmv;
   }
-  __syncthreads();
-  // bins high to low: thread t owns bins [4095 - 4t - 3, 4095 - 4t]
   const uint32_t need = (uint32_t)keff;
-  uint32_t mine = 0;
+  uint4 p0 = make_uint4(0u, 0u, 0u, 0u);
+  uint32_t above;
+  if (NBc <= 8) {
+    // one packed scan gives the counts above the thread's bins, in all and per slice
+    p0 = group_scan(0);
+    above = 0;
 #pragma unroll
-  for (int k = 0; k < 4; ++k) mine += sh.hist[kMBBins - 1 - 4 * tid - k];
-  uint32_t tot;
-  uint32_t above = mb_excl_scan(mine, sh.red[0], tot);
+    for (int u = 0; u < 8; ++u) above += half(p0, u);
+  } else {
+    uint32_t tot;
+    above = mb_excl_scan(binc[0] + binc[1] + binc[2] + binc[3], sh.red[0], tot);
+  }
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    const int b = kMBBins - 1 - 4 * tid - k;
-    const uint32_t c = sh.hist[b];
+    const uint32_t c = binc[3 - k];
     if (above < need && above + c >= need) {
-      sh.bc[0] = (uint32_t)b;
+      // the threshold bin (up to 8 slices, with every slice's count above and in it)
+      sh.bc[0] = (uint32_t)(4 * ch + 3 - k);
       sh.bc[1] = above;
+      sh.bc[5] = c;
+      sh.bc[6] = (uint32_t)k;
+      sh.bc[7] = (uint32_t)ch;
+      if (NBc <= 8) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          uint32_t gt = half(p0, u), in = 0;
+#pragma unroll
+          for (int kk = 0; kk < 4; ++kk) {
+            gt += kk < k ? field(hv[u], 3 - kk) : 0u;
+            in = kk == k ? field(hv[u], 3 - kk) : in;
+          }
+          if (u < NBc) {
+            sh.sl_gt[u] = (int)gt;
+            sh.sl_b1[u] = in;
+          }
+        }
+      }
     }
     above += c;
   }
   __syncthreads();
-  const uint32_t b1 = sh.bc[0], above1 = sh.bc[1], cnt1 = sh.hist[b1];
+  const uint32_t b1 = sh.bc[0], above1 = sh.bc[1], cnt1 = sh.bc[5];
+  if (NBc > 8) {
+    // per group: the packed scan again (chunks reloaded); the owner of the
+    // threshold bin keeps every slice's count above its bins, then thread jj
+    // adds slice jj's bins of the owner's chunk above the threshold bin
+    const int own = kMBThreads - 1 - (int)sh.bc[7];
+    for (int g = 0; g * 8 < NBc; ++g) {
+      load_group(g);
+      const uint4 pg = group_scan(g);
+      if (tid == own) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          if (g * 8 + u < NBc) sh.sl_gt[g * 8 + u] = (int)half(pg, u);
+      }
+    }
+    __syncthreads();
+    if (tid < NBc) {
+      const int k = (int)sh.bc[6];
+      const uint2 x = hist2[(int64_t)tid * (kMBBins / 4) + (int)sh.bc[7]];
+      uint32_t gt = 0, in = 0;
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        gt += kk < k ? field(x, 3 - kk) : 0u;
+        in = kk == k ? field(x, 3 - kk) : in;
+      }
+      sh.sl_gt[tid] += (int)gt;
+      sh.sl_b1[tid] = in;
+    }
+    __syncthreads();
+  }
   const uint32_t r = need - above1;  // 1 <= r <= cnt1
   const uint32_t lo1 = mn + (b1 << sh1);
   // last key of bin b1, saturated (the top bin can end past 2^32 - 1)
@@ -1187,70 +1310,40 @@ topk_mb_hist(const float* scores, int64_t P, int64_t s, int64_t keff, int64_t* o
     if (tid == 0) w.thr[h * 4 + 2] = 1u;
     return;
   }
-  // the slices' counts in bin b1 (known for up to 8 slices: the last group in hv)
-  if (NBc <= 8 && tid == (int)(b1 % kMBThreads)) {
-    const int k4 = (int)(b1 / kMBThreads);
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      uint32_t v = 0;
-#pragma unroll
-      for (int kk = 0; kk < KB; ++kk) v = kk == k4 ? hv[kk][u] : v;
-      if (u < NBc) sh.sl_b1[u] = v;
-    }
-  }
   if (tid == 0) {
     sh.ncand = 0u;
     sh.bc[3] = 0u;
     sh.bc[4] = 0xffffffffu;
   }
-  if (tid < kMBMaxSlices) sh.sl_eq[tid] = 0;
-  // per-slice counts of keys in bins above b1: thread sums, wave sums, one
-  // exchange through LDS per group of 8 slices
-  for (int j0 = 0; j0 < NBc; j0 += 8) {
-    if (j0 + 8 < NBc || j0 > 0) {  // more than 8 slices: reload this group
-#pragma unroll
-      for (int k4 = 0; k4 < KB; ++k4)
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const int jj = j0 + u < NBc ? j0 + u : NBc - 1;
-          hv[k4][u] = w.hist[((int64_t)h * NB + jj) * kMBBins + k4 * kMBThreads + tid];
-        }
-    }
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      uint32_t c = 0;
-#pragma unroll
-      for (int k4 = 0; k4 < KB; ++k4) c += (uint32_t)(k4 * kMBThreads + tid) > b1 ? hv[k4][u] : 0u;
-      c = wave_sum_u(c);
-      if ((tid & 63) == 0) sh.slw[tid >> 6][u] = c;
-    }
-    __syncthreads();
-    if (tid < 8 && j0 + tid < NBc) {
-      uint32_t t = 0;
-      for (int i = 0; i < kMBWaves; ++i) t += sh.slw[i][tid];
-      sh.sl_gt[j0 + tid] = (int)t;
-    }
-    __syncthreads();
-  }
-
   // the windows hold every key of bin b1 if b1 lies in every window of a slice
-  // with keys there (and no window overflowed)
-  bool use_win = win_regs;
-  for (int jj = 0; jj < NBc && use_win; ++jj) {
-    const bool covers = (int)b1 >= sh.wm[jj][0] && (int)b1 <= sh.wm[jj][1];
-    const bool empty = NBc <= 8 && sh.sl_b1[jj] == 0u;
-    if (sh.wm[jj][3] || !(covers || empty)) use_win = false;
+  // with keys there (and no window overflowed); one slice per thread
+  bool bad = false;
+  if (tid < NBc) {
+    const bool covers = (int)b1 >= sh.wm[tid][0] && (int)b1 <= sh.wm[tid][1];
+    bad = sh.wm[tid][3] != 0 || !(covers || sh.sl_b1[tid] == 0u);
   }
+  const bool use_win = win_regs && !__syncthreads_or(bad);
   if (use_win) {
+    // the thread's keys of bin b1 (a mask over the slices' windows), their
+    // offset among the wave's by a wave scan, one LDS atomic per wave
+    uint32_t m = 0;
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      const int f = u * kMBThreads + tid;
-      const int jj = f / kMBWin, e = f - jj * kMBWin;
-      if (jj < NBc && e < sh.wm[jj][2]) {
-        const uint32_t k = (uint32_t)(wcr[u] >> 32);
-        if (k >= lo1 && k <= hi1) {
-          const uint32_t slot = atomicAdd(&sh.ncand, 1u);
-          if (slot < (uint32_t)kMBCand) sh.cand[slot] = wcr[u];
+      const int cntu = u < NBc ? sh.wm[u][2] : 0;
+      m |= (tid < cntu && wcr[u] >= lo1 && wcr[u] <= hi1) ? 1u << u : 0u;
+    }
+    const uint32_t cm = (uint32_t)__builtin_popcount(m);
+    const uint32_t incl = wave_incl_scan_u(cm);
+    const uint32_t wtot = rl_u(incl, 63);
+    if (wtot) {
+      uint32_t b0 = 0;
+      if ((tid & 63) == 0) b0 = atomicAdd(&sh.ncand, wtot);
+      uint32_t slot = rl_u(b0, 0) + incl - cm;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        if ((m >> u) & 1u) {
+          if (slot < (uint32_t)kMBCand) sh.cand[slot] = ((unsigned long long)wcr[u] << 32) | (uint32_t)u;
+          ++slot;
         }
       }
     }
@@ -1274,7 +1367,7 @@ topk_mb_hist(const float* scores, int64_t P, int64_t s, int64_t keff, int64_t* o
         if (idx < n && k >= lo1 && k <= hi1) {
           const uint32_t slot = atomicAdd(&sh.ncand, 1u);
           if (slot < (uint32_t)kMBCand)
-            sh.cand[slot] = ((unsigned long long)k << 32) | (uint32_t)~(uint32_t)idx;
+            sh.cand[slot] = ((unsigned long long)k << 32) | (uint32_t)(idx / slice);
         }
       }
     };
@@ -1298,18 +1391,20 @@ topk_mb_hist(const float* scores, int64_t P, int64_t s, int64_t keff, int64_t* o
     const uint32_t* ck = reinterpret_cast<const uint32_t*>(sh.cand);  // key of candidate u: ck[2u + 1]
     const uint32_t mk = tid < (int)nc ? ck[2 * tid + 1] : 0u;
     uint32_t gtc = 0, gec = 0, u = 0;
-    for (; u + 8 <= nc; u += 8) {
+    if ((uint32_t)(tid & ~63) < nc) {  // waves holding candidates
+      for (; u + 8 <= nc; u += 8) {
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const uint32_t k = ck[2 * (u + q) + 1];
+        for (int q = 0; q < 8; ++q) {
+          const uint32_t k = ck[2 * (u + q) + 1];
+          gtc += k > mk ? 1u : 0u;
+          gec += k >= mk ? 1u : 0u;
+        }
+      }
+      for (; u < nc; ++u) {
+        const uint32_t k = ck[2 * u + 1];
         gtc += k > mk ? 1u : 0u;
         gec += k >= mk ? 1u : 0u;
       }
-    }
-    for (; u < nc; ++u) {
-      const uint32_t k = ck[2 * u + 1];
-      gtc += k > mk ? 1u : 0u;
-      gec += k >= mk ? 1u : 0u;
     }
     if (tid < (int)nc && gtc < rr && rr <= gec) {  // every such candidate has key T
       sh.bc[4] = mk;
@@ -1349,13 +1444,14 @@ topk_mb_hist(const float* scores, int64_t P, int64_t s, int64_t keff, int64_t* o
     ngt = sh.bc[3];
   }
   const uint32_t need_eq = rr - ngt;  // T-equal keys taken, lowest pages first
-  // the slices' candidates above and equal to T
+  // the slices' candidates above and equal to T (a candidate's low word is
+  // its slice)
   for (uint32_t i = tid; i < nc; i += kMBThreads) {
     const unsigned long long v = sh.cand[i];
     const uint32_t k = (uint32_t)(v >> 32);
-    const int idx = (int)~(uint32_t)v;
-    if (k > T) atomicAdd(&sh.sl_gt[idx / slice], 1);
-    else if (k == T) atomicAdd(&sh.sl_eq[idx / slice], 1);
+    const int jj = (int)(uint32_t)v;
+    if (k > T) atomicAdd(&sh.sl_gt[jj], 1);
+    else if (k == T) atomicAdd(&sh.sl_eq[jj], 1);
   }
   __syncthreads();
   if (tid == 0) {
@@ -1704,9 +1800,9 @@ SelectWs select_ws_layout(int64_t P, int H) {
   l.thr_off = al(sizeof(uint32_t) * H);
   l.mm_off = l.thr_off + al(sizeof(uint32_t) * 4 * H);
   l.hist_off = l.mm_off + al(sizeof(uint2) * (size_t)num_cus() * 4 * H);
-  l.meta_off = l.hist_off + al(sizeof(uint32_t) * (size_t)H * nb * kMBBins);
+  l.meta_off = l.hist_off + al(sizeof(uint32_t) * (size_t)H * nb * (kMBBins / 2));
   l.wcand_off = l.meta_off + al(sizeof(int) * 2 * (size_t)H * nb);
-  l.wmeta_off = l.wcand_off + al(sizeof(unsigned long long) * (size_t)H * nb * kMBWin);
+  l.wmeta_off = l.wcand_off + al(sizeof(uint32_t) * (size_t)H * nb * kMBWin);
   l.bytes = l.wmeta_off + al(sizeof(int) * 4 * (size_t)H * nb);
   return l;
 }
@@ -1772,7 +1868,7 @@ extern "C" int hkv_quest_select(const void* q, int q_dtype, int Hq, const void* 
   w.hist = (uint32_t*)(ws + lay.hist_off);
   w.meta = (int*)(ws + lay.meta_off);
   w.thr = (uint32_t*)(ws + lay.thr_off);
-  w.wcand = (unsigned long long*)(ws + lay.wcand_off);
+  w.wcand = (uint32_t*)(ws + lay.wcand_off);
   w.wmeta = (int*)(ws + lay.wmeta_off);
   const dim3 grid((unsigned)lay.NB, (unsigned)H);
   if (lay.kpt == 8) {

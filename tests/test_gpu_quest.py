@@ -150,6 +150,7 @@ def test_fused_select_small_and_per_kv_head(dev):
     (65536, 4, 1, 65532, 4, "normal"),     # every candidate
     (50000, 1, 3, 12345, 7, "ties"),       # few distinct scores: big equal runs
     (70000, 4, 7, 17500, 4, "equal"),      # all scores equal: the huge-bin fallback
+    (131072, 2, 7, 32768, 4, "normal"),    # 16 slices: per-slice counts from reloaded groups
     (600000, 2, 7, 150000, 4, "normal"),   # many slices (KPT 32)
     (65536, 2, 7, 100, 4, "nan"),          # NaN ranks highest: the threshold in the top bin
     (65536, 2, 7, 5000, 1, "nan"),         # NaN present (coarse bins), one sink: unaligned column
