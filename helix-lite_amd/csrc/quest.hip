@@ -335,7 +335,7 @@ constexpr int kQRawChunks = 4;
 template <int G, bool HFIX>
 HKV_DEV void bound_f16_rows(const void* q, int qdt, int group, const uint16_t* __restrict__ kmin,
                             const uint16_t* __restrict__ kmax, int64_t P, int H, void* out, int odt,
-                            int head_major, int64_t out_p, int64_t out_off,
+                            int head_major, int64_t out_p, int64_t out_off, int bx, int gx,
                             uint2* __restrict__ mm = nullptr, int q_lds = 0) {
   constexpr int D = 8 * G;
   constexpr int RB = 256 / G;  // rows per block per row group
@@ -350,7 +350,7 @@ HKV_DEV void bound_f16_rows(const void* q, int qdt, int group, const uint16_t* _
   // No rows (an empty sequence of a ragged batch): nothing to load.  The loads
   // below clamp to row nr - 1, which must exist.  Uniform over the block.
   if (nr <= 0) return;
-  const int step = gridDim.x * span;
+  const int step = gx * span;  // block bx of gx over these rows
   uint4 a0[U], b0[U], a1[U], b1[U];
   // Loads are unconditional, rows past the end clamped to the last row (their
   // results are not written): a fixed number of loads per step lets the
@@ -365,7 +365,7 @@ HKV_DEV void bound_f16_rows(const void* q, int qdt, int group, const uint16_t* _
       b[u] = reinterpret_cast<const uint4*>(kmax + (uint32_t)r * D)[c];
     }
   };
-  int r0 = blockIdx.x * span;
+  int r0 = bx * span;
   // the block's clamped, group-summed query, [2][H][D] in LDS
   if (q_lds) {
     // raw query chunks first, then two steps of statistics: waiting for the
@@ -500,17 +500,20 @@ __global__ void __launch_bounds__(256)
 bound_f16_kernel(const void* q, int qdt, int group, const uint16_t* __restrict__ kmin,
                  const uint16_t* __restrict__ kmax, int64_t P, int H, void* out, int odt,
                  int head_major, uint2* mm, int q_lds) {
-  bound_f16_rows<G, HFIX>(q, qdt, group, kmin, kmax, P, H, out, odt, head_major, P, 0, mm, q_lds);
+  bound_f16_rows<G, HFIX>(q, qdt, group, kmin, kmax, P, H, out, odt, head_major, P, 0, blockIdx.x,
+                          gridDim.x, mm, q_lds);
 }
 
-// Ragged batch: sequence s = blockIdx.y owns pages [off[s], off[s+1]) of the
-// concatenated statistics and query q + s * q_bytes; scores head-major over
-// the concatenated page axis, (H, off[nseg]).
+// Ragged batch: sequence s owns pages [off[s], off[s+1]) of the concatenated
+// statistics and query q + s * q_bytes (the bound kernel's blocks
+// [blk[s], blk[s+1]), the top-K kernel's blockIdx.y = s); scores head-major
+// over the concatenated page axis, (H, off[nseg]).
 constexpr int kMaxSeqs = 64;
 struct Segs {
   int64_t off[kMaxSeqs + 1];
   int64_t k[kMaxSeqs];
   int64_t out_off[kMaxSeqs + 1];
+  int blk[kMaxSeqs + 1];  // the bound kernel's blocks of sequence b: [blk[b], blk[b+1])
   int nseg;
 };
 
@@ -519,11 +522,14 @@ __global__ void __launch_bounds__(256)
 bound_f16_ragged_kernel(const char* q, int64_t q_bytes, int qdt, int group,
                         const uint16_t* __restrict__ kmin, const uint16_t* __restrict__ kmax, int H,
                         float* out, const Segs segs, int q_lds) {
-  const int sq = blockIdx.y;
+  // blocks are given to the sequences in proportion to their pages
+  int sq = 0;
+  while (sq + 1 < segs.nseg && segs.blk[sq + 1] <= (int)blockIdx.x) ++sq;
+  const int bx = (int)blockIdx.x - segs.blk[sq], gx = segs.blk[sq + 1] - segs.blk[sq];
   const int64_t o0 = segs.off[sq], P = segs.off[sq + 1] - o0;
   bound_f16_rows<G, HFIX>(q + sq * q_bytes, qdt, group, kmin + o0 * H * (8 * G),
                           kmax + o0 * H * (8 * G), P, H, out, HKV_DT_F32, 1, segs.off[segs.nseg], o0,
-                          nullptr, q_lds);
+                          bx, gx, nullptr, q_lds);
 }
 
 // --------------------------------------------------------- a10: top-K
@@ -1957,12 +1963,22 @@ extern "C" int hkv_quest_select_ragged(const void* q, int q_dtype, int B, int Hq
   hipStream_t st = (hipStream_t)stream;
   const size_t lds = sizeof(float) * 2 * H * D;
   if (lds > 64 * 1024) return HKV_ERR_SHAPE;
-  // blocks per sequence: enough for the longest one to fill the chip with B sequences
-  int64_t maxP = 0;
-  for (int b = 0; b < B; ++b) maxP = std::max<int64_t>(maxP, page_offsets[b + 1] - page_offsets[b]);
+  // blocks per sequence: num_cus * 4 in all, shared in proportion to the
+  // sequences' pages (at least one for a non-empty sequence, at most one per
+  // row group); an empty sequence gets none
   const int64_t span = (int64_t)(256 / G) * kBoundUnrollF16;
-  const int64_t want = std::max<int64_t>(1, ((int64_t)num_cus() * 4 + B - 1) / B);
-  const unsigned gx = (unsigned)std::max<int64_t>(1, std::min<int64_t>((maxP * H + span - 1) / span, want));
+  const int64_t nbt = (int64_t)num_cus() * 4;
+  sg.blk[0] = 0;
+  for (int b = 0; b < B; ++b) {
+    const int64_t rows_b = (page_offsets[b + 1] - page_offsets[b]) * H;
+    int64_t nb = 0;
+    if (rows_b > 0) {
+      nb = (nbt * rows_b + Ptot * H / 2) / (Ptot * H);
+      nb = std::max<int64_t>(1, std::min<int64_t>(nb, (rows_b + span - 1) / span));
+    }
+    sg.blk[b + 1] = sg.blk[b] + (int)nb;
+  }
+  const unsigned gx = (unsigned)sg.blk[B];
   const int64_t q_bytes = (int64_t)Hq * D * (q_dtype == HKV_DT_F32 ? 4 : 2);
   const bool hfix = (64 / G) % H == 0;
   auto mn = (const uint16_t*)kmin;
@@ -1974,10 +1990,10 @@ extern "C" int hkv_quest_select_ragged(const void* q, int q_dtype, int B, int Hq
   const size_t ldsq = lds + qraw;
 #define HKV_RB(GG)                                                                                \
   if (hfix)                                                                                       \
-    hipLaunchKernelGGL((bound_f16_ragged_kernel<GG, true>), dim3(gx, B), dim3(256), ldsq, st,     \
+    hipLaunchKernelGGL((bound_f16_ragged_kernel<GG, true>), dim3(gx), dim3(256), ldsq, st,        \
                        (const char*)q, q_bytes, q_dtype, group, mn, mx, H, scores, sg, qlds);     \
   else                                                                                            \
-    hipLaunchKernelGGL((bound_f16_ragged_kernel<GG, false>), dim3(gx, B), dim3(256), ldsq, st,    \
+    hipLaunchKernelGGL((bound_f16_ragged_kernel<GG, false>), dim3(gx), dim3(256), ldsq, st,       \
                        (const char*)q, q_bytes, q_dtype, group, mn, mx, H, scores, sg, qlds);
   switch (G) {
     case 1: HKV_RB(1) break;
