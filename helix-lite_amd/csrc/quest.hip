@@ -958,6 +958,7 @@ struct MBShared {
   uint32_t sl_b1[kMBMaxSlices];
   uint4 red4[kMBWaves];
   int sl_gt[kMBMaxSlices], sl_eq[kMBMaxSlices];
+  int win_half;  // the slice's window half-width in bins
 };
 
 // Block-wide minimum of a and maximum of b (one pair of barriers).
@@ -1097,8 +1098,30 @@ topk_mb_hist(const float* scores, int64_t P, int64_t s, int64_t keff, int64_t* o
     if (tid == 0) sh.ncand = 0u;
     __syncthreads();
     const int bj = (int)sh.bc[2];
-    const int wlo = bj - kMBWinBins > 0 ? bj - kMBWinBins : 0;
-    const int whi = bj + kMBWinBins < kMBBins - 1 ? bj + kMBWinBins : kMBBins - 1;
+    // The window: the widest (half-width up to kMBWinBins) whose keys fit in
+    // kMBWin.  Where the bins are dense the estimate is also sharp in bins,
+    // so a narrow window still holds the threshold bin.  Lane i of wave 0
+    // takes bin bj - kMBWinBins + i; a wave scan gives every window's count.
+    static_assert(2 * kMBWinBins + 1 <= 64, "one bin per lane");
+    if (tid < 64) {
+      const int b = bj - kMBWinBins + tid;
+      const uint32_t c = (tid <= 2 * kMBWinBins && b >= 0 && b < kMBBins) ? sh.hist[b] : 0u;
+      const uint32_t incl = wave_incl_scan_u(c);  // bins bj - kMBWinBins .. b
+      // window of half-width a = tid: lanes kMBWinBins - a .. kMBWinBins + a
+      const int a = tid;
+      const int hi_l = kMBWinBins + a < 63 ? kMBWinBins + a : 63;
+      const int lo_l = kMBWinBins - a - 1;
+      const uint32_t at_hi = (uint32_t)__shfl((int)incl, hi_l, 64);
+      const uint32_t at_lo = (uint32_t)__shfl((int)incl, lo_l < 0 ? 0 : lo_l, 64);
+      const uint32_t cnt = at_hi - (lo_l < 0 ? 0u : at_lo);
+      // windows nest, so the ones that fit are a prefix of the half-widths
+      const uint64_t fit = __ballot(a <= kMBWinBins && cnt <= (uint32_t)kMBWin);
+      if (tid == 0) sh.win_half = fit ? 63 - __builtin_clzll(fit) : 0;
+    }
+    __syncthreads();
+    const int wh = sh.win_half;
+    const int wlo = bj - wh > 0 ? bj - wh : 0;
+    const int whi = bj + wh < kMBBins - 1 ? bj + wh : kMBBins - 1;
     uint32_t* wc = w.wcand + ((int64_t)h * NB + j) * kMBWin;
     // the thread's window keys (a mask), their offset among the wave's by a
     // wave scan, and one LDS atomic per wave for the wave's base
