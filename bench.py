@@ -252,7 +252,7 @@ def bench_quest(args, dev):
     step holds one selection per layer), so the timing is HBM-bound and free
     of Python and graph-launch overhead (a replay of a single-selection graph
     costs about 8 us of host submission)."""
-    from helix_kv.ops import quest_page_stats, quest_select
+    from helix_kv.ops import quest_page_stats, quest_page_stats_u8, quest_select, quest_select_u8
 
     P, page, Hq = 65536, 16, 28
     g = torch.Generator(device=dev).manual_seed(3)
@@ -294,8 +294,37 @@ def bench_quest(args, dev):
     algo = 2 * P * H * D * 2 + Hq * D * 2 + (k + s) * H * 8
     log(f"[bench] quest select: {us:.1f} us/step ({algo / (us * 1e-6) / 1e9:.0f} GB/s); "
         f"stats build {stats_ms * 1e3:.0f} us")
+
+    # the same selections over the compact u8 metadata of the same sets
+    u8sets = [quest_page_stats_u8(mn, mx) for mn, mx in sets]
+    u8_ms = time_events(lambda: quest_page_stats_u8(*sets[0]), max(3, args.steps))
+    with torch.cuda.stream(stream):
+        for i, st8 in enumerate(u8sets):
+            quest_select_u8(q, st8, k, s, scores=scores[i], out=outs[i])
+        torch.cuda.synchronize()
+        gr8 = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr8, stream=stream):
+            for j in range(per_graph):
+                quest_select_u8(q, u8sets[j % 3], k, s, scores=scores[j % 3], out=outs[j % 3])
+    torch.cuda.synchronize()
+    ref8 = [o.clone() for o in outs]
+    gr8.replay()
+    torch.cuda.synchronize()
+    a.record()
+    for i in range(replays):
+        gr8.replay()
+    b.record()
+    torch.cuda.synchronize()
+    us8 = a.elapsed_time(b) / (replays * per_graph) * 1e3
+    for o, r in zip(outs, ref8):
+        if not torch.equal(o, r):
+            raise RuntimeError("u8 Quest selection changed between graph replays")
+    algo8 = 2 * P * H * D + 2 * H * D * 4 + Hq * D * 2 + (k + s) * H * 8
+    log(f"[bench] quest select, u8 metadata: {us8:.1f} us/step ({algo8 / (us8 * 1e-6) / 1e9:.0f} GB/s); "
+        f"u8 conversion {u8_ms * 1e3:.0f} us")
     return dict(quest_us=us, quest_algo_bytes=algo, stats_ms=stats_ms,
-                stats_bytes=P * page * H * D * 2 + 2 * P * H * D * 2)
+                stats_bytes=P * page * H * D * 2 + 2 * P * H * D * 2,
+                quest_u8_us=us8, quest_u8_algo_bytes=algo8, stats_u8_ms=u8_ms)
 
 
 DEC_TOK, HQ = 1 << 20, 28
@@ -622,6 +651,12 @@ def main() -> None:
                                    "per HIP graph over 3 metadata sets (HBM-resident)",
                          "page_stats_build_us": round(res["stats_ms"] * 1e3, 1),
                          "page_stats_build_GBps": round(res["stats_bytes"] / (res["stats_ms"] * 1e-3) / 1e9, 1)}
+        q8 = res["quest_u8_algo_bytes"] / (res["quest_u8_us"] * 1e-6)
+        line["quest"]["u8_metadata"] = {
+            "us_per_step": round(res["quest_u8_us"], 2), "achieved_GBps": round(q8 / 1e9, 1),
+            "frac": round(q8 / HBM_PEAK, 4), "conversion_us": round(res["stats_u8_ms"] * 1e3, 1),
+            "config": "the same selections over u8 page min/max codes with per-(head, channel) "
+                      "lo/step (conservatively rounded: every bound >= the fp16 one)"}
     if "rag_us" in res:
         rach = res["rag_bytes"] / (res["rag_us"] * 1e-6)
         line["ragged"] = {"us_per_step": round(res["rag_us"], 1), "achieved_GBps": round(rach / 1e9, 1),

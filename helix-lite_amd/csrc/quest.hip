@@ -12,6 +12,8 @@
 // n/2 ... 1); bound = pos + neg, then + 0.0f so a zero bound is +0.
 #include "hkv_common.h"
 
+#include <type_traits>
+
 namespace {
 
 // --------------------------------------------------------------- a8: stats
@@ -332,11 +334,22 @@ constexpr int kBoundUnrollF16 = 4;  // row groups per step (two steps of loads i
 // wait only for them.
 constexpr int kQRawChunks = 4;
 
-template <int G, bool HFIX>
-HKV_DEV void bound_f16_rows(const void* q, int qdt, int group, const uint16_t* __restrict__ kmin,
-                            const uint16_t* __restrict__ kmax, int64_t P, int H, void* out, int odt,
+// U8: the statistics are u8 codes of the compact page metadata, read as
+// fl(lo + fl(code * step)) with lo / step per (head, channel) (dq_lo,
+// dq_step); a lane's head is fixed (HFIX), so its 8 channels' lo / step are
+// loaded once.  The products and the order are the fp16 path's.
+template <int G, bool HFIX, bool U8 = false>
+HKV_DEV void bound_f16_rows(const void* q, int qdt, int group, const void* kmin_v,
+                            const void* kmax_v, int64_t P, int H, void* out, int odt,
                             int head_major, int64_t out_p, int64_t out_off, int bx, int gx,
-                            uint2* __restrict__ mm = nullptr, int q_lds = 0) {
+                            uint2* __restrict__ mm = nullptr, int q_lds = 0,
+                            const float* __restrict__ dq_lo = nullptr,
+                            const float* __restrict__ dq_step = nullptr) {
+  static_assert(!U8 || HFIX, "u8 statistics need a fixed head per lane");
+  using ET = typename std::conditional<U8, uint8_t, uint16_t>::type;  // one statistic
+  using LT = typename std::conditional<U8, uint2, uint4>::type;       // a lane's 8 channels
+  const ET* __restrict__ kmin = static_cast<const ET*>(kmin_v);
+  const ET* __restrict__ kmax = static_cast<const ET*>(kmax_v);
   constexpr int D = 8 * G;
   constexpr int RB = 256 / G;  // rows per block per row group
   constexpr int U = kBoundUnrollF16;
@@ -351,18 +364,18 @@ HKV_DEV void bound_f16_rows(const void* q, int qdt, int group, const uint16_t* _
   // below clamp to row nr - 1, which must exist.  Uniform over the block.
   if (nr <= 0) return;
   const int step = gx * span;  // block bx of gx over these rows
-  uint4 a0[U], b0[U], a1[U], b1[U];
+  LT a0[U], b0[U], a1[U], b1[U];
   // Loads are unconditional, rows past the end clamped to the last row (their
   // results are not written): a fixed number of loads per step lets the
   // compiler wait for exactly one step's loads while the next step's are in
   // flight.
-  auto load = [&](int r0, uint4 (&a)[U], uint4 (&b)[U]) {
+  auto load = [&](int r0, LT (&a)[U], LT (&b)[U]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       int r = r0 + u * RB + rl;
       r = r < nr ? r : nr - 1;
-      a[u] = reinterpret_cast<const uint4*>(kmin + (uint32_t)r * D)[c];
-      b[u] = reinterpret_cast<const uint4*>(kmax + (uint32_t)r * D)[c];
+      a[u] = reinterpret_cast<const LT*>(kmin + (uint32_t)r * D)[c];
+      b[u] = reinterpret_cast<const LT*>(kmax + (uint32_t)r * D)[c];
     }
   };
   int r0 = bx * span;
@@ -415,8 +428,17 @@ HKV_DEV void bound_f16_rows(const void* q, int qdt, int group, const uint16_t* _
       qn[i] = qs[H * D + h * D + 8 * c + i];
     }
   }
+  float dlo[8], dst[8];  // U8: the lane's channels' lo / step
+  if constexpr (U8) {
+    const int h = rl % H;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      dlo[i] = dq_lo[h * D + 8 * c + i];
+      dst[i] = dq_step[h * D + 8 * c + i];
+    }
+  }
   uint32_t kmn_t = 0xffffffffu, kmx_t = 0u;  // key range of this thread's rows (HFIX: one head)
-  auto compute = [&](int rs, int pb, const uint4 (&a)[U], const uint4 (&b)[U]) {
+  auto compute = [&](int rs, int pb, const LT (&a)[U], const LT (&b)[U]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int r = rs + u * RB + rl;
@@ -433,15 +455,27 @@ HKV_DEV void bound_f16_rows(const void* q, int qdt, int group, const uint16_t* _
           qn[i] = qs[H * D + h * D + 8 * c + i];
         }
       }
-      const uint32_t wa[4] = {a[u].x, a[u].y, a[u].z, a[u].w};
-      const uint32_t wb[4] = {b[u].x, b[u].y, b[u].z, b[u].w};
       float ps = 0.0f, ns = 0.0f;
+      if constexpr (U8) {
+        const uint32_t wa[2] = {a[u].x, a[u].y};
+        const uint32_t wb[2] = {b[u].x, b[u].y};
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float px = (i & 1) ? mul_f16<1>(wb[i >> 1], qp[i]) : mul_f16<0>(wb[i >> 1], qp[i]);
-        const float pn = (i & 1) ? mul_f16<1>(wa[i >> 1], qn[i]) : mul_f16<0>(wa[i >> 1], qn[i]);
-        ps = __fadd_rn(ps, px);
-        ns = __fadd_rn(ns, pn);
+        for (int i = 0; i < 8; ++i) {
+          const float kx = __fadd_rn(dlo[i], __fmul_rn((float)((wb[i >> 2] >> (8 * (i & 3))) & 255u), dst[i]));
+          const float kn = __fadd_rn(dlo[i], __fmul_rn((float)((wa[i >> 2] >> (8 * (i & 3))) & 255u), dst[i]));
+          ps = __fadd_rn(ps, __fmul_rn(kx, qp[i]));
+          ns = __fadd_rn(ns, __fmul_rn(kn, qn[i]));
+        }
+      } else {
+        const uint32_t wa[4] = {a[u].x, a[u].y, a[u].z, a[u].w};
+        const uint32_t wb[4] = {b[u].x, b[u].y, b[u].z, b[u].w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float px = (i & 1) ? mul_f16<1>(wb[i >> 1], qp[i]) : mul_f16<0>(wb[i >> 1], qp[i]);
+          const float pn = (i & 1) ? mul_f16<1>(wa[i >> 1], qn[i]) : mul_f16<0>(wa[i >> 1], qn[i]);
+          ps = __fadd_rn(ps, px);
+          ns = __fadd_rn(ns, pn);
+        }
       }
       if constexpr (G == 16) {
         ps = row16_reduce(ps);
@@ -1618,6 +1652,15 @@ extern "C" int hkv_quest_page_stats(const void* k_pages, int dtype, int64_t P, i
 namespace {
 
 template <int G>
+__global__ void __launch_bounds__(256)
+bound_u8_kernel(const void* q, int qdt, int group, const uint8_t* __restrict__ kmin,
+                const uint8_t* __restrict__ kmax, const float* __restrict__ lo,
+                const float* __restrict__ step, int64_t P, int H, float* out, uint2* mm, int q_lds) {
+  bound_f16_rows<G, true, true>(q, qdt, group, kmin, kmax, P, H, out, HKV_DT_F32, 1, P, 0, blockIdx.x,
+                                gridDim.x, mm, q_lds, lo, step);
+}
+
+template <int G>
 void launch_bound_f16(bool hfix, unsigned grid, size_t lds, hipStream_t s, const void* q, int qdt,
                       int group, const uint16_t* kmin, const uint16_t* kmax, int64_t P, int H,
                       void* out, int odt, int head_major, uint2* mm, int q_lds) {
@@ -1801,6 +1844,176 @@ compact_blocks_kernel(uint8_t* __restrict__ flags, int64_t nblocks, int64_t bloc
   if (tid == 0) *n_out = carry;
 }
 
+// ------------------------------------------- compact (u8) page metadata
+//
+// Per (head, channel) over the finite statistics of all pages: lo = the
+// smallest, hi = the largest; step = fl((hi - lo) / 255), raised one ulp at a
+// time (at most 16) until deq(255) >= hi, with deq(q) = fl(lo + fl(q * step))
+// (step = 1 when hi <= lo or nothing is finite, lo = 0 then).  A minimum
+// codes as the floor of fl(fl(x - lo) / step), clamped to [0, 255] and lowered
+// (at most 4 times, then 0) while deq(q) > x; a maximum as the ceiling,
+// raised (at most 4 times, then 255) while deq(q) < x.  So deq(qmin) <= min
+// and deq(qmax) >= max for every finite statistic, and the bound from the
+// dequantised statistics is never below the fp16 one.  A non-finite
+// statistic codes as 0 (minimum) / 255 (maximum).
+
+HKV_DEV float u8_deq(uint32_t q, float lo, float step) { return __fadd_rn(lo, __fmul_rn((float)q, step)); }
+
+HKV_DEV float u8_step(float lo, float hi) {
+  if (!(hi > lo)) return 1.0f;
+  float st = __fdiv_rn(__fsub_rn(hi, lo), 255.0f);
+  for (int i = 0; i < 16 && u8_deq(255u, lo, st) < hi; ++i)
+    st = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, st) + 1u);  // next float up
+  return st;
+}
+
+HKV_DEV uint32_t u8_code(float x, float lo, float st, bool up) {
+  if (!__builtin_isfinite(x)) return up ? 255u : 0u;
+  float t = __fdiv_rn(__fsub_rn(x, lo), st);
+  t = up ? ceilf(t) : floorf(t);
+  int q = t < 0.0f ? 0 : (t > 255.0f ? 255 : (int)t);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float d = u8_deq((uint32_t)q, lo, st);
+    if (up) q = (q < 255 && d < x) ? q + 1 : q;
+    else q = (q > 0 && d > x) ? q - 1 : q;
+  }
+  const float d = u8_deq((uint32_t)q, lo, st);
+  if (up) q = d < x ? 255 : q;
+  else q = d > x ? 0 : q;
+  return (uint32_t)q;
+}
+
+HKV_DEV float key_to_f(uint32_t k) {  // inverse of ukey for finite values
+  return __builtin_bit_cast(float, (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+template <typename KT>
+HKV_DEV float stat_f(KT v) {
+  if constexpr (sizeof(KT) == 2) return h2f(v);
+  else return v;
+}
+
+__global__ void __launch_bounds__(256) stats_u8_init_kernel(uint32_t* __restrict__ rk, int HD) {
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < HD; i += gridDim.x * 256) {
+    rk[i] = 0xffffffffu;  // smallest key seen
+    rk[HD + i] = 0u;      // largest key seen
+  }
+}
+
+// Each thread keeps channels tid, tid + 256, ... over the block's pages
+// (consecutive threads read consecutive channels) and folds them into the
+// channel's range with device-scope atomics on the ordered keys.
+template <typename KT>
+__global__ void __launch_bounds__(256)
+stats_u8_range_kernel(const KT* __restrict__ kmin, const KT* __restrict__ kmax, int64_t P, int HD,
+                      uint32_t* __restrict__ rk) {
+  for (int ch = threadIdx.x; ch < HD; ch += 256) {
+    uint32_t lo = 0xffffffffu, hi = 0u;
+    bool any = false;
+    for (int64_t p = blockIdx.x; p < P; p += gridDim.x) {
+      const float a = stat_f(kmin[p * HD + ch]), b = stat_f(kmax[p * HD + ch]);
+      if (__builtin_isfinite(a)) {
+        const uint32_t k = ukey(a);
+        lo = k < lo ? k : lo;
+        hi = k > hi ? k : hi;
+        any = true;
+      }
+      if (__builtin_isfinite(b)) {
+        const uint32_t k = ukey(b);
+        lo = k < lo ? k : lo;
+        hi = k > hi ? k : hi;
+        any = true;
+      }
+    }
+    if (any) {
+      atomicMin(&rk[ch], lo);
+      atomicMax(&rk[HD + ch], hi);
+    }
+  }
+}
+
+__global__ void __launch_bounds__(256)
+stats_u8_params_kernel(const uint32_t* __restrict__ rk, int HD, float* __restrict__ lo,
+                       float* __restrict__ step) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= HD) return;
+  float l = 0.0f, h = 0.0f;
+  if (rk[i] != 0xffffffffu) {
+    l = key_to_f(rk[i]);
+    h = key_to_f(rk[HD + i]);
+  }
+  lo[i] = l;
+  step[i] = u8_step(l, h);
+}
+
+// Four statistics per thread (HD is a multiple of 4), one 32-bit store each.
+template <typename KT>
+__global__ void __launch_bounds__(256)
+stats_u8_quant_kernel(const KT* __restrict__ kmin, const KT* __restrict__ kmax, int64_t n4, int HD,
+                      const float* __restrict__ lo, const float* __restrict__ step,
+                      uint8_t* __restrict__ qmin, uint8_t* __restrict__ qmax) {
+  for (int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x; j < n4; j += (int64_t)gridDim.x * 256) {
+    const int64_t i0 = 4 * j;
+    const int ch0 = (int)(i0 % HD);
+    uint32_t wn = 0, wx = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float l = lo[ch0 + e], st = step[ch0 + e];
+      wn |= u8_code(stat_f(kmin[i0 + e]), l, st, false) << (8 * e);
+      wx |= u8_code(stat_f(kmax[i0 + e]), l, st, true) << (8 * e);
+    }
+    reinterpret_cast<uint32_t*>(qmin)[j] = wn;
+    reinterpret_cast<uint32_t*>(qmax)[j] = wx;
+  }
+}
+
+// Group-summed bound from the u8 metadata, (H, P) fp32 scores, plus each
+// block's key range (mm) when given.  Shapes: D a multiple of 8 with
+// G = D / 8 a power of two <= 64 and H dividing 64 / G (a lane's head is
+// fixed), P * H * D < 2^32.
+int page_bound_u8(const void* q, int q_dtype, int Hq, const uint8_t* kmin, const uint8_t* kmax,
+                  const float* lo, const float* step, int64_t P, int H, int D, float* out,
+                  hipStream_t s, uint2* mm, int* nmm) {
+  if (nmm) *nmm = 0;
+  if (!fdt(q_dtype) && q_dtype != HKV_DT_BF16) return HKV_ERR_DTYPE;
+  if (P < 0 || H < 1 || D < 8 || D % 8 || Hq < H || Hq % H) return HKV_ERR_SHAPE;
+  const int G = D / 8;
+  if ((G & (G - 1)) || G > 64 || (64 / G) % H) return HKV_ERR_SHAPE;
+  if (P * H * D >= ((int64_t)1 << 32) || P * H >= ((int64_t)1 << 31)) return HKV_ERR_SHAPE;
+  if (P == 0) return HKV_OK;
+  if (!q || !kmin || !kmax || !lo || !step || !out) return HKV_ERR_ARG;
+  if ((((uintptr_t)kmin | (uintptr_t)kmax) & 7u) || (((uintptr_t)lo | (uintptr_t)step) & 3u))
+    return HKV_ERR_ARG;
+  size_t lds = sizeof(float) * 2 * H * D;
+  if (lds > 64 * 1024) return HKV_ERR_SHAPE;
+  size_t qraw = q_raw_lds(q, q_dtype, Hq, D);
+  if (lds + qraw > 64 * 1024) qraw = 0;
+  const int qlds = qraw != 0;
+  lds += qraw;
+  const int64_t rows = P * H;
+  const int64_t span = (int64_t)(256 / G) * kBoundUnrollF16;
+  const unsigned grid = (unsigned)std::min<int64_t>((rows + span - 1) / span, (int64_t)num_cus() * 4);
+  uint2* mmp = (mm && H <= kMaxMMHeads) ? mm : nullptr;
+  const int group = Hq / H;
+#define HKV_BU8(GG)                                                                                 \
+  hipLaunchKernelGGL((bound_u8_kernel<GG>), dim3(grid), dim3(256), lds, s, q, q_dtype, group, kmin, \
+                     kmax, lo, step, P, H, out, mmp, qlds)
+  switch (G) {
+    case 1: HKV_BU8(1); break;
+    case 2: HKV_BU8(2); break;
+    case 4: HKV_BU8(4); break;
+    case 8: HKV_BU8(8); break;
+    case 16: HKV_BU8(16); break;
+    case 32: HKV_BU8(32); break;
+    default: HKV_BU8(64); break;
+  }
+#undef HKV_BU8
+  HKV_CHECK_LAUNCH();
+  if (nmm && mmp) *nmm = (int)grid;
+  return HKV_OK;
+}
+
 }  // namespace
 
 namespace {
@@ -1810,6 +2023,10 @@ struct SelectWs {
   int NB, kpt;
   size_t ctr_off, thr_off, mm_off, hist_off, meta_off, wcand_off, wmeta_off, bytes;
 };
+
+int select_after_bound(const float* scores, int64_t P, int H, int64_t k, int64_t sink_pages, int64_t s,
+                       int64_t keff, int64_t* out, const struct SelectWs& lay, bool mb, char* ws,
+                       int nmm, hipStream_t st);
 
 SelectWs select_ws_layout(int64_t P, int H) {
   SelectWs l{};
@@ -1889,6 +2106,39 @@ extern "C" int hkv_quest_select(const void* q, int q_dtype, int Hq, const void* 
   const int rc = page_bound(q, q_dtype, Hq, kmin, kmax, k_dtype, P, H, D, scores, HKV_DT_F32, 1, st,
                             nullptr, 0, mb ? (uint2*)(ws + lay.mm_off) : nullptr, &nmm);
   if (rc != HKV_OK) return rc;
+  return select_after_bound(scores, P, H, k, sink_pages, s, keff, out, lay, mb, ws, nmm, st);
+}
+
+extern "C" int hkv_quest_select_u8(const void* q, int q_dtype, int Hq, const uint8_t* kmin,
+                                   const uint8_t* kmax, const float* lo, const float* step, int64_t P,
+                                   int H, int D, int64_t k, int64_t sink_pages, float* scores,
+                                   int64_t* out, int64_t* n_out, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
+  if (P < 0 || H < 1 || D < 1 || D > 512 || Hq < H || Hq % H) return HKV_ERR_SHAPE;
+  const int64_t s = sink_pages < 0 ? 0 : (sink_pages > P ? P : sink_pages);
+  const int64_t keff = k < 0 ? 0 : (k > P - s ? P - s : k);
+  if (n_out) *n_out = s + keff;
+  if (P == 0) return HKV_OK;
+  if (!scores || !out) return HKV_ERR_ARG;
+  hipStream_t st = (hipStream_t)stream;
+  const SelectWs lay = select_ws_layout(P, H);
+  const bool mb = workspace && workspace_bytes >= lay.bytes && lay.NB > 0 && keff > 0 &&
+                  ((uintptr_t)workspace & 255u) == 0;
+  char* ws = (char*)workspace;
+  int nmm = 0;
+  const int rc = page_bound_u8(q, q_dtype, Hq, kmin, kmax, lo, step, P, H, D, scores, st,
+                               mb ? (uint2*)(ws + lay.mm_off) : nullptr, &nmm);
+  if (rc != HKV_OK) return rc;
+  return select_after_bound(scores, P, H, k, sink_pages, s, keff, out, lay, mb, ws, nmm, st);
+}
+
+namespace {
+
+// The top-K half of a select: the multi-block top-K when the workspace and
+// the bound kernel's key ranges allow it, else the single-block selector.
+int select_after_bound(const float* scores, int64_t P, int H, int64_t k, int64_t sink_pages, int64_t s,
+                       int64_t keff, int64_t* out, const SelectWs& lay, bool mb, char* ws, int nmm,
+                       hipStream_t st) {
   if (!mb || nmm == 0) return topk(scores, HKV_DT_F32, P, H, 1, P, k, sink_pages, out, nullptr, st);
   MBWork w;
   w.ctr = (uint32_t*)(ws + lay.ctr_off);
@@ -1910,6 +2160,54 @@ extern "C" int hkv_quest_select(const void* q, int q_dtype, int Hq, const void* 
     hipLaunchKernelGGL((topk_mb_write<32>), grid, dim3(kMBThreads), 0, st, scores, P, s, out, H, w);
   }
   HKV_CHECK_LAUNCH();
+  return HKV_OK;
+}
+
+}  // namespace
+
+extern "C" size_t hkv_quest_page_stats_u8_workspace_bytes(int H, int D) {
+  return H < 1 || D < 1 ? 0 : sizeof(uint32_t) * 2 * (size_t)H * D;
+}
+
+extern "C" int hkv_quest_page_stats_u8(const void* kmin, const void* kmax, int dtype, int64_t P, int H,
+                                       int D, uint8_t* qmin, uint8_t* qmax, float* lo, float* step,
+                                       void* workspace, size_t workspace_bytes, void* stream) {
+  if (!fdt(dtype)) return HKV_ERR_DTYPE;
+  if (P < 0 || H < 1 || D < 1 || D % 4) return HKV_ERR_SHAPE;
+  const int HD = H * D;
+  if (!lo || !step || !workspace) return HKV_ERR_ARG;
+  if (workspace_bytes < hkv_quest_page_stats_u8_workspace_bytes(H, D) || ((uintptr_t)workspace & 3u))
+    return HKV_ERR_WORKSPACE;
+  if (P > 0 && (!kmin || !kmax || !qmin || !qmax)) return HKV_ERR_ARG;
+  if (((uintptr_t)qmin | (uintptr_t)qmax) & 3u) return HKV_ERR_ARG;
+  hipStream_t st = (hipStream_t)stream;
+  uint32_t* rk = (uint32_t*)workspace;
+  const unsigned gch = (unsigned)((HD + 255) / 256);
+  hipLaunchKernelGGL(stats_u8_init_kernel, dim3(gch), dim3(256), 0, st, rk, HD);
+  HKV_CHECK_LAUNCH();
+  if (P > 0) {
+    const unsigned gr = (unsigned)std::min<int64_t>(P, (int64_t)num_cus() * 4);
+    if (dtype == HKV_DT_F16)
+      hipLaunchKernelGGL(stats_u8_range_kernel<uint16_t>, dim3(gr), dim3(256), 0, st,
+                         (const uint16_t*)kmin, (const uint16_t*)kmax, P, HD, rk);
+    else
+      hipLaunchKernelGGL(stats_u8_range_kernel<float>, dim3(gr), dim3(256), 0, st, (const float*)kmin,
+                         (const float*)kmax, P, HD, rk);
+    HKV_CHECK_LAUNCH();
+  }
+  hipLaunchKernelGGL(stats_u8_params_kernel, dim3(gch), dim3(256), 0, st, rk, HD, lo, step);
+  HKV_CHECK_LAUNCH();
+  if (P > 0) {
+    const int64_t n4 = P * HD / 4;
+    const unsigned gq = (unsigned)std::min<int64_t>((n4 + 255) / 256, (int64_t)num_cus() * 16);
+    if (dtype == HKV_DT_F16)
+      hipLaunchKernelGGL(stats_u8_quant_kernel<uint16_t>, dim3(gq), dim3(256), 0, st,
+                         (const uint16_t*)kmin, (const uint16_t*)kmax, n4, HD, lo, step, qmin, qmax);
+    else
+      hipLaunchKernelGGL(stats_u8_quant_kernel<float>, dim3(gq), dim3(256), 0, st, (const float*)kmin,
+                         (const float*)kmax, n4, HD, lo, step, qmin, qmax);
+    HKV_CHECK_LAUNCH();
+  }
   return HKV_OK;
 }
 

@@ -81,6 +81,10 @@ _SIGS = {
     "hkv_quest_select_workspace_bytes": ([_i64, _i32], _sz),
     "hkv_quest_select": ([_p, _i32, _i32, _p, _p, _i32, _i64, _i32, _i32, _i64, _i64, _p, _p,
                           ctypes.POINTER(_i64), _p, _sz, _p], _i32),
+    "hkv_quest_page_stats_u8_workspace_bytes": ([_i32, _i32], _sz),
+    "hkv_quest_page_stats_u8": ([_p, _p, _i32, _i64, _i32, _i32, _p, _p, _p, _p, _p, _sz, _p], _i32),
+    "hkv_quest_select_u8": ([_p, _i32, _i32, _p, _p, _p, _p, _i64, _i32, _i32, _i64, _i64, _p, _p,
+                             ctypes.POINTER(_i64), _p, _sz, _p], _i32),
     "hkv_quest_select_blocks": ([_p, _i32, _i32, _p, _p, _i32, _i64, _i32, _p, _i64, _i64, _i64,
                                  _i64, _p, _p, _p, _p, _p, _p, _p], _i32),
     "hkv_decode_workspace_bytes": ([_i64, _i32, _i32], _sz),

@@ -8,6 +8,7 @@ stream.  Nothing here computes on the CPU.
 from __future__ import annotations
 
 from dataclasses import dataclass
+from typing import NamedTuple
 
 import torch
 
@@ -368,6 +369,71 @@ def quest_select(query: torch.Tensor, K_min: torch.Tensor, K_max: torch.Tensor, 
                                   _fdt(kmin), P, H, D, int(k), int(sink_pages), N.ptr(scores),
                                   N.ptr(out), n_out, N.ptr(ws), ws.numel(), N.stream_of(q))
     N.check(st, "hkv_quest_select", ValueError)
+    return out, scores
+
+
+class QuestStatsU8(NamedTuple):
+    """Compact page metadata: u8 codes of the page min / max (P,H,D) and the
+    per-(head, channel) lo / step (H,D) fp32 that read them back."""
+    qmin: torch.Tensor
+    qmax: torch.Tensor
+    lo: torch.Tensor
+    step: torch.Tensor
+
+
+def quest_page_stats_u8(K_min: torch.Tensor, K_max: torch.Tensor) -> QuestStatsU8:
+    """(P,H,D) fp16/fp32 page statistics -> their compact u8 form, rounded so
+    that the bound read from it is never below the bound from the originals
+    (hkv_quest_page_stats_u8)."""
+    N.require_gpu(K_min, K_max)
+    if K_min.dim() != 3 or K_min.shape != K_max.shape:
+        raise ValueError("K_min/K_max should be (P, H, D)")
+    P, H, D = (int(x) for x in K_min.shape)
+    kmin = K_min.contiguous()
+    kmax = K_max.to(kmin.dtype).contiguous()
+    dev = kmin.device
+    qmin = torch.empty((P, H, D), dtype=torch.uint8, device=dev)
+    qmax = torch.empty((P, H, D), dtype=torch.uint8, device=dev)
+    lo = torch.empty((H, D), dtype=torch.float32, device=dev)
+    step = torch.empty((H, D), dtype=torch.float32, device=dev)
+    ws = torch.empty(max(4, int(N.lib().hkv_quest_page_stats_u8_workspace_bytes(H, D))) // 4,
+                     dtype=torch.int32, device=dev)
+    st = N.lib().hkv_quest_page_stats_u8(N.ptr(kmin), N.ptr(kmax), _fdt(kmin), P, H, D, N.ptr(qmin),
+                                         N.ptr(qmax), N.ptr(lo), N.ptr(step), N.ptr(ws),
+                                         ws.numel() * 4, N.stream_of(kmin))
+    N.check(st, "hkv_quest_page_stats_u8", ValueError)
+    return QuestStatsU8(qmin, qmax, lo, step)
+
+
+def quest_select_u8(query: torch.Tensor, stats: QuestStatsU8, k: int, sink_pages: int, *,
+                    scores: torch.Tensor | None = None, out: torch.Tensor | None = None):
+    """quest_select over the compact u8 metadata (hkv_quest_select_u8): returns
+    (indices (sinks + k_eff, H) int64, scores (H,P) fp32)."""
+    N.require_gpu(query, stats.qmin, stats.qmax, stats.lo, stats.step)
+    if stats.qmin.dim() != 3 or stats.qmin.shape != stats.qmax.shape:
+        raise ValueError("qmin/qmax should be (P, H, D)")
+    P, H, D = (int(x) for x in stats.qmin.shape)
+    if tuple(stats.lo.shape) != (H, D) or tuple(stats.step.shape) != (H, D):
+        raise ValueError("lo/step should be (H, D)")
+    Hq = int(query.shape[0])
+    if query.dim() != 2 or int(query.shape[1]) != D or Hq % H:
+        raise ValueError(f"query {tuple(query.shape)} incompatible with stats {(P, H, D)}")
+    q = query.contiguous()
+    s = max(0, min(int(sink_pages), P))
+    keff = max(0, min(int(k), P - s))
+    if out is None:
+        out = torch.empty((s + keff, H), dtype=torch.int64, device=q.device)
+    if scores is None:
+        scores = torch.empty((H, P), dtype=torch.float32, device=q.device)
+    if tuple(out.shape) != (s + keff, H) or tuple(scores.shape) != (H, P):
+        raise ValueError("out must be (sinks + k_eff, H) and scores (H, P)")
+    n_out = N._i64(0)
+    ws = N.workspace("quest_select", int(N.lib().hkv_quest_select_workspace_bytes(P, H)), q.device)
+    st = N.lib().hkv_quest_select_u8(
+        N.ptr(q), N.dtype_code(q), Hq, N.ptr(stats.qmin.contiguous()), N.ptr(stats.qmax.contiguous()),
+        N.ptr(stats.lo.contiguous()), N.ptr(stats.step.contiguous()), P, H, D, int(k), int(sink_pages),
+        N.ptr(scores), N.ptr(out), n_out, N.ptr(ws), ws.numel(), N.stream_of(q))
+    N.check(st, "hkv_quest_select_u8", ValueError)
     return out, scores
 
 

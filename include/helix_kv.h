@@ -261,6 +261,41 @@ int hkv_quest_select(const void *q, int q_dtype, int Hq, const void *kmin, const
                      size_t workspace_bytes, void *stream);
 
 /*
+ * Compact page metadata: u8 codes of the page minima / maxima with a per
+ * (head, channel) lo and step (f32), half the bytes of fp16 statistics.  No
+ * counterpart in the reference, whose pool keeps f32 page statistics
+ * (src/kvquant/compact_pool.py:434-441); for callers whose selection is bound
+ * by reading the statistics.
+ *
+ * hkv_quest_page_stats_u8: from (P,H,D) f16/f32 kmin / kmax (as
+ * hkv_quest_page_stats writes them) to qmin / qmax (P,H,D) u8 and lo / step
+ * (H,D) f32.  Per (head, channel) over the finite statistics of all pages:
+ * lo = the smallest, hi = the largest; step = fl((hi - lo) / 255) raised one
+ * ulp at a time until fl(lo + fl(255 * step)) >= hi (1 when hi <= lo).
+ * Codes are rounded conservatively: fl(lo + fl(qmin * step)) <= min and
+ * fl(lo + fl(qmax * step)) >= max for every finite statistic, so the bound
+ * from the codes is never below the bound from the statistics; a non-finite
+ * statistic codes as 0 (minimum) / 255 (maximum).  D a multiple of 4; qmin /
+ * qmax 4-byte aligned.  workspace: hkv_quest_page_stats_u8_workspace_bytes(H,
+ * D) bytes, 4-byte aligned (no initial contents needed).  Four launches.
+ *
+ * hkv_quest_select_u8: hkv_quest_select over the u8 metadata: the bound of
+ * every page from the dequantised statistics fl(lo + fl(code * step)) in the
+ * fp16 path's products and order (scores (H,P) f32), then the same top-K with
+ * sinks and the same workspace (hkv_quest_select_workspace_bytes).  D a
+ * multiple of 8 with D/8 a power of two <= 64 and H dividing 64/(D/8)
+ * (D = 128: H in {1, 2, 4}); qmin / qmax 8-byte aligned.
+ */
+size_t hkv_quest_page_stats_u8_workspace_bytes(int H, int D);
+int hkv_quest_page_stats_u8(const void *kmin, const void *kmax, int dtype, int64_t P, int H, int D,
+                            uint8_t *qmin, uint8_t *qmax, float *lo, float *step, void *workspace,
+                            size_t workspace_bytes, void *stream);
+int hkv_quest_select_u8(const void *q, int q_dtype, int Hq, const uint8_t *kmin,
+                        const uint8_t *kmax, const float *lo, const float *step, int64_t P, int H,
+                        int D, int64_t k, int64_t sink_pages, float *scores, int64_t *out,
+                        int64_t *n_out, void *workspace, size_t workspace_bytes, void *stream);
+
+/*
  * Quest block selection over a compact pool layer
  * (src/kvquant/quest_selector.py:38-90): q (H,D) (one query per KV head),
  * pool statistics kmin/kmax (num_blocks,H,D) (f32 or f16), the sequence's

@@ -303,6 +303,69 @@ def page_bound_group(query, kmin, kmax, group: int):
     return out
 
 
+def _u8_deq(q, lo, step):
+    """lo + q * step in float32, two roundings (the device's order)."""
+    return (np.float32(lo) + (np.asarray(q).astype(np.float32) * np.float32(step)).astype(np.float32)).astype(np.float32)
+
+
+def page_stats_u8(kmin, kmax):
+    """Compact page metadata: (P,H,D) min/max -> (qmin u8, qmax u8, lo f32 (H,D), step f32 (H,D)).
+
+    No counterpart in the reference, whose pool keeps fp32 page statistics
+    (src/kvquant/compact_pool.py:434-441; the bound they feed is
+    src/quest/reference.py:59-93).  Per (head, channel), over the finite
+    statistics of all pages: lo = the smallest, hi = the largest;
+    step = fl((hi - lo) / 255), raised one ulp at a time (at most 16) until
+    deq(255) >= hi, where deq(q) = fl(lo + fl(q * step)) (step = 1 when
+    hi <= lo or no statistic is finite, lo = 0 then).  A minimum x codes as
+    floor(fl(fl(x - lo) / step)) clamped to [0, 255] and lowered (at most 4
+    times, then 0) while deq(q) > x; a maximum as the ceiling, raised (at
+    most 4 times, then 255) while deq(q) < x.  So deq(qmin) <= min and
+    deq(qmax) >= max for every finite statistic: the bound computed from
+    the dequantised statistics is never below the one from the originals.
+    A non-finite statistic codes as 0 (minimum) / 255 (maximum).
+    """
+    mn, mx = _f32(kmin), _f32(kmax)
+    P, H, D = mn.shape
+    allv = np.concatenate([mn, mx], 0)
+    fin = np.isfinite(allv)
+    lo = np.where(fin, allv, np.inf).min(0).astype(np.float32)
+    hi = np.where(fin, allv, -np.inf).max(0).astype(np.float32)
+    none = ~np.isfinite(lo)
+    lo = (np.where(none, np.float32(0), lo) + np.float32(0)).astype(np.float32)  # -0 -> +0
+    hi = (np.where(none, np.float32(0), hi) + np.float32(0)).astype(np.float32)
+    wide = hi > lo
+    step = np.where(wide, ((hi - lo).astype(np.float32) / np.float32(255)).astype(np.float32),
+                    np.float32(1)).astype(np.float32)
+    for _ in range(16):
+        short = wide & (_u8_deq(255, lo, step) < hi)
+        if not short.any():
+            break
+        step = np.where(short, (step.view(np.uint32) + np.uint32(1)).view(np.float32), step)
+
+    def code(x, up):
+        t = ((x - lo).astype(np.float32) / step).astype(np.float32)
+        t = np.ceil(t) if up else np.floor(t)
+        q = np.clip(np.nan_to_num(t, nan=0.0, posinf=255.0, neginf=0.0), 0, 255).astype(np.int32)
+        for _ in range(4):
+            d = _u8_deq(q, lo, step)
+            if up:
+                q = np.where((q < 255) & (d < x), q + 1, q)
+            else:
+                q = np.where((q > 0) & (d > x), q - 1, q)
+        d = _u8_deq(q, lo, step)
+        q = np.where(up & (d < x), 255, q) if up else np.where(d > x, 0, q)
+        q = np.where(np.isfinite(x), q, 255 if up else 0)
+        return q.astype(np.uint8)
+
+    return code(mn, False), code(mx, True), lo, step
+
+
+def page_stats_u8_deq(qmin, qmax, lo, step):
+    """The float32 statistics the bound reads from the compact metadata."""
+    return _u8_deq(qmin, lo, step), _u8_deq(qmax, lo, step)
+
+
 def topk_sinks(bound, k: int, sink_pages: int):
     """src/quest/reference.py:96-133 with lowest-index tie-break -> (s+k_eff, H) int64."""
     b = _f32(bound)

@@ -185,3 +185,49 @@ def test_multiblock_select_vs_oracle(dev, P, H, g, k, s, mode):
         assert np.array_equal(np.isnan(got_b), nan)  # NaN payloads are not compared
         assert np.array_equal(got_b[~nan].view(np.uint32), want_b[~nan].view(np.uint32))
         assert np.array_equal(idx.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("P,H,g,k,s,mode,dt", [
+    (65536, 4, 7, 16384, 4, "normal", np.float16),   # 1M tokens
+    (1000, 2, 7, 250, 4, "normal", np.float32),      # fp32 statistics
+    (40000, 4, 1, 100, 0, "heavy", np.float16),      # Student-t tails: wide ranges, dense bins
+    (300, 1, 3, 50, 2, "const", np.float16),         # constant channels (step 1, codes 0)
+    (5000, 4, 7, 1000, 4, "nonfinite", np.float16),  # NaN / inf statistics code as the full range
+])
+def test_u8_metadata_select_vs_oracle(dev, P, H, g, k, s, mode, dt):
+    """Compact u8 page metadata: the conversion bit-exact against the oracle,
+    the select's scores bit-exact against the oracle bound over the
+    dequantised statistics, its pages against the oracle top-K, and no score
+    below the fp16 select's for the same page."""
+    from helix_kv.ops import quest_page_stats_u8, quest_select, quest_select_u8
+
+    D = 128
+    if mode == "const":
+        mn = np.broadcast_to(RNG.standard_normal((1, H, D)), (P, H, D)).astype(dt)
+        mx = (mn.astype(np.float32) + 1).astype(dt)
+    else:
+        gen = RNG.standard_t(3, (P, H, D)) if mode == "heavy" else RNG.standard_normal((P, H, D))
+        mn = gen.astype(dt)
+        mx = (mn.astype(np.float32) + np.abs(RNG.standard_normal((P, H, D)))).astype(dt)
+    if mode == "nonfinite":
+        bad = RNG.choice(P, 40, replace=False)
+        mn[bad[:20], :, 3] = np.nan
+        mx[bad[20:], :, 7] = np.inf
+    q = RNG.standard_normal((H * g, D)).astype(np.float16)
+    qmin, qmax, lo, st = O.page_stats_u8(mn, mx)
+    got = quest_page_stats_u8(_t(mn, dev), _t(mx, dev))
+    assert np.array_equal(got.qmin.cpu().numpy(), qmin) and np.array_equal(got.qmax.cpu().numpy(), qmax)
+    assert np.array_equal(got.lo.cpu().numpy().view(np.uint32), lo.view(np.uint32))
+    assert np.array_equal(got.step.cpu().numpy().view(np.uint32), st.view(np.uint32))
+    dmn, dmx = O.page_stats_u8_deq(qmin, qmax, lo, st)
+    want_b = O.page_bound_group(q, dmn, dmx, g)
+    for _ in range(2):  # the workspace is reused
+        idx, sc = quest_select_u8(_t(q, dev), got, k, s)
+        b = sc.cpu().numpy().T
+        assert np.array_equal(b.view(np.uint32), want_b.view(np.uint32))
+        assert np.array_equal(idx.cpu().numpy(), O.topk_sinks(want_b, k, s))
+    if dt == np.float16:
+        _, sc16 = quest_select(_t(q, dev), _t(mn, dev), _t(mx, dev), k, s)
+        b16 = sc16.cpu().numpy().T
+        fin = np.isfinite(b16)
+        assert (b[fin] >= b16[fin]).all()

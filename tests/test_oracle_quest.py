@@ -251,3 +251,53 @@ def test_gather_pages_known_answer():
     assert not st[1, :, 1].any()                            # id -1
     assert st[2, 0, 0, 0] == ((3 + 1) * S) * 10             # seq 1 page 1 = global page 4
     assert not st[3, :, 0].any() and st[3, 5, 1, 0] == ((3 + 1) * S + 5) * 10 + 1
+
+
+def _all_finite_f16(lo=-np.inf, hi=np.inf):
+    v = np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.float16)
+    v = v[np.isfinite(v)]
+    return v[(v >= lo) & (v <= hi)]
+
+
+@pytest.mark.parametrize("lo,hi", [(-np.inf, np.inf), (-4.0, 4.0), (0.5, 0.75), (-1e-3, 2e-3),
+                                   (1000.0, 1024.0)])
+def test_page_stats_u8_brackets_every_fp16_value(lo, hi):
+    """Every finite fp16 statistic in a channel's range: deq(qmin) <= v <= deq(qmax)."""
+    v = _all_finite_f16(lo, hi)
+    P = v.shape[0]
+    mn = v.reshape(P, 1, 1)
+    qmin, qmax, l, st = O.page_stats_u8(mn, mn)
+    dmn, dmx = O.page_stats_u8_deq(qmin, qmax, l, st)
+    x = mn.astype(np.float32)
+    assert (dmn <= x).all() and (dmx >= x).all()
+    assert l[0, 0] == x.min() and O.page_stats_u8_deq(255, 255, l, st)[0][0, 0] >= x.max()
+    # the codes are tight to within a couple of steps (the rounding loop stops early)
+    assert ((x - dmn) <= 2 * st).all() and ((dmx - x) <= 2 * st).all()
+
+
+def test_page_stats_u8_degenerate_and_non_finite():
+    mn = np.full((5, 2, 3), 1.5, np.float16)
+    qmin, qmax, lo, st = O.page_stats_u8(mn, mn)
+    assert (qmin == 0).all() and (qmax == 0).all() and (lo == 1.5).all() and (st == 1.0).all()
+    mn = np.array([[[np.nan, -np.inf]], [[1.0, 2.0]]], np.float16)   # (P=2, H=1, D=2)
+    mx = np.array([[[np.inf, 3.0]], [[np.nan, 2.0]]], np.float16)
+    qmin, qmax, lo, st = O.page_stats_u8(mn, mx)
+    assert qmin[0, 0, 0] == 0 and qmin[0, 0, 1] == 0 and qmax[0, 0, 0] == 255 and qmax[1, 0, 0] == 255
+    assert lo[0, 0] == 1.0 and lo[0, 1] == 2.0  # ranges over the finite statistics only
+    dmn, dmx = O.page_stats_u8_deq(qmin, qmax, lo, st)
+    assert dmn[1, 0, 0] <= 1.0 and dmx[0, 0, 1] >= 3.0 and dmx[1, 0, 1] >= 2.0
+
+
+def test_page_bound_u8_never_below_fp16_bound():
+    """Dequantised statistics bracket the originals, products and sums round
+    monotonically, and the order is the same: no page's bound drops."""
+    rng = np.random.default_rng(11)
+    P, H, D, g = 2000, 4, 128, 7
+    mn = (rng.standard_t(3, (P, H, D)) * 0.7).astype(np.float16)
+    mx = (mn.astype(np.float32) + np.abs(rng.standard_t(3, (P, H, D)))).astype(np.float16)
+    q = rng.standard_normal((H * g, D)).astype(np.float16)
+    dmn, dmx = O.page_stats_u8_deq(*O.page_stats_u8(mn, mx))
+    b16 = O.page_bound_group(q, mn, mx, g)
+    b8 = O.page_bound_group(q, dmn, dmx, g)
+    assert (b8 >= b16).all()
+    assert np.median((b8 - b16) / np.abs(b16).max()) < 0.05  # still a useful bound
