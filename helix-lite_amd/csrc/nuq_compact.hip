@@ -63,6 +63,9 @@ pack_stage_kernel(const uint16_t* __restrict__ x, int64_t nrows, int H, hkv_nuq_
   constexpr bool STAGE = PT && WT * 80 <= 4096;
   constexpr int TW = 20;  // staged words per row (80 bytes, 16-byte aligned)
   __shared__ __align__(16) uint32_t s_tab[STAGE ? NW * WT * TW : 1];
+  // each lane's current 8 values, read back by element index in the
+  // outlier loop (one 16-byte slot per lane)
+  __shared__ __align__(16) uint4 s_x[NW * 64];
 
   // the wave index through readfirstlane: tile bases are then uniform and
   // stay in scalar registers, addressed with 32-bit lane offsets
@@ -147,7 +150,8 @@ pack_stage_kernel(const uint16_t* __restrict__ x, int64_t nrows, int H, hkv_nuq_
           h = (int)(r - t * H);
         }
         const uint4 xv = make_uint4(xs[p][0], xs[p][1], xs[p][2], xs[p][3]);
-        uint32_t c[4], om[4];
+        s_x[wv * 64 + lane] = xv;
+        uint32_t pk;
         if constexpr (PT) {
           const RowTabAt tab{sc.rows, sc.positions, sc.pos_offset, h, t};  // for the exact scan only
           if constexpr (STAGE) {
@@ -160,7 +164,7 @@ pack_stage_kernel(const uint16_t* __restrict__ x, int64_t nrows, int H, hkv_nuq_
           } else {
             load_search_bcast<NB>(tabs + tab(0), S[0]);
           }
-          quant8<NB, PT, RowTabAt, true>(xv, S, si, tab, c, om);
+          quant8_packed<NB, PT, BITS>(xv, S, si, tab, &pk, &m);
         } else {
           const int64_t tab0 = (int64_t)h * D + 8 * cg;
           if constexpr (!KFIX) {
@@ -168,31 +172,33 @@ pack_stage_kernel(const uint16_t* __restrict__ x, int64_t nrows, int H, hkv_nuq_
             for (int j = 0; j < 4; ++j)
               load_search_pair<NB>(tabs + tab0 + 2 * j, tabs + tab0 + 2 * j + 1, S[j]);
           }
-          if constexpr (KFIX) quant8<NB, PT, ChanTab, true, true>(xv, S, si, ChanTab{tab0}, c, om, xmin);
-          else quant8<NB, PT, ChanTab, true>(xv, S, si, ChanTab{tab0}, c, om);
+          if constexpr (KFIX) quant8_packed<NB, PT, BITS, ChanTab, true>(xv, S, si, ChanTab{tab0}, &pk, &m, xmin);
+          else quant8_packed<NB, PT, BITS>(xv, S, si, ChanTab{tab0}, &pk, &m);
         }
         if constexpr (BITS == 4) {
-          store_stream(reinterpret_cast<uint32_t*>(pt + (uint32_t)(rr * RB + 4 * cg)), pack_nibbles(c));
+          store_stream(reinterpret_cast<uint32_t*>(pt + (uint32_t)(rr * RB + 4 * cg)), pk);
         } else {
-          store_stream(reinterpret_cast<uint16_t*>(pt + (uint32_t)(rr * RB + 2 * cg)), (uint16_t)pack_crumbs(c));
+          store_stream(reinterpret_cast<uint16_t*>(pt + (uint32_t)(rr * RB + 2 * cg)), (uint16_t)pk);
         }
-        m = mask_bits_sign(om);
       }
       // lanes are in (row, channel) order, so the wave's exclusive count is
       // the position in (row, col) order
       uint32_t tot;
-      uint32_t pos = run + wave_excl_count(__builtin_popcount(m), &tot);
+      uint32_t pos = run + wave_excl_count_fused(__builtin_popcount(m), &tot);
       run += tot;
       if (rr < nv && cg == 0)
         *reinterpret_cast<int32_t*>(reinterpret_cast<char*>(rpt) + 4u * (uint32_t)rr) = (int32_t)pos;
+      // pos counts the tile's outliers before this one, so pos < WT * D: every
+      // entry stays inside the tile's staging region
+      const uint16_t* xl = reinterpret_cast<const uint16_t*>(s_x + wv * 64 + lane);
+      const uint32_t colb = (uint32_t)(8 * cg) << 16;
+      uint32_t off = 4u * pos;
       while (m) {
         const int e = __builtin_ctz(m);
         m &= m - 1u;
-        const uint32_t w = pick4(xs[p][0], xs[p][1], xs[p][2], xs[p][3], e >> 1);
-        if (pos < (uint32_t)(WT * D))  // always true; keeps the region bound explicit
-          *reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(st) + 4u * pos) =
-              ((w >> (16 * (e & 1))) & 0xffffu) | ((uint32_t)(8 * cg + e) << 16);
-        ++pos;
+        *reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(st) + off) =
+            (uint32_t)xl[e] | (colb + ((uint32_t)e << 16));
+        off += 4u;
       }
     }
     if (lane == 0) wt_cnt[wt] = run;

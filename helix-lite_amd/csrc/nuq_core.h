@@ -187,3 +187,156 @@ HKV_DEV uint32_t mask_bits(const uint32_t om[4]) {
   for (int j = 0; j < 4; ++j) r |= ((om[j] & 1u) | ((om[j] >> 15) & 2u)) << (2 * j);
   return r;
 }
+
+// ------------------------------------------- packed output by bit placement
+//
+// The search yields one full-lane mask per code bit (0xffff in a 16-bit lane
+// where that bit of the lane's code is 0).  Each bit is moved straight to its
+// place in the packed output by one v_bitop3 against a constant position
+// mask, so no code is ever formed in a lane and then shifted into place.
+
+// Per bit: p ? v : acc.
+HKV_DEV uint32_t place(uint32_t p, uint32_t v, uint32_t acc) {
+  return __builtin_amdgcn_bitop3_b32(p, v, acc, 0xCA);
+}
+// Per bit: p ? ~m : acc.
+HKV_DEV uint32_t place_not(uint32_t p, uint32_t m, uint32_t acc) {
+  return __builtin_amdgcn_bitop3_b32(p, m, acc, 0x3A);
+}
+
+// Masks of the code bits of two fp16 lanes: m[b] is 0xffff in a lane whose
+// code has bit b clear (the same binary search as search2).
+template <int NB>
+HKV_DEV void search_masks(uint32_t x, const Search2<NB>& s, uint32_t m[NB]) {
+  if constexpr (NB == 2) {
+    m[1] = lt2(x, s.bp[1]);
+    m[0] = lt2(x, bsel(m[1], s.bp[0], s.bp[2]));
+  } else {
+    static_assert(NB == 4, "placement is used for 4 and 16 levels");
+    m[3] = lt2(x, s.bp[7]);
+    const uint32_t t2 = bsel(m[3], s.bp[3], s.bp[11]);
+    const uint32_t a = bsel(m[3], s.bp[1], s.bp[9]);
+    const uint32_t b = bsel(m[3], s.bp[5], s.bp[13]);
+    const uint32_t q0 = bsel(m[3], s.bp[0], s.bp[8]);
+    const uint32_t q1 = bsel(m[3], s.bp[2], s.bp[10]);
+    const uint32_t q2 = bsel(m[3], s.bp[4], s.bp[12]);
+    const uint32_t q3 = bsel(m[3], s.bp[6], s.bp[14]);
+    m[2] = lt2(x, t2);
+    const uint32_t t1 = bsel(m[2], a, b);
+    const uint32_t r0 = bsel(m[2], q0, q2);
+    const uint32_t r1 = bsel(m[2], q1, q3);
+    m[1] = lt2(x, t1);
+    m[0] = lt2(x, bsel(m[1], r0, r1));
+  }
+}
+
+// Position masks.  Element e = 2j (low lane of pair j) and e = 2j + 1 (high
+// lane).  Packed codes:
+//   2-bit: element e's bit b at bit 2e + b of the 16-bit word.  The low lane
+//     places it directly (bit 4j + b); the high lane at 16 + 4j + 2 + b,
+//     brought down by acc | acc >> 16.
+//   4-bit: element e's bit b at bit 4e + b of the 32-bit word, built from two
+//     accumulators (pairs 0-1 and 2-3), each a 16-bit half in the same way:
+//     low lane at 8(j & 1) + b, high lane at 16 + 8(j & 1) + 4 + b.
+// Outlier flags: element e at bit e of the 8-bit mask: low lane at 2j, high
+// lane at 16 + 2j + 1.
+HKV_DEV constexpr uint32_t pos2(int j, int b) { return (1u << (4 * j + b)) | (1u << (16 + 4 * j + 2 + b)); }
+HKV_DEV constexpr uint32_t pos4(int j, int b) {
+  return (1u << (8 * (j & 1) + b)) | (1u << (16 + 8 * (j & 1) + 4 + b));
+}
+HKV_DEV constexpr uint32_t posm(int j) { return (1u << (2 * j)) | (1u << (16 + 2 * j + 1)); }
+
+// Quantise 8 channels straight into packed form: *packed receives the 8
+// codes packed at BITS bits (element e at bits BITS*e..; for BITS = 2 only
+// the low 16 bits are meaningful), *mask8 the 8-bit outlier mask (element e
+// at bit e).  Same semantics and fast/exact split as quant8.
+template <int NB, bool PT, int BITS, typename TabFn, bool XMIN = false>
+HKV_DEV void quant8_packed(const uint4 xv, const Search2<NB>* S, const SlowInfo& si, TabFn tab,
+                           uint32_t* packed, uint32_t* mask8, uint32_t xmin = 0) {
+  const uint32_t x[4] = {xv.x, xv.y, xv.z, xv.w};
+  uint32_t uns = 0;
+  if constexpr (PT || XMIN) {
+    u2_t mg = __builtin_bit_cast(u2_t, x[0] & 0x7fff7fffu);
+#pragma unroll
+    for (int j = 1; j < 4; ++j) mg = __builtin_elementwise_max(mg, __builtin_bit_cast(u2_t, x[j] & 0x7fff7fffu));
+    if constexpr (PT) {
+      uns = unsafe2<NB>(__builtin_bit_cast(uint32_t, mg), S[0]);
+    } else {
+      const s2_t d = as_s2(xmin) - as_s2(__builtin_bit_cast(uint32_t, mg));
+      uns = as_u32(d) & 0x80008000u;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) uns |= unsafe2<NB>(x[j], S[j]);
+  }
+  if (__builtin_expect(uns == 0, 1)) {
+    uint32_t M = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t o = as_u32(as_s2(outlier2_sign<NB>(x[j], S[PT ? 0 : j])) >> (s2_t){15, 15});
+      M = place(posm(j), o, M);
+    }
+    *mask8 = (M | (M >> 16)) & 0xffu;
+    if constexpr ((BITS == 2 && NB == 2) || (BITS == 4 && NB == 4)) {
+      uint32_t A = 0, B = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uint32_t m[NB];
+        search_masks<NB>(x[j], S[PT ? 0 : j], m);
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          if constexpr (BITS == 2) A = place_not(pos2(j, b), m[b], A);
+          else if (j < 2) A = place_not(pos4(j, b), m[b], A);
+          else B = place_not(pos4(j, b), m[b], B);
+        }
+      }
+      if constexpr (BITS == 2) *packed = A | (A >> 16);
+      else *packed = ((A & 0xffffu) | (B & 0xffff0000u)) | __builtin_amdgcn_alignbit(B, A, 16);
+    } else {
+      uint32_t c[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) c[j] = search2<NB>(x[j], S[PT ? 0 : j]);
+      *packed = BITS == 4 ? pack_nibbles(c) : pack_crumbs(c);
+    }
+  } else {
+    uint32_t c[4], om[4];
+#pragma unroll 1
+    for (int j = 0; j < 4; ++j) {
+      int o0, o1;
+      int c0 = slow_one((uint16_t)(x[j] & 0xffffu), si, tab(2 * j), &o0);
+      int c1 = slow_one((uint16_t)(x[j] >> 16), si, tab(2 * j + 1), &o1);
+      c[j] = (uint32_t)c0 | ((uint32_t)c1 << 16);
+      om[j] = (o0 ? 0xffffu : 0u) | (o1 ? 0xffff0000u : 0u);
+    }
+    *packed = BITS == 4 ? pack_nibbles(c) : pack_crumbs(c);
+    *mask8 = mask_bits(om);
+  }
+}
+
+// Wave-wide inclusive prefix sum with the adds fused into DPP (one
+// v_add_u32_dpp per step).  Every lane of the wave must be active.  Each step
+// reads the previous step's result through DPP, which needs two wait states
+// after the VALU write (s_nop 1).
+HKV_DEV uint32_t wave_incl_sum_fused(uint32_t v) {
+  asm("s_nop 1\n\t"
+      "v_add_u32_dpp %0, %0, %0 row_shr:1 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+      "s_nop 1\n\t"
+      "v_add_u32_dpp %0, %0, %0 row_shr:2 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+      "s_nop 1\n\t"
+      "v_add_u32_dpp %0, %0, %0 row_shr:4 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+      "s_nop 1\n\t"
+      "v_add_u32_dpp %0, %0, %0 row_shr:8 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+      "s_nop 1\n\t"
+      "v_add_u32_dpp %0, %0, %0 row_bcast:15 row_mask:0xa bank_mask:0xf\n\t"
+      "s_nop 1\n\t"
+      "v_add_u32_dpp %0, %0, %0 row_bcast:31 row_mask:0xc bank_mask:0xf\n\t"
+      "s_nop 1"
+      : "+v"(v));
+  return v;
+}
+
+HKV_DEV uint32_t wave_excl_count_fused(uint32_t cnt, uint32_t* total) {
+  const uint32_t inc = wave_incl_sum_fused(cnt);
+  *total = (uint32_t)__builtin_amdgcn_readlane((int)inc, 63);
+  return inc - cnt;
+}
