@@ -8,14 +8,14 @@
 //   CSR outliers over rows r = t*H + h: row_ptr (T*H+1) int32, col u8 = d,
 //   val fp16 = the original value; (row, col) ascending.
 //
-// Pack runs as three kernels.  pack_stage_kernel streams the fp16 input once;
+// Pack runs as two kernels.  pack_stage_kernel streams the fp16 input once;
 // its unit of work is a wave tile (PASSES passes of 64/G rows, G = D/8 lanes
 // per row), handled by one wave on its own: no block-level barrier.  A wave
 // writes the packed codes, each row's outlier offset within its wave tile
 // (into row_ptr), the tile's outliers into the tile's own staging region, and
-// the tile's outlier count.  scan_kernel turns the counts into offsets;
-// copy_kernel adds them to row_ptr and copies the staged outliers into the
-// dense col/val arrays.  No block ever waits on another: on gfx950 the eight XCDs' L2
+// the tile's outlier count.  copy_kernel turns the counts into offsets, adds
+// them to row_ptr and copies the staged outliers into the dense col/val
+// arrays.  No block ever waits on another: on gfx950 the eight XCDs' L2
 // caches are not coherent, so a single-pass scan whose tiles wait on their
 // predecessors pays a memory round trip per step.
 #include "nuq_core.h"
@@ -27,8 +27,9 @@ constexpr int kThreads = 256;
 // (their search state takes 72 registers; smaller tiles keep 3 waves a SIMD).
 __host__ __device__ inline int pack_passes(bool per_token, int nb) { return (!per_token && nb == 4) ? 4 : 8; }
 
-// Workspace: header, per-wave-tile counts and bases, then the staged entries
-// (u32: value | column << 16), each region 256-byte aligned.  Staging holds a
+// Workspace: header, per-wave-tile counts, a region of (ntiles + 1) words
+// kept so the workspace size stays what earlier versions asked for, then the
+// staged entries (u32: value | column << 16), each region 256-byte aligned.  Staging holds a
 // whole wave tile per wave tile, so no input can overflow it.
 struct PackLayout {
   int64_t ntiles, tile_rows, tile_elems;
@@ -206,106 +207,138 @@ pack_stage_kernel(const uint16_t* __restrict__ x, int64_t nrows, int H, hkv_nuq_
   }
 }
 
-// Offsets from the wave-tile counts: one block scans all counts into
-// exclusive bases (base[nwt] = nnz, also written to row_ptr[nrows]).  Counts
-// pass through LDS in windows of kScanWindow: coalesced loads, a sequential
-// scan of each thread's contiguous run, a block scan of the run totals, then
-// coalesced stores.
-constexpr int kScanThreads = 1024;
-constexpr int kScanPer = 16;
-constexpr int kScanWindow = kScanThreads * kScanPer;
+// The dense CSR, in one kernel after the stage kernel.  Block b owns the
+// wave tiles [b * tpb, (b + 1) * tpb) (tpb: a power of two from 32 to 256,
+// the smallest that keeps the grid within kCopyBlocks blocks, or 256).  Its
+// base is the sum of the counts of all earlier tiles, which it reads itself
+// (at most nwt counts, from L2: no separate scan kernel and no inter-block
+// waiting); its tiles' offsets are a block scan of their counts, one tile per
+// thread.  Each wave then copies a run of the block's tiles, requesting the
+// staged entries of several tiles (and the block's row_ptr entries) before
+// storing any, so a block waits on few memory round trips.  The last block
+// writes row_ptr[nrows] = nnz.
+constexpr int kCopyBlocks = 512;
+constexpr int kCopyThreads = 1024;
+constexpr int kCopyMaxTPB = 256;
+constexpr int kCopyU = 4;   // loads in flight per thread: prefix counts, row_ptr
+constexpr int kCopyTW = 4;  // tiles per wave and batch of staged-entry loads
+constexpr int kCopyUT = 4;  // staged-entry loads per lane and tile in a batch
 
-__global__ void __launch_bounds__(kScanThreads)
-scan_kernel(const uint32_t* __restrict__ wt_cnt, int64_t nwt, uint32_t* __restrict__ base,
-            int32_t* __restrict__ row_ptr, int64_t nrows) {
-  constexpr int NW = kScanThreads / 64;
-  __shared__ uint32_t s_v[kScanWindow];
-  __shared__ uint32_t s_w[NW];
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  uint32_t carry = 0;
-  for (int64_t w0 = 0; w0 < nwt; w0 += kScanWindow) {
-    uint32_t v[kScanPer];
+HKV_DEV uint32_t wave_sum(uint32_t v) {
 #pragma unroll
-    for (int k = 0; k < kScanPer; ++k) {
-      const int64_t i = w0 + k * kScanThreads + tid;
-      v[k] = i < nwt ? wt_cnt[i] : 0u;
-    }
-#pragma unroll
-    for (int k = 0; k < kScanPer; ++k) s_v[k * kScanThreads + tid] = v[k];
-    __syncthreads();
-    uint32_t run[kScanPer], sum = 0;
-#pragma unroll
-    for (int k = 0; k < kScanPer; ++k) {
-      run[k] = sum;
-      sum += s_v[tid * kScanPer + k];
-    }
-    uint32_t inc = sum;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const uint32_t y = __shfl_up(inc, o, 64);
-      if (lane >= o) inc += y;
-    }
-    if (lane == 63) s_w[wv] = inc;
-    __syncthreads();
-    uint32_t before = carry + inc - sum, total = carry;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) {
-      before += w < wv ? s_w[w] : 0u;
-      total += s_w[w];
-    }
-#pragma unroll
-    for (int k = 0; k < kScanPer; ++k) s_v[tid * kScanPer + k] = before + run[k];
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < kScanPer; ++k) {
-      const int64_t i = w0 + k * kScanThreads + tid;
-      if (i < nwt) base[i] = s_v[k * kScanThreads + tid];
-    }
-    carry = total;
-    __syncthreads();  // s_v / s_w are reused by the next window
-  }
-  if (tid == 0) {
-    base[nwt] = carry;
-    row_ptr[nrows] = (int32_t)carry;
-  }
+  for (int o = 32; o > 0; o >>= 1) v += (uint32_t)__shfl_xor((int)v, o, 64);
+  return v;
 }
 
-// The dense CSR: one wave per wave tile adds the tile's base to its rows'
-// row_ptr entries and copies its staged entries.
-constexpr int kCopyUnroll = 4;
-
-__global__ void __launch_bounds__(kThreads)
-copy_kernel(const uint32_t* __restrict__ base_arr, int64_t nwt, int64_t WT, int64_t D,
+__global__ void __launch_bounds__(kCopyThreads)
+copy_kernel(const uint32_t* __restrict__ cnt, int64_t nwt, int tpb, int64_t WT, int64_t D,
             int64_t nrows, const uint32_t* __restrict__ sent, int32_t* __restrict__ row_ptr,
             uint8_t* __restrict__ col, uint16_t* __restrict__ val, uint32_t cap) {
-  constexpr int NW = kThreads / 64;
-  const int lane = threadIdx.x & 63;
-  const int64_t wt = (int64_t)blockIdx.x * NW + (threadIdx.x >> 6);
-  if (wt >= nwt) return;
-  const uint32_t base = base_arr[wt];
-  const uint32_t n = min(base_arr[wt + 1] - base, (uint32_t)(WT * D));  // staging region bound
-  const int64_t r0 = wt * WT;
-  for (int64_t i = lane; i < WT; i += 64) {
-    const int64_t r = r0 + i;
-    if (r < nrows) row_ptr[r] += (int32_t)base;
-  }
-  const int64_t src = r0 * D;
-  for (uint32_t i0 = 0; i0 < n; i0 += 64 * kCopyUnroll) {
-    uint32_t ev[kCopyUnroll];
+  constexpr int NW = kCopyThreads / 64;
+  __shared__ uint32_t s_off[kCopyMaxTPB + 1];
+  __shared__ uint32_t s_pre[NW], s_run[NW];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int64_t t0 = (int64_t)blockIdx.x * tpb;
+  const int nt = (int)min<int64_t>(tpb, nwt - t0);
+  const uint32_t region = (uint32_t)(WT * D);  // staging capacity of a tile
+  // this block's tiles, one per thread, and the counts of all earlier tiles
+  // (t0 is a multiple of 4: whole 16-byte groups), all requested together
+  const uint32_t own = tid < nt ? min(cnt[t0 + tid], region) : 0u;
+  uint32_t pre = 0;
+  const uint4* c4 = reinterpret_cast<const uint4*>(cnt);
+  for (int64_t i0 = tid; i0 < t0 / 4; i0 += (int64_t)kCopyThreads * kCopyU) {
+    uint4 v[kCopyU];
 #pragma unroll
-    for (int u = 0; u < kCopyUnroll; ++u) {
-      const uint32_t i = i0 + u * 64 + lane;
-      if (i < n) ev[u] = sent[src + i];
+    for (int u = 0; u < kCopyU; ++u) {
+      const int64_t i = i0 + (int64_t)u * kCopyThreads;
+      v[u] = i < t0 / 4 ? c4[i] : make_uint4(0u, 0u, 0u, 0u);
     }
 #pragma unroll
-    for (int u = 0; u < kCopyUnroll; ++u) {
-      const uint32_t i = i0 + u * 64 + lane;
-      if (i < n && base + i < cap) {
-        col[base + i] = (uint8_t)(ev[u] >> 16);
-        val[base + i] = (uint16_t)ev[u];
+    for (int u = 0; u < kCopyU; ++u) pre += v[u].x + v[u].y + v[u].z + v[u].w;
+  }
+  pre = wave_sum(pre);
+  const uint32_t inc = wave_incl_sum_fused(own);
+  if (lane == 63) s_run[wv] = inc;
+  if (lane == 0) s_pre[wv] = pre;
+  __syncthreads();
+  uint32_t base = 0, before = inc - own;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    base += s_pre[w];
+    before += w < wv ? s_run[w] : 0u;
+  }
+  if (tid < tpb) s_off[tid] = before;
+  if (tid == kCopyThreads - 1) s_off[tpb] = before + own;  // the block's total (tiles < tpb <= 256)
+  __syncthreads();
+  const uint32_t total = s_off[tpb];
+  const int64_t r0 = t0 * WT;
+  const uint32_t nr = (uint32_t)min<int64_t>(nrows - r0, (int64_t)nt * WT);
+  const uint32_t wt32 = (uint32_t)WT;
+  const uint32_t* src = sent + r0 * D;
+  auto put = [&](uint32_t o, uint32_t e) {
+    if (o < cap) {
+      col[o] = (uint8_t)(e >> 16);
+      val[o] = (uint16_t)e;
+    }
+  };
+  // row_ptr: the first kCopyU rows per thread are requested together with
+  // the first batch of entries; larger blocks loop over the rest
+  int32_t rv[kCopyU];
+#pragma unroll
+  for (int u = 0; u < kCopyU; ++u) {
+    const uint32_t i = tid + u * kCopyThreads;
+    rv[u] = i < nr ? row_ptr[r0 + i] : 0;
+  }
+  // entries: wave wv copies tiles [wv * tpw, (wv + 1) * tpw), kCopyTW tiles
+  // per batch, kCopyUT entries per lane and tile requested before any store
+  // (a tile with more entries finishes in a loop after the batch)
+  const int tpw = tpb / NW;  // 2 to 16
+  for (int m0 = 0; m0 < tpw; m0 += kCopyTW) {
+    uint32_t e[kCopyTW][kCopyUT];
+#pragma unroll
+    for (int m = 0; m < kCopyTW; ++m) {
+      const int j = wv * tpw + m0 + m;
+      const uint32_t n = (m0 + m < tpw && j < nt) ? s_off[j + 1] - s_off[j] : 0u;
+#pragma unroll
+      for (int u = 0; u < kCopyUT; ++u) {
+        const uint32_t i = lane + 64u * u;
+        e[m][u] = i < n ? src[(int64_t)j * region + i] : 0u;
       }
     }
+    if (m0 == 0) {
+#pragma unroll
+      for (int u = 0; u < kCopyU; ++u) {
+        const uint32_t i = tid + u * kCopyThreads;
+        if (i < nr) row_ptr[r0 + i] = rv[u] + (int32_t)(base + s_off[i / wt32]);
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < kCopyTW; ++m) {
+      const int j = wv * tpw + m0 + m;
+      const bool own_tile = m0 + m < tpw && j < nt;
+      const uint32_t n = own_tile ? s_off[j + 1] - s_off[j] : 0u;
+      const uint32_t o0 = base + (own_tile ? s_off[j] : 0u);
+#pragma unroll
+      for (int u = 0; u < kCopyUT; ++u) {
+        const uint32_t i = lane + 64u * u;
+        if (i < n) put(o0 + i, e[m][u]);
+      }
+      for (uint32_t i = lane + 64u * kCopyUT; i < n; i += 64u) put(o0 + i, src[(int64_t)j * region + i]);
+    }
   }
+  for (uint32_t i0 = tid + kCopyU * kCopyThreads; i0 < nr; i0 += kCopyThreads * kCopyU) {
+#pragma unroll
+    for (int u = 0; u < kCopyU; ++u) {
+      const uint32_t i = i0 + u * kCopyThreads;
+      rv[u] = i < nr ? row_ptr[r0 + i] : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < kCopyU; ++u) {
+      const uint32_t i = i0 + u * kCopyThreads;
+      if (i < nr) row_ptr[r0 + i] = rv[u] + (int32_t)(base + s_off[i / wt32]);
+    }
+  }
+  if (t0 + nt == nwt && tid == 0) row_ptr[nrows] = (int32_t)(base + total);
 }
 
 // Compact unpack.  Each wave owns a private LDS segment of kUPasses * RW
@@ -820,12 +853,10 @@ extern "C" int hkv_nuq_pack_compact(const void* values, int64_t T, int H, int D,
   }
   HKV_CHECK_LAUNCH();
   const uint32_t cap = (uint32_t)std::min<int64_t>(capacity, 0x7fffffff);
-  uint32_t* bases = (uint32_t*)(ws + lay.base_off);
-  hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(kScanThreads), 0, s, a.cnt, a.ntiles, bases,
-                     row_ptr, nrows);
-  HKV_CHECK_LAUNCH();
-  const unsigned cgrid = (unsigned)((lay.ntiles + kThreads / 64 - 1) / (kThreads / 64));
-  hipLaunchKernelGGL(copy_kernel, dim3(cgrid), dim3(kThreads), 0, s, bases, a.ntiles,
+  int tpb = 32;
+  while (tpb < kCopyMaxTPB && (a.ntiles + tpb - 1) / tpb > kCopyBlocks) tpb *= 2;
+  const unsigned cgrid = (unsigned)((a.ntiles + tpb - 1) / tpb);
+  hipLaunchKernelGGL(copy_kernel, dim3(cgrid), dim3(kCopyThreads), 0, s, a.cnt, a.ntiles, tpb,
                      lay.tile_rows, (int64_t)D, nrows, a.sent, row_ptr, col, val, cap);
   HKV_CHECK_LAUNCH();
   return HKV_OK;

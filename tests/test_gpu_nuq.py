@@ -252,7 +252,7 @@ def test_compact_values_vs_oracle(dev, T, Tcal, L, offset):
 @pytest.mark.parametrize("per_token,L", [(False, 16), (True, 4)])
 def test_compact_many_tiles_vs_oracle(dev, per_token, L):
     """65,536 tokens x 4 heads: thousands of tiles, so the CSR offsets cross
-    many look-back windows; every byte against the oracle."""
+    many copy blocks; every byte against the oracle."""
     from helix_kv.ops import NuqLayerTables, nuq_pack_compact, nuq_unpack_compact
 
     T, H, D = 65536, 4, 128
@@ -278,6 +278,34 @@ def test_compact_many_tiles_vs_oracle(dev, per_token, L):
     want = O.unpack(wc, wv, wm, f32[0], "v" if per_token else "k",
                     positions=np.arange(T) if per_token else None)
     assert np.array_equal(_bits(out), want)
+
+
+@pytest.mark.parametrize("per_token,L,T", [(False, 16, 262144), (True, 4, 131072)])
+def test_compact_full_size_vs_oracle(dev, per_token, L, T):
+    """Prefill-sized calls (65,536 / 16,384 wave tiles): the CSR copy then runs
+    with 128 / 32 tiles per block; every byte against the oracle."""
+    from helix_kv.ops import NuqLayerTables, nuq_pack_compact
+
+    H, D = 4, 128
+    bits = 2 if L <= 4 else 4
+    rng = np.random.default_rng(11)
+    x = rng.standard_t(3, (T, H, D)).astype(np.float16)
+    rows = D if not per_token else 4096
+    poles = np.sort(rng.standard_normal((H, rows, L)), axis=-1).astype(np.float16)
+    up = rng.uniform(1.5, 3.0, (H, rows)).astype(np.float16)
+    t = NuqLayerTables(_t(poles, dev), _t(up, dev), _t(-up, dev), per_token=per_token)
+    cc = nuq_pack_compact(_t(x, dev), t, bits)
+    f32 = [a.astype(np.float32) for a in (poles, up, -up)]
+    if per_token:
+        wc, wv, wm = O.pack_v(x, *f32, positions=np.arange(T))
+    else:
+        wc, wv, wm = O.pack_k(x, *f32)
+    pk, rp, col, val = O.pack_compact(wc, wv, wm, bits)
+    assert cc.nnz == len(col) and 0.01 < cc.nnz / x.size < 0.5
+    assert np.array_equal(cc.row_ptr.cpu().numpy(), rp)
+    assert np.array_equal(cc.packed.cpu().numpy(), pk)
+    assert np.array_equal(cc.col.cpu().numpy(), col)
+    assert np.array_equal(_bits(cc.val), val)
 
 
 @pytest.mark.parametrize("H,per_token,L,T", [(1, False, 16, 257), (2, False, 4, 129), (8, False, 16, 333),
