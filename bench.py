@@ -633,7 +633,7 @@ def main() -> None:
         line["roofline"] = {"bound": "hbm", "achieved": round(ach / 1e9, 1), "peak": HBM_PEAK / 1e9,
                             "unit": "GB/s", "frac": round(ach / HBM_PEAK, 4),
                             "traffic": profiled_traffic(PACK_PROFILE),
-                            "kernel": "hkv_nuq_pack_compact call (stage + scan + copy kernels), "
+                            "kernel": "hkv_nuq_pack_compact call (stage + copy kernels), "
                                       f"{n_l} calls per step, event-timed one by one",
                             "algorithmic_bytes_per_launch": round(res["algo_bytes"] / n_l),
                             "launch_us": round(res["pack_kernel_ms"] * 1e3 / n_l, 2),

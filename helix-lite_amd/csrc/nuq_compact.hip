@@ -23,9 +23,12 @@
 namespace {
 
 constexpr int kThreads = 256;
-// Passes of 64/G rows per wave tile: 8, or 4 for per-channel 16-level tables
-// (their search state takes 72 registers; smaller tiles keep 3 waves a SIMD).
-__host__ __device__ inline int pack_passes(bool per_token, int nb) { return (!per_token && nb == 4) ? 4 : 8; }
+// Passes of 64/G rows per wave tile: 4 (smaller tiles, fewer registers, more
+// waves a SIMD), or 8 for per-channel tables of up to 8 levels, whose search
+// state is small enough that the longer tile's loads pay off (131072-token
+// layers, us per stage kernel, 8 -> 4 passes: K nuq2 49.2 -> 50.5, V nuq2
+// 48.1 -> 42.8, V nuq4 64.8 -> 59.3).
+__host__ __device__ constexpr int pack_passes(bool per_token, int nb) { return (!per_token && nb < 4) ? 8 : 4; }
 
 // Workspace: header, per-wave-tile counts, a region of (ntiles + 1) words
 // kept so the workspace size stays what earlier versions asked for, then the
@@ -46,12 +49,8 @@ HKV_DEV void wave_sync() {
 
 // KFIX: the rows of one pass of a wave (RW = 64/G) are a multiple of H, so a
 // lane's head is fixed (rw % H) and its token advances by RW / H per pass.
-// Per-token 4-level tables run four waves per SIMD (at most 128 VGPRs): the
-// fast path fits without spills, only the exact-scan path uses scratch
-// (measured 53.9 -> 48.9 us on a 131072-token V layer).  The other variants
-// are faster at three waves per SIMD with no spills.
 template <int NB, bool PT, int G, int BITS, bool KFIX, int PASSES>
-__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu((PT && NB == 2) ? 4 : 1)))
+__global__ void __launch_bounds__(kThreads)
 pack_stage_kernel(const uint16_t* __restrict__ x, int64_t nrows, int H, hkv_nuq_scales sc,
                   uint8_t* __restrict__ packed, int32_t* __restrict__ row_ptr,
                   uint32_t* __restrict__ sent, uint32_t* __restrict__ wt_cnt, int64_t nwt) {
@@ -749,7 +748,7 @@ struct PackArgs {
 
 template <int NB, bool PT, int G, int BITS, bool KFIX>
 void launch_stage(const PackArgs& a) {
-  auto k = pack_stage_kernel<NB, PT, G, BITS, KFIX, (!PT && NB == 4) ? 4 : 8>;  // pack_passes
+  auto k = pack_stage_kernel<NB, PT, G, BITS, KFIX, pack_passes(PT, NB)>;
   const int64_t nblocks = (a.ntiles + kThreads / 64 - 1) / (kThreads / 64);
   hipLaunchKernelGGL(k, dim3(resident_grid(k, nblocks)), dim3(kThreads), 0, a.s, a.x, a.nrows,
                      a.H, a.sc, a.pk, a.rp, a.sent, a.cnt, a.ntiles);
