@@ -118,15 +118,16 @@ int hkv_nuq_unpack_dense(const void *codes, const void *outlier_v, const void *o
  * c[4j+2]<<4 | c[4j+3]<<6) plus CSR outliers over rows r = t*H + h:
  * row_ptr (T*H+1) int32, col u8 (channel d), val fp16 (original value), in
  * ascending (row, col) order.  Entries beyond `capacity` are not written;
- * row_ptr is always complete, so row_ptr[T*H] is the true nnz and the call
- * returns HKV_ERR_CAPACITY only after the stream has run (see
- * hkv_nuq_pack_compact_status).  bits = 2 or 4 (levels <= 2^bits).  Requires
+ * row_ptr is always complete, so row_ptr[T*H] is the true nnz, which a
+ * caller compares with `capacity` once the stream has run (the call itself
+ * cannot know it).  bits = 2 or 4 (levels <= 2^bits).  Requires
  * scales->tables, D % 8 == 0, D <= 256.  The planned format of
  * src/kvquant/triton_kernels.py:7-18 and src/kvquant/compact_pool.py:11-12
- * (the reference never implemented it).  Three kernels on `stream`: a stage
- * kernel (codes, per-tile outlier counts, outliers staged per tile), a scan of
- * the tile counts and a copy into col/val.  `workspace` (256-byte aligned, no
- * initialisation needed) holds the counts, bases and staged outliers:
+ * (the reference never implemented it).  Two kernels on `stream`: a stage
+ * kernel (codes, per-tile outlier counts, outliers staged per tile) and a
+ * copy kernel that turns the counts into offsets and copies the staged
+ * outliers into col/val.  `workspace` (256-byte aligned, no initialisation
+ * needed) holds the counts and staged outliers:
  * hkv_nuq_pack_compact_workspace_bytes(T, H, D) bytes; calls that may overlap
  * must not share it.
  */
@@ -135,7 +136,7 @@ int hkv_nuq_pack_compact(const void *values, int64_t T, int H, int D, int bits,
                          const hkv_nuq_scales *scales, void *packed, int32_t *row_ptr,
                          uint8_t *col, uint16_t *val, int64_t capacity, void *workspace,
                          size_t workspace_bytes, void *stream);
-/* Device-side error word of a pack workspace.  The three-kernel pack has no
+/* Device-side error word of a pack workspace.  The two-kernel pack has no
  * device-side failure mode, so this returns 0 for any workspace (kept for
  * callers of the status protocol); HKV_ERR_ARG for NULL. */
 int hkv_nuq_pack_compact_status(const void *workspace, void *stream);
