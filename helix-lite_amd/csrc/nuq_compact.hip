@@ -220,7 +220,7 @@ pack_stage_kernel(const uint16_t* __restrict__ x, int64_t nrows, int H, hkv_nuq_
 // staged entries of several tiles (and the block's row_ptr entries) before
 // storing any, so a block waits on few memory round trips.  The last block
 // writes row_ptr[nrows] = nnz.
-constexpr int kCopyBlocks = 512;
+constexpr int kCopyBlocks = 256;
 constexpr int kCopyThreads = 1024;
 constexpr int kCopyMaxTPB = 256;
 constexpr int kCopyU = 4;   // loads in flight per thread: prefix counts, row_ptr
