@@ -495,6 +495,57 @@ def decode_attention(query: torch.Tensor, k: CompactCodes, kt: NuqLayerTables, v
     return out
 
 
+def decode_step(query: torch.Tensor, k: CompactCodes, kt: NuqLayerTables, v: CompactCodes,
+                vt: NuqLayerTables, K_min: torch.Tensor, K_max: torch.Tensor, top_k: int,
+                sink_pages: int = 4, *, gqa: str = "mean", select: str = "union",
+                scale: float | None = None, out: torch.Tensor | None = None,
+                out_dtype: torch.dtype = torch.float16) -> torch.Tensor:
+    """One decode step of one sequence held in the compact format: Quest page
+    selection from the page statistics, then the fused dequant + attention over
+    the selected pages.  Every size is known on the host, so the step reads
+    nothing back from the device and can be captured in a HIP graph.
+
+    The sync-free counterpart of the compact backend's decode forward
+    (src/kvquant/compact_backend.py:194-299), which reads seq_len, the selected
+    count and the last block's position back to the host:
+      - gqa="mean": the query heads of a group are averaged into one query per
+        KV head, in the query's dtype (compact_backend.py:225-231); "sum": the
+        bound of every query head, summed over the group.
+      - select="union": every query head attends to the union over KV heads of
+        the selected pages (src/kvquant/quest_selector.py:80, then all heads
+        of each kept block, compact_pool.py:492-537); "per_head": each KV head
+        attends to its own pages.  Sinks are the first sink_pages pages.
+      - The sequence is the k.shape[0] tokens of k / v; the last page may be
+        partial and its missing slots are masked (compact_backend.py:253-262).
+    query (Hq, 128) fp16; K_min / K_max (ceil(T / 16), H, 128) page statistics
+    of the sequence's K.  Returns (Hq, 128).
+    """
+    N.require_gpu(query, K_min, K_max)
+    T, H, D = k.shape
+    P = -(-T // 16)
+    if K_min.dim() != 3 or tuple(K_min.shape) != (P, H, D) or K_max.shape != K_min.shape:
+        raise ValueError(f"K_min/K_max should be ({P}, {H}, {D}), got {tuple(K_min.shape)}")
+    if query.dim() != 2 or int(query.shape[0]) % H or int(query.shape[1]) != D:
+        raise ValueError(f"query {tuple(query.shape)} incompatible with (T, H, D) = {(T, H, D)}")
+    Hq = int(query.shape[0])
+    if gqa == "mean":
+        qs = query.reshape(H, Hq // H, D).mean(dim=1).to(torch.float16)
+    elif gqa == "sum":
+        qs = query
+    else:
+        raise ValueError(f"gqa must be 'mean' or 'sum', got {gqa!r}")
+    sel, _ = quest_select(qs, K_min, K_max, top_k, sink_pages)
+    if select == "union":
+        flags = torch.zeros(P, dtype=torch.bool, device=query.device)
+        flags.index_fill_(0, sel.reshape(-1), True)
+        pages = torch.arange(P, dtype=torch.int64, device=query.device)
+        union = torch.where(flags, pages, torch.full_like(pages, -1))
+        sel = union.view(P, 1).expand(P, H).contiguous()
+    elif select != "per_head":
+        raise ValueError(f"select must be 'union' or 'per_head', got {select!r}")
+    return decode_attention(query, k, kt, v, vt, sel, scale=scale, out=out, out_dtype=out_dtype)
+
+
 def selected_attention(query: torch.Tensor, K_pages: torch.Tensor, V_pages: torch.Tensor,
                        page_indices: torch.Tensor, *, gqa: bool = False,
                        scale: float | None = None) -> torch.Tensor:

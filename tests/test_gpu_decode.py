@@ -189,3 +189,76 @@ def test_dense_selected_attention_vs_oracle(dev, dt, S, H, D, gqa):
     g = got.double().cpu().numpy()
     for h in range(Hq):
         assert np.linalg.norm(g[h] - want[h]) <= tol * np.linalg.norm(want[h]), h
+
+
+def _stats(k, T, H):
+    """Page min/max of the fp16 K over valid tokens (a partial last page is
+    padded with its last token, so padding changes nothing)."""
+    P = -(-T // PS)
+    pad = np.repeat(k[-1:], P * PS - T, axis=0)
+    return O.page_stats(np.concatenate([k, pad]).reshape(P, PS, H, 128))
+
+
+@pytest.mark.parametrize("gqa,select", [("mean", "union"), ("mean", "per_head"),
+                                        ("sum", "union"), ("sum", "per_head")])
+def test_decode_step_vs_oracle(dev, gqa, select):
+    """decode_step (src/kvquant/compact_backend.py:194-299 without host reads):
+    the selection restated by the oracle (mean-q per KV head, or the
+    group-summed bound; top-K with the first pages as sinks; union over KV
+    heads, src/kvquant/quest_selector.py:80) and the attention over the
+    selected pages with the partial last page masked."""
+    from helix_kv.ops import decode_step
+
+    T, H, group, top_k, sinks = 3000, 4, 7, 40, 4   # 188 pages, the last one 8 tokens
+    kc, kt, kd, vc, vt, vd = _problem(dev, T, H, 16, 4, 2048)
+    P = kd.shape[0]
+    k16 = kd.reshape(-1, H, 128)[:T].astype(np.float16)
+    kmin, kmax = _stats(k16, T, H)
+    q = RNG.standard_normal((H * group, 128)).astype(np.float16)
+    qd = _t(q, dev)
+    if gqa == "mean":
+        # the reference's own torch op (fp16 mean), evaluated where the step runs
+        qs = qd.reshape(H, group, 128).mean(dim=1).to(torch.float16).cpu().numpy()
+        bound = O.page_bound(qs, kmin, kmax)
+    else:
+        bound = O.page_bound_group(q, kmin, kmax, group)
+    sel = O.topk_sinks(bound, min(top_k, P - sinks), sinks)
+    if select == "union":
+        ids = np.unique(sel.reshape(-1))
+        assert sinks + top_k < ids.size < P
+        sel = np.repeat(ids[:, None], H, axis=1)
+    want = O.selected_attention(q.astype(np.float64), kd, vd, sel, lambda h: h // group,
+                                num_tokens=T)
+    got = decode_step(qd, kc, kt, vc, vt, _t(kmin, dev), _t(kmax, dev), top_k, sinks, gqa=gqa,
+                      select=select, out_dtype=torch.float32)
+    _check(got, want)
+
+
+def test_decode_step_graph_replay(dev):
+    """The step reads nothing back to the host, so it records into a HIP graph;
+    three replays, with eager steps between them, equal the eager result."""
+    from helix_kv.ops import decode_step
+
+    T, H, group = 2500, 4, 7
+    kc, kt, kd, vc, vt, vd = _problem(dev, T, H, 4, 16, 1024)
+    k16 = kd.reshape(-1, H, 128)[:T].astype(np.float16)
+    kmin, kmax = (_t(a, dev) for a in _stats(k16, T, H))
+    q = _t(RNG.standard_normal((H * group, 128)).astype(np.float16), dev)
+    eager = decode_step(q, kc, kt, vc, vt, kmin, kmax, 30, 4).clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        decode_step(q, kc, kt, vc, vt, kmin, kmax, 30, 4)
+    torch.cuda.current_stream().wait_stream(side)
+    out = torch.empty_like(eager)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        decode_step(q, kc, kt, vc, vt, kmin, kmax, 30, 4, out=out)
+    for _ in range(3):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+        other = decode_step(q, kc, kt, vc, vt, kmin, kmax, 30, 4, select="per_head")
+        torch.cuda.synchronize()
+        assert not torch.equal(other, eager)
