@@ -384,7 +384,8 @@ def bench_decode(args, dev):
     per layer Quest selection (group-sum bound, top 16384 + 4 sink pages per
     KV head) and the fused decode attention over the selected pages, read from
     the mixed nuq2/nuq4 compact pool.  The 28-layer step is one HIP graph."""
-    from helix_kv.ops import decode_attention, decode_pages_per_split, nuq_unpack_compact, quest_select
+    from helix_kv.ops import (decode_attention, decode_pages_per_split, decode_step,
+                              nuq_unpack_compact, quest_select)
 
     P = DEC_TOK // 16
     k, s = P // 4, 4
@@ -435,6 +436,40 @@ def bench_decode(args, dev):
         del Kf, Vf
     if worst > 1e-3:
         raise RuntimeError(f"decode attention differs from fp32 attention: rel {worst:.2e}")
+    # the reference's decode semantics (compact_backend.py:194-299): mean of the
+    # group's queries per KV head, every query head over the union of the KV
+    # heads' pages; one sync-free decode_step per layer, the step one HIP graph
+    for Ld in layers:
+        Ld["out_u"] = torch.empty((HQ, D), dtype=torch.float16, device=dev)
+
+    def step_union():
+        for Ld in layers:
+            decode_step(Ld["q"], Ld["ck"], Ld["kt"], Ld["cv"], Ld["vt"], Ld["kmin"], Ld["kmax"],
+                        k, s, gqa="mean", select="union", out=Ld["out_u"])
+
+    union_us = graph_us(step_union, stream, iters)
+    Ld = layers[-1]
+    qm = Ld["q"].reshape(H, HQ // H, D).mean(dim=1).to(torch.float16)
+    usel, _ = quest_select(qm, Ld["kmin"], Ld["kmax"], k, s)
+    flags = torch.zeros(P, dtype=torch.bool, device=dev)
+    flags[usel.reshape(-1)] = True
+    upages = flags.nonzero().reshape(-1)
+    tok = (upages[:, None] * 16 + torch.arange(16, device=dev)).reshape(-1)
+    Kf = nuq_unpack_compact(Ld["ck"], Ld["kt"])
+    Vf = nuq_unpack_compact(Ld["cv"], Ld["vt"])
+    uworst = 0.0
+    for g in range(H):
+        Kg, Vg = Kf[tok, g].float(), Vf[tok, g].float()
+        qs = Ld["q"][g * (HQ // H):(g + 1) * (HQ // H)].float()
+        ref = torch.softmax((qs @ Kg.T) * D ** -0.5, dim=-1) @ Vg
+        got = Ld["out_u"][g * (HQ // H):(g + 1) * (HQ // H)].float()
+        uworst = max(uworst, ((got - ref).norm(dim=-1) / ref.norm(dim=-1)).max().item())
+    del Kf, Vf
+    if uworst > 1e-3:
+        raise RuntimeError(f"union decode differs from fp32 attention: rel {uworst:.2e}")
+    union_pages = int(upages.numel())
+    log(f"[bench] decode step, union of heads' pages: {union_us:.1f} us; layer {LAYERS - 1}: "
+        f"{union_pages} of {P} pages, check rel err {uworst:.2e}")
     # algorithmic bytes
     sel_bytes = LAYERS * (2 * P * H * D * 2 + HQ * D * 2 + nsel * H * 8)
     dec_bytes = 0
@@ -454,7 +489,8 @@ def bench_decode(args, dev):
     torch.cuda.empty_cache()
     return dict(dec_step_us=step_us, dec_select_us=sel_us, dec_attn_us=dec_us,
                 dec_sel_bytes=sel_bytes, dec_attn_bytes=dec_bytes, dec_rel_err=worst,
-                dec_pps=pps, dec_sel_outliers=sel_out)
+                dec_pps=pps, dec_sel_outliers=sel_out, dec_union_us=union_us,
+                dec_union_pages=union_pages, dec_union_rel_err=uworst)
 
 
 def bench_ragged(args, dev):
@@ -679,6 +715,14 @@ def main() -> None:
             "algorithmic_bytes": res["dec_sel_bytes"] + res["dec_attn_bytes"],
             "selected_outliers": res["dec_sel_outliers"], "pages_per_split": res["dec_pps"],
             "check_rel_err": float(f"{res['dec_rel_err']:.3g}"),
+            "union_mean_q": {
+                "us_per_step": round(res["dec_union_us"], 1),
+                "pages_last_layer": res["dec_union_pages"],
+                "check_rel_err": float(f"{res['dec_union_rel_err']:.3g}"),
+                "config": "the reference's decode semantics: per layer the mean of each GQA "
+                          "group's queries selects top 16384 + 4 sink pages per KV head, and "
+                          "every query head attends to the union of the KV heads' pages; "
+                          "decode_step (no host reads), one HIP graph per step"},
             "config": f"Qwen2.5-7B shapes: {LAYERS} layers, 28 q heads, 4 KV heads, 128; "
                       f"{DEC_TOK} tokens in the mixed nuq2/nuq4 compact pool (~5% CSR "
                       "outliers); per layer Quest top 16384 + 4 sink pages per KV head, then "
