@@ -98,6 +98,7 @@ _SIGS = {
     "hkv_nuq_gather_pages": ([_p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32,
                               ctypes.POINTER(NuqScales), _i32, _i32, ctypes.POINTER(_i64),
                               ctypes.POINTER(_i64), _p, _p, _p], _i32),
+    "hkv_kmeans_1d": ([_p, _p, _i64, _i32, _i32, _p, _p], _i32),
     "hkv_selected_attention_workspace_bytes": ([_i64, _i32, _i32, _i32], _sz),
     "hkv_selected_attention": ([_p, _i32, _i32, _i32, _p, _p, _i32, _i64, _i32, _i32, _i32, _i32,
                                 _p, _i64, _i32, _i32, ctypes.c_float, _p, _i32, _p, _sz, _p], _i32),

@@ -664,3 +664,27 @@ def nuq_gather_pages(cc: CompactCodes, t: NuqLayerTables, sel: torch.Tensor, pag
         c_out, N.ptr(s), N.ptr(out), N.stream_of(out))
     N.check(st, "hkv_nuq_gather_pages", AssertionError)
     return out
+
+
+# ------------------------------------------------------------ calibration
+
+def kmeans_1d(values: torch.Tensor, offsets: torch.Tensor, k: int, iters: int = 20) -> torch.Tensor:
+    """Batched 1-D k-means (hkv_kmeans_1d): problem p is
+    values[offsets[p]:offsets[p+1]] (fp32, finite); returns (n, k) fp32
+    centres sorted ascending.  Replaces the sklearn fit of
+    src/kvquant/calibration.py:106-123 (_kmeans_1d), one problem per call there;
+    here every problem of a layer in one launch, with a deterministic start
+    (centres evenly over [min, max]) and a fixed number of Lloyd steps."""
+    N.require_gpu(values, offsets)
+    if values.dim() != 1 or offsets.dim() != 1 or offsets.numel() < 1:
+        raise ValueError("values must be (N,) and offsets (n + 1,)")
+    v = values.to(torch.float32).contiguous()
+    if v.numel() == 0:
+        v = torch.zeros(1, dtype=torch.float32, device=values.device)
+    off = offsets.to(torch.int64).contiguous()
+    n = int(off.numel()) - 1
+    centers = torch.empty((n, int(k)), dtype=torch.float32, device=values.device)
+    st = N.lib().hkv_kmeans_1d(N.ptr(v), N.ptr(off), n, int(k), int(iters), N.ptr(centers),
+                               N.stream_of(v))
+    N.check(st, "hkv_kmeans_1d", ValueError)
+    return centers

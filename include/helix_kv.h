@@ -402,6 +402,25 @@ int hkv_selected_attention(const void *q, int q_dtype, int Hq, int D, const void
                            int head_map, float scale, void *out, int out_dtype, void *workspace,
                            size_t workspace_bytes, void *stream);
 
+/*
+ * Batched 1-D k-means for nuq calibration: replaces the per-(head, channel)
+ * and per-(head, position) sklearn fits of src/kvquant/calibration.py:106-188
+ * (_kmeans_1d in the _calibrate_keys / _calibrate_values loops).  Problem p is
+ * values[offsets[p] .. offsets[p+1]) (fp32, finite; offsets int64,
+ * n_problems + 1 entries, each problem < 2^31 values).  k <= 16 centres start
+ * at order statistics, c_l = sorted[floor((2l + 1) n / 2k)], for n <= 8192
+ * values, else evenly spread over [min, max] (c_l = min + (max - min) *
+ * (2l + 1) / 2k in fp32), and take `iters` Lloyd steps: each value joins the
+ * first centre of least fp32 |v - c|, a centre with members moves to their
+ * mean (float64 sum / count, rounded to fp32), one without stays.  centers
+ * (n_problems, k) fp32 receive the centres sorted ascending.  As the
+ * reference's _kmeans_1d: no values give k zeros, n < k values give the
+ * values and k - n zeros, sorted.  Malformed offsets give NaN centres.
+ * Deterministic; no workspace.
+ */
+int hkv_kmeans_1d(const float *values, const int64_t *offsets, int64_t n_problems, int k,
+                  int iters, float *centers, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

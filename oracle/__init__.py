@@ -545,3 +545,43 @@ def f2h(x) -> np.ndarray:
 
 
 __all__ = [n for n in dir() if not n.startswith("_")]
+
+
+# ------------------------------------------------------- calibration (f4)
+
+def kmeans_1d(values, k: int, iters: int):
+    """One 1-D k-means problem -> k fp32 centres, sorted ascending.
+
+    The build's GPU calibration fit, restated (src/kvquant/calibration.py:106-123
+    fits sklearn KMeans there): centres start at order statistics,
+    c_l = sorted[floor((2l+1) n / 2k)], for n <= 8192 values, else evenly over
+    [min, max], c_l = fl32(min + fl32(fl32(max - min) * fl32((2l+1) / 2k))); each of `iters`
+    Lloyd steps assigns every value to the first centre of least fp32 |v - c|
+    and moves each centre with members to fl32(float64 sum / count).  No values
+    -> k zeros; n < k values -> the values and k - n zeros, sorted (the
+    reference's padding, calibration.py:116-119).
+    """
+    v = np.asarray(values, np.float32).reshape(-1)
+    n = v.size
+    if n < k:
+        return np.sort(np.concatenate([v, np.zeros(k - n, np.float32)])).astype(np.float32)
+    if n <= 8192:
+        c = np.sort(v)[((2 * np.arange(k) + 1) * n) // (2 * k)].astype(np.float32)
+    else:
+        mn, mx = v.min(), v.max()
+        frac = (np.arange(k, dtype=np.float32) * np.float32(2) + np.float32(1)) / np.float32(2 * k)
+        c = (mn + (mx - mn) * frac).astype(np.float32)
+    for _ in range(iters):
+        d = np.abs(v[:, None] - c[None, :])
+        idx = np.argmin(d, axis=1)
+        s = np.bincount(idx, weights=v.astype(np.float64), minlength=k)
+        m = np.bincount(idx, minlength=k)
+        c = np.where(m > 0, (s / np.maximum(m, 1)).astype(np.float32), c).astype(np.float32)
+    return np.sort(c)
+
+
+def kmeans_inertia(values, centers) -> float:
+    """Sum of squared distances to the nearest centre (float64)."""
+    v = np.asarray(values, np.float64).reshape(-1, 1)
+    c = np.asarray(centers, np.float64).reshape(1, -1)
+    return float(np.min((v - c) ** 2, axis=1).sum())
