@@ -493,6 +493,82 @@ def bench_decode(args, dev):
                 dec_union_pages=union_pages, dec_union_rel_err=uworst)
 
 
+def bench_calibration(args, dev):
+    """nuq calibration of one layer at the reference's default config
+    (src/kvquant/calibration.py:45-59): K from 32 prompts x 4096 tokens
+    (131072 x 4 x 128), V (32, 4096, 4, 128), nuq2 and nuq4, 0.5 % outlier
+    thresholds, 5000-value subsample; 512 + 16384 fits per layer, all on the
+    GPU (sorted quantiles, device compaction, one hkv_kmeans_1d launch per
+    side).  Beside it, the reference's own fit (sklearn KMeans, n_init=3,
+    max_iter=20, calibration.py:106-123) timed on a sample of the same
+    problems on the host, one problem at a time as the reference runs them."""
+    import time
+
+    from kvquant.calibration import CalibrationConfig, calibrate_keys, calibrate_values
+
+    torch.manual_seed(6)
+    t3 = torch.distributions.StudentT(torch.tensor(3.0, device=dev))
+    K = (t3.sample((32 * 4096, H, D)) * torch.exp(0.5 * torch.randn((1, H, D), device=dev))).half()
+    V = t3.sample((32, 4096, H, D)).half()
+    out, poles = {}, {}
+    for bits in (2, 4):
+        cfg = CalibrationConfig(num_bits=bits)
+        calibrate_keys(K, cfg)   # first use at these sizes: sort and allocator set-up
+        calibrate_values(V, cfg)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ks = calibrate_keys(K, cfg)
+        vs = calibrate_values(V, cfg)
+        torch.cuda.synchronize()
+        out[bits] = (time.perf_counter() - t0) * 1e3
+        assert torch.isfinite(ks.poles).all() and torch.isfinite(vs.poles).all()
+        poles[bits] = ([ks.poles[0, d].cpu().numpy() for d in range(8)] +
+                       [vs.poles[0, t].cpu().numpy() for t in range(24)])
+    # the reference's fit on a sample of problems: 8 K channels and 24 V positions
+    from sklearn.cluster import KMeans
+
+    sample = []
+    Kc = K[:, 0, :8].float().cpu().numpy()
+    for d in range(8):
+        sample.append(Kc[:, d])
+    Vc = V[:, :24, 0, :].float().cpu().numpy()
+    for t in range(24):
+        sample.append(Vc[:, t, :].reshape(-1))
+    rng = np.random.default_rng(0)
+    fit_s, ratio = {}, {}
+
+    def inertia(x, c):
+        return float(np.min((x.astype(np.float64)[:, None] - np.asarray(c, np.float64)[None, :]) ** 2,
+                            axis=1).sum())
+
+    for bits in (2, 4):
+        t0 = time.perf_counter()
+        centers = []
+        for x in sample:
+            lo, up = np.quantile(x, 0.005), np.quantile(x, 0.995)
+            m = x[(x >= lo) & (x <= up)]
+            if m.size > 5000:
+                m = m[rng.choice(m.size, 5000, replace=False)]
+            km = KMeans(n_clusters=2 ** bits, n_init=3, max_iter=20, random_state=0)
+            centers.append(km.fit(m.reshape(-1, 1)).cluster_centers_.ravel())
+        fit_s[bits] = (time.perf_counter() - t0) / len(sample) * (H * D + H * 4096)
+        # fit quality: inertia over each problem's in-threshold values, GPU / sklearn
+        r = []
+        for x, ours, ref in zip(sample, poles[bits], centers):
+            lo, up = np.quantile(x, 0.005), np.quantile(x, 0.995)
+            m = x[(x >= lo) & (x <= up)]
+            r.append(inertia(m, ours) / inertia(m, ref))
+        ratio[bits] = (float(np.mean(r)), float(np.max(r)))
+    log(f"[bench] calibration per layer: GPU nuq2 {out[2]:.1f} ms, nuq4 {out[4]:.1f} ms; "
+        f"reference fit on the host (estimated from {len(sample)} problems) "
+        f"{fit_s[2]:.0f} s / {fit_s[4]:.0f} s; inertia GPU / sklearn mean (max) "
+        f"nuq2 {ratio[2][0]:.3f} ({ratio[2][1]:.3f}), nuq4 {ratio[4][0]:.3f} ({ratio[4][1]:.3f})")
+    del K, V
+    torch.cuda.empty_cache()
+    return dict(cal_ms={b: out[b] for b in out}, cal_cpu_s=fit_s, cal_sample=len(sample),
+                cal_ratio=ratio)
+
+
 def bench_ragged(args, dev):
     """Ragged batched Quest + gather-dequant: 8 sequences of 2048-16384 pages
     (numpy default_rng(4)), one concatenated nuq4 compact pool (no outliers),
@@ -613,7 +689,8 @@ def main() -> None:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--only", choices=["all", "nuq", "quest", "ragged", "decode"], default="all")
+    ap.add_argument("--only", choices=["all", "nuq", "quest", "ragged", "decode", "calibration"],
+                    default="all")
     ap.add_argument("--profile", choices=["pack", "unpack", "quest", "ragged", "decode"], default=None,
                     help="run a short fixed launch sequence for rocprofv3 counters and exit")
     ap.add_argument("--cpu-layers", default="0,1,16,17",
@@ -640,6 +717,8 @@ def main() -> None:
         res.update(bench_ragged(args, dev))
     if args.only in ("all", "decode"):
         res.update(bench_decode(args, dev))
+    if args.only in ("all", "calibration"):
+        res.update(bench_calibration(args, dev))
     cpu = None
     if not args.no_cpu and args.only in ("all", "nuq"):
         cpu = cpu_baseline([int(x) for x in args.cpu_layers.split(",")], dev)
@@ -702,6 +781,20 @@ def main() -> None:
                                     "concatenated nuq4 compact pool, 4 KV heads x 128, q (8, 28, 128); "
                                     "per sequence top 25% + 4 sinks per KV head, then per-head "
                                     "gather + dequant of K and V into fp16 staging; one HIP graph"}
+    if "cal_ms" in res:
+        line["calibration"] = {
+            "gpu_ms_per_layer": {f"nuq{b}": round(v, 1) for b, v in res["cal_ms"].items()},
+            "reference_fit_cpu_s_per_layer": {f"nuq{b}": round(v, 1)
+                                              for b, v in res["cal_cpu_s"].items()},
+            "cpu_sample_problems": res["cal_sample"],
+            "inertia_vs_reference_fit": {f"nuq{b}": {"mean": round(v[0], 4), "max": round(v[1], 4)}
+                                         for b, v in res["cal_ratio"].items()},
+            "config": "one layer at the reference's default calibration config: K (131072, 4, "
+                      "128) and V (32, 4096, 4, 128) fp16 Student-t(3), 0.5% thresholds, "
+                      "5000-value subsample, 512 + 16384 fits; GPU: quantiles, compaction "
+                      "and hkv_kmeans_1d (order-statistic start, 50 Lloyd steps); host: "
+                      "sklearn KMeans(n_init=3, max_iter=20) per problem as the reference "
+                      "runs it, timed on a sample and scaled to the layer's problems"}
     if "dec_step_us" in res:
         dsel = res["dec_sel_bytes"] / (res["dec_select_us"] * 1e-6)
         datt = res["dec_attn_bytes"] / (res["dec_attn_us"] * 1e-6)
