@@ -22,8 +22,8 @@
 // The fp64 sums run per thread over a fixed stride of the values, then across
 // the block in a fixed order, so the result does not depend on scheduling.
 // A problem that fits (kKmLds floats) is staged in LDS once and sorted there
-// by a bitonic network (padded with +inf); larger ones are re-read from global
-// (L2) at each step.
+// by a bitonic network over the next power of two (padded with +inf); larger
+// ones are re-read from global (L2) at each step.
 #include "hkv_common.h"
 
 namespace {
@@ -103,11 +103,13 @@ kmeans_kernel(const float* __restrict__ values, const int64_t* __restrict__ offs
   }
   __syncthreads();
   if (staged) {
-    for (int i = n + tid; i < kKmLds; i += kKmT) s_v[i] = __builtin_inff();
+    int sz = 2;  // the sort's size: the next power of two >= n
+    while (sz < n) sz <<= 1;
+    for (int i = n + tid; i < sz; i += kKmT) s_v[i] = __builtin_inff();
     __syncthreads();
-    for (int size = 2; size <= kKmLds; size <<= 1) {
+    for (int size = 2; size <= sz; size <<= 1) {
       for (int stride = size >> 1; stride > 0; stride >>= 1) {
-        for (int t = tid; t < kKmLds / 2; t += kKmT) {
+        for (int t = tid; t < sz / 2; t += kKmT) {
           const int i = 2 * t - (t & (stride - 1));  // low element of the pair
           const int j = i + stride;
           const bool up = (i & size) == 0;
