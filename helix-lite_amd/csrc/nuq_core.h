@@ -43,28 +43,16 @@ HKV_DEV int slow_one(uint16_t xb, const SlowInfo& si, int64_t tab, int* o) {
 // index of element e (0..7); it is evaluated only on the exact-scan path.
 // code[j]: codes of elements 2j, 2j+1 in bits 0..3 / 16..19; om[j]: 0xffff lanes
 // for outliers.
-// SIGN: om[j] flags outliers in its sign bits only (bits 15 and 31) instead of
-// whole 0xffff lanes.
-//
-// XMIN: the fast path is taken when the largest |x| of the 8 elements is within
-// xmin, the smallest bound of the 8 tables (both halves; see xsafe_min),
-// instead of comparing each pair with its own bounds.  Never less exact: the
-// scan decides whatever the fast path does not.
-template <int NB, bool PT, typename TabFn, bool SIGN = false, bool XMIN = false>
+template <int NB, bool PT, typename TabFn>
 HKV_DEV void quant8(const uint4 xv, const Search2<NB>* S, const SlowInfo& si, TabFn tab,
-                    uint32_t code[4], uint32_t om[4], uint32_t xmin = 0) {
+                    uint32_t code[4], uint32_t om[4]) {
   const uint32_t x[4] = {xv.x, xv.y, xv.z, xv.w};
   uint32_t uns = 0;
-  if constexpr (PT || XMIN) {  // one bound: compare the largest magnitude
+  if constexpr (PT) {  // one bound: compare the largest magnitude
     u2_t mg = __builtin_bit_cast(u2_t, x[0] & 0x7fff7fffu);
 #pragma unroll
     for (int j = 1; j < 4; ++j) mg = __builtin_elementwise_max(mg, __builtin_bit_cast(u2_t, x[j] & 0x7fff7fffu));
-    if constexpr (PT) {
-      uns = unsafe2<NB>(__builtin_bit_cast(uint32_t, mg), S[0]);
-    } else {
-      const s2_t d = as_s2(xmin) - as_s2(__builtin_bit_cast(uint32_t, mg));
-      uns = as_u32(d) & 0x80008000u;
-    }
+    uns = unsafe2<NB>(__builtin_bit_cast(uint32_t, mg), S[0]);
   } else {
 #pragma unroll
     for (int j = 0; j < 4; ++j) uns |= unsafe2<NB>(x[j], S[j]);
@@ -73,8 +61,7 @@ HKV_DEV void quant8(const uint4 xv, const Search2<NB>* S, const SlowInfo& si, Ta
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       code[j] = search2<NB>(x[j], S[PT ? 0 : j]);
-      if constexpr (SIGN) om[j] = outlier2_sign<NB>(x[j], S[PT ? 0 : j]);
-      else om[j] = outlier2<NB>(x[j], S[PT ? 0 : j]);
+      om[j] = outlier2<NB>(x[j], S[PT ? 0 : j]);
     }
   } else {
 #pragma unroll 1
@@ -122,37 +109,6 @@ struct RowTabAt {
   }
 };
 
-// Word k (0..3) of a 4-word register group, by an explicit select tree (a
-// dynamic index into a register array becomes a compare chain over all of
-// the array's registers).
-HKV_DEV uint32_t pick4(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3, int k) {
-  const uint32_t lo = (k & 1) ? w1 : w0, hi = (k & 1) ? w3 : w2;
-  return (k & 2) ? hi : lo;
-}
-
-// Wave-wide inclusive prefix sum (row scans by DPP row_shr, then
-// row_bcast:15 / row_bcast:31 across the four 16-lane rows).
-template <int CTRL, int ROW_MASK>
-HKV_DEV uint32_t dpp_shifted(uint32_t v) {
-  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, 0xf, true);
-}
-HKV_DEV uint32_t wave_incl_sum(uint32_t v) {
-  v += dpp_shifted<0x111, 0xf>(v);  // row_shr:1
-  v += dpp_shifted<0x112, 0xf>(v);  // row_shr:2
-  v += dpp_shifted<0x114, 0xf>(v);  // row_shr:4
-  v += dpp_shifted<0x118, 0xf>(v);  // row_shr:8
-  v += dpp_shifted<0x142, 0xa>(v);  // row_bcast:15 into rows 1, 3
-  v += dpp_shifted<0x143, 0xc>(v);  // row_bcast:31 into rows 2, 3
-  return v;
-}
-
-// Wave-wide exclusive prefix of a per-lane count, and the wave total.
-HKV_DEV uint32_t wave_excl_count(uint32_t cnt, uint32_t* total) {
-  const uint32_t inc = wave_incl_sum(cnt);
-  *total = (uint32_t)__builtin_amdgcn_readlane((int)inc, 63);
-  return inc - cnt;
-}
-
 // Two 16-bit lanes holding small values -> two bytes (lane0 -> byte0).
 HKV_DEV uint32_t lanes_to_bytes(uint32_t v) { return (v & 0xffu) | ((v >> 8) & 0xff00u); }
 
@@ -169,14 +125,6 @@ HKV_DEV uint32_t pack_crumbs(const uint32_t c[4]) {
   uint32_t r = 0;
 #pragma unroll
   for (int j = 0; j < 4; ++j) r |= ((c[j] & 0x3u) | ((c[j] >> 14) & 0xcu)) << (4 * j);
-  return r;
-}
-
-// 8 outlier sign-bit flags (quant8<..., SIGN>) -> 8-bit mask, element e at bit e.
-HKV_DEV uint32_t mask_bits_sign(const uint32_t om[4]) {
-  uint32_t r = 0;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) r |= (((om[j] >> 15) & 1u) | ((om[j] >> 30) & 2u)) << (2 * j);
   return r;
 }
 
@@ -250,6 +198,11 @@ HKV_DEV constexpr uint32_t posm(int j) { return (1u << (2 * j)) | (1u << (16 + 2
 // codes packed at BITS bits (element e at bits BITS*e..; for BITS = 2 only
 // the low 16 bits are meaningful), *mask8 the 8-bit outlier mask (element e
 // at bit e).  Same semantics and fast/exact split as quant8.
+//
+// XMIN (per-channel tables): the fast path is taken when the largest |x| of
+// the 8 elements is within xmin, the smallest bound of the 8 tables (see
+// xsafe_min), instead of comparing each pair with its own bounds.  Never less
+// exact: the scan decides whatever the fast path does not.
 template <int NB, bool PT, int BITS, typename TabFn, bool XMIN = false>
 HKV_DEV void quant8_packed(const uint4 xv, const Search2<NB>* S, const SlowInfo& si, TabFn tab,
                            uint32_t* packed, uint32_t* mask8, uint32_t xmin = 0) {

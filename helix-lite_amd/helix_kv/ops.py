@@ -546,6 +546,48 @@ def decode_step(query: torch.Tensor, k: CompactCodes, kt: NuqLayerTables, v: Com
     return decode_attention(query, k, kt, v, vt, sel, scale=scale, out=out, out_dtype=out_dtype)
 
 
+def compact_view(c: CompactCodes, t0: int, t1: int) -> CompactCodes:
+    """Tokens [t0, t1) of a CompactCodes, without copies: the packed rows and
+    row_ptr entries are sliced, col / val stay whole (row_ptr holds absolute
+    offsets into them)."""
+    T, H, _ = c.shape
+    if not 0 <= t0 <= t1 <= T:
+        raise ValueError(f"token range [{t0}, {t1}) outside [0, {T})")
+    return CompactCodes(packed=c.packed[t0:t1], row_ptr=c.row_ptr[t0 * H:t1 * H + 1], col=c.col,
+                        val=c.val, bits=c.bits, nnz=c.nnz)
+
+
+def decode_step_batch(queries: torch.Tensor, k: CompactCodes, kt: NuqLayerTables, v: CompactCodes,
+                      vt: NuqLayerTables, K_min: torch.Tensor, K_max: torch.Tensor,
+                      seq_starts, seq_lens, top_k: int, sink_pages: int = 4, *, gqa: str = "mean",
+                      select: str = "union", scale: float | None = None,
+                      out: torch.Tensor | None = None,
+                      out_dtype: torch.dtype = torch.float16) -> torch.Tensor:
+    """decode_step for B sequences held in one compact-format tensor, still
+    without host reads.  Sequence b is tokens [seq_starts[b], seq_starts[b] +
+    seq_lens[b]) of k / v (starts are multiples of the 16-token page; V was
+    packed with positions counted from each sequence's start), its page
+    statistics are K_min / K_max rows [seq_starts[b] / 16, ...).  The reference
+    forward handles batch 1 only (src/kvquant/compact_backend.py:184-203).
+    queries (B, Hq, 128) fp16; returns (B, Hq, 128)."""
+    N.require_gpu(queries, K_min, K_max)
+    starts = [int(s) for s in seq_starts]
+    lens = [int(n) for n in seq_lens]
+    B = len(starts)
+    if queries.dim() != 3 or int(queries.shape[0]) != B or len(lens) != B:
+        raise ValueError(f"queries {tuple(queries.shape)} do not match {B} sequences")
+    if any(s % 16 for s in starts) or any(n < 1 for n in lens):
+        raise ValueError("sequence starts must be multiples of 16 and lengths positive")
+    if out is None:
+        out = torch.empty(tuple(queries.shape), dtype=out_dtype, device=queries.device)
+    for b, (t0, n) in enumerate(zip(starts, lens)):
+        p0, p1 = t0 // 16, (t0 + n + 15) // 16
+        decode_step(queries[b], compact_view(k, t0, t0 + n), kt, compact_view(v, t0, t0 + n), vt,
+                    K_min[p0:p1], K_max[p0:p1], top_k, sink_pages, gqa=gqa, select=select,
+                    scale=scale, out=out[b])
+    return out
+
+
 def selected_attention(query: torch.Tensor, K_pages: torch.Tensor, V_pages: torch.Tensor,
                        page_indices: torch.Tensor, *, gqa: bool = False,
                        scale: float | None = None) -> torch.Tensor:

@@ -262,3 +262,59 @@ def test_decode_step_graph_replay(dev):
         other = decode_step(q, kc, kt, vc, vt, kmin, kmax, 30, 4, select="per_head")
         torch.cuda.synchronize()
         assert not torch.equal(other, eager)
+
+
+def test_decode_step_batch_vs_oracle(dev):
+    """Three sequences in one compact tensor (page-aligned starts, V packed with
+    positions from each sequence's start): decode_step_batch equals the oracle
+    pipeline per sequence, union and mean-q as the reference forward."""
+    from helix_kv.ops import NuqLayerTables, decode_step_batch, nuq_pack_compact
+
+    H, group, D, top_k, sinks = 4, 7, 128, 12, 4
+    lens = [1000, 2500, 333]
+    starts = [0]
+    for n in lens[:-1]:
+        starts.append(starts[-1] + -(-n // PS) * PS)
+    T = starts[-1] + -(-lens[-1] // PS) * PS
+    pos = np.zeros(T, np.int64)
+    for s0, n in zip(starts, lens):
+        pos[s0:s0 + -(-n // PS) * PS] = np.arange(-(-n // PS) * PS)
+    k = (RNG.standard_t(3, (T, H, D)) * 0.7).astype(np.float16)
+    v = (RNG.standard_t(3, (T, H, D)) * 0.7).astype(np.float16)
+    kp, ku, kl = _scales(H, D, 16, 1.2)
+    vp, vu, vl = _scales(H, 1024, 4, 1.2)
+    kt = NuqLayerTables(_t(kp, dev), _t(ku, dev), _t(kl, dev), per_token=False)
+    vt = NuqLayerTables(_t(vp, dev), _t(vu, dev), _t(vl, dev), per_token=True)
+    kc = nuq_pack_compact(_t(k, dev), kt, 4)
+    vc = nuq_pack_compact(_t(v, dev), vt, 2, positions=torch.from_numpy(pos))
+
+    def deq(cc, poles, bits, kind, positions=None):
+        codes = O.bitunpack(cc.packed.cpu().numpy(), bits, D)
+        m, val = O.csr_decode(cc.row_ptr.cpu().numpy(), cc.col.cpu().numpy(),
+                              cc.val.cpu().numpy().view(np.uint16), T * H, D)
+        return O.h2f(O.unpack(codes, val.reshape(T, H, D), m.reshape(T, H, D),
+                              poles.astype(np.float32), kind, positions=positions))
+
+    kd = deq(kc, kp, 4, "k")
+    vd = deq(vc, vp, 2, "v", positions=pos)
+    stats = [_stats(k[s0:s0 + n], n, H) for s0, n in zip(starts, lens)]
+    kmin = np.concatenate([s[0] for s in stats])
+    kmax = np.concatenate([s[1] for s in stats])
+    assert kmin.shape[0] == T // PS
+    q = RNG.standard_normal((len(lens), H * group, D)).astype(np.float16)
+    qd = _t(q, dev)
+    got = decode_step_batch(qd, kc, kt, vc, vt, _t(kmin, dev), _t(kmax, dev), starts, lens,
+                            top_k, sinks, out_dtype=torch.float32)
+    for b, (s0, n) in enumerate(zip(starts, lens)):
+        P = -(-n // PS)
+        pad = P * PS - n
+        kb = np.concatenate([kd[s0:s0 + n], np.zeros((pad, H, D))]).reshape(P, PS, H, D)
+        vb = np.concatenate([vd[s0:s0 + n], np.zeros((pad, H, D))]).reshape(P, PS, H, D)
+        qs = qd[b].reshape(H, group, D).mean(dim=1).to(torch.float16).cpu().numpy()
+        bound = O.page_bound(qs, stats[b][0], stats[b][1])
+        sel = O.topk_sinks(bound, min(top_k, P - sinks), sinks)
+        ids = np.unique(sel.reshape(-1))
+        want = O.selected_attention(q[b].astype(np.float64), kb, vb,
+                                    np.repeat(ids[:, None], H, axis=1), lambda h: h // group,
+                                    num_tokens=n)
+        _check(got[b], want)
