@@ -215,12 +215,22 @@ decode_kernel(DecodeArgs A) {
 
   // the wave's page ids, one per lane (-1: none / out of range)
   const int64_t nw64 = j1 - j0 > wv ? (j1 - j0 - wv + kW - 1) / kW : 0;
-  const int nw = (int)nw64;  // <= kMaxPPS / kW = 64
+  const int nslots = (int)nw64;  // <= kMaxPPS / kW = 64
   int my_p = -1;
-  if (lane < nw) {
+  if (lane < nslots) {
     const int64_t s = A.sel[(j0 + wv + (int64_t)kW * lane) * H + g];
     my_p = (s >= 0 && s < A.npages) ? (int)s : -1;
   }
+  // Only valid ids are visited: they move, in order, to the wave's first nw
+  // lanes (one ds_permute over a permutation of the 64 lanes: the invalid
+  // ids go to the lanes after them).  A selection with holes (the union of
+  // the heads' pages written with -1 in place of the pages left out) then
+  // costs no pipeline steps for its holes.
+  const uint64_t vm = __builtin_amdgcn_ballot_w64(my_p >= 0);
+  const int below = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(vm >> 32),
+                                                   __builtin_amdgcn_mbcnt_lo((uint32_t)vm, 0u));
+  const int nw = __builtin_popcountll(vm);
+  my_p = __builtin_amdgcn_ds_permute((my_p >= 0 ? below : nw + (lane - below)) << 2, my_p);
   auto page_at = [&](int i) -> int { return i < nw ? __builtin_amdgcn_readlane(my_p, i) : -1; };
 
   // B operand of S^T = K Q^T: lane l holds q[qh = l%16][16i + 4(l/16) .. +3]

@@ -536,11 +536,15 @@ def decode_step(query: torch.Tensor, k: CompactCodes, kt: NuqLayerTables, v: Com
         raise ValueError(f"gqa must be 'mean' or 'sum', got {gqa!r}")
     sel, _ = quest_select(qs, K_min, K_max, top_k, sink_pages)
     if select == "union":
+        # the union's pages ascending at the front, -1 after them: the decode
+        # kernel's splits past the union's end find no valid page and return
         flags = torch.zeros(P, dtype=torch.bool, device=query.device)
         flags.index_fill_(0, sel.reshape(-1), True)
         pages = torch.arange(P, dtype=torch.int64, device=query.device)
-        union = torch.where(flags, pages, torch.full_like(pages, -1))
-        sel = union.view(P, 1).expand(P, H).contiguous()
+        dest = torch.where(flags, torch.cumsum(flags, 0) - 1, torch.full_like(pages, P))
+        union = torch.full((P + 1,), -1, dtype=torch.int64, device=query.device)
+        union.scatter_(0, dest, torch.where(flags, pages, torch.full_like(pages, -1)))
+        sel = union[:P].view(P, 1).expand(P, H).contiguous()
     elif select != "per_head":
         raise ValueError(f"select must be 'union' or 'per_head', got {select!r}")
     return decode_attention(query, k, kt, v, vt, sel, scale=scale, out=out, out_dtype=out_dtype)
