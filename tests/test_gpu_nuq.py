@@ -422,3 +422,46 @@ def test_spec_known_answers_on_gpu(dev):
     out, mask = quantize_nuq(vals, pl, torch.full((256,), 100.0, device=dev),
                              torch.full((256,), -100.0, device=dev))
     assert mask.sum() == 0 and (out - vals).abs().max().item() < 0.34
+
+
+@pytest.mark.parametrize("per_token", [False, True])
+def test_compact_pack_capacity_guard(dev, per_token):
+    """hkv_nuq_pack_compact with a CSR capacity below nnz, called through the C
+    ABI: row_ptr is complete (row_ptr[T*H] = the true nnz), the entries below
+    the capacity are the oracle's, and nothing at or past the capacity is
+    written (sentinel-filled guard region)."""
+    from helix_kv import _native as N
+    from helix_kv.ops import NuqLayerTables, pack_workspace
+
+    T, H, D, L = 8192, 4, 128, 16
+    x = RNG.standard_t(3, (T, H, D)).astype(np.float16)
+    rows = D if not per_token else 1024
+    poles = np.sort(RNG.standard_normal((H, rows, L)), axis=-1).astype(np.float16)
+    up = RNG.uniform(1.5, 3.0, (H, rows)).astype(np.float16)
+    t = NuqLayerTables(_t(poles, dev), _t(up, dev), _t(-up, dev), per_token=per_token)
+    f32 = [a.astype(np.float32) for a in (poles, up, -up)]
+    if per_token:
+        wc, wv, wm = O.pack_v(x, *f32, positions=np.arange(T))
+    else:
+        wc, wv, wm = O.pack_k(x, *f32)
+    pk, rp, col, val = O.pack_compact(wc, wv, wm, 4)
+    nnz = len(col)
+    cap = nnz // 3 + 7
+    guard = 4096
+    xd = _t(x, dev)
+    packed = torch.empty((T, H, D // 2), dtype=torch.uint8, device=dev)
+    row_ptr = torch.empty(T * H + 1, dtype=torch.int32, device=dev)
+    gcol = torch.full((cap + guard,), 0xAB, dtype=torch.uint8, device=dev)
+    gval = torch.full((cap + guard,), 0x1234, dtype=torch.int16, device=dev)
+    ws = pack_workspace(T, H, D, dev)
+    st = N.lib().hkv_nuq_pack_compact(N.ptr(xd), T, H, D, 4, t.struct(), N.ptr(packed),
+                                      N.ptr(row_ptr), N.ptr(gcol), N.ptr(gval), cap, N.ptr(ws),
+                                      ws.numel(), N.stream_of(xd))
+    assert st == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(row_ptr.cpu().numpy(), rp) and int(row_ptr[-1]) == nnz > cap
+    assert np.array_equal(packed.cpu().numpy(), pk)
+    gc = gcol.cpu().numpy()
+    gv = gval.cpu().numpy().view(np.uint16)
+    assert np.array_equal(gc[:cap], col[:cap]) and np.array_equal(gv[:cap], val[:cap])
+    assert (gc[cap:] == 0xAB).all() and (gv[cap:] == 0x1234).all()
