@@ -325,7 +325,8 @@ int hkv_quest_select_blocks(const void *q, int q_dtype, int H, const void *kmin,
  * map: query head hq attends with KV head hq / (Hq / H), over the tokens of
  * pages sel[0..nsel)[hq / (Hq / H)] (sel (nsel, H) int64, as hkv_quest_topk
  * returns; page p = tokens [16p, 16p+16), tokens >= T masked, page ids outside
- * [0, ceil(T/16)) skipped), softmax(q.K^T * scale) in fp32.
+ * [0, ceil(T/16)) skipped at no cost: a list with holes, such as the union of
+ * the heads' pages padded with -1, is fine), softmax(q.K^T * scale) in fp32.
  * K and V are in the compact format of hkv_nuq_pack_compact over (T, H, 128)
  * (packed 16-byte aligned); tables are the decision tables of the K scales
  * (H*128 per-channel) and of the V scales (H*v_rows per-token, row
