@@ -111,9 +111,17 @@ pack_stage_kernel(const uint16_t* __restrict__ x, int64_t nrows, int H, hkv_nuq_
       for (int i = lane; i < WT * 3; i += 64) {
         const int rr = i / 3, q = i - rr * 3;
         if (rr < nv) {
-          const int64_t r = r0 + rr;
-          const int64_t t = r / H;
-          const int h = (int)(r - t * H);
+          int64_t t;
+          int h;
+          if constexpr (KFIX) {  // H divides r0: the row's token and head from rr
+            const int k = rr / H;
+            t = t0 + k;
+            h = rr - k * H;
+          } else {
+            const int64_t r = r0 + rr;
+            t = r / H;
+            h = (int)(r - t * H);
+          }
           const int64_t tab = (int64_t)h * sc.rows + clamp_row(token_pos(sc, t), sc.rows);
           const uint4 v = reinterpret_cast<const uint4*>(tabs + tab)[q == 2 ? 4 : q];
           uint32_t* dw = wtab + rr * TW;
