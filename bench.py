@@ -569,6 +569,54 @@ def bench_calibration(args, dev):
                 cal_ratio=ratio)
 
 
+def bench_roundtrip(args, dev):
+    """The reference's CPU-runnable case: one layer's nuq4 quantise -> pack ->
+    unpack round trip, K and V each (4096 tokens, 4 KV heads, 128) fp16 N(0,1)
+    times a LogNormal(0, 0.5) per-channel scale; 16-entry LUT of N(0,1)
+    quantiles; K poles per (head, channel) = mean + std * LUT, V poles per
+    (head, position) = RMS * LUT; thresholds +-inf (no outliers).  Pack and
+    unpack of K and V in the compact format, one HIP graph per round trip (the
+    work is a few microseconds, so launches would dominate otherwise)."""
+    from helix_kv.ops import CompactCodes, NuqLayerTables, nuq_pack_compact, nuq_unpack_compact
+
+    T = 4096
+    g = torch.Generator(device=dev).manual_seed(0)
+    c = torch.exp(0.5 * torch.randn((H, D), generator=g, device=dev))
+    K = (torch.randn((T, H, D), generator=g, device=dev) * c).half()
+    V = (torch.randn((T, H, D), generator=g, device=dev) * c).half()
+    lv = lut(16).to(dev)
+    kf, vf = K.float(), V.float()
+    k_poles = (kf.mean(0)[..., None] + kf.std(0)[..., None] * lv).half()
+    v_poles = (vf.pow(2).mean(-1).sqrt().t()[..., None] * lv).half()   # (H, T, 16)
+    inf = torch.full((H, D), float("inf"), device=dev).half()
+    vinf = torch.full((H, T), float("inf"), device=dev).half()
+    kt = NuqLayerTables(k_poles, inf, -inf, per_token=False)
+    vt = NuqLayerTables(v_poles, vinf, -vinf, per_token=True)
+    ck = CompactCodes.empty(T, H, D, 4, 1024, dev)
+    cv = CompactCodes.empty(T, H, D, 4, 1024, dev)
+    ok, ov = torch.empty_like(K), torch.empty_like(V)
+
+    def trip():
+        nuq_pack_compact(K, kt, 4, out=ck, sync=False)
+        nuq_pack_compact(V, vt, 4, out=cv, sync=False)
+        nuq_unpack_compact(ck, kt, out=ok)
+        nuq_unpack_compact(cv, vt, out=ov)
+
+    stream = torch.cuda.Stream()
+    us = graph_us(trip, stream, max(200, 20 * args.steps))
+    # the round trip reproduces the poles: every value is its code's pole
+    err_k = ((ok.float() - kf).abs() / kf.abs().clamp_min(1e-3)).median().item()
+    if not (torch.isfinite(ok).all() and torch.isfinite(ov).all()) or int(ck.row_ptr[-1]) != 0:
+        raise RuntimeError("round trip produced non-finite values or outliers")
+    # algorithmic bytes of the trip: each of K, V is read and written in fp16
+    # once and its packed codes and row_ptr written and read once, plus scales
+    one = T * H * D * 2 + T * H * D // 2 + (T * H + 1) * 4
+    by = 2 * 2 * one + 2 * (scale_bytes((k_poles, inf, inf)) + scale_bytes((v_poles, vinf, vinf)))
+    log(f"[bench] round trip (4096 tokens, nuq4, K+V pack + unpack): {us:.1f} us in one graph, "
+        f"{by / (us * 1e-6) / 1e9:.0f} GB/s; median relative error of K {err_k:.3f}")
+    return dict(rt_us=us, rt_bytes=by, rt_err=err_k)
+
+
 def bench_ragged(args, dev):
     """Ragged batched Quest + gather-dequant: 8 sequences of 2048-16384 pages
     (numpy default_rng(4)), one concatenated nuq4 compact pool (no outliers),
@@ -689,8 +737,8 @@ def main() -> None:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--only", choices=["all", "nuq", "quest", "ragged", "decode", "calibration"],
-                    default="all")
+    ap.add_argument("--only", choices=["all", "nuq", "quest", "ragged", "decode", "calibration",
+                                       "roundtrip"], default="all")
     ap.add_argument("--profile", choices=["pack", "unpack", "quest", "ragged", "decode"], default=None,
                     help="run a short fixed launch sequence for rocprofv3 counters and exit")
     ap.add_argument("--cpu-layers", default="0,1,16,17",
@@ -719,6 +767,8 @@ def main() -> None:
         res.update(bench_decode(args, dev))
     if args.only in ("all", "calibration"):
         res.update(bench_calibration(args, dev))
+    if args.only in ("all", "roundtrip"):
+        res.update(bench_roundtrip(args, dev))
     cpu = None
     if not args.no_cpu and args.only in ("all", "nuq"):
         cpu = cpu_baseline([int(x) for x in args.cpu_layers.split(",")], dev)
@@ -781,6 +831,15 @@ def main() -> None:
                                     "concatenated nuq4 compact pool, 4 KV heads x 128, q (8, 28, 128); "
                                     "per sequence top 25% + 4 sinks per KV head, then per-head "
                                     "gather + dequant of K and V into fp16 staging; one HIP graph"}
+    if "rt_us" in res:
+        line["roundtrip_4096"] = {
+            "us_per_round_trip": round(res["rt_us"], 2),
+            "achieved_GBps": round(res["rt_bytes"] / (res["rt_us"] * 1e-6) / 1e9, 1),
+            "algorithmic_bytes": res["rt_bytes"],
+            "median_rel_err_k": round(res["rt_err"], 4),
+            "config": "one layer, K and V (4096, 4, 128) fp16 N(0,1) x LogNormal(0, 0.5) "
+                      "channel scales, nuq4 (16-entry N(0,1) quantile LUT), no outliers: "
+                      "pack + unpack of K and V in the compact format, one HIP graph"}
     if "cal_ms" in res:
         line["calibration"] = {
             "gpu_ms_per_layer": {f"nuq{b}": round(v, 1) for b, v in res["cal_ms"].items()},
