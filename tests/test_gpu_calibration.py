@@ -89,3 +89,47 @@ def test_kmeans_errors(dev):
         kmeans_1d(v, off, 17)        # k > 16
     with pytest.raises(ValueError):
         kmeans_1d(v, off, 4, -1)     # negative steps
+
+
+def test_calibrated_mixed_scales_pack_end_to_end(dev, tmp_path):
+    """Calibration -> a spliced nuq2 / nuq4 KVScales -> .pt -> device tables ->
+    pack_layer / unpack_layer of each layer, against the oracle's pack and
+    compact encoding with each layer's own level count (fp32 scales, as
+    calibration writes them)."""
+    from kvquant.calibration import CalibrationConfig, calibrate_keys, calibrate_values
+    from kvquant.packed import device_tables, pack_layer, unpack_layer
+    from kvquant.scales import KVScales
+
+    T, H, D = 512, 2, 128
+    layers = []
+    for bits in (2, 4):
+        cfg = CalibrationConfig(num_bits=bits, kmeans_subsample=400, outlier_pct=0.02)
+        K = torch.from_numpy(RNG.standard_t(3, (T, H, D)).astype(np.float16)).to(dev)
+        V = torch.from_numpy(RNG.standard_t(3, (2, 64, H, D)).astype(np.float16)).to(dev)
+        layers.append(KVScales([calibrate_keys(K, cfg).to("cpu")], [calibrate_values(V, cfg).to("cpu")],
+                               num_bits=bits))
+    mixed = KVScales(layers[0].per_layer_keys + layers[1].per_layer_keys,
+                     layers[0].per_layer_values + layers[1].per_layer_values)
+    p = tmp_path / "mixed.pt"
+    mixed.save(str(p))
+    tabs = device_tables(KVScales.load(str(p)), dev)
+    for i, lt in enumerate(tabs):
+        ks, vs = mixed.per_layer_keys[i], mixed.per_layer_values[i]
+        bits = 2 if ks.poles.shape[-1] <= 4 else 4
+        assert lt.k_bits == bits and lt.v_bits == bits
+        x = RNG.standard_t(3, (300, H, D)).astype(np.float16)
+        y = RNG.standard_t(3, (300, H, D)).astype(np.float16)
+        ck, cv = pack_layer(torch.from_numpy(x).to(dev), torch.from_numpy(y).to(dev), lt)
+        f = lambda t: t.float().numpy()
+        wk = O.pack_k(x, f(ks.poles), f(ks.upper_threshold), f(ks.lower_threshold))
+        wv = O.pack_v(y, f(vs.poles), f(vs.upper_threshold), f(vs.lower_threshold))
+        for cc, w in ((ck, wk), (cv, wv)):
+            pk, rp, col, val = O.pack_compact(*w, bits)
+            assert np.array_equal(cc.packed.cpu().numpy(), pk)
+            assert np.array_equal(cc.row_ptr.cpu().numpy(), rp)
+            assert np.array_equal(cc.col.cpu().numpy(), col)
+        ok, ov = unpack_layer(ck, cv, lt)
+        assert np.array_equal(ok.cpu().view(torch.int16).numpy().view(np.uint16),
+                              O.unpack(*wk, f(ks.poles), "k"))
+        assert np.array_equal(ov.cpu().view(torch.int16).numpy().view(np.uint16),
+                              O.unpack(*wv, f(vs.poles), "v"))
