@@ -96,6 +96,41 @@ def make_layer(layer: int, dev, T: int = T_TOK, seed_base: int = 1000):
     return (K, V, (k_poles, k_hi.half(), k_lo.half()), (v_poles, v_hi.half(), v_lo.half()), L)
 
 
+def round_trip_mismatches(x, cc, lt, back, chunk: int = 8192) -> int:
+    """Elements of a packed-then-unpacked (T,H,D) tensor that differ from the
+    definition, checked with torch on the GPU: the CSR holds exactly the
+    elements with x < lower or x > upper (thresholds per channel for K, per
+    (head, min(t, rows - 1)) for V), which come back bit-exact; the others
+    come back as fp16 of their nearest pole (first index of least fp32
+    |x - p|)."""
+    T, Hh, Dd = x.shape
+    rp = cc.row_ptr.long()
+    n = int(rp[-1].item())
+    rows = torch.repeat_interleave(torch.arange(T * Hh, device=x.device), rp[1:] - rp[:-1])
+    mask = torch.zeros((T * Hh, Dd), dtype=torch.bool, device=x.device)
+    mask[rows, cc.col[:n].long()] = True
+    mask = mask.view(T, Hh, Dd)
+    bad = 0
+    for t0 in range(0, T, chunk):
+        t1 = min(T, t0 + chunk)
+        xs = x[t0:t1].float()
+        if lt.per_token:
+            r = torch.arange(t0, t1, device=x.device).clamp(max=lt.rows - 1)
+            up = lt.upper[:, r].float().T[..., None]
+            lo = lt.lower[:, r].float().T[..., None]
+            p = lt.poles[:, r].float().permute(1, 0, 2)[:, :, None, :]
+        else:
+            up, lo = lt.upper.float(), lt.lower.float()
+            p = lt.poles.float()[None]
+        m = mask[t0:t1]
+        bad += int(((xs < lo) | (xs > up) != m).sum().item())
+        code = (xs[..., None] - p).abs().argmin(-1, keepdim=True)
+        pole = torch.gather(p.expand(t1 - t0, Hh, Dd, p.shape[-1]), -1, code)[..., 0].half()
+        want = torch.where(m, x[t0:t1], pole)
+        bad += int((back[t0:t1].view(torch.int16) != want.view(torch.int16)).sum().item())
+    return bad
+
+
 def scale_bytes(t) -> int:
     return sum(x.numel() * x.element_size() for x in t)
 
@@ -126,40 +161,122 @@ def per_launch_ms(launches) -> list[float]:
     return [a.elapsed_time(b) for a, b in evs]
 
 
-def cpu_baseline(layers: list[int], dev) -> dict:
-    """The CPU oracle (one thread) on a bounded sample of the same workload:
-    every token of the given layers, K and V, quantised, bit-packed and
-    CSR-encoded (about 3.5 s of CPU work per layer)."""
-    import oracle as O
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
 
-    total_bytes, total_s = 0.0, 0.0
+
+def host_threads() -> int:
+    """Threads of the host share this process may use: the CPU affinity set,
+    capped by OMP_NUM_THREADS when set."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    return max(1, min(n, int(env))) if env.isdigit() and int(env) > 0 else n
+
+
+def cpu_baseline(dev, layers=(0, 16), chunks: int = 3) -> dict:
+    """The reference's PyTorch CPU path, restated with the same torch op
+    sequence (oracle/torch_ref.py), timed on this host's cores in the same run
+    as the GPU figures, at all threads of the host share and at one thread.
+
+    nuq leg: find_outliers + quantize_nuq, then dequantize_nuq
+    (src/kvquant/nuq.py:22-156), over the first `chunks` 8192-token chunks of
+    K and V of the given layers of the benchmark workload (identical seeded
+    tensors), plus the numpy bit-pack + CSR step the reference lacks, timed
+    apart.  Rates use the GPU pack's algorithmic bytes for the same elements.
+    Quest leg: compute_page_stats + page_upper_bound (summed over the 7:1
+    group) + topk_pages_with_sinks (src/quest/reference.py:38-133) at 65,536
+    pages, fp16 metadata, top 16384 + 4 sinks: warm-up, median of 5."""
+    from oracle import torch_ref as R
+
+    chunk = 8192
+    n_tok = chunk * chunks
+    data = []
     for layer in layers:
         K, V, ks, vs, L = make_layer(layer, dev)
         bits = 2 if L <= 4 else 4
-        k = K.cpu().numpy()
-        v = V.cpu().numpy()
-        kp, ku, kl = (x.float().cpu().numpy() for x in ks)
-        vp, vu, vl = (x.float().cpu().numpy() for x in vs)
-        sb = scale_bytes(ks) + scale_bytes(vs)
+        kc, vc = K[:n_tok].cpu(), V[:n_tok].cpu()
         del K, V
-        t0 = time.perf_counter()
-        c, ov, om = O.pack_k(k, kp, ku, kl)
-        pk = O.pack_compact(c, ov, om, bits)
-        c2, ov2, om2 = O.pack_v(v, vp, vu, vl)
-        pv = O.pack_compact(c2, ov2, om2, bits)
-        total_s += time.perf_counter() - t0
-        n = k.size
-        tokens = k.shape[0]
-        total_bytes += (2 * (n * 2 + n * bits // 8 + (tokens * H + 1) * 4) + sb
-                        + 3 * (len(pk[2]) + len(pv[2])))
-        log(f"[bench] cpu baseline: layer {layer} done ({total_s:.1f} s so far)")
-    names = ", ".join(f"{l} (nuq{2 if l < CUT else 4})" for l in layers)
-    return {"value": round(total_bytes / total_s / 1e9, 4), "unit": "GB/s", "cores": 1,
-            "kind": "port",
-            "sample": f"oracle C quant+pack + numpy bit-pack/CSR over all {T_TOK} tokens x {H} heads "
-                      f"x {D} of layers {names}, K and V ({len(layers)} of the {LAYERS} layers); "
-                      f"{total_s:.1f} s",
-            "cpu": platform.processor() or platform.machine(), "host_cores": os.cpu_count()}
+        data.append((layer, bits, [(kc, [x.cpu() for x in ks], False),
+                                   (vc, [x.cpu() for x in vs], True)]))
+    g = torch.Generator(device=dev).manual_seed(3)
+    Kp = torch.randn((65536, 16, H, D), generator=g, device=dev).half().cpu()
+    q = torch.randn((HQ, D), generator=g, device=dev).half().cpu()
+    torch.cuda.synchronize()
+    n_all = host_threads()
+    prev = torch.get_num_threads()
+    legs = {}
+    try:
+        for n in (n_all, 1):
+            torch.set_num_threads(n)
+            tq = td = tp = 0.0
+            nbytes = 0
+            R.nuq_round_trip(data[0][2][0][0][:chunk], *data[0][2][0][1], False)  # warm-up
+            for layer, bits, tensors in data:
+                for x, (poles, up, lo), per_token in tensors:
+                    for t0 in range(0, n_tok, chunk):
+                        v = x[t0:t0 + chunk]
+                        a = time.perf_counter()
+                        if per_token:
+                            p, u, l = R.v_pole_rows(poles, up, lo, t0, t0 + chunk)
+                            p = p.expand(chunk, H, D, p.shape[-1])
+                        else:
+                            p, u, l = poles.expand(chunk, *poles.shape), up, lo
+                        _, m, idx = R.quantize_nuq(v, p, u, l)
+                        b = time.perf_counter()
+                        outl = torch.where(m, v, torch.zeros_like(v))
+                        R.dequantize_nuq(idx, outl, m, p)
+                        c = time.perf_counter()
+                        mk = m.numpy()
+                        packed = R.pack_codes_csr(idx.to(torch.uint8).numpy(), mk, v.numpy(), bits)
+                        d = time.perf_counter()
+                        tq += b - a
+                        td += c - b
+                        tp += d - c
+                        nel = v.numel()
+                        nbytes += nel * 2 + nel * bits // 8 + (chunk * H + 1) * 4 + 3 * len(packed[2])
+            stats_a = time.perf_counter()
+            mn, mx = R.compute_page_stats(Kp)
+            stats_s = time.perf_counter() - stats_a
+            sel_t = []
+            for i in range(6):
+                a = time.perf_counter()
+                bound = R.page_upper_bound_group(q, mn, mx, HQ // H)
+                R.topk_pages_with_sinks(bound, 16384, 4)
+                if i:
+                    sel_t.append(time.perf_counter() - a)
+            legs[n] = dict(quant_pack_GBps=nbytes / (tq + tp) / 1e9, quant_s=tq, pack_s=tp,
+                           unpack_GBps=nbytes / td / 1e9, dequant_s=td, bytes=nbytes,
+                           quest_select_us=float(np.median(sel_t)) * 1e6,
+                           quest_stats_ms=stats_s * 1e3)
+            log(f"[bench] cpu baseline, {n} threads: quant+pack {legs[n]['quant_pack_GBps']:.3f} GB/s "
+                f"(quant {tq:.2f} s + bit-pack/CSR {tp:.2f} s), dequant {legs[n]['unpack_GBps']:.3f} GB/s, "
+                f"Quest select {legs[n]['quest_select_us'] / 1e3:.1f} ms, stats build {stats_s * 1e3:.0f} ms")
+    finally:
+        torch.set_num_threads(prev)
+    A, O1 = legs[n_all], legs[1]
+    names = ", ".join(f"{l} (nuq{b})" for l, b, _ in data)
+    r4 = lambda x: float(f"{x:.4g}")  # noqa: E731
+    return {"value": r4(A["quant_pack_GBps"]), "unit": "GB/s", "cores": n_all, "kind": "port",
+            "sample": f"the reference's torch CPU op sequence (find_outliers + quantize_nuq; "
+                      f"nuq.py:22-132) + numpy bit-pack/CSR over the first {n_tok} tokens "
+                      f"({chunks} chunks of {chunk}) x {H} heads x {D} of K and V of layers {names} "
+                      f"of the same workload; Quest leg at 65,536 pages",
+            "cpu": cpu_model(), "host_cores": os.cpu_count(),
+            "quant_s": r4(A["quant_s"]), "bitpack_csr_s": r4(A["pack_s"]),
+            "unpack_GBps": r4(A["unpack_GBps"]),
+            "one_thread": {"quant_pack_GBps": r4(O1["quant_pack_GBps"]),
+                           "unpack_GBps": r4(O1["unpack_GBps"]),
+                           "quest_select_us": r4(O1["quest_select_us"]),
+                           "quest_stats_ms": r4(O1["quest_stats_ms"])},
+            "quest": {"select_us": r4(A["quest_select_us"]), "stats_build_ms": r4(A["quest_stats_ms"]),
+                      "config": "compute_page_stats + 7 x page_upper_bound (fp16, summed over the "
+                                "GQA group) + topk_pages_with_sinks(16384, 4); median of 5"}}
 
 
 def bench_nuq(args, dev):
@@ -230,10 +347,17 @@ def bench_nuq(args, dev):
     for _ in range(max(1, args.warmup)):
         ustep()
     torch.cuda.synchronize()
-    # round trip spot check: outliers come back exactly
-    Ld = layers[-1]
-    m = Ld["ck"]
-    assert m.nnz > 0
+    # full round-trip check of the last layer (nuq4) and the first (nuq2), K and
+    # V, against torch: the CSR marks exactly the elements outside the
+    # thresholds, those come back bit-exact, every other element comes back as
+    # fp16 of its nearest pole (first of equals, fp32 |v - p|)
+    for li in (len(layers) - 1, 0):
+        Ld, (ok, ov) = layers[li], outs[li]
+        for name, x, cc, lt, back in (("K", Ld["K"], Ld["ck"], Ld["kt"], ok),
+                                      ("V", Ld["V"], Ld["cv"], Ld["vt"], ov)):
+            bad = round_trip_mismatches(x, cc, lt, back)
+            if bad:
+                raise RuntimeError(f"round trip of layer {li} {name}: {bad} elements differ")
     ums = time_events(ustep, args.steps)
     unpack_gbs = algo / (ums * 1e-3) / 1e9
     udurs = per_launch_ms(unpacks)
@@ -617,14 +741,13 @@ def bench_roundtrip(args, dev):
     return dict(rt_us=us, rt_bytes=by, rt_err=err_k)
 
 
-def bench_ragged(args, dev):
-    """Ragged batched Quest + gather-dequant: 8 sequences of 2048-16384 pages
-    (numpy default_rng(4)), one concatenated nuq4 compact pool (no outliers),
-    per sequence top 25% + 4 sink pages per KV head, then the selected
-    (page, head) pairs of K and V dequantised into fp16 staging.  One HIP
-    graph per step (bound, top-K, two gathers)."""
-    from helix_kv.ops import (NuqLayerTables, nuq_gather_pages, nuq_pack_compact,
-                              nuq_unpack_compact, quest_page_stats, quest_select_ragged)
+def build_ragged(dev):
+    """The ragged workload: 8 sequences of U{2048..16384} pages (numpy
+    default_rng(4)) in one concatenated nuq4 compact pool (thresholds +-inf:
+    no outliers), V packed with each token's position in its sequence; the
+    fp16 page min / max of the reconstructed K; one decode query per sequence
+    (28, 128) fp16; per sequence top 25% of its pages."""
+    from helix_kv.ops import NuqLayerTables, nuq_pack_compact, nuq_unpack_compact, quest_page_stats
 
     rng = np.random.default_rng(4)
     lens = rng.integers(2048, 16385, size=8)
@@ -632,7 +755,6 @@ def bench_ragged(args, dev):
     Ptot = int(offs[-1])
     T = Ptot * 16
     ks = [int(n) // 4 for n in lens]
-    log(f"[bench] ragged: {len(lens)} sequences, {Ptot} pages ({T} tokens)")
     g = torch.Generator(device=dev).manual_seed(4)
     lv = lut(16).to(dev)
     K = torch.randn((T, H, D), generator=g, device=dev).half()
@@ -654,6 +776,22 @@ def bench_ragged(args, dev):
     kmin, kmax = quest_page_stats(kr.view(Ptot, 16, H, D))
     del kr
     q = torch.randn((len(lens), HQ, D), generator=g, device=dev).half()
+    return dict(lens=lens, offs=offs, Ptot=Ptot, T=T, ks=ks, kt=kt, vt=vt, ck=ck, cv=cv,
+                kmin=kmin, kmax=kmax, q=q, pos=pos)
+
+
+def bench_ragged(args, dev):
+    """Ragged batched Quest + gather-dequant: 8 sequences of 2048-16384 pages
+    (numpy default_rng(4)), one concatenated nuq4 compact pool (no outliers),
+    per sequence top 25% + 4 sink pages per KV head, then the selected
+    (page, head) pairs of K and V dequantised into fp16 staging.  One HIP
+    graph per step (bound, top-K, two gathers)."""
+    from helix_kv.ops import nuq_gather_pages, nuq_unpack_compact, quest_select_ragged
+
+    W = build_ragged(dev)
+    lens, offs, Ptot, T, ks = W["lens"], W["offs"], W["Ptot"], W["T"], W["ks"]
+    kt, vt, ck, cv, kmin, kmax, q = (W[n] for n in ("kt", "vt", "ck", "cv", "kmin", "kmax", "q"))
+    log(f"[bench] ragged: {len(lens)} sequences, {Ptot} pages ({T} tokens)")
     scores = torch.empty((H, Ptot), dtype=torch.float32, device=dev)
     res = {}
 
@@ -741,8 +879,8 @@ def main() -> None:
                                        "roundtrip"], default="all")
     ap.add_argument("--profile", choices=["pack", "unpack", "quest", "ragged", "decode"], default=None,
                     help="run a short fixed launch sequence for rocprofv3 counters and exit")
-    ap.add_argument("--cpu-layers", default="0,1,16,17",
-                    help="layers timed on the CPU oracle for the baseline")
+    ap.add_argument("--cpu-layers", default="0,16",
+                    help="layers of the workload timed on the CPU baseline")
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -771,8 +909,7 @@ def main() -> None:
         res.update(bench_roundtrip(args, dev))
     cpu = None
     if not args.no_cpu and args.only in ("all", "nuq"):
-        cpu = cpu_baseline([int(x) for x in args.cpu_layers.split(",")], dev)
-        log(f"[bench] cpu baseline {cpu['value']:.3f} GB/s")
+        cpu = cpu_baseline(dev, [int(x) for x in args.cpu_layers.split(",")])
     line = {
         "metric": METRIC,
         "value": round(res["pack_gbs"], 2) if "pack_gbs" in res else None,

@@ -873,13 +873,6 @@ extern "C" int hkv_nuq_pack_compact(const void* values, int64_t T, int H, int D,
   return HKV_OK;
 }
 
-extern "C" int hkv_nuq_pack_compact_status(const void* workspace, void* stream) {
-  // The two-kernel pack has no device-side failure mode; kept for callers
-  // that check it.
-  (void)stream;
-  return workspace ? 0 : HKV_ERR_ARG;
-}
-
 extern "C" int hkv_nuq_unpack_compact(const void* packed, const int32_t* row_ptr,
                                       const uint8_t* col, const uint16_t* val, int64_t capacity,
                                       int64_t T, int H, int D, int bits,

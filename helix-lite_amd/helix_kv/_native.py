@@ -61,7 +61,6 @@ _SIGS = {
     "hkv_nuq_pack_compact_workspace_bytes": ([_i64, _i32, _i32], _sz),
     "hkv_nuq_pack_compact": ([_p, _i64, _i32, _i32, _i32, ctypes.POINTER(NuqScales), _p, _p, _p,
                               _p, _i64, _p, _sz, _p], _i32),
-    "hkv_nuq_pack_compact_status": ([_p, _p], _i32),
     "hkv_nuq_unpack_compact": ([_p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32,
                                 ctypes.POINTER(NuqScales), _p, _p], _i32),
     "hkv_nuq_quantize_generic": ([_i32, ctypes.POINTER(_i64), ctypes.POINTER(TensorDesc),
@@ -165,6 +164,11 @@ def require_gpu(*ts: torch.Tensor) -> None:
 # --------------------------------------------------------------- workspaces
 
 _ws: dict[tuple, torch.Tensor] = {}
+# Buffers replaced by larger ones.  They are never freed: a HIP graph captured
+# while one of them was current keeps its raw address and writes to it on
+# every replay, so handing that memory back to the caching allocator would
+# let a replay corrupt whatever tensor received it next.
+_ws_retired: list[torch.Tensor] = []
 
 
 def workspace(kind: str, nbytes: int, device: torch.device) -> torch.Tensor:
@@ -172,12 +176,15 @@ def workspace(kind: str, nbytes: int, device: torch.device) -> torch.Tensor:
 
     One buffer per (kind, device, current stream); grown (and re-zeroed) when a
     larger one is needed.  Calls that share a buffer are ordered on that
-    stream, which the kernels rely on.
+    stream, which the kernels rely on.  A superseded buffer stays allocated
+    for the life of the process (graphs captured earlier still address it).
     """
     dev = torch.device(device)
     key = (kind, dev.index, torch.cuda.current_stream(dev).cuda_stream)
     buf = _ws.get(key)
     if buf is None or buf.numel() < nbytes:
+        if buf is not None:
+            _ws_retired.append(buf)
         buf = torch.zeros(max(int(nbytes), 64), dtype=torch.uint8, device=dev)
         _ws[key] = buf
     return buf

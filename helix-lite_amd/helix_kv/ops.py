@@ -200,9 +200,16 @@ def pack_workspace(T: int, H: int, D: int, device) -> torch.Tensor:
 def nuq_pack_compact(values: torch.Tensor, t: NuqLayerTables, bits: int, *,
                      capacity: int | None = None, positions=None, pos_offset: int = 0,
                      out: CompactCodes | None = None, sync: bool = True) -> CompactCodes:
-    """(T,H,D) fp16 -> CompactCodes.  With sync=True the true nnz is read back and
-    the call is re-issued with a larger capacity if needed (the returned col/val
-    are trimmed to nnz).  With sync=False nothing is read back."""
+    """(T,H,D) fp16 -> CompactCodes.
+
+    With sync=True the true nnz is read back.  The result is a new
+    CompactCodes whose col / val are views trimmed to nnz; the tensors of a
+    caller's ``out`` keep their full capacity (its ``nnz`` field is recorded).
+    If nnz exceeds the capacity, the call is re-issued into larger buffers,
+    unless ``out`` was given: then it raises, since the caller's buffers cannot
+    hold the result.  With sync=False nothing is read back and ``out`` (or the
+    new buffers) is returned as written; the caller compares row_ptr[-1] with
+    the capacity when it next synchronises."""
     H, D = _HD(t, values)
     _check_values(values, H, D)
     if bits not in (2, 4):
@@ -212,8 +219,12 @@ def nuq_pack_compact(values: torch.Tensor, t: NuqLayerTables, bits: int, *,
     T = int(values.shape[0])
     if capacity is None:
         capacity = max(1024, (T * H * D) // 8)
+    caller_out = out is not None
     if out is None:
         out = CompactCodes.empty(T, H, D, bits, capacity, values.device)
+    elif out.shape != (T, H, D) or out.bits != bits or out.row_ptr.numel() != T * H + 1:
+        raise AssertionError(f"out is {out.shape} at {out.bits} bits, the pack is {(T, H, D)} "
+                             f"at {bits} bits")
     pos = _positions(positions, T, values.device)
     ws = pack_workspace(T, H, D, values.device)
     s = t.struct(pos, pos_offset)
@@ -228,17 +239,16 @@ def nuq_pack_compact(values: torch.Tensor, t: NuqLayerTables, bits: int, *,
     if not sync:
         return out
     nnz = out.read_nnz()
-    if nnz > out.col.numel():
-        bigger = CompactCodes.empty(T, H, D, bits, nnz, values.device)
-        launch(bigger)
-        bigger.read_nnz()
-        out = bigger
-    err = N.lib().hkv_nuq_pack_compact_status(N.ptr(ws), N.stream_of(values))
-    if err:
-        raise RuntimeError(f"hkv_nuq_pack_compact: device reported error word {err}")
-    out.col = out.col[: out.nnz]
-    out.val = out.val[: out.nnz]
-    return out
+    cap = min(int(out.col.numel()), int(out.val.numel()))
+    if nnz > cap:
+        if caller_out:
+            raise RuntimeError(f"hkv_nuq_pack_compact: {nnz} outliers exceed the capacity {cap} "
+                               "of the given out")
+        out = CompactCodes.empty(T, H, D, bits, nnz, values.device)
+        launch(out)
+        out.read_nnz()
+    return CompactCodes(packed=out.packed, row_ptr=out.row_ptr, col=out.col[:nnz],
+                        val=out.val[:nnz], bits=bits, nnz=nnz)
 
 
 def nuq_unpack_compact(cc: CompactCodes, t: NuqLayerTables, *, positions=None, pos_offset: int = 0,
@@ -499,7 +509,8 @@ def decode_step(query: torch.Tensor, k: CompactCodes, kt: NuqLayerTables, v: Com
                 vt: NuqLayerTables, K_min: torch.Tensor, K_max: torch.Tensor, top_k: int,
                 sink_pages: int = 4, *, gqa: str = "mean", select: str = "union",
                 scale: float | None = None, out: torch.Tensor | None = None,
-                out_dtype: torch.dtype = torch.float16) -> torch.Tensor:
+                out_dtype: torch.dtype = torch.float16,
+                pages_per_split: int | None = None) -> torch.Tensor:
     """One decode step of one sequence held in the compact format: Quest page
     selection from the page statistics, then the fused dequant + attention over
     the selected pages.  Every size is known on the host, so the step reads
@@ -547,7 +558,8 @@ def decode_step(query: torch.Tensor, k: CompactCodes, kt: NuqLayerTables, v: Com
         sel = union[:P].view(P, 1).expand(P, H).contiguous()
     elif select != "per_head":
         raise ValueError(f"select must be 'union' or 'per_head', got {select!r}")
-    return decode_attention(query, k, kt, v, vt, sel, scale=scale, out=out, out_dtype=out_dtype)
+    return decode_attention(query, k, kt, v, vt, sel, scale=scale, out=out, out_dtype=out_dtype,
+                            pages_per_split=pages_per_split)
 
 
 def compact_view(c: CompactCodes, t0: int, t1: int) -> CompactCodes:

@@ -11,7 +11,8 @@ position) of V over all prompts and channels, it takes
 one problem at a time: about 17,000 fits per layer at the default config.
 
 Here every problem of a layer runs at once: the quantiles from a per-row sort
-(linear interpolation in float64, rounded to fp32), the in-threshold values
+(np.quantile's linear rule, in float32 as numpy computes it for the
+reference's float32 rows), the in-threshold values
 compacted on the device, and the fits in one launch of hkv_kmeans_1d.  Two
 steps are this build's own and differ from the reference's:
   - the subsample keeps, per problem, the first kmeans_subsample in-threshold
@@ -56,16 +57,27 @@ class CalibrationConfig:
 
 
 def row_quantiles(X: torch.Tensor, q: float) -> torch.Tensor:
-    """Per row of X (R, n) fp32: the q-quantile with linear interpolation
-    (np.quantile's default: position q * (n - 1) in the sorted row), computed
-    in float64 and rounded to fp32."""
+    """Per row of X (R, n) fp32: the q-quantile exactly as np.quantile
+    computes it for a float32 row (the reference's call,
+    src/kvquant/calibration.py:141-142, :176-177), all in float32:
+      position v = fl32(fl32(n - 1) * fl32(q)), i = floor(v), g = fl32(v - i);
+      a, b = sorted[i], sorted[i + 1], d = fl32(b - a);
+      result = fl32(a + fl32(d * g)) when g < 0.5, else fl32(b - fl32(d * fl32(1 - g)));
+      v >= n - 1 gives the largest value."""
+    import numpy as np
+
     n = int(X.shape[1])
-    s = torch.sort(X, dim=1).values.double()
-    pos = q * (n - 1)
-    i = min(int(pos), n - 1)
-    j = min(i + 1, n - 1)
-    frac = pos - i
-    return (s[:, i] + (s[:, j] - s[:, i]) * frac).float()
+    s = torch.sort(X.float(), dim=1).values
+    v = np.float32(n - 1) * np.float32(q)
+    if v >= np.float32(n - 1):
+        return s[:, n - 1].clone()
+    i = int(np.floor(v))
+    g = np.float32(v - np.float32(i))
+    a, b = s[:, i], s[:, i + 1]
+    d = b - a
+    if g >= np.float32(0.5):
+        return b - d * float(np.float32(1) - g)
+    return a + d * float(g)
 
 
 def _fit_rows(X: torch.Tensor, cfg: CalibrationConfig):

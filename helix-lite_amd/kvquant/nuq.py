@@ -120,8 +120,13 @@ def quantize_nuq(values: torch.Tensor, poles: torch.Tensor, upper_threshold: tor
 
 
 def dequantize_nuq(codes: torch.Tensor, outliers: torch.Tensor, outlier_mask: torch.Tensor,
-                   poles: torch.Tensor) -> torch.Tensor:
-    """where(mask, outliers, poles[code]) in the outliers' dtype.  nuq.py:135-156."""
+                   poles: torch.Tensor, *, check_codes: bool = False) -> torch.Tensor:
+    """where(mask, outliers, poles[code]) in the outliers' dtype.  nuq.py:135-156.
+
+    Asynchronous, like the reference's gather (nuq.py:155-156).  A code
+    outside [0, L) reads pole 0; with check_codes=True the call waits for the
+    kernel and raises RuntimeError if any code was out of range (the
+    reference's gather raises on such an index)."""
     N.require_gpu(codes, outliers, outlier_mask, poles)
     outliers = _float(outliers)
     poles = _float(poles)
@@ -140,7 +145,7 @@ def dequantize_nuq(codes: torch.Tensor, outliers: torch.Tensor, outlier_mask: to
         N.desc(m.expand(S), nd), N.desc(p, nd), int(p.stride(-1)), L, N.ptr(out),
         N.dtype_code(out), N.ptr(err), N.stream_of(outliers))
     N.check(st, "hkv_nuq_dequantize_generic", ValueError)
-    if int(err.item()):
+    if check_codes and int(err.item()):
         raise RuntimeError("dequantize_nuq: code index out of range")
     return out
 

@@ -136,10 +136,6 @@ int hkv_nuq_pack_compact(const void *values, int64_t T, int H, int D, int bits,
                          const hkv_nuq_scales *scales, void *packed, int32_t *row_ptr,
                          uint8_t *col, uint16_t *val, int64_t capacity, void *workspace,
                          size_t workspace_bytes, void *stream);
-/* Device-side error word of a pack workspace.  The two-kernel pack has no
- * device-side failure mode, so this returns 0 for any workspace (kept for
- * callers of the status protocol); HKV_ERR_ARG for NULL. */
-int hkv_nuq_pack_compact_status(const void *workspace, void *stream);
 
 /*
  * Compact unpack: packed codes + CSR -> out (T,H,D) fp16.  Inverse of

@@ -264,6 +264,45 @@ def test_decode_step_graph_replay(dev):
         assert not torch.equal(other, eager)
 
 
+def test_graph_survives_workspace_growth(dev):
+    """A graph captured while the step's workspaces were small keeps working
+    after an eager step on the same stream has grown them: the superseded
+    buffers stay allocated, so replays write only where they did at capture
+    (tensors allocated afterwards are untouched) and equal the eager result."""
+    from helix_kv.ops import decode_step
+
+    H, group = 4, 7
+    small = _problem(dev, 700, H, 16, 4, 1024)
+    large = _problem(dev, 9000, H, 16, 4, 1024)
+
+    def step(prob, q, **kw):
+        kc, kt, kd, vc, vt, vd = prob
+        T = kd.shape[0] * PS
+        k16 = kd.reshape(-1, H, 128)[:T].astype(np.float16)
+        kmin, kmax = (_t(a, dev) for a in _stats(k16, T, H))
+        return decode_step(q, kc, kt, vc, vt, kmin, kmax, kd.shape[0] // 3, 4, **kw)
+
+    q = _t(RNG.standard_normal((H * group, 128)).astype(np.float16), dev)
+    side = torch.cuda.Stream()   # workspaces are per stream: this one starts empty
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        eager = step(small, q).clone()
+        torch.cuda.synchronize()
+        out = torch.empty_like(eager)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            step(small, q, out=out)
+        step(large, q)                # grows the workspaces of this stream
+        torch.cuda.synchronize()
+    fillers = [torch.full((1 << 18,), 7, dtype=torch.int32, device=dev) for _ in range(64)]
+    for _ in range(3):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+    assert all(bool((f == 7).all()) for f in fillers)
+
+
 def test_decode_step_batch_vs_oracle(dev):
     """Three sequences in one compact tensor (page-aligned starts, V packed with
     positions from each sequence's start): decode_step_batch equals the oracle

@@ -280,10 +280,13 @@ def test_compact_many_tiles_vs_oracle(dev, per_token, L):
     assert np.array_equal(_bits(out), want)
 
 
-@pytest.mark.parametrize("per_token,L,T", [(False, 16, 262144), (True, 4, 131072)])
+@pytest.mark.parametrize("per_token,L,T", [(False, 16, 262144), (True, 4, 131072),
+                                           (False, 4, 131072), (True, 16, 131072)])
 def test_compact_full_size_vs_oracle(dev, per_token, L, T):
-    """Prefill-sized calls (65,536 / 16,384 wave tiles): the CSR copy then runs
-    with 128 / 32 tiles per block; every byte against the oracle."""
+    """Prefill-sized calls, all four stage kernels (K / V at nuq2 / nuq4) at
+    the full (131072, 4, 128) layer shape or larger: thousands of wave tiles,
+    so the CSR copy runs with 32 to 128 tiles per block; every byte against
+    the oracle."""
     from helix_kv.ops import NuqLayerTables, nuq_pack_compact
 
     H, D = 4, 128
@@ -365,6 +368,38 @@ def test_compact_unpack_respects_capacity(dev):
     flat_m[idx[keep:]] = 0
     want = O.unpack(wc, wv, flat_m.reshape(wm.shape), poles.astype(np.float32), "k")
     assert np.array_equal(got, want)
+
+
+def test_compact_reused_out_keeps_capacity(dev):
+    """A sync=True pack into a caller's CompactCodes returns trimmed views and
+    leaves the caller's col / val at full capacity, so a later sync=False pack
+    into the same object with more outliers is complete; a sync=True pack
+    whose outliers exceed the given capacity raises."""
+    from helix_kv.ops import CompactCodes, NuqLayerTables, nuq_pack_compact
+
+    T, H, D, L = 1024, 4, 128, 16
+    poles, up, lo = _kscales(H, D, L, thr=2.0)
+    t = NuqLayerTables(_t(poles, dev), _t(up, dev), _t(lo, dev), per_token=False)
+    f32 = [a.astype(np.float32) for a in (poles, up, lo)]
+    few = (RNG.standard_normal((T, H, D)) * 0.7).astype(np.float16)
+    many = (RNG.standard_t(3, (T, H, D)) * 1.5).astype(np.float16)
+    cap = T * H * D // 4
+    out = CompactCodes.empty(T, H, D, 4, cap, dev)
+    r1 = nuq_pack_compact(_t(few, dev), t, 4, out=out, sync=True)
+    assert out.col.numel() == cap and out.val.numel() == cap
+    assert r1.col.numel() == r1.nnz and out.nnz == r1.nnz
+    r2 = nuq_pack_compact(_t(many, dev), t, 4, out=out, sync=False)
+    assert r2 is out
+    torch.cuda.synchronize()
+    nnz2 = int(out.row_ptr[-1])
+    assert r1.nnz < nnz2 <= cap
+    pk, rp, col, val = O.pack_compact(*O.pack_k(many, *f32), 4)
+    assert np.array_equal(out.row_ptr.cpu().numpy(), rp)
+    assert np.array_equal(out.col[:nnz2].cpu().numpy(), col)
+    assert np.array_equal(_bits(out.val[:nnz2]), val)
+    small = CompactCodes.empty(T, H, D, 4, r1.nnz, dev)
+    with pytest.raises(RuntimeError, match="exceed the capacity"):
+        nuq_pack_compact(_t(many, dev), t, 4, out=small, sync=True)
 
 
 def test_compact_empty_and_repeat_calls(dev):

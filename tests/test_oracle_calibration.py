@@ -69,8 +69,12 @@ def test_row_quantiles_match_numpy():
     import torch
     from kvquant.calibration import row_quantiles
 
-    X = RNG.standard_t(3, (7, 1001)).astype(np.float32)
-    for q in (0.005, 0.5, 0.995, 0.0, 1.0):
-        got = row_quantiles(torch.from_numpy(X), q).numpy()
-        want = np.quantile(X.astype(np.float64), q, axis=1).astype(np.float32)
-        assert np.array_equal(got, want), q
+    # the reference calls np.quantile on float32 rows (calibration.py:141-142,
+    # :176-177), which interpolates in float32; bit-equal on every row
+    for n in (1, 2, 1001, 16384):
+        X = RNG.standard_t(3, (64, n)).astype(np.float32)
+        for q in (0.005, 0.5, 0.995, 0.0, 1.0, 0.025):
+            got = row_quantiles(torch.from_numpy(X), q).numpy()
+            want = np.quantile(X, q, axis=1)
+            assert want.dtype == np.float32
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (n, q)
