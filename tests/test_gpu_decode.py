@@ -275,24 +275,28 @@ def test_graph_survives_workspace_growth(dev):
     small = _problem(dev, 700, H, 16, 4, 1024)
     large = _problem(dev, 9000, H, 16, 4, 1024)
 
-    def step(prob, q, **kw):
-        kc, kt, kd, vc, vt, vd = prob
+    def stats(prob):
+        kd = prob[2]
         T = kd.shape[0] * PS
-        k16 = kd.reshape(-1, H, 128)[:T].astype(np.float16)
-        kmin, kmax = (_t(a, dev) for a in _stats(k16, T, H))
-        return decode_step(q, kc, kt, vc, vt, kmin, kmax, kd.shape[0] // 3, 4, **kw)
+        return tuple(_t(a, dev) for a in _stats(kd.reshape(-1, H, 128)[:T].astype(np.float16), T, H))
+
+    st_small, st_large = stats(small), stats(large)   # uploaded before the capture
+
+    def step(prob, st, q, **kw):
+        kc, kt, kd, vc, vt, vd = prob
+        return decode_step(q, kc, kt, vc, vt, st[0], st[1], kd.shape[0] // 3, 4, **kw)
 
     q = _t(RNG.standard_normal((H * group, 128)).astype(np.float16), dev)
     side = torch.cuda.Stream()   # workspaces are per stream: this one starts empty
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
-        eager = step(small, q).clone()
+        eager = step(small, st_small, q).clone()
         torch.cuda.synchronize()
         out = torch.empty_like(eager)
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, stream=side):
-            step(small, q, out=out)
-        step(large, q)                # grows the workspaces of this stream
+            step(small, st_small, q, out=out)
+        step(large, st_large, q)      # grows the workspaces of this stream
         torch.cuda.synchronize()
     fillers = [torch.full((1 << 18,), 7, dtype=torch.int32, device=dev) for _ in range(64)]
     for _ in range(3):

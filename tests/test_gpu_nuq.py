@@ -383,7 +383,7 @@ def test_compact_reused_out_keeps_capacity(dev):
     f32 = [a.astype(np.float32) for a in (poles, up, lo)]
     few = (RNG.standard_normal((T, H, D)) * 0.7).astype(np.float16)
     many = (RNG.standard_t(3, (T, H, D)) * 1.5).astype(np.float16)
-    cap = T * H * D // 4
+    cap = T * H * D // 2
     out = CompactCodes.empty(T, H, D, 4, cap, dev)
     r1 = nuq_pack_compact(_t(few, dev), t, 4, out=out, sync=True)
     assert out.col.numel() == cap and out.val.numel() == cap
