@@ -125,6 +125,7 @@ extern "C" const char* hkv_status_string(int s) {
     case HKV_ERR_CAPACITY: return "output capacity too small";
     case HKV_ERR_LAUNCH: return "kernel launch failed";
     case HKV_ERR_WORKSPACE: return "workspace missing or too small";
+    case HKV_ERR_SCRATCH: return "problem exceeds the fixed scratch of the no-allocation entry point";
     default: return "unknown status";
   }
 }

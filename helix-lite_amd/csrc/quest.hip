@@ -12,6 +12,7 @@
 // n/2 ... 1); bound = pos + neg, then + 0.0f so a zero bound is +0.
 #include "hkv_common.h"
 
+#include <mutex>
 #include <type_traits>
 
 namespace {
@@ -2338,3 +2339,80 @@ extern "C" int hkv_quest_select_ragged(const void* q, int q_dtype, int B, int Hq
   HKV_CHECK_LAUNCH();
   return HKV_OK;
 }
+
+// ------------------------------------------------ allocation-free selection
+//
+// hkv_quest_select_noalloc: hkv_quest_select with its workspace in a fixed
+// file-scope device array instead of a caller buffer, for callers that cannot
+// allocate device memory (code under graph capture, serving loops).  Each GPU
+// holds its own copy of the array for the life of the process; its address on
+// a device is looked up once, with that device current, and used for every
+// later call there.  The array's name is never passed to a kernel or copy
+// from host code: on the host it only names the symbol.
+
+namespace {
+
+constexpr size_t kSelectScratchBytes = (size_t)8 << 20;
+static __device__ __align__(256) unsigned char scratch[kSelectScratchBytes];
+
+constexpr int kScratchDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kScratchDevices];
+
+__global__ void __launch_bounds__(256) zero_words_kernel(uint4* __restrict__ p, size_t n16) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (size_t)gridDim.x * 256)
+    p[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+// The device address of the current device's scratch.  The first call on a
+// device looks it up and clears it with a fill kernel on `st` (ordered before
+// the caller's kernels on that stream; a fill kernel, not a memset, so the
+// call may also be captured into a graph).
+static int scratch_for_current_device(hipStream_t st, char** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kScratchDevices) return HKV_ERR_ARG;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return HKV_ERR_LAUNCH;
+    hipLaunchKernelGGL(zero_words_kernel, dim3(256), dim3(256), 0, st, (uint4*)p,
+                       kSelectScratchBytes / 16);
+    HKV_CHECK_LAUNCH();
+    g_scratch_ptr[dev] = p;
+  }
+  *out = (char*)g_scratch_ptr[dev];
+  return HKV_OK;
+}
+
+}  // namespace
+
+extern "C" size_t hkv_quest_select_noalloc_max_workspace(void) { return kSelectScratchBytes; }
+
+extern "C" int hkv_quest_select_noalloc(const void* q, int q_dtype, int Hq, const void* kmin,
+                                        const void* kmax, int k_dtype, int64_t P, int H, int D,
+                                        int64_t k, int64_t sink_pages, float* scores, int64_t* out,
+                                        int64_t* n_out, void* stream) {
+  if (!fdt(q_dtype) && q_dtype != HKV_DT_BF16) return HKV_ERR_DTYPE;
+  if (!fdt(k_dtype)) return HKV_ERR_DTYPE;
+  if (P < 0 || H < 1 || D < 1 || D > 512 || Hq < H || Hq % H) return HKV_ERR_SHAPE;
+  const SelectWs lay = select_ws_layout(P, H);
+  if (lay.NB > 0 && lay.bytes > kSelectScratchBytes) return HKV_ERR_SCRATCH;
+  const int64_t s = sink_pages < 0 ? 0 : (sink_pages > P ? P : sink_pages);
+  const int64_t keff = k < 0 ? 0 : (k > P - s ? P - s : k);
+  if (n_out) *n_out = s + keff;
+  if (P == 0) return HKV_OK;
+  if (!q || !kmin || !kmax || !scores || !out) return HKV_ERR_ARG;
+  hipStream_t st = (hipStream_t)stream;
+  char* ws = nullptr;
+  if (lay.NB > 0) {
+    const int rc = scratch_for_current_device(st, &ws);
+    if (rc != HKV_OK) return rc;
+  }
+  const bool mb = ws != nullptr && keff > 0;
+  int nmm = 0;
+  const int rc = page_bound(q, q_dtype, Hq, kmin, kmax, k_dtype, P, H, D, scores, HKV_DT_F32, 1, st,
+                            nullptr, 0, mb ? (uint2*)(ws + lay.mm_off) : nullptr, &nmm);
+  if (rc != HKV_OK) return rc;
+  return select_after_bound(scores, P, H, k, sink_pages, s, keff, out, lay, mb, ws, nmm, st);
+}
+

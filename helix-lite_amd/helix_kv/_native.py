@@ -21,6 +21,7 @@ HKV_ERR_DTYPE = 3
 HKV_ERR_CAPACITY = 4
 HKV_ERR_LAUNCH = 5
 HKV_ERR_WORKSPACE = 6
+HKV_ERR_SCRATCH = 7
 
 DT_F16, DT_F32, DT_BF16, DT_I64, DT_U8, DT_I32 = 0, 1, 2, 3, 4, 5
 TABLE_BYTES = 80
@@ -80,6 +81,9 @@ _SIGS = {
     "hkv_quest_select_workspace_bytes": ([_i64, _i32], _sz),
     "hkv_quest_select": ([_p, _i32, _i32, _p, _p, _i32, _i64, _i32, _i32, _i64, _i64, _p, _p,
                           ctypes.POINTER(_i64), _p, _sz, _p], _i32),
+    "hkv_quest_select_noalloc_max_workspace": ([], _sz),
+    "hkv_quest_select_noalloc": ([_p, _i32, _i32, _p, _p, _i32, _i64, _i32, _i32, _i64, _i64, _p, _p,
+                                  ctypes.POINTER(_i64), _p], _i32),
     "hkv_quest_page_stats_u8_workspace_bytes": ([_i32, _i32], _sz),
     "hkv_quest_page_stats_u8": ([_p, _p, _i32, _i64, _i32, _i32, _p, _p, _p, _p, _p, _sz, _p], _i32),
     "hkv_quest_select_u8": ([_p, _i32, _i32, _p, _p, _p, _p, _i64, _i32, _i32, _i64, _i64, _p, _p,

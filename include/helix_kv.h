@@ -28,7 +28,8 @@ enum hkv_status {
   HKV_ERR_DTYPE = 3,     /* unsupported dtype */
   HKV_ERR_CAPACITY = 4,  /* output capacity too small (result still sized) */
   HKV_ERR_LAUNCH = 5,    /* kernel launch failed */
-  HKV_ERR_WORKSPACE = 6  /* workspace missing or too small */
+  HKV_ERR_WORKSPACE = 6, /* workspace missing or too small */
+  HKV_ERR_SCRATCH = 7    /* problem larger than the fixed scratch of a no-allocation entry point */
 };
 
 enum hkv_dtype {
@@ -256,6 +257,26 @@ int hkv_quest_select(const void *q, int q_dtype, int Hq, const void *kmin, const
                      int k_dtype, int64_t P, int H, int D, int64_t k, int64_t sink_pages,
                      float *scores, int64_t *out, int64_t *n_out, void *workspace,
                      size_t workspace_bytes, void *stream);
+
+/*
+ * hkv_quest_select without a workspace argument and without allocating: the
+ * multi-block top-K keeps its state in a fixed device array of the library
+ * (hkv_quest_select_noalloc_max_workspace() = 8 MiB per GPU, held until the
+ * process ends) instead of a caller buffer.  No counterpart in the
+ * reference; for callers that cannot allocate device memory (code under HIP
+ * graph capture, serving loops that forbid hipMalloc).  Results are
+ * identical to hkv_quest_select's.  A problem whose workspace
+ * (hkv_quest_select_workspace_bytes(P, H)) exceeds the array returns
+ * HKV_ERR_SCRATCH before anything is launched.  The array's address on a
+ * device is looked up at the first call there, which also clears it with a
+ * fill kernel on `stream`; every call leaves it cleared for the next.  All
+ * calls on one GPU share the array: calls that may overlap on one GPU (other
+ * streams without ordering between them) race.
+ */
+size_t hkv_quest_select_noalloc_max_workspace(void);
+int hkv_quest_select_noalloc(const void *q, int q_dtype, int Hq, const void *kmin, const void *kmax,
+                             int k_dtype, int64_t P, int H, int D, int64_t k, int64_t sink_pages,
+                             float *scores, int64_t *out, int64_t *n_out, void *stream);
 
 /*
  * Compact page metadata: u8 codes of the page minima / maxima with a per
