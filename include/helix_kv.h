@@ -205,6 +205,49 @@ int hkv_pool_gather(const void *codes, const void *outlier_v, const void *outlie
                     const int64_t *first_pos, int64_t NK, void *staging, void *stream);
 
 /*
+ * Paged compact pool, one layer and side (K or V), D = 128, block_size 16:
+ *   codes (num_blocks, H, 16, D*bits/8) u8 -- page-head blocks, slot rows in
+ *     order, codes little-endian within a byte (nuq4: byte j = c[2j] |
+ *     c[2j+1] << 4; nuq2: c[4j] in the low bits);
+ *   ocnt (num_blocks, H) int32 -- outliers recorded for the page-head;
+ *   oent (num_blocks, H, cap) u32 -- the first min(ocnt, cap) of them,
+ *     (slot, channel) ascending, as fp16 value | channel << 16 | slot << 24;
+ *   kmin / kmax (num_blocks, H, D) fp16 -- K only: min / max over the written
+ *     slots of the dequantised values (outlier value, else fp16 pole), a zero
+ *     stored as +0;
+ *   status (1) int32 -- bit 0 set once a page-head's outliers exceed cap.
+ * The reference's pool is byte-per-code with dense outliers
+ * (src/kvquant/compact_pool.py:398-446); this is its planned bit-packed
+ * layout with outliers kept per block (compact_pool.py:11-12,
+ * src/kvquant/vllm_integration.md:51-55), page-head contiguous.
+ *
+ * hkv_paged_write replaces CompactKVPool.write_kv (compact_pool.py:447-489,
+ * kernels :160-287): token t of values (T,H,128) fp16 goes to slot
+ * slot_mapping[t] (block slot / 16, row slot % 16; slots < 0 or past the pool
+ * are skipped).  A run -- consecutive tokens with consecutive slots in one
+ * block -- starting at row w0 keeps the block's outliers of rows < w0 and
+ * replaces the rest; kmin / kmax (K: both given, or both NULL for no
+ * statistics; V: NULL) restart at w0 = 0 and otherwise fold in.  The tokens
+ * of one call that fall in one block must form one run.  V: per-token scales
+ * with scales->positions = absolute positions (row min(pos, rows - 1)).
+ * values / codes / kmin / kmax 16-byte aligned.
+ *
+ * hkv_paged_gather replaces CompactKVPool.unpack_to_staging
+ * (compact_pool.py:492-537, kernels :292-395): staging (NK, 16, H, 128) fp16
+ * row k = block block_ids[k] dequantised (ids outside the pool give zeros);
+ * V row p of kept block k uses scale row min(first_pos[k] + p, rows - 1).
+ * H <= 16.
+ */
+int hkv_paged_write(const void *values, int64_t T, int H, int D, int bits,
+                    const hkv_nuq_scales *scales, const int64_t *slot_mapping, int64_t num_blocks,
+                    int block_size, uint8_t *codes, int32_t *ocnt, uint32_t *oent, int cap,
+                    uint16_t *kmin, uint16_t *kmax, int32_t *status, void *stream);
+int hkv_paged_gather(const uint8_t *codes, const int32_t *ocnt, const uint32_t *oent, int cap,
+                     int64_t num_blocks, int block_size, int H, int D, int bits,
+                     const hkv_nuq_scales *scales, const int64_t *block_ids,
+                     const int64_t *first_pos, int64_t NK, void *staging, void *stream);
+
+/*
  * Quest page statistics: K_pages (P,S,H,D) -> kmin, kmax (P,H,D), same dtype
  * (f16 or f32).  -0 orders below +0; a NaN in a page-channel gives NaN.
  * src/quest/reference.py:38-56.

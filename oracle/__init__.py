@@ -585,3 +585,131 @@ def kmeans_inertia(values, centers) -> float:
     v = np.asarray(values, np.float64).reshape(-1, 1)
     c = np.asarray(centers, np.float64).reshape(1, -1)
     return float(np.min((v - c) ** 2, axis=1).sum())
+
+
+# ----------------------------------------------------- paged compact pool (f1)
+
+PAGE = 16
+
+
+def paged_empty(NB: int, H: int, D: int, bits: int, cap: int, stats: bool) -> dict:
+    """An empty paged pool side (numpy): codes (NB,H,16,D*bits/8) u8, ocnt
+    (NB,H) int64, oent (NB,H,cap) u32, kmin / kmax (NB,H,D) fp16 bits (K only;
+    +inf / -inf), status int."""
+    p = dict(codes=np.zeros((NB, H, PAGE, D * bits // 8), np.uint8), ocnt=np.zeros((NB, H), np.int64),
+             oent=np.zeros((NB, H, cap), np.uint32), bits=bits, cap=cap, status=0)
+    if stats:
+        p["kmin"] = np.full((NB, H, D), 0x7C00, np.uint16)
+        p["kmax"] = np.full((NB, H, D), 0xFC00, np.uint16)
+    return p
+
+
+def paged_runs(slots, nslots: int):
+    """Runs of a slot mapping: maximal stretches of consecutive tokens whose
+    slots are in the pool and consecutive within one page, as (first token,
+    length, page, first row)."""
+    s = np.asarray(slots, np.int64)
+    valid = (s >= 0) & (s < nslots)
+    runs = []
+    t = 0
+    T = s.size
+    while t < T:
+        if not valid[t]:
+            t += 1
+            continue
+        n = 1
+        while (t + n < T and valid[t + n] and s[t + n] == s[t + n - 1] + 1 and s[t + n] % PAGE != 0):
+            n += 1
+        runs.append((t, n, int(s[t]) // PAGE, int(s[t]) % PAGE))
+        t += n
+    return runs
+
+
+def _zero_plus(bits16):
+    b = np.asarray(bits16, np.uint16).copy()
+    b[b == 0x8000] = 0
+    return b
+
+
+def paged_write(pool: dict, values, slot_mapping, scale, per_token: bool, positions=None) -> None:
+    """hkv_paged_write restated, in place on ``pool`` (see paged_empty).
+
+    The pool's write of src/kvquant/compact_pool.py:447-489 (kernels :160-287)
+    in the bit-packed, per-page-outlier layout: each run (paged_runs) writes
+    its rows' codes (the K / V pack of pack_k / pack_v) into rows w0.. of its
+    page for every head; the page-head keeps the outliers of rows < w0 (all of
+    them, counted, when every stored one is below w0) and appends the run's
+    outliers in (row, channel) order, storing the first cap; K statistics are
+    the min / max of the dequantised values over the run's rows (a zero as
+    +0), replacing the page's at w0 = 0 and folded in otherwise.  scale =
+    (poles, upper, lower) float32 arrays; V rows min(positions[t], rows - 1)."""
+    x = _h16(values)
+    T, H, D = x.shape
+    bits, cap = pool["bits"], pool["cap"]
+    NB = pool["codes"].shape[0]
+    pos = np.arange(T, dtype=np.int64) if positions is None else np.asarray(positions, np.int64)
+    if per_token:
+        codes, outv, outm = pack_v(x, *scale, positions=pos)
+    else:
+        codes, outv, outm = pack_k(x, *scale)
+    stats = "kmin" in pool
+    if stats:
+        deq = unpack(codes, outv, outm, scale[0], "k")
+    for t0, n, pg, w0 in paged_runs(slot_mapping, NB * PAGE):
+        pool["codes"][pg, :, w0:w0 + n] = bitpack(codes[t0:t0 + n], bits).transpose(1, 0, 2)
+        for h in range(H):
+            cnt = int(pool["ocnt"][pg, h])
+            m = min(cnt, cap)
+            stored = pool["oent"][pg, h, :m]
+            below = int(((stored >> 24) < w0).sum()) if w0 > 0 else 0
+            base = 0 if w0 == 0 else (cnt if below == m else below)
+            rr, dd = np.nonzero(outm[t0:t0 + n, h])
+            ent = (outv[t0 + rr, h, dd].astype(np.uint32) | (dd.astype(np.uint32) << 16)
+                   | ((w0 + rr).astype(np.uint32) << 24))
+            idx = base + np.arange(ent.size)
+            keep = idx < cap
+            pool["oent"][pg, h, idx[keep]] = ent[keep]
+            pool["ocnt"][pg, h] = base + ent.size
+            if base + ent.size > cap:
+                pool["status"] |= 1
+            if stats:
+                v = h2f(deq[t0:t0 + n, h])
+                lo = _zero_plus(f2h(v.min(axis=0)))
+                hi = _zero_plus(f2h(v.max(axis=0)))
+                if w0 > 0:
+                    lo = f2h(np.minimum(h2f(lo), h2f(pool["kmin"][pg, h])))
+                    hi = f2h(np.maximum(h2f(hi), h2f(pool["kmax"][pg, h])))
+                pool["kmin"][pg, h], pool["kmax"][pg, h] = lo, hi
+
+
+def paged_gather(pool: dict, block_ids, first_pos, poles, per_token: bool, D: int = 128):
+    """hkv_paged_gather restated: staging (NK,16,H,D) fp16 bits, kept block
+    k dequantised (ids outside the pool: zeros), V row p at scale row
+    min(first_pos[k] + p, rows - 1).  The pool's unpack_to_staging
+    (src/kvquant/compact_pool.py:492-537) over the paged layout."""
+    ids = np.asarray(block_ids, np.int64)
+    NB, H = pool["codes"].shape[:2]
+    bits, cap = pool["bits"], pool["cap"]
+    NK = ids.size
+    out = np.zeros((NK, PAGE, H, D), np.uint16)
+    for k, b in enumerate(ids):
+        if not 0 <= b < NB:
+            continue
+        codes = bitunpack(pool["codes"][b], bits, D).transpose(1, 0, 2)  # (16, H, D)
+        outv = np.zeros((PAGE, H, D), np.uint16)
+        outm = np.zeros((PAGE, H, D), np.uint8)
+        for h in range(H):
+            m = min(int(pool["ocnt"][b, h]), cap)
+            e = pool["oent"][b, h, :m]
+            sl, ch = (e >> 24).astype(np.int64), ((e >> 16) & 255).astype(np.int64)
+            outm[sl, h, ch] = 1
+            outv[sl, h, ch] = (e & 0xFFFF).astype(np.uint16)
+        if per_token:
+            p = int(np.asarray(first_pos, np.int64)[k]) + np.arange(PAGE)
+            out[k] = unpack(codes, outv, outm, poles, "v", positions=p)
+        else:
+            out[k] = unpack(codes, outv, outm, poles, "k")
+    return out
+
+
+__all__ = [n for n in dir() if not n.startswith("_")]
