@@ -58,14 +58,16 @@ constexpr float kLog2e = 1.4426950408889634f;
 // q puts the four q groups on disjoint banks (32 or 64 banks).
 HKV_DEV int klut_index(int ch, int c) { return ch * 16 + 16 * (ch >> 5) + c; }
 
-struct Side {  // one of K / V in the compact format
-  const uint8_t* packed;   // (T, H, D*bits/8)
-  const int32_t* row_ptr;  // (T*H + 1)
-  const uint8_t* col;      // (cap)
-  const uint16_t* val;     // (cap)
-  int64_t cap;
+struct Side {  // one of K / V in the compact format, or in the paged pool
+  const uint8_t* packed;   // compact: (T, H, D*bits/8); paged: (NB, H, 16, D*bits/8)
+  const int32_t* row_ptr;  // compact: (T*H + 1)
+  const uint8_t* col;      // compact: (cap)
+  const uint16_t* val;     // compact: (cap)
+  int64_t cap;             // compact: CSR entries; paged: entries per page-head
   const hkv_table_t* tabs; // decision tables: pf16 are the dequantised poles
   int64_t rows;            // per-token scale rows (V); unused for K
+  const int32_t* ocnt;     // paged: (NB, H) outliers per page-head
+  const uint32_t* oent;    // paged: (NB, H, cap) value | channel << 16 | slot << 24
 };
 
 struct DecodeArgs {
@@ -75,6 +77,8 @@ struct DecodeArgs {
   int64_t T, npages;
   const int64_t* sel;  // (nsel, H)
   int64_t nsel;
+  const int64_t* bt;   // paged: logical page -> pool block (npages entries)
+  int64_t nblocks;     // paged: blocks in the pool
   int pps;             // pages per split
   float scale;
   float* part_m;       // (splits, Hq)
@@ -121,16 +125,28 @@ HKV_DEV void load_codes(const uint8_t* packed, int r, int q, uint32_t (&w)[NB]) 
   }
 }
 
-template <int KB, int VB>
-HKV_DEV void load_page(const DecodeArgs& A, int p, int g, int lane, PageLoad<KB, VB>& L) {
+// PG (paged pool): p is the logical page, b its pool block; the codes of row
+// l/4 are row l/4 of page-head block (b, g), and kr / vr hold the page-head's
+// outlier count and index (count, b * H + g) instead of row_ptr entries.
+template <int KB, int VB, bool PG>
+HKV_DEV void load_page(const DecodeArgs& A, int p, int b, int g, int lane, PageLoad<KB, VB>& L) {
   const int row = lane >> 2, q = lane & 3;
   const int t = p < 0 ? 0 : p * kPS + row;
-  const int tc = t < (int)A.T ? t : 0;
-  const int r = tc * A.H + g;
-  L.kr = *reinterpret_cast<const int2*>(A.k.row_ptr + (uint32_t)r);
-  L.vr = *reinterpret_cast<const int2*>(A.v.row_ptr + (uint32_t)r);
-  load_codes<KB>(A.k.packed, r, q, L.kc);
-  load_codes<VB>(A.v.packed, r, q, L.vc);
+  if constexpr (PG) {
+    const int ph = p < 0 ? 0 : b * A.H + g;
+    const int r = ph * kPS + row;
+    L.kr = make_int2(A.k.ocnt[ph], ph);
+    L.vr = make_int2(A.v.ocnt[ph], ph);
+    load_codes<KB>(A.k.packed, r, q, L.kc);
+    load_codes<VB>(A.v.packed, r, q, L.vc);
+  } else {
+    const int tc = t < (int)A.T ? t : 0;
+    const int r = tc * A.H + g;
+    L.kr = *reinterpret_cast<const int2*>(A.k.row_ptr + (uint32_t)r);
+    L.vr = *reinterpret_cast<const int2*>(A.v.row_ptr + (uint32_t)r);
+    load_codes<KB>(A.k.packed, r, q, L.kc);
+    load_codes<VB>(A.v.packed, r, q, L.vc);
+  }
   const int vrow = t < (int)A.v.rows ? t : (int)A.v.rows - 1;
   L.vtab = *reinterpret_cast<const uint2*>(A.v.tabs[(uint32_t)(g * (int)A.v.rows + vrow)].pf16 + 4 * q);
 }
@@ -140,10 +156,21 @@ HKV_DEV int csr_slot(int a, int sub, int s, int cap) {
   return i < cap ? i : cap - 1;
 }
 
-template <int KB, int VB>
+// PG: lane l holds entries l + 64 s (s < kSlots) of the page-head (index
+// clamped into [0, cap)) in kval[s] / vval[s].
+template <int KB, int VB, bool PG>
 HKV_DEV void load_outl(const DecodeArgs& A, const PageLoad<KB, VB>& L, int lane, PageOutl& O) {
-  const int sub = lane & 3;
   const int kcap = (int)A.k.cap, vcap = (int)A.v.cap;
+  if constexpr (PG) {
+#pragma unroll
+    for (int s = 0; s < kSlots; ++s) {
+      const int i = lane + 64 * s;
+      if (kcap > 0) O.kval[s] = A.k.oent[(int64_t)L.kr.y * kcap + (i < kcap ? i : kcap - 1)];
+      if (vcap > 0) O.vval[s] = A.v.oent[(int64_t)L.vr.y * vcap + (i < vcap ? i : vcap - 1)];
+    }
+    return;
+  }
+  const int sub = lane & 3;
 #pragma unroll
   for (int s = 0; s < kSlots; ++s) {
     if (kcap > 0) {
@@ -195,7 +222,17 @@ HKV_DEV void patch_rest(const Side& sd, int2 rb, int lane, uint16_t* tile) {
   }
 }
 
-template <int KB, int VB>
+// Page-head entries beyond the kSlots * 64 held in registers (PG).
+HKV_DEV void patch_rest_paged(const Side& sd, int2 cr, int lane, uint16_t* tile) {
+  const int n = cr.x < (int)sd.cap ? cr.x : (int)sd.cap;
+  for (int i = 64 * kSlots + lane; i < n; i += 64) {
+    const uint32_t e = sd.oent[(int64_t)cr.y * sd.cap + i];
+    const uint32_t slot = e >> 24, ch = (e >> 16) & 255u;
+    if (slot < (uint32_t)kPS && ch < (uint32_t)kHD) tile[slot * kTS + ch] = (uint16_t)e;
+  }
+}
+
+template <int KB, int VB, bool PG>
 __global__ void __launch_bounds__(kDT) __attribute__((amdgpu_waves_per_eu(3, 3)))
 decode_kernel(DecodeArgs A) {
   __shared__ __align__(16) uint16_t s_klut[kKLut];
@@ -216,10 +253,17 @@ decode_kernel(DecodeArgs A) {
   // the wave's page ids, one per lane (-1: none / out of range)
   const int64_t nw64 = j1 - j0 > wv ? (j1 - j0 - wv + kW - 1) / kW : 0;
   const int nslots = (int)nw64;  // <= kMaxPPS / kW = 64
-  int my_p = -1;
+  int my_p = -1, my_b = 0;  // logical page and (PG) its pool block
   if (lane < nslots) {
     const int64_t s = A.sel[(j0 + wv + (int64_t)kW * lane) * H + g];
     my_p = (s >= 0 && s < A.npages) ? (int)s : -1;
+    if constexpr (PG) {
+      if (my_p >= 0) {
+        const int64_t b = A.bt[my_p];
+        if (b >= 0 && b < A.nblocks) my_b = (int)b;
+        else my_p = -1;  // a page without a block is skipped
+      }
+    }
   }
   // Only valid ids are visited: they move, in order, to the wave's first nw
   // lanes (one ds_permute over a permutation of the 64 lanes: the invalid
@@ -230,8 +274,11 @@ decode_kernel(DecodeArgs A) {
   const int below = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(vm >> 32),
                                                    __builtin_amdgcn_mbcnt_lo((uint32_t)vm, 0u));
   const int nw = __builtin_popcountll(vm);
-  my_p = __builtin_amdgcn_ds_permute((my_p >= 0 ? below : nw + (lane - below)) << 2, my_p);
+  const int dst = (my_p >= 0 ? below : nw + (lane - below)) << 2;
+  my_p = __builtin_amdgcn_ds_permute(dst, my_p);
+  if constexpr (PG) my_b = __builtin_amdgcn_ds_permute(dst, my_b);
   auto page_at = [&](int i) -> int { return i < nw ? __builtin_amdgcn_readlane(my_p, i) : -1; };
+  auto block_at = [&](int i) -> int { return PG && i < nw ? __builtin_amdgcn_readlane(my_b, i) : 0; };
 
   // B operand of S^T = K Q^T: lane l holds q[qh = l%16][16i + 4(l/16) .. +3]
   const int qh = lane & 15, kg = lane >> 4;
@@ -268,7 +315,25 @@ decode_kernel(DecodeArgs A) {
     dequant_rows<VB>(L.vc, valid, lane, vt,
                      [&](int, uint32_t c) { return vl[row * 16 + (int)c]; });
     wave_sync();
-    if (valid) {
+    if constexpr (PG) {
+      // the page-head's entries (rows past the context are masked below)
+      const int kn = L.kr.x < (int)A.k.cap ? L.kr.x : (int)A.k.cap;
+      const int vn = L.vr.x < (int)A.v.cap ? L.vr.x : (int)A.v.cap;
+#pragma unroll
+      for (int s = 0; s < kSlots; ++s) {
+        const int i = lane + 64 * s;
+        if (i < kn) {
+          const uint32_t e = Ob.kval[s], sl = e >> 24, ch = (e >> 16) & 255u;
+          if (sl < (uint32_t)kPS && t0 + (int64_t)sl < A.T && ch < (uint32_t)kHD) kt[sl * kTS + ch] = (uint16_t)e;
+        }
+        if (i < vn) {
+          const uint32_t e = Ob.vval[s], sl = e >> 24, ch = (e >> 16) & 255u;
+          if (sl < (uint32_t)kPS && t0 + (int64_t)sl < A.T && ch < (uint32_t)kHD) vt[sl * kTS + ch] = (uint16_t)e;
+        }
+      }
+      if (kn > 64 * kSlots) patch_rest_paged(A.k, L.kr, lane, kt);
+      if (vn > 64 * kSlots) patch_rest_paged(A.v, L.vr, lane, vt);
+    } else if (valid) {
       const int sub = lane & 3;
       const int ka = L.kr.x < 0 ? 0 : L.kr.x, va = L.vr.x < 0 ? 0 : L.vr.x;
       const int ke = L.kr.y < (int)A.k.cap ? L.kr.y : (int)A.k.cap;
@@ -334,13 +399,13 @@ decode_kernel(DecodeArgs A) {
   // in-flight load keeps its registers (no copies of pending loads)
   PageLoad<KB, VB> L0, L1, L2;
   PageOutl O0, O1, O2;
-  load_page(A, page_at(0), g, lane, L0);
-  load_page(A, page_at(1), g, lane, L1);
-  load_outl(A, L0, lane, O0);
+  load_page<KB, VB, PG>(A, page_at(0), block_at(0), g, lane, L0);
+  load_page<KB, VB, PG>(A, page_at(1), block_at(1), g, lane, L1);
+  load_outl<KB, VB, PG>(A, L0, lane, O0);
   auto step = [&](int i, const PageLoad<KB, VB>& Lc, const PageOutl& Oc, const PageLoad<KB, VB>& Ln,
                   PageOutl& On, PageLoad<KB, VB>& Lw) {
-    load_page(A, page_at(i + 2), g, lane, Lw);
-    if (i + 1 < nw) load_outl(A, Ln, lane, On);
+    load_page<KB, VB, PG>(A, page_at(i + 2), block_at(i + 2), g, lane, Lw);
+    if (i + 1 < nw) load_outl<KB, VB, PG>(A, Ln, lane, On);
     const int p = page_at(i);
     if (p >= 0) compute(Lc, Oc, p);
   };
@@ -544,13 +609,77 @@ void launch_merge(const float* pm, const float* pl, const float* po, int64_t spl
 
 int64_t n_splits(int64_t nsel, int pps) { return nsel == 0 ? 1 : (nsel + pps - 1) / pps; }
 
-template <int KB, int VB>
+template <int KB, int VB, bool PG = false>
 void launch_decode(const DecodeArgs& a, int64_t splits, hipStream_t s) {
-  hipLaunchKernelGGL((decode_kernel<KB, VB>), dim3((unsigned)splits, (unsigned)a.H), dim3(kDT), 0,
-                     s, a);
+  hipLaunchKernelGGL((decode_kernel<KB, VB, PG>), dim3((unsigned)splits, (unsigned)a.H), dim3(kDT),
+                     0, s, a);
 }
 
 }  // namespace
+
+extern "C" int hkv_paged_decode_attn(const void* q, int Hq, int H, int D, int64_t T,
+                                     const int64_t* block_table, int64_t num_blocks,
+                                     const uint8_t* k_codes, const int32_t* k_ocnt,
+                                     const uint32_t* k_oent, int k_cap, int k_bits,
+                                     const void* k_tables, const uint8_t* v_codes,
+                                     const int32_t* v_ocnt, const uint32_t* v_oent, int v_cap,
+                                     int v_bits, const void* v_tables, int64_t v_rows,
+                                     const int64_t* sel, int64_t nsel, int pages_per_split,
+                                     float scale, void* out, int out_dtype, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
+  if (D != kHD) return HKV_ERR_SHAPE;
+  if (H < 1 || H > 65535 || Hq < H || Hq % H || Hq / H > 16 || T < 1 || nsel < 0 ||
+      num_blocks < 1)
+    return HKV_ERR_SHAPE;
+  if (pages_per_split < 1 || pages_per_split > kMaxPPS) return HKV_ERR_ARG;
+  if ((k_bits != 2 && k_bits != 4) || (v_bits != 2 && v_bits != 4)) return HKV_ERR_ARG;
+  if (out_dtype != HKV_DT_F16 && out_dtype != HKV_DT_F32) return HKV_ERR_DTYPE;
+  if (v_rows < 1 || k_cap < 0 || v_cap < 0) return HKV_ERR_ARG;
+  // page-head blocks and their rows are addressed in 32 bits
+  if (num_blocks * H * kPS * kHD >= ((int64_t)1 << 31) || (int64_t)H * v_rows >= ((int64_t)1 << 31) ||
+      T >= ((int64_t)1 << 31) - kPS)
+    return HKV_ERR_SHAPE;
+  if (!q || !block_table || !k_codes || !k_ocnt || !k_tables || !v_codes || !v_ocnt || !v_tables ||
+      !out)
+    return HKV_ERR_ARG;
+  if ((k_cap > 0 && !k_oent) || (v_cap > 0 && !v_oent)) return HKV_ERR_ARG;
+  if (nsel > 0 && !sel) return HKV_ERR_ARG;
+  if ((((uintptr_t)k_codes | (uintptr_t)v_codes) & 15u) || ((uintptr_t)q & 7u)) return HKV_ERR_ARG;
+  const size_t need = hkv_decode_workspace_bytes(nsel, Hq, pages_per_split);
+  if (!workspace || workspace_bytes < need) return HKV_ERR_WORKSPACE;
+  const int64_t splits = n_splits(nsel, pages_per_split);
+  if (splits > 0x7fffffff) return HKV_ERR_SHAPE;
+  hipStream_t s = (hipStream_t)stream;
+  float* pm = (float*)workspace;
+  float* pl = pm + splits * Hq;
+  float* po = pl + splits * Hq;
+  DecodeArgs a;
+  a.q = (const uint16_t*)q;
+  a.k = Side{k_codes, nullptr, nullptr, nullptr, k_cap, (const hkv_table_t*)k_tables, 0, k_ocnt, k_oent};
+  a.v = Side{v_codes, nullptr, nullptr, nullptr, v_cap, (const hkv_table_t*)v_tables, v_rows, v_ocnt,
+             v_oent};
+  a.H = H;
+  a.group = Hq / H;
+  a.T = T;
+  a.npages = (T + kPS - 1) / kPS;
+  a.sel = sel;
+  a.nsel = nsel;
+  a.bt = block_table;
+  a.nblocks = num_blocks;
+  a.pps = pages_per_split;
+  a.scale = scale;
+  a.part_m = pm;
+  a.part_l = pl;
+  a.part_o = po;
+  if (k_bits == 4 && v_bits == 4) launch_decode<4, 4, true>(a, splits, s);
+  else if (k_bits == 4) launch_decode<4, 2, true>(a, splits, s);
+  else if (v_bits == 4) launch_decode<2, 4, true>(a, splits, s);
+  else launch_decode<2, 2, true>(a, splits, s);
+  HKV_CHECK_LAUNCH();
+  launch_merge(pm, pl, po, splits, Hq, kHD, out, out_dtype, s);
+  HKV_CHECK_LAUNCH();
+  return HKV_OK;
+}
 
 extern "C" size_t hkv_decode_workspace_bytes(int64_t nsel, int Hq, int pages_per_split) {
   if (nsel < 0 || Hq < 1 || pages_per_split < 1) return 0;
@@ -592,9 +721,12 @@ extern "C" int hkv_decode_attn(const void* q, int Hq, int H, int D, int64_t T,
   float* po = pl + splits * Hq;
   DecodeArgs a;
   a.q = (const uint16_t*)q;
-  a.k = Side{(const uint8_t*)k_packed, k_row_ptr, k_col, k_val, k_cap, (const hkv_table_t*)k_tables, 0};
+  a.k = Side{(const uint8_t*)k_packed, k_row_ptr, k_col, k_val, k_cap, (const hkv_table_t*)k_tables, 0,
+             nullptr, nullptr};
   a.v = Side{(const uint8_t*)v_packed, v_row_ptr, v_col, v_val, v_cap, (const hkv_table_t*)v_tables,
-             v_rows};
+             v_rows, nullptr, nullptr};
+  a.bt = nullptr;
+  a.nblocks = 0;
   a.H = H;
   a.group = Hq / H;
   a.T = T;

@@ -345,7 +345,8 @@ HKV_DEV void bound_f16_rows(const void* q, int qdt, int group, const void* kmin_
                             int head_major, int64_t out_p, int64_t out_off, int bx, int gx,
                             uint2* __restrict__ mm = nullptr, int q_lds = 0,
                             const float* __restrict__ dq_lo = nullptr,
-                            const float* __restrict__ dq_step = nullptr) {
+                            const float* __restrict__ dq_step = nullptr,
+                            const int64_t* __restrict__ pids = nullptr, int64_t nstat = 0) {
   static_assert(!U8 || HFIX, "u8 statistics need a fixed head per lane");
   using ET = typename std::conditional<U8, uint8_t, uint16_t>::type;  // one statistic
   using LT = typename std::conditional<U8, uint2, uint4>::type;       // a lane's 8 channels
@@ -370,11 +371,23 @@ HKV_DEV void bound_f16_rows(const void* q, int qdt, int group, const void* kmin_
   // results are not written): a fixed number of loads per step lets the
   // compiler wait for exactly one step's loads while the next step's are in
   // flight.
+  // pids (HFIX only): page p's statistics are row pids[p] of (nstat, H, D)
+  // -- a block table mapping the logical pages scored here to the pool's
+  // blocks; an id outside [0, nstat) reads block 0.
   auto load = [&](int r0, LT (&a)[U], LT (&b)[U]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       int r = r0 + u * RB + rl;
       r = r < nr ? r : nr - 1;
+      if constexpr (HFIX) {
+        if (pids) {  // r0 is a multiple of H, and so is RB
+          int p = r0 / H + u * (RB / H) + rl / H;
+          p = p < (int)P ? p : (int)P - 1;
+          int64_t bk = pids[p];
+          bk = (bk < 0 || bk >= nstat) ? 0 : bk;
+          r = (int)bk * H + rl % H;
+        }
+      }
       a[u] = reinterpret_cast<const LT*>(kmin + (uint32_t)r * D)[c];
       b[u] = reinterpret_cast<const LT*>(kmax + (uint32_t)r * D)[c];
     }
@@ -486,7 +499,13 @@ HKV_DEV void bound_f16_rows(const void* q, int qdt, int group, const void* kmin_
         ns = row_reduce(ns, G);
       }
       if (r < nr && c == 0) {
-        const float v = __fadd_rn(__fadd_rn(ps, ns), 0.0f);
+        float v = __fadd_rn(__fadd_rn(ps, ns), 0.0f);
+        if constexpr (HFIX) {
+          if (pids) {  // a page id outside the statistics gets bound -inf (never preferred)
+            const int64_t bk = pids[p];
+            if (bk < 0 || bk >= nstat) v = -__builtin_inff();
+          }
+        }
         const int64_t o = head_major ? (int64_t)h * out_p + out_off + p : out_off * H + r;
         if (odt == HKV_DT_F16) ((uint16_t*)out)[o] = f2h(v);
         else ((float*)out)[o] = v;
@@ -534,9 +553,9 @@ template <int G, bool HFIX>
 __global__ void __launch_bounds__(256)
 bound_f16_kernel(const void* q, int qdt, int group, const uint16_t* __restrict__ kmin,
                  const uint16_t* __restrict__ kmax, int64_t P, int H, void* out, int odt,
-                 int head_major, uint2* mm, int q_lds) {
+                 int head_major, uint2* mm, int q_lds, const int64_t* pids, int64_t nstat) {
   bound_f16_rows<G, HFIX>(q, qdt, group, kmin, kmax, P, H, out, odt, head_major, P, 0, blockIdx.x,
-                          gridDim.x, mm, q_lds);
+                          gridDim.x, mm, q_lds, nullptr, nullptr, pids, nstat);
 }
 
 // Ragged batch: sequence s owns pages [off[s], off[s+1]) of the concatenated
@@ -1664,13 +1683,14 @@ bound_u8_kernel(const void* q, int qdt, int group, const uint8_t* __restrict__ k
 template <int G>
 void launch_bound_f16(bool hfix, unsigned grid, size_t lds, hipStream_t s, const void* q, int qdt,
                       int group, const uint16_t* kmin, const uint16_t* kmax, int64_t P, int H,
-                      void* out, int odt, int head_major, uint2* mm, int q_lds) {
+                      void* out, int odt, int head_major, uint2* mm, int q_lds,
+                      const int64_t* pids = nullptr, int64_t nstat = 0) {
   if (hfix)
     hipLaunchKernelGGL((bound_f16_kernel<G, true>), dim3(grid), dim3(256), lds, s, q, qdt, group,
-                       kmin, kmax, P, H, out, odt, head_major, mm, q_lds);
+                       kmin, kmax, P, H, out, odt, head_major, mm, q_lds, pids, nstat);
   else
     hipLaunchKernelGGL((bound_f16_kernel<G, false>), dim3(grid), dim3(256), lds, s, q, qdt, group,
-                       kmin, kmax, P, H, out, odt, head_major, nullptr, q_lds);
+                       kmin, kmax, P, H, out, odt, head_major, nullptr, q_lds, nullptr, (int64_t)0);
 }
 
 // Bytes of LDS for the raw query of the fp16 bound kernels (0: read it from
@@ -1698,13 +1718,15 @@ int page_bound(const void* q, int q_dtype, int Hq, const void* kmin, const void*
   size_t lds = sizeof(float) * 2 * H * D;
   if (lds > 64 * 1024) return HKV_ERR_SHAPE;
   const int G = D / 8;
-  // (the fp16 kernel indexes elements r * D in 32 bits)
-  if (!page_ids && k_dtype == HKV_DT_F16 && D % 8 == 0 && (G & (G - 1)) == 0 && G <= 64 &&
+  // (the fp16 kernel indexes elements r * D in 32 bits; with page ids, a lane's
+  // head must be fixed and the statistics' rows too must fit)
+  const bool hfix = G <= 64 && G > 0 && (64 / G) % H == 0;
+  if ((!page_ids || (hfix && page_ids && nstat * H * D < ((int64_t)1 << 31))) &&
+      k_dtype == HKV_DT_F16 && D % 8 == 0 && (G & (G - 1)) == 0 && G <= 64 &&
       rows * D < ((int64_t)1 << 32)) {
     const int64_t span = (int64_t)(256 / G) * kBoundUnrollF16;
     const unsigned grid =
         (unsigned)std::min<int64_t>((rows + span - 1) / span, (int64_t)num_cus() * 4);
-    const bool hfix = (64 / G) % H == 0;
     auto mn = (const uint16_t*)kmin;
     auto mx = (const uint16_t*)kmax;
     const int group = Hq / H;
@@ -1715,13 +1737,13 @@ int page_bound(const void* q, int q_dtype, int Hq, const void* kmin, const void*
     const int qlds = qraw != 0;
     lds += qraw;
     switch (G) {
-      case 1: launch_bound_f16<1>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major, mmp, qlds); break;
-      case 2: launch_bound_f16<2>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major, mmp, qlds); break;
-      case 4: launch_bound_f16<4>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major, mmp, qlds); break;
-      case 8: launch_bound_f16<8>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major, mmp, qlds); break;
-      case 16: launch_bound_f16<16>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major, mmp, qlds); break;
-      case 32: launch_bound_f16<32>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major, mmp, qlds); break;
-      default: launch_bound_f16<64>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major, mmp, qlds); break;
+      case 1: launch_bound_f16<1>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major, mmp, qlds, page_ids, nstat); break;
+      case 2: launch_bound_f16<2>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major, mmp, qlds, page_ids, nstat); break;
+      case 4: launch_bound_f16<4>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major, mmp, qlds, page_ids, nstat); break;
+      case 8: launch_bound_f16<8>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major, mmp, qlds, page_ids, nstat); break;
+      case 16: launch_bound_f16<16>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major, mmp, qlds, page_ids, nstat); break;
+      case 32: launch_bound_f16<32>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major, mmp, qlds, page_ids, nstat); break;
+      default: launch_bound_f16<64>(hfix, grid, lds, s, q, q_dtype, group, mn, mx, P, H, out, out_dtype, head_major, mmp, qlds, page_ids, nstat); break;
     }
     HKV_CHECK_LAUNCH();
     if (nmm && mmp) *nmm = (int)grid;
@@ -2106,6 +2128,32 @@ extern "C" int hkv_quest_select(const void* q, int q_dtype, int Hq, const void* 
   int nmm = 0;
   const int rc = page_bound(q, q_dtype, Hq, kmin, kmax, k_dtype, P, H, D, scores, HKV_DT_F32, 1, st,
                             nullptr, 0, mb ? (uint2*)(ws + lay.mm_off) : nullptr, &nmm);
+  if (rc != HKV_OK) return rc;
+  return select_after_bound(scores, P, H, k, sink_pages, s, keff, out, lay, mb, ws, nmm, st);
+}
+
+extern "C" int hkv_quest_select_paged(const void* q, int q_dtype, int Hq, const void* kmin,
+                                      const void* kmax, int k_dtype, int64_t num_blocks,
+                                      const int64_t* block_table, int64_t P, int H, int D,
+                                      int64_t k, int64_t sink_pages, float* scores, int64_t* out,
+                                      int64_t* n_out, void* workspace, size_t workspace_bytes,
+                                      void* stream) {
+  if (!fdt(q_dtype) && q_dtype != HKV_DT_BF16) return HKV_ERR_DTYPE;
+  if (!fdt(k_dtype)) return HKV_ERR_DTYPE;
+  if (P < 0 || num_blocks < 0 || H < 1 || D < 1 || D > 512 || Hq < H || Hq % H) return HKV_ERR_SHAPE;
+  const int64_t s = sink_pages < 0 ? 0 : (sink_pages > P ? P : sink_pages);
+  const int64_t keff = k < 0 ? 0 : (k > P - s ? P - s : k);
+  if (n_out) *n_out = s + keff;
+  if (P == 0) return HKV_OK;
+  if (!q || !kmin || !kmax || !scores || !out || !block_table) return HKV_ERR_ARG;
+  hipStream_t st = (hipStream_t)stream;
+  const SelectWs lay = select_ws_layout(P, H);
+  const bool mb = workspace && workspace_bytes >= lay.bytes && lay.NB > 0 && keff > 0 &&
+                  ((uintptr_t)workspace & 255u) == 0;
+  char* ws = (char*)workspace;
+  int nmm = 0;
+  const int rc = page_bound(q, q_dtype, Hq, kmin, kmax, k_dtype, P, H, D, scores, HKV_DT_F32, 1, st,
+                            block_table, num_blocks, mb ? (uint2*)(ws + lay.mm_off) : nullptr, &nmm);
   if (rc != HKV_OK) return rc;
   return select_after_bound(scores, P, H, k, sink_pages, s, keff, out, lay, mb, ws, nmm, st);
 }

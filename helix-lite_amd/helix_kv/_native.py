@@ -78,6 +78,12 @@ _SIGS = {
                          _p, _p, _i32, _p, _p, _p, _p], _i32),
     "hkv_paged_gather": ([_p, _p, _p, _i32, _i64, _i32, _i32, _i32, _i32, ctypes.POINTER(NuqScales),
                           _p, _p, _i64, _p, _p], _i32),
+    "hkv_quest_select_paged": ([_p, _i32, _i32, _p, _p, _i32, _i64, _p, _i64, _i32, _i32, _i64, _i64,
+                                _p, _p, ctypes.POINTER(_i64), _p, _sz, _p], _i32),
+    "hkv_paged_decode_attn": ([_p, _i32, _i32, _i32, _i64, _p, _i64,
+                               _p, _p, _p, _i32, _i32, _p,
+                               _p, _p, _p, _i32, _i32, _p, _i64,
+                               _p, _i64, _i32, ctypes.c_float, _p, _i32, _p, _sz, _p], _i32),
     "hkv_quest_page_stats": ([_p, _i32, _i64, _i32, _i32, _i32, _p, _p, _p], _i32),
     "hkv_quest_page_bound": ([_p, _i32, _i32, _p, _p, _i32, _i64, _i32, _i32, _p, _i32, _p], _i32),
     "hkv_quest_topk_workspace_bytes": ([_i64, _i32], _sz),

@@ -127,3 +127,147 @@ def paged_gather(side: PagedSide, t: NuqLayerTables, block_ids: torch.Tensor,
         HEAD_DIM, side.bits, t.struct(), N.ptr(ids), N.ptr(fp), NK, N.ptr(out), N.stream_of(out))
     N.check(st, "hkv_paged_gather", AssertionError)
     return out
+
+
+def _block_table(block_table: torch.Tensor, P: int) -> torch.Tensor:
+    bt = block_table.to(torch.int64).contiguous()
+    if bt.dim() != 1 or int(bt.numel()) < P:
+        raise ValueError(f"block_table must list at least {P} blocks, got {tuple(bt.shape)}")
+    return bt
+
+
+def paged_select(query: torch.Tensor, kside: PagedSide, block_table: torch.Tensor, seq_len: int,
+                 k: int, sink_pages: int, *, scores: torch.Tensor | None = None,
+                 out: torch.Tensor | None = None):
+    """Quest selection over the K page statistics of a paged sequence
+    (hkv_quest_select_paged): logical page p of the sequence's ceil(seq_len /
+    16) pages reads block block_table[p].  query (Hq, 128), Hq a multiple of
+    H (the group's bounds summed; pass one query per KV head for the plain
+    bound).  Returns (logical pages (sinks + k_eff, H) int64 ascending per
+    head, scores (H, P) fp32)."""
+    N.require_gpu(query, block_table)
+    if kside.kmin is None:
+        raise ValueError("the side holds no page statistics (K written with stats)")
+    P = -(-int(seq_len) // PAGE)
+    H = kside.heads
+    Hq = int(query.shape[0])
+    if query.dim() != 2 or int(query.shape[1]) != HEAD_DIM or Hq % H:
+        raise ValueError(f"query {tuple(query.shape)} incompatible with {H} KV heads x {HEAD_DIM}")
+    bt = _block_table(block_table, P)
+    q = query.contiguous()
+    s = max(0, min(int(sink_pages), P))
+    keff = max(0, min(int(k), P - s))
+    if out is None:
+        out = torch.empty((s + keff, H), dtype=torch.int64, device=q.device)
+    if scores is None:
+        scores = torch.empty((H, max(P, 1)), dtype=torch.float32, device=q.device)
+    n_out = N._i64(0)
+    ws = N.workspace("quest_select", int(N.lib().hkv_quest_select_workspace_bytes(P, H)), q.device)
+    st = N.lib().hkv_quest_select_paged(
+        N.ptr(q), N.dtype_code(q), Hq, N.ptr(kside.kmin), N.ptr(kside.kmax), N.DT_F16,
+        kside.num_blocks, N.ptr(bt), P, H, HEAD_DIM, int(k), int(sink_pages), N.ptr(scores),
+        N.ptr(out), n_out, N.ptr(ws), ws.numel(), N.stream_of(q))
+    N.check(st, "hkv_quest_select_paged", ValueError)
+    return out, scores
+
+
+def paged_decode_attention(query: torch.Tensor, kside: PagedSide, kt: NuqLayerTables,
+                           vside: PagedSide, vt: NuqLayerTables, block_table: torch.Tensor,
+                           seq_len: int, sel: torch.Tensor, *, scale: float | None = None,
+                           pages_per_split: int | None = None, out: torch.Tensor | None = None,
+                           out_dtype: torch.dtype = torch.float16) -> torch.Tensor:
+    """softmax(q.K^T * scale).V per query head over its KV head's selected
+    logical pages of a paged sequence (hkv_paged_decode_attn).  query
+    (Hq, 128) fp16; sel (n, H) logical pages; query head hq uses KV head
+    hq // (Hq // H).  Returns (Hq, 128)."""
+    from .ops import decode_pages_per_split
+
+    N.require_gpu(query, sel, block_table)
+    H = kside.heads
+    Hq = int(query.shape[0])
+    if query.dim() != 2 or int(query.shape[1]) != HEAD_DIM or Hq % H:
+        raise ValueError(f"query {tuple(query.shape)} incompatible with {H} KV heads x {HEAD_DIM}")
+    if query.dtype != torch.float16:
+        raise AssertionError("query must be fp16")
+    if kt.per_token or not vt.per_token:
+        raise AssertionError("K scales are per-channel, V scales per-token")
+    if vside.heads != H or vside.num_blocks != kside.num_blocks:
+        raise AssertionError("K and V sides must have the same blocks and heads")
+    if sel.dim() != 2 or int(sel.shape[1]) != H:
+        raise ValueError(f"sel should be (n, {H}), got {tuple(sel.shape)}")
+    T = int(seq_len)
+    if T < 1:
+        raise ValueError("the sequence must hold at least one token")
+    bt = _block_table(block_table, -(-T // PAGE))
+    s = sel.to(torch.int64).contiguous()
+    nsel = int(s.shape[0])
+    pps = int(pages_per_split) if pages_per_split else decode_pages_per_split(nsel, H)
+    q = query.contiguous()
+    if out is None:
+        out = torch.empty((Hq, HEAD_DIM), dtype=out_dtype, device=q.device)
+    if tuple(out.shape) != (Hq, HEAD_DIM) or out.dtype not in (torch.float16, torch.float32):
+        raise AssertionError("out must be (Hq, 128) fp16 or fp32")
+    nb = int(N.lib().hkv_decode_workspace_bytes(nsel, Hq, pps))
+    ws = N.workspace("decode", nb, q.device)
+    sc = float(scale) if scale is not None else HEAD_DIM ** -0.5
+    st = N.lib().hkv_paged_decode_attn(
+        N.ptr(q), Hq, H, HEAD_DIM, T, N.ptr(bt), kside.num_blocks,
+        N.ptr(kside.codes), N.ptr(kside.ocnt), N.ptr(kside.oent), kside.cap, kside.bits,
+        N.ptr(kt.ensure_tables()),
+        N.ptr(vside.codes), N.ptr(vside.ocnt), N.ptr(vside.oent), vside.cap, vside.bits,
+        N.ptr(vt.ensure_tables()), vt.rows,
+        N.ptr(s), nsel, pps, sc, N.ptr(out), N.dtype_code(out), N.ptr(ws), ws.numel(),
+        N.stream_of(q))
+    N.check(st, "hkv_paged_decode_attn", AssertionError)
+    return out
+
+
+def union_pages(sel: torch.Tensor, P: int) -> torch.Tensor:
+    """The union over KV heads of a selection (n, H), as a (P, H) list of the
+    union's pages ascending followed by -1 (every size known on the host: no
+    read-back).  src/kvquant/quest_selector.py:80."""
+    H = int(sel.shape[1])
+    flags = torch.zeros(P, dtype=torch.bool, device=sel.device)
+    flags.index_fill_(0, sel.reshape(-1), True)
+    pages = torch.arange(P, dtype=torch.int64, device=sel.device)
+    dest = torch.where(flags, torch.cumsum(flags, 0) - 1, torch.full_like(pages, P))
+    union = torch.full((P + 1,), -1, dtype=torch.int64, device=sel.device)
+    union.scatter_(0, dest, torch.where(flags, pages, torch.full_like(pages, -1)))
+    return union[:P].view(P, 1).expand(P, H).contiguous()
+
+
+def paged_decode_step(query: torch.Tensor, kside: PagedSide, kt: NuqLayerTables, vside: PagedSide,
+                      vt: NuqLayerTables, block_table: torch.Tensor, seq_len: int, top_k: int,
+                      sink_pages: int = 4, *, gqa: str = "mean", select: str = "union",
+                      scale: float | None = None, out: torch.Tensor | None = None,
+                      out_dtype: torch.dtype = torch.float16,
+                      pages_per_split: int | None = None) -> torch.Tensor:
+    """One decode step of one paged sequence, with no host reads (graph
+    capturable): Quest selection from the pool's K page statistics through
+    the block table, then the fused dequant + attention over the selected
+    logical pages.  The compact backend's forward (src/kvquant/
+    compact_backend.py:194-299) without its host synchronisations, with the
+    sinks the first logical pages and positions from the block table (not
+    block id * block size, src/kvquant/quest_selector.py:85-89):
+      gqa="mean": the group's queries averaged per KV head, in fp16
+      (compact_backend.py:225-231); "sum": the group's bounds summed.
+      select="union": every head attends to the union of the heads' pages
+      (quest_selector.py:80); "per_head": each KV head to its own."""
+    H = kside.heads
+    Hq = int(query.shape[0])
+    if query.dim() != 2 or Hq % H or int(query.shape[1]) != HEAD_DIM:
+        raise ValueError(f"query {tuple(query.shape)} incompatible with {H} KV heads x {HEAD_DIM}")
+    if gqa == "mean":
+        qs = query.reshape(H, Hq // H, HEAD_DIM).mean(dim=1).to(torch.float16)
+    elif gqa == "sum":
+        qs = query
+    else:
+        raise ValueError(f"gqa must be 'mean' or 'sum', got {gqa!r}")
+    P = -(-int(seq_len) // PAGE)
+    sel, _ = paged_select(qs, kside, block_table, seq_len, top_k, sink_pages)
+    if select == "union":
+        sel = union_pages(sel, P)
+    elif select != "per_head":
+        raise ValueError(f"select must be 'union' or 'per_head', got {select!r}")
+    return paged_decode_attention(query, kside, kt, vside, vt, block_table, seq_len, sel, scale=scale,
+                                  pages_per_split=pages_per_split, out=out, out_dtype=out_dtype)

@@ -248,6 +248,41 @@ int hkv_paged_gather(const uint8_t *codes, const int32_t *ocnt, const uint32_t *
                      const int64_t *first_pos, int64_t NK, void *staging, void *stream);
 
 /*
+ * Quest selection over a paged pool's K statistics: as hkv_quest_select, with
+ * logical page p's statistics at block block_table[p] of kmin / kmax
+ * (num_blocks, H, D); a block id outside [0, num_blocks) gets bound -inf.
+ * The selection (sinks + k_eff, H) holds logical pages, the sinks being the
+ * first logical pages: the block positions follow from the block table
+ * rather than from the block ids (src/kvquant/quest_selector.py:38-90 takes
+ * the first used block ids as sinks and id * block_size as positions,
+ * :85-89).  Same workspace as hkv_quest_select.
+ */
+int hkv_quest_select_paged(const void *q, int q_dtype, int Hq, const void *kmin, const void *kmax,
+                           int k_dtype, int64_t num_blocks, const int64_t *block_table, int64_t P,
+                           int H, int D, int64_t k, int64_t sink_pages, float *scores, int64_t *out,
+                           int64_t *n_out, void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * Fused dequant + sparse decode attention over a paged pool (batch 1, head
+ * dim 128): hkv_decode_attn with logical page p of the sequence (tokens
+ * [16p, 16p+16), tokens >= T masked) read from block block_table[p] of the
+ * paged K / V (hkv_paged_write's layout, the entries of each page-head patched
+ * over its codes); sel (nsel, H) holds logical pages, ids outside
+ * [0, ceil(T/16)) or whose block is outside the pool are skipped; V rows
+ * min(16p + slot, v_rows - 1).  The counterpart of the compact backend's
+ * forward over its block table (src/kvquant/compact_backend.py:194-299).
+ * Workspace: hkv_decode_workspace_bytes(nsel, Hq, pages_per_split).
+ */
+int hkv_paged_decode_attn(const void *q, int Hq, int H, int D, int64_t T, const int64_t *block_table,
+                          int64_t num_blocks, const uint8_t *k_codes, const int32_t *k_ocnt,
+                          const uint32_t *k_oent, int k_cap, int k_bits, const void *k_tables,
+                          const uint8_t *v_codes, const int32_t *v_ocnt, const uint32_t *v_oent,
+                          int v_cap, int v_bits, const void *v_tables, int64_t v_rows,
+                          const int64_t *sel, int64_t nsel, int pages_per_split, float scale,
+                          void *out, int out_dtype, void *workspace, size_t workspace_bytes,
+                          void *stream);
+
+/*
  * Quest page statistics: K_pages (P,S,H,D) -> kmin, kmax (P,H,D), same dtype
  * (f16 or f32).  -0 orders below +0; a NaN in a page-channel gives NaN.
  * src/quest/reference.py:38-56.

@@ -1,0 +1,182 @@
+"""GPU parity of Quest selection and fused decode attention over the paged
+compact pool (a block table scattering a sequence's pages over the pool):
+the selection bit-exact against the oracle's bound + top-K over the logical
+pages' statistics, the attention against the oracle's float64
+selected_attention (h // group head map) over pages the oracle gathers from
+the pool bytes.  Tolerance: per query head, relative L2 error and max-abs
+error over max |ref| both <= 1e-3."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+RNG = np.random.default_rng(2602)
+H, D, PS, TOL = 4, 128, 16, 1e-3
+
+
+def _t(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _scales(n, L, thr=1.2):
+    poles = np.sort(RNG.standard_normal((H, n, L)), axis=-1).astype(np.float16)
+    up = np.full((H, n), thr, np.float16)
+    return poles, up, (-up).astype(np.float16)
+
+
+def _sequence(dev, T, Lk, Lv, NB, rows=2048, cap=256):
+    """A T-token sequence written into a pool of NB blocks through a random
+    block table: returns the device sides and tables, the block table, and
+    the oracle's pools."""
+    from helix_kv.ops import NuqLayerTables
+    from helix_kv.paged import PagedSide, paged_write
+
+    P = -(-T // PS)
+    bt = RNG.permutation(NB)[:P].astype(np.int64)
+    slots = bt[np.arange(T) // PS] * PS + np.arange(T) % PS
+    k = (RNG.standard_t(3, (T, H, D)) * 0.7).astype(np.float16)
+    v = (RNG.standard_t(3, (T, H, D)) * 0.7).astype(np.float16)
+    ks, vs = _scales(D, Lk), _scales(rows, Lv)
+    kt = NuqLayerTables(*(_t(a, dev) for a in ks), per_token=False)
+    vt = NuqLayerTables(*(_t(a, dev) for a in vs), per_token=True)
+    kb, vb = (2 if Lk <= 4 else 4), (2 if Lv <= 4 else 4)
+    kside = PagedSide.empty(NB, H, kb, cap, dev, stats=True)
+    vside = PagedSide.empty(NB, H, vb, cap, dev)
+    pos = np.arange(T)
+    paged_write(kside, _t(k, dev), kt, _t(slots, dev))
+    paged_write(vside, _t(v, dev), vt, _t(slots, dev), _t(pos, dev))
+    kp = O.paged_empty(NB, H, D, kb, cap, stats=True)
+    vp = O.paged_empty(NB, H, D, vb, cap, stats=False)
+    O.paged_write(kp, k, slots, [a.astype(np.float32) for a in ks], False)
+    O.paged_write(vp, v, slots, [a.astype(np.float32) for a in vs], True, positions=pos)
+    first = np.arange(P) * PS
+    kpages = O.h2f(O.paged_gather(kp, bt, first, ks[0].astype(np.float32), False))
+    vpages = O.h2f(O.paged_gather(vp, bt, first, vs[0].astype(np.float32), True))
+    return dict(kside=kside, vside=vside, kt=kt, vt=vt, bt=bt, btd=_t(bt, dev), kp=kp, T=T, P=P,
+                kpages=kpages, vpages=vpages)
+
+
+def _stats(S):
+    """The logical pages' K statistics from the oracle pool, as float32."""
+    return O.h2f(S["kp"]["kmin"][S["bt"]]), O.h2f(S["kp"]["kmax"][S["bt"]])
+
+
+def _check(got, want):
+    got = got.float().cpu().numpy().astype(np.float64)
+    for h in range(want.shape[0]):
+        ref = want[h]
+        err = got[h] - ref
+        assert np.linalg.norm(err) <= TOL * np.linalg.norm(ref), h
+        assert np.abs(err).max() <= TOL * np.abs(ref).max(), h
+
+
+@pytest.mark.parametrize("T,group,k,s", [(3000, 7, 40, 4), (16 * 2600, 7, 650, 4), (100, 1, 3, 2)])
+def test_paged_select_vs_oracle(dev, T, group, k, s):
+    from helix_kv.paged import paged_select
+
+    S = _sequence(dev, T, 16, 4, NB=-(-T // PS) + 37)
+    mn, mx = _stats(S)
+    q = RNG.standard_normal((H * group, D)).astype(np.float16)
+    sel, scores = paged_select(_t(q, dev), S["kside"], S["btd"], T, k, s)
+    want = O.page_bound_group(q, mn, mx, group)
+    assert np.array_equal(scores.cpu().numpy(), want.T)
+    assert np.array_equal(sel.cpu().numpy(), O.topk_sinks(want, k, s))
+
+
+def test_paged_select_invalid_block_is_never_chosen(dev):
+    from helix_kv.paged import paged_select
+
+    S = _sequence(dev, 1600, 16, 4, NB=120)
+    bt = S["bt"].copy()
+    bt[[7, 50]] = [-1, 10**6]
+    q = RNG.standard_normal((H, D)).astype(np.float16)
+    sel, scores = paged_select(_t(q, dev), S["kside"], _t(bt, dev), S["T"], 30, 4)
+    sc = scores.cpu().numpy()
+    assert np.isneginf(sc[:, [7, 50]]).all()
+    assert not np.isin(sel.cpu().numpy(), [7, 50]).any()
+
+
+@pytest.mark.parametrize("T,group,Lk,Lv,frac,pps", [
+    (3000, 7, 16, 4, 0.3, 8),      # partial last page, nuq4 K / nuq2 V
+    (4096, 7, 4, 16, 0.25, 88),    # nuq2 K / nuq4 V, one split per head
+    (257, 1, 16, 16, 1.0, 1),      # group 1, every page
+    (2000, 16, 4, 4, 0.5, 12),     # group 16
+])
+def test_paged_decode_vs_oracle(dev, T, group, Lk, Lv, frac, pps):
+    from helix_kv.paged import paged_decode_attention
+
+    S = _sequence(dev, T, Lk, Lv, NB=-(-T // PS) + 11)
+    P = S["P"]
+    n = P if frac >= 1 else max(min(P, 4) + 1, int(frac * P))
+    cols = [np.sort(np.concatenate([np.arange(min(4, P)),
+                                    RNG.permutation(np.arange(min(4, P), P))[: n - min(4, P)]]))
+            for _ in range(H)]
+    sel = np.stack(cols, 1).astype(np.int64)
+    bad = np.concatenate([sel, [[-1] * H, [P] * H]]).astype(np.int64)   # skipped ids
+    q = RNG.standard_normal((H * group, D)).astype(np.float16)
+    want = O.selected_attention(q.astype(np.float64), S["kpages"], S["vpages"], sel,
+                                lambda h: h // group, num_tokens=T)
+    got = paged_decode_attention(_t(q, dev), S["kside"], S["kt"], S["vside"], S["vt"], S["btd"], T,
+                                 _t(bad, dev), pages_per_split=pps, out_dtype=torch.float32)
+    _check(got, want)
+
+
+@pytest.mark.parametrize("gqa,select", [("mean", "union"), ("sum", "per_head")])
+def test_paged_decode_step_vs_oracle(dev, gqa, select):
+    from helix_kv.paged import paged_decode_step
+
+    T, group, top_k, sinks = 5000, 7, 60, 4
+    S = _sequence(dev, T, 16, 4, NB=400)
+    P = S["P"]
+    mn, mx = _stats(S)
+    q = RNG.standard_normal((H * group, D)).astype(np.float16)
+    qd = _t(q, dev)
+    if gqa == "mean":
+        qs = qd.reshape(H, group, D).mean(dim=1).to(torch.float16).cpu().numpy()  # the reference's op
+        bound = O.page_bound(qs, mn, mx)
+    else:
+        bound = O.page_bound_group(q, mn, mx, group)
+    sel = O.topk_sinks(bound, top_k, sinks)
+    if select == "union":
+        ids = np.unique(sel.reshape(-1))
+        assert sinks + top_k < ids.size < P
+        sel = np.repeat(ids[:, None], H, axis=1)
+    want = O.selected_attention(q.astype(np.float64), S["kpages"], S["vpages"], sel,
+                                lambda h: h // group, num_tokens=T)
+    got = paged_decode_step(qd, S["kside"], S["kt"], S["vside"], S["vt"], S["btd"], T, top_k, sinks,
+                            gqa=gqa, select=select, out_dtype=torch.float32)
+    _check(got, want)
+
+
+def test_paged_decode_step_graph_replay(dev):
+    """The paged step reads nothing back, so it records into a HIP graph:
+    three replays, with eager work between them, equal the eager result."""
+    from helix_kv.paged import paged_decode_step
+
+    T, group = 3300, 7
+    S = _sequence(dev, T, 4, 16, NB=300)
+    q = _t(RNG.standard_normal((H * group, D)).astype(np.float16), dev)
+    args = (q, S["kside"], S["kt"], S["vside"], S["vt"], S["btd"], T, 50, 4)
+    eager = paged_decode_step(*args).clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        paged_decode_step(*args)
+    torch.cuda.current_stream().wait_stream(side)
+    out = torch.empty_like(eager)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        paged_decode_step(*args, out=out)
+    for _ in range(3):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+        other = paged_decode_step(*args, select="per_head")
+        torch.cuda.synchronize()
+        assert not torch.equal(other, eager)
