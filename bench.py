@@ -823,6 +823,142 @@ def bench_ragged(args, dev):
                 rag_sel_bytes=sel_bytes, rag_gather_bytes=gather_bytes)
 
 
+PAGED_CAP = 256  # outlier entries per page-head (12.5% of its 2048 elements)
+
+
+def paged_write_bytes(T: int, bits: int, nnz: int, stats: bool) -> int:
+    """Algorithmic bytes of one paged write of a (T, 4, 128) tensor: fp16 in,
+    the slot mapping, packed codes, one count per page-head, 4 B per outlier
+    entry, and (K) two fp16 statistics per (page, head, channel)."""
+    n = T * H * D
+    pages = T // 16
+    b = n * 2 + T * 8 + n * bits // 8 + pages * H * 4 + 4 * nnz
+    if stats:
+        b += 2 * pages * H * D * 2
+    return b
+
+
+def bench_paged(args, dev):
+    """The same 28-layer mixed nuq2/nuq4 prefill (K and V (131072, 4, 128)
+    fp16 per layer), written into the paged compact pool: each sequence page
+    at a random block of the pool, per page-head outlier lists, K page
+    statistics of the dequantised values computed on write.  A step is 56
+    write launches; the unpack step gathers every block of every layer back
+    to fp16 in token order (56 gather launches)."""
+    from helix_kv.ops import NuqLayerTables
+    from helix_kv.paged import PagedSide, paged_gather, paged_write
+
+    NB = T_TOK // 16
+    gperm = torch.Generator(device="cpu").manual_seed(7)
+    bt = torch.randperm(NB, generator=gperm).to(dev)
+    slots = (bt[torch.arange(T_TOK, device=dev) // 16] * 16 + torch.arange(T_TOK, device=dev) % 16)
+    first = torch.arange(NB, device=dev) * 16
+    layers = []
+    for l in range(LAYERS):
+        K, V, ks, vs, L = make_layer(l, dev)
+        kt = NuqLayerTables(*ks, per_token=False)
+        vt = NuqLayerTables(*vs, per_token=True)
+        kt.ensure_tables()
+        vt.ensure_tables()
+        bits = 2 if L <= 4 else 4
+        kside = PagedSide.empty(NB, H, bits, PAGED_CAP, dev, stats=True)
+        vside = PagedSide.empty(NB, H, bits, PAGED_CAP, dev)
+        layers.append(dict(K=K, V=V, kt=kt, vt=vt, bits=bits, ks=kside, vs=vside,
+                           sbytes=scale_bytes(ks) + scale_bytes(vs)))
+    torch.cuda.synchronize()
+    log(f"[bench] paged: {LAYERS} layers ready, {torch.cuda.memory_allocated() / 2**30:.1f} GiB allocated")
+    writes = []
+    for Ld in layers:
+        writes.append(lambda Ld=Ld: paged_write(Ld["ks"], Ld["K"], Ld["kt"], slots))
+        writes.append(lambda Ld=Ld: paged_write(Ld["vs"], Ld["V"], Ld["vt"], slots))
+
+    def step():
+        for f in writes:
+            f()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    algo, nnz = 0, 0
+    for Ld in layers:
+        for side, stats in ((Ld["ks"], True), (Ld["vs"], False)):
+            if int(side.status.item()):
+                raise RuntimeError("a page-head's outliers exceeded the capacity")
+            n = int(side.ocnt.sum().item())
+            nnz += n
+            algo += paged_write_bytes(T_TOK, Ld["bits"], n, stats)
+        algo += Ld["sbytes"]
+    ms = time_events(step, args.steps)
+    durs = per_launch_ms(writes)
+    log(f"[bench] paged prefill write: {ms:.3f} ms/step, {algo / (ms * 1e-3) / 1e9:.0f} GB/s; "
+        f"kernels {sum(durs):.3f} ms; nnz {nnz} ({nnz / (2 * LAYERS * T_TOK * H * D):.2%})")
+    # the round trip of the last and first layers against torch, as for the compact pack
+    outs = [torch.empty((NB, 16, H, D), dtype=torch.float16, device=dev) for _ in range(2)]
+    gathers = []
+    for Ld in layers:
+        gathers.append(lambda Ld=Ld: paged_gather(Ld["ks"], Ld["kt"], bt, out=outs[0]))
+        gathers.append(lambda Ld=Ld: paged_gather(Ld["vs"], Ld["vt"], bt, first, out=outs[1]))
+
+    def ustep():
+        for f in gathers:
+            f()
+
+    for _ in range(max(1, args.warmup)):
+        ustep()
+    ums = time_events(ustep, args.steps)
+    for li in (len(layers) - 1, 0):
+        Ld = layers[li]
+        for name, x, side, lt in (("K", Ld["K"], Ld["ks"], Ld["kt"]), ("V", Ld["V"], Ld["vs"], Ld["vt"])):
+            back = paged_gather(side, lt, bt, first).view(T_TOK, H, D)
+            bad = paged_round_trip_mismatches(x, side, lt, back, bt)
+            if bad:
+                raise RuntimeError(f"paged round trip of layer {li} {name}: {bad} elements differ")
+    log(f"[bench] paged unpack (gather of every block): {ums:.3f} ms/step, "
+        f"{algo / (ums * 1e-3) / 1e9:.0f} GB/s")
+    del layers, outs
+    torch.cuda.empty_cache()
+    return dict(paged_ms=ms, paged_bytes=algo, paged_nnz=nnz, paged_kernel_ms=sum(durs),
+                paged_launches=len(writes), paged_unpack_ms=ums)
+
+
+def paged_round_trip_mismatches(x, side, lt, back, bt, chunk: int = 8192) -> int:
+    """As round_trip_mismatches, for a paged side read back in token order:
+    the page-heads' outlier entries mark exactly the elements outside the
+    thresholds, which come back bit-exact; the rest come back as their fp16
+    nearest pole."""
+    T, Hh, Dd = x.shape
+    cnt = side.ocnt.long()
+    ent = side.all_entries()[bt]
+    n = ent.shape[-1]
+    # every entry of every page-head, in sequence order (blocks through bt)
+    live = (torch.arange(n, device=x.device)[None, None, :] < cnt[bt][..., None])
+    e = ent[live].long() & 0xFFFFFFFF
+    pg = torch.arange(bt.numel(), device=x.device)[:, None, None].expand(-1, Hh, n)[live]
+    hh = torch.arange(Hh, device=x.device)[None, :, None].expand(bt.numel(), -1, n)[live]
+    tok = pg * 16 + (e >> 24)
+    mask = torch.zeros((T, Hh, Dd), dtype=torch.bool, device=x.device)
+    mask[tok, hh, (e >> 16) & 255] = True
+    bad = 0
+    for t0 in range(0, T, chunk):
+        t1 = min(T, t0 + chunk)
+        xs = x[t0:t1].float()
+        if lt.per_token:
+            r = torch.arange(t0, t1, device=x.device).clamp(max=lt.rows - 1)
+            up = lt.upper[:, r].float().T[..., None]
+            lo = lt.lower[:, r].float().T[..., None]
+            p = lt.poles[:, r].float().permute(1, 0, 2)[:, :, None, :]
+        else:
+            up, lo = lt.upper.float(), lt.lower.float()
+            p = lt.poles.float()[None]
+        m = mask[t0:t1]
+        bad += int(((xs < lo) | (xs > up) != m).sum().item())
+        code = (xs[..., None] - p).abs().argmin(-1, keepdim=True)
+        pole = torch.gather(p.expand(t1 - t0, Hh, Dd, p.shape[-1]), -1, code)[..., 0].half()
+        want = torch.where(m, x[t0:t1], pole)
+        bad += int((back[t0:t1].view(torch.int16) != want.view(torch.int16)).sum().item())
+    return bad
+
+
 def profile_pass(what: str, dev) -> None:
     """A short, fixed sequence of launches for counter collection: three
     copies of 1 GiB (the calibration kernel: 1 GiB read + 1 GiB written each),
@@ -875,8 +1011,8 @@ def main() -> None:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--only", choices=["all", "nuq", "quest", "ragged", "decode", "calibration",
-                                       "roundtrip"], default="all")
+    ap.add_argument("--only", choices=["all", "nuq", "paged", "quest", "ragged", "decode",
+                                       "calibration", "roundtrip"], default="all")
     ap.add_argument("--profile", choices=["pack", "unpack", "quest", "ragged", "decode"], default=None,
                     help="run a short fixed launch sequence for rocprofv3 counters and exit")
     ap.add_argument("--cpu-layers", default="0,16",
@@ -897,6 +1033,8 @@ def main() -> None:
     res = {}
     if args.only in ("all", "nuq"):
         res.update(bench_nuq(args, dev))
+    if args.only in ("all", "paged"):
+        res.update(bench_paged(args, dev))
     if args.only in ("all", "quest"):
         res.update(bench_quest(args, dev))
     if args.only in ("all", "ragged"):

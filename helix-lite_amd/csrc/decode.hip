@@ -68,6 +68,8 @@ struct Side {  // one of K / V in the compact format, or in the paged pool
   int64_t rows;            // per-token scale rows (V); unused for K
   const int32_t* ocnt;     // paged: (NB, H) outliers per page-head
   const uint32_t* oent;    // paged: (NB, H, cap) value | channel << 16 | slot << 24
+  const int32_t* ovf;      // paged: (NB, H) overflow chunk (entries cap..), -1 none; or NULL
+  const uint32_t* ovf_ent; // paged: (chunks, 16 * 128 - cap)
 };
 
 struct DecodeArgs {
@@ -222,13 +224,19 @@ HKV_DEV void patch_rest(const Side& sd, int2 rb, int lane, uint16_t* tile) {
   }
 }
 
-// Page-head entries beyond the kSlots * 64 held in registers (PG).
-HKV_DEV void patch_rest_paged(const Side& sd, int2 cr, int lane, uint16_t* tile) {
-  const int n = cr.x < (int)sd.cap ? cr.x : (int)sd.cap;
-  for (int i = 64 * kSlots + lane; i < n; i += 64) {
-    const uint32_t e = sd.oent[(int64_t)cr.y * sd.cap + i];
+// Page-head entries past those held in registers (PG): the inline ones from
+// index 64 * kSlots, then those of the page-head's overflow chunk.
+HKV_DEV void patch_rest_paged(const Side& sd, int2 cr, int lane, uint16_t* tile, int64_t t0, int64_t T) {
+  const int cap = (int)sd.cap;
+  const int ov = (cr.x > cap && sd.ovf) ? sd.ovf[cr.y] : -1;
+  const int room = cap + (ov >= 0 ? kPS * kHD - cap : 0);
+  const int n = cr.x < room ? cr.x : room;
+  const int first = cap < 64 * kSlots ? cap : 64 * kSlots;
+  for (int i = first + lane; i < n; i += 64) {
+    const uint32_t e = i < cap ? sd.oent[(int64_t)cr.y * cap + i]
+                               : sd.ovf_ent[(int64_t)ov * (kPS * kHD - cap) + (i - cap)];
     const uint32_t slot = e >> 24, ch = (e >> 16) & 255u;
-    if (slot < (uint32_t)kPS && ch < (uint32_t)kHD) tile[slot * kTS + ch] = (uint16_t)e;
+    if (slot < (uint32_t)kPS && t0 + (int64_t)slot < T && ch < (uint32_t)kHD) tile[slot * kTS + ch] = (uint16_t)e;
   }
 }
 
@@ -331,8 +339,9 @@ decode_kernel(DecodeArgs A) {
           if (sl < (uint32_t)kPS && t0 + (int64_t)sl < A.T && ch < (uint32_t)kHD) vt[sl * kTS + ch] = (uint16_t)e;
         }
       }
-      if (kn > 64 * kSlots) patch_rest_paged(A.k, L.kr, lane, kt);
-      if (vn > 64 * kSlots) patch_rest_paged(A.v, L.vr, lane, vt);
+      // past the registers: more inline entries, or an overflow chunk
+      if (L.kr.x > (kn < 64 * kSlots ? kn : 64 * kSlots)) patch_rest_paged(A.k, L.kr, lane, kt, t0, A.T);
+      if (L.vr.x > (vn < 64 * kSlots ? vn : 64 * kSlots)) patch_rest_paged(A.v, L.vr, lane, vt, t0, A.T);
     } else if (valid) {
       const int sub = lane & 3;
       const int ka = L.kr.x < 0 ? 0 : L.kr.x, va = L.vr.x < 0 ? 0 : L.vr.x;
@@ -617,34 +626,34 @@ void launch_decode(const DecodeArgs& a, int64_t splits, hipStream_t s) {
 
 }  // namespace
 
-extern "C" int hkv_paged_decode_attn(const void* q, int Hq, int H, int D, int64_t T,
-                                     const int64_t* block_table, int64_t num_blocks,
-                                     const uint8_t* k_codes, const int32_t* k_ocnt,
-                                     const uint32_t* k_oent, int k_cap, int k_bits,
-                                     const void* k_tables, const uint8_t* v_codes,
-                                     const int32_t* v_ocnt, const uint32_t* v_oent, int v_cap,
-                                     int v_bits, const void* v_tables, int64_t v_rows,
+extern "C" int hkv_paged_decode_attn(const void* q, int Hq, int64_t T, const int64_t* block_table,
+                                     const hkv_paged_side* ks, const void* k_tables,
+                                     const hkv_paged_side* vs, const void* v_tables, int64_t v_rows,
                                      const int64_t* sel, int64_t nsel, int pages_per_split,
                                      float scale, void* out, int out_dtype, void* workspace,
                                      size_t workspace_bytes, void* stream) {
-  if (D != kHD) return HKV_ERR_SHAPE;
-  if (H < 1 || H > 65535 || Hq < H || Hq % H || Hq / H > 16 || T < 1 || nsel < 0 ||
-      num_blocks < 1)
+  if (!ks || !vs) return HKV_ERR_ARG;
+  const int H = ks->heads;
+  const int64_t num_blocks = ks->num_blocks;
+  const int k_bits = ks->bits, v_bits = vs->bits, k_cap = ks->cap, v_cap = vs->cap;
+  if (vs->heads != H || vs->num_blocks != num_blocks) return HKV_ERR_SHAPE;
+  if (H < 1 || H > 16 || Hq < H || Hq % H || Hq / H > 16 || T < 1 || nsel < 0 || num_blocks < 1)
     return HKV_ERR_SHAPE;
   if (pages_per_split < 1 || pages_per_split > kMaxPPS) return HKV_ERR_ARG;
   if ((k_bits != 2 && k_bits != 4) || (v_bits != 2 && v_bits != 4)) return HKV_ERR_ARG;
   if (out_dtype != HKV_DT_F16 && out_dtype != HKV_DT_F32) return HKV_ERR_DTYPE;
-  if (v_rows < 1 || k_cap < 0 || v_cap < 0) return HKV_ERR_ARG;
+  if (v_rows < 1 || k_cap < 0 || v_cap < 0 || k_cap > kPS * kHD || v_cap > kPS * kHD) return HKV_ERR_ARG;
   // page-head blocks and their rows are addressed in 32 bits
   if (num_blocks * H * kPS * kHD >= ((int64_t)1 << 31) || (int64_t)H * v_rows >= ((int64_t)1 << 31) ||
       T >= ((int64_t)1 << 31) - kPS)
     return HKV_ERR_SHAPE;
-  if (!q || !block_table || !k_codes || !k_ocnt || !k_tables || !v_codes || !v_ocnt || !v_tables ||
-      !out)
+  if (!q || !block_table || !ks->codes || !ks->ocnt || !k_tables || !vs->codes || !vs->ocnt ||
+      !v_tables || !out)
     return HKV_ERR_ARG;
-  if ((k_cap > 0 && !k_oent) || (v_cap > 0 && !v_oent)) return HKV_ERR_ARG;
+  if ((k_cap > 0 && !ks->oent) || (v_cap > 0 && !vs->oent)) return HKV_ERR_ARG;
+  if ((ks->ovf && !ks->ovf_ent) || (vs->ovf && !vs->ovf_ent)) return HKV_ERR_ARG;
   if (nsel > 0 && !sel) return HKV_ERR_ARG;
-  if ((((uintptr_t)k_codes | (uintptr_t)v_codes) & 15u) || ((uintptr_t)q & 7u)) return HKV_ERR_ARG;
+  if ((((uintptr_t)ks->codes | (uintptr_t)vs->codes) & 15u) || ((uintptr_t)q & 7u)) return HKV_ERR_ARG;
   const size_t need = hkv_decode_workspace_bytes(nsel, Hq, pages_per_split);
   if (!workspace || workspace_bytes < need) return HKV_ERR_WORKSPACE;
   const int64_t splits = n_splits(nsel, pages_per_split);
@@ -655,9 +664,10 @@ extern "C" int hkv_paged_decode_attn(const void* q, int Hq, int H, int D, int64_
   float* po = pl + splits * Hq;
   DecodeArgs a;
   a.q = (const uint16_t*)q;
-  a.k = Side{k_codes, nullptr, nullptr, nullptr, k_cap, (const hkv_table_t*)k_tables, 0, k_ocnt, k_oent};
-  a.v = Side{v_codes, nullptr, nullptr, nullptr, v_cap, (const hkv_table_t*)v_tables, v_rows, v_ocnt,
-             v_oent};
+  a.k = Side{ks->codes, nullptr, nullptr, nullptr, k_cap, (const hkv_table_t*)k_tables, 0, ks->ocnt,
+             ks->oent, ks->ovf, ks->ovf_ent};
+  a.v = Side{vs->codes, nullptr, nullptr, nullptr, v_cap, (const hkv_table_t*)v_tables, v_rows,
+             vs->ocnt, vs->oent, vs->ovf, vs->ovf_ent};
   a.H = H;
   a.group = Hq / H;
   a.T = T;

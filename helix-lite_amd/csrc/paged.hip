@@ -68,7 +68,17 @@ struct PagedWriteArgs {
   uint16_t* kmax;
   int32_t* status;
   int64_t nunits;      // ceil(T / 16) * H
+  int32_t* ovf;        // (NB, H) overflow chunk of the page-head, -1: none
+  uint32_t* ovf_ent;   // (n_chunks, 16 * 128 - cap)
+  int32_t* ovf_next;   // chunks handed out so far
+  int n_chunks;
 };
+
+// Entry i of a page-head's list: the first cap inline, the rest in its
+// overflow chunk (ovf >= 0).
+HKV_DEV uint32_t* entry_ptr(uint32_t* oent, uint32_t* ovf_ent, int64_t ph, int cap, int ovf, int i) {
+  return i < cap ? oent + ph * cap + i : ovf_ent + (int64_t)ovf * (kPBS * kPD - cap) + (i - cap);
+}
 
 // Codes and outlier flags of one lane's 8 channels (quant8_packed with the
 // per-pair outlier masks and codes kept for the statistics): returns true on
@@ -226,14 +236,17 @@ paged_write_kernel(PagedWriteArgs A) {
       const int w0 = (int)(s0 - pg * kPBS);
       const int64_t ph = pg * H + h;
       // entries kept from earlier writes: those of slots < w0
+      // the page-head's overflow chunk (kept across writes once allocated)
+      int ovf = A.ovf ? A.ovf[ph] : -1;
+      const int room = A.cap + (ovf >= 0 ? kPBS * kPD - A.cap : 0);  // entries it can store
       int base = 0;
       if (w0 > 0) {
         const int cnt = A.ocnt[ph];
-        const int m = cnt < A.cap ? cnt : A.cap;
+        const int m = cnt < room ? cnt : room;
         int below = 0;
         for (int i0 = 0; i0 < m; i0 += 64) {
           const int i = i0 + lane;
-          const bool lt = i < m && (int)(A.oent[ph * A.cap + i] >> 24) < w0;
+          const bool lt = i < m && (int)(*entry_ptr(A.oent, A.ovf_ent, ph, A.cap, ovf, i) >> 24) < w0;
           below += __builtin_popcountll(__builtin_amdgcn_ballot_w64(lt));
         }
         base = below == m ? cnt : below;
@@ -339,6 +352,18 @@ paged_write_kernel(PagedWriteArgs A) {
           uint32_t tot;
           const uint32_t pos = run + wave_excl_count_fused(__builtin_popcount(m), &tot);
           run += tot;
+          if (ovf == -1 && A.ovf && base + (int)run > A.cap && A.cap < kPBS * kPD) {
+            // uniform: the first entry past the inline capacity takes a chunk
+            int got = -2;  // -2: the arena is used up (entries past cap are dropped)
+            if (lane == 0) {
+              const int i = atomicAdd(A.ovf_next, 1);
+              if (i < A.n_chunks) {
+                got = i;
+                A.ovf[ph] = i;
+              }
+            }
+            ovf = __builtin_amdgcn_readfirstlane(got);
+          }
           const uint16_t* xl = reinterpret_cast<const uint16_t*>(s_x + wv * 64 + lane);
           const uint32_t tag = ((uint32_t)(w0 + rr) << 24) | ((uint32_t)(8 * cg) << 16);
           uint32_t idx = (uint32_t)base + pos;
@@ -346,7 +371,9 @@ paged_write_kernel(PagedWriteArgs A) {
             const int e = __builtin_ctz(m);
             m &= m - 1u;
             const uint16_t v = xl[e];
-            if (idx < (uint32_t)A.cap) epage[idx] = (uint32_t)v | (tag + ((uint32_t)e << 16));
+            const uint32_t ent = (uint32_t)v | (tag + ((uint32_t)e << 16));
+            if (idx < (uint32_t)A.cap) epage[idx] = ent;
+            else if (ovf >= 0) A.ovf_ent[(int64_t)ovf * (kPBS * kPD - A.cap) + (idx - A.cap)] = ent;
             ++idx;
             if constexpr (STATS) {
               if (fold) {
@@ -360,7 +387,7 @@ paged_write_kernel(PagedWriteArgs A) {
       if (lane == 0) {
         const int total = base + (int)run;
         A.ocnt[ph] = total;
-        if (total > A.cap) atomicOr(A.status, 1);
+        if (total > A.cap + (ovf >= 0 ? kPBS * kPD - A.cap : 0)) atomicOr(A.status, 1);
       }
       if constexpr (STATS) {
         // over the four row groups of the wave (lanes cg, cg+16, cg+32, cg+48)
@@ -469,6 +496,8 @@ struct PagedGatherArgs {
   const int64_t* first_pos;
   int64_t NK;
   uint16_t* out;   // (NK, 16, H, 128)
+  const int32_t* ovf;       // (NB, H) overflow chunk per page-head, or NULL
+  const uint32_t* ovf_ent;  // (chunks, 16 * 128 - cap)
 };
 
 template <bool PT, int BITS>
@@ -518,7 +547,9 @@ paged_gather_kernel(PagedGatherArgs A) {
       else cw[p] = *reinterpret_cast<const uint16_t*>(cp + (p * 4 + rw) * RB + 2 * cg);
     }
     const int cnt = A.ocnt[ph];
-    const int m = cnt < A.cap ? cnt : A.cap;
+    const int ov = (cnt > A.cap && A.ovf) ? A.ovf[ph] : -1;
+    const int room = A.cap + (ov >= 0 ? kPBS * kPD - A.cap : 0);
+    const int m = cnt < room ? cnt : room;
     if constexpr (PT) {
       const int64_t fp = A.first_pos[k];
       for (int i = lane; i < kPBS * 16; i += 64) {
@@ -549,7 +580,8 @@ paged_gather_kernel(PagedGatherArgs A) {
     }
     pwave_sync();
     for (int i = lane; i < m; i += 64) {
-      const uint32_t e = A.oent[ph * A.cap + i];
+      const uint32_t e = *entry_ptr(const_cast<uint32_t*>(A.oent), const_cast<uint32_t*>(A.ovf_ent),
+                                    ph, A.cap, ov, i);
       const uint32_t slot = e >> 24, ch = (e >> 16) & 255u;
       if (slot < (uint32_t)kPBS && ch < (uint32_t)kPD) tile[slot * kPD + ch] = (uint16_t)e;
     }
@@ -566,41 +598,57 @@ paged_gather_kernel(PagedGatherArgs A) {
 
 }  // namespace
 
-extern "C" int hkv_paged_write(const void* values, int64_t T, int H, int D, int bits,
-                               const hkv_nuq_scales* scales, const int64_t* slot_mapping,
-                               int64_t num_blocks, int block_size, uint8_t* codes, int32_t* ocnt,
-                               uint32_t* oent, int cap, uint16_t* kmin, uint16_t* kmax,
-                               int32_t* status, void* stream) {
+// Shape / pointer checks of a paged side (the host half of every paged call).
+static int check_side(const hkv_paged_side* d, bool stats_allowed) {
+  if (!d) return HKV_ERR_ARG;
+  if (d->bits != 2 && d->bits != 4) return HKV_ERR_ARG;
+  if (d->num_blocks < 0 || d->heads < 1 || d->heads > 16 || d->cap < 0 || d->cap > kPBS * kPD ||
+      d->n_chunks < 0)
+    return HKV_ERR_SHAPE;
+  if (d->num_blocks * d->heads * kPBS * kPD >= ((int64_t)1 << 31)) return HKV_ERR_SHAPE;
+  if (!d->codes || !d->ocnt || !d->status || (d->cap > 0 && !d->oent)) return HKV_ERR_ARG;
+  if (d->ovf && (!d->ovf_next || (d->n_chunks > 0 && !d->ovf_ent))) return HKV_ERR_ARG;
+  if ((d->kmin == nullptr) != (d->kmax == nullptr)) return HKV_ERR_ARG;
+  if (d->kmin && !stats_allowed) return HKV_ERR_ARG;
+  if ((((uintptr_t)d->codes) | ((uintptr_t)d->kmin) | ((uintptr_t)d->kmax)) & 15u) return HKV_ERR_ARG;
+  return HKV_OK;
+}
+
+extern "C" int hkv_paged_write(const void* values, int64_t T, const hkv_nuq_scales* scales,
+                               const int64_t* slot_mapping, const hkv_paged_side* side,
+                               void* stream) {
   if (!scales || !scales->tables) return HKV_ERR_ARG;
-  if (D != kPD || block_size != kPBS) return HKV_ERR_SHAPE;
-  if (bits != 2 && bits != 4) return HKV_ERR_ARG;
+  int rc = check_side(side, !scales->per_token);
+  if (rc != HKV_OK) return rc;
+  const int bits = side->bits, H = side->heads;
   if (scales->levels < 1 || scales->levels > (1 << bits)) return HKV_ERR_ARG;
-  if (T < 0 || H < 1 || H > 65535 || num_blocks < 0 || cap < 0 || cap > (1 << 24)) return HKV_ERR_SHAPE;
+  if (T < 0) return HKV_ERR_SHAPE;
   if (scales->per_token && scales->rows < 1) return HKV_ERR_SHAPE;
-  if (!scales->per_token && (kmin == nullptr) != (kmax == nullptr)) return HKV_ERR_ARG;
-  if (scales->per_token && (kmin || kmax)) return HKV_ERR_ARG;
-  if (T == 0 || num_blocks == 0) return HKV_OK;
-  if (!values || !slot_mapping || !codes || !ocnt || !status || (cap > 0 && !oent)) return HKV_ERR_ARG;
-  if ((((uintptr_t)values | (uintptr_t)codes) & 15u) || (((uintptr_t)kmin | (uintptr_t)kmax) & 15u))
-    return HKV_ERR_ARG;
+  if (T == 0 || side->num_blocks == 0) return HKV_OK;
+  if (!values || !slot_mapping) return HKV_ERR_ARG;
+  if ((uintptr_t)values & 15u) return HKV_ERR_ARG;
   PagedWriteArgs a;
   a.x = (const uint16_t*)values;
   a.T = T;
   a.H = H;
   a.sc = *scales;
   a.slots = slot_mapping;
-  a.nslots = num_blocks * kPBS;
-  a.codes = codes;
-  a.ocnt = ocnt;
-  a.oent = oent;
-  a.cap = cap;
-  a.kmin = kmin;
-  a.kmax = kmax;
-  a.status = status;
+  a.nslots = side->num_blocks * kPBS;
+  a.codes = side->codes;
+  a.ocnt = side->ocnt;
+  a.oent = side->oent;
+  a.cap = side->cap;
+  a.kmin = side->kmin;
+  a.kmax = side->kmax;
+  a.status = side->status;
   a.nunits = ((T + kPBS - 1) / kPBS) * H;
+  a.ovf = side->ovf;
+  a.ovf_ent = side->ovf_ent;
+  a.ovf_next = side->ovf_next;
+  a.n_chunks = side->ovf ? side->n_chunks : 0;
   hipStream_t s = (hipStream_t)stream;
   const int nb = nb_for_levels_host(scales->levels);
-  const bool stats = kmin != nullptr;
+  const bool stats = side->kmin != nullptr;
   if (scales->per_token) {
     if (bits == 4) launch_write_nb<true, 4, false>(nb, a, s);
     else launch_write_nb<true, 2, false>(nb < 2 ? nb : 2, a, s);
@@ -615,32 +663,32 @@ extern "C" int hkv_paged_write(const void* values, int64_t T, int H, int D, int 
   return HKV_OK;
 }
 
-extern "C" int hkv_paged_gather(const uint8_t* codes, const int32_t* ocnt, const uint32_t* oent,
-                                int cap, int64_t num_blocks, int block_size, int H, int D, int bits,
-                                const hkv_nuq_scales* scales, const int64_t* block_ids,
-                                const int64_t* first_pos, int64_t NK, void* staging, void* stream) {
+extern "C" int hkv_paged_gather(const hkv_paged_side* side, const hkv_nuq_scales* scales,
+                                const int64_t* block_ids, const int64_t* first_pos, int64_t NK,
+                                void* staging, void* stream) {
   if (!scales || !scales->tables) return HKV_ERR_ARG;
-  if (D != kPD || block_size != kPBS) return HKV_ERR_SHAPE;
-  if (bits != 2 && bits != 4) return HKV_ERR_ARG;
-  if (H < 1 || H > 16 || NK < 0 || num_blocks < 0 || cap < 0) return HKV_ERR_SHAPE;
+  int rc = check_side(side, true);
+  if (rc != HKV_OK) return rc;
+  const int bits = side->bits, H = side->heads;
+  if (NK < 0) return HKV_ERR_SHAPE;
   if (scales->per_token && scales->rows < 1) return HKV_ERR_SHAPE;
   if (NK == 0) return HKV_OK;
-  if (!codes || !ocnt || !block_ids || !staging || (cap > 0 && !oent) ||
-      (scales->per_token && !first_pos))
-    return HKV_ERR_ARG;
-  if (((uintptr_t)codes | (uintptr_t)staging) & 15u) return HKV_ERR_ARG;
+  if (!block_ids || !staging || (scales->per_token && !first_pos)) return HKV_ERR_ARG;
+  if ((uintptr_t)staging & 15u) return HKV_ERR_ARG;
   PagedGatherArgs a;
-  a.codes = codes;
-  a.ocnt = ocnt;
-  a.oent = oent;
-  a.cap = cap;
-  a.NB = num_blocks;
+  a.codes = side->codes;
+  a.ocnt = side->ocnt;
+  a.oent = side->oent;
+  a.cap = side->cap;
+  a.NB = side->num_blocks;
   a.H = H;
   a.sc = *scales;
   a.ids = block_ids;
   a.first_pos = first_pos;
   a.NK = NK;
   a.out = (uint16_t*)staging;
+  a.ovf = side->ovf;
+  a.ovf_ent = side->ovf_ent;
   hipStream_t s = (hipStream_t)stream;
   const int NL = 1 << bits;
   const size_t lds = (size_t)kPW * kPBS * kPD * 2 +

@@ -2132,15 +2132,18 @@ extern "C" int hkv_quest_select(const void* q, int q_dtype, int Hq, const void* 
   return select_after_bound(scores, P, H, k, sink_pages, s, keff, out, lay, mb, ws, nmm, st);
 }
 
-extern "C" int hkv_quest_select_paged(const void* q, int q_dtype, int Hq, const void* kmin,
-                                      const void* kmax, int k_dtype, int64_t num_blocks,
-                                      const int64_t* block_table, int64_t P, int H, int D,
-                                      int64_t k, int64_t sink_pages, float* scores, int64_t* out,
+extern "C" int hkv_quest_select_paged(const void* q, int q_dtype, int Hq, const hkv_paged_side* kside,
+                                      const int64_t* block_table, int64_t P, int64_t k,
+                                      int64_t sink_pages, float* scores, int64_t* out,
                                       int64_t* n_out, void* workspace, size_t workspace_bytes,
                                       void* stream) {
+  if (!kside) return HKV_ERR_ARG;
+  const int H = kside->heads, D = 128, k_dtype = HKV_DT_F16;
+  const int64_t num_blocks = kside->num_blocks;
+  const void* kmin = kside->kmin;
+  const void* kmax = kside->kmax;
   if (!fdt(q_dtype) && q_dtype != HKV_DT_BF16) return HKV_ERR_DTYPE;
-  if (!fdt(k_dtype)) return HKV_ERR_DTYPE;
-  if (P < 0 || num_blocks < 0 || H < 1 || D < 1 || D > 512 || Hq < H || Hq % H) return HKV_ERR_SHAPE;
+  if (P < 0 || num_blocks < 0 || H < 1 || H > 16 || Hq < H || Hq % H) return HKV_ERR_SHAPE;
   const int64_t s = sink_pages < 0 ? 0 : (sink_pages > P ? P : sink_pages);
   const int64_t keff = k < 0 ? 0 : (k > P - s ? P - s : k);
   if (n_out) *n_out = s + keff;

@@ -46,6 +46,17 @@ class NuqScales(ctypes.Structure):
     ]
 
 
+class PagedSideDesc(ctypes.Structure):
+    """Mirror of ``hkv_paged_side``."""
+
+    _fields_ = [
+        ("codes", _p), ("ocnt", _p), ("oent", _p), ("ovf", _p), ("ovf_ent", _p), ("ovf_next", _p),
+        ("kmin", _p), ("kmax", _p), ("status", _p), ("num_blocks", _i64),
+        ("heads", ctypes.c_int32), ("bits", ctypes.c_int32), ("cap", ctypes.c_int32),
+        ("n_chunks", ctypes.c_int32),
+    ]
+
+
 class TensorDesc(ctypes.Structure):
     """Mirror of ``hkv_tensor_desc``."""
 
@@ -74,16 +85,15 @@ _SIGS = {
                         _p, _p, _p], _i32),
     "hkv_pool_gather": ([_p, _p, _p, _i64, _i32, _i32, _i32, ctypes.POINTER(NuqScales), _p, _p, _i64,
                          _p, _p], _i32),
-    "hkv_paged_write": ([_p, _i64, _i32, _i32, _i32, ctypes.POINTER(NuqScales), _p, _i64, _i32, _p,
-                         _p, _p, _i32, _p, _p, _p, _p], _i32),
-    "hkv_paged_gather": ([_p, _p, _p, _i32, _i64, _i32, _i32, _i32, _i32, ctypes.POINTER(NuqScales),
-                          _p, _p, _i64, _p, _p], _i32),
-    "hkv_quest_select_paged": ([_p, _i32, _i32, _p, _p, _i32, _i64, _p, _i64, _i32, _i32, _i64, _i64,
+    "hkv_paged_write": ([_p, _i64, ctypes.POINTER(NuqScales), _p, ctypes.POINTER(PagedSideDesc), _p],
+                        _i32),
+    "hkv_paged_gather": ([ctypes.POINTER(PagedSideDesc), ctypes.POINTER(NuqScales), _p, _p, _i64, _p,
+                          _p], _i32),
+    "hkv_quest_select_paged": ([_p, _i32, _i32, ctypes.POINTER(PagedSideDesc), _p, _i64, _i64, _i64,
                                 _p, _p, ctypes.POINTER(_i64), _p, _sz, _p], _i32),
-    "hkv_paged_decode_attn": ([_p, _i32, _i32, _i32, _i64, _p, _i64,
-                               _p, _p, _p, _i32, _i32, _p,
-                               _p, _p, _p, _i32, _i32, _p, _i64,
-                               _p, _i64, _i32, ctypes.c_float, _p, _i32, _p, _sz, _p], _i32),
+    "hkv_paged_decode_attn": ([_p, _i32, _i64, _p, ctypes.POINTER(PagedSideDesc), _p,
+                               ctypes.POINTER(PagedSideDesc), _p, _i64, _p, _i64, _i32,
+                               ctypes.c_float, _p, _i32, _p, _sz, _p], _i32),
     "hkv_quest_page_stats": ([_p, _i32, _i64, _i32, _i32, _i32, _p, _p, _p], _i32),
     "hkv_quest_page_bound": ([_p, _i32, _i32, _p, _p, _i32, _i64, _i32, _i32, _p, _i32, _p], _i32),
     "hkv_quest_topk_workspace_bytes": ([_i64, _i32], _sz),

@@ -3,9 +3,13 @@
 One layer's K or V side of the pool (D = 128, 16 slots per block):
   codes (NB, H, 16, D*bits/8) u8 -- page-head blocks of bit-packed codes;
   ocnt (NB, H) int32, oent (NB, H, cap) int32 (u32 bit patterns: fp16 value |
-  channel << 16 | slot << 24) -- each page-head's outliers;
+  channel << 16 | slot << 24) -- each page-head's outliers, the first cap
+  inline;
+  ovf (NB, H) int32 -- the page-head's overflow chunk (-1: none) in ovf_ent
+  (n_chunks, 2048 - cap), handed out from ovf_next when a page-head's
+  outliers first pass cap;
   kmin / kmax (NB, H, D) fp16 -- K page statistics of the dequantised values;
-  status (1,) int32 -- bit 0 once a page-head's outliers exceeded cap.
+  status (1,) int32 -- bit 0 once outliers were dropped (no room left).
 Calls launch on torch's current stream and read nothing back.
 """
 from __future__ import annotations
@@ -19,6 +23,8 @@ from .ops import NuqLayerTables
 
 PAGE = 16
 HEAD_DIM = 128
+PAGE_ELEMS = PAGE * HEAD_DIM
+DEFAULT_CAP = PAGE_ELEMS // 8   # 256 inline entries: 12.5% of a page-head
 
 
 def bits_for_levels(levels: int) -> int:
@@ -35,6 +41,9 @@ class PagedSide:
     ocnt: torch.Tensor
     oent: torch.Tensor
     bits: int
+    ovf: torch.Tensor | None = None
+    ovf_ent: torch.Tensor | None = None
+    ovf_next: torch.Tensor | None = None
     kmin: torch.Tensor | None = None
     kmax: torch.Tensor | None = None
     status: torch.Tensor | None = None
@@ -51,21 +60,68 @@ class PagedSide:
     def cap(self) -> int:
         return int(self.oent.shape[2])
 
+    @property
+    def n_chunks(self) -> int:
+        return 0 if self.ovf_ent is None else int(self.ovf_ent.shape[0])
+
     @staticmethod
-    def empty(num_blocks: int, H: int, bits: int, cap: int, device, stats: bool = False,
-              status: torch.Tensor | None = None) -> "PagedSide":
+    def empty(num_blocks: int, H: int, bits: int, cap: int = DEFAULT_CAP, device="cuda",
+              stats: bool = False, n_chunks: int | None = None) -> "PagedSide":
+        """A zeroed side.  n_chunks overflow chunks of 2048 - cap entries
+        (default: one per 8 page-heads; 0: no arena, outliers past cap are
+        dropped and flagged)."""
         dev = torch.device(device)
-        D = HEAD_DIM
+        if not 0 <= cap <= PAGE_ELEMS:
+            raise ValueError(f"cap must be in [0, {PAGE_ELEMS}]")
+        if n_chunks is None:
+            n_chunks = max(1, num_blocks * H // 8) if cap < PAGE_ELEMS else 0
         side = PagedSide(
-            codes=torch.zeros((num_blocks, H, PAGE, D * bits // 8), dtype=torch.uint8, device=dev),
+            codes=torch.zeros((num_blocks, H, PAGE, HEAD_DIM * bits // 8), dtype=torch.uint8, device=dev),
             ocnt=torch.zeros((num_blocks, H), dtype=torch.int32, device=dev),
-            oent=torch.zeros((num_blocks, H, max(cap, 0)), dtype=torch.int32, device=dev),
+            oent=torch.zeros((num_blocks, H, cap), dtype=torch.int32, device=dev),
             bits=bits,
-            status=status if status is not None else torch.zeros(1, dtype=torch.int32, device=dev))
+            status=torch.zeros(1, dtype=torch.int32, device=dev))
+        if n_chunks > 0:
+            side.ovf = torch.full((num_blocks, H), -1, dtype=torch.int32, device=dev)
+            side.ovf_ent = torch.zeros((n_chunks, PAGE_ELEMS - cap), dtype=torch.int32, device=dev)
+            side.ovf_next = torch.zeros(1, dtype=torch.int32, device=dev)
         if stats:
-            side.kmin = torch.full((num_blocks, H, D), float("inf"), dtype=torch.float16, device=dev)
-            side.kmax = torch.full((num_blocks, H, D), float("-inf"), dtype=torch.float16, device=dev)
+            side.kmin = torch.full((num_blocks, H, HEAD_DIM), float("inf"), dtype=torch.float16, device=dev)
+            side.kmax = torch.full((num_blocks, H, HEAD_DIM), float("-inf"), dtype=torch.float16, device=dev)
         return side
+
+    def desc(self) -> N.PagedSideDesc:
+        d = N.PagedSideDesc()
+        for name in ("codes", "ocnt", "oent", "ovf", "ovf_ent", "ovf_next", "kmin", "kmax", "status"):
+            t = getattr(self, name)
+            setattr(d, name, None if t is None else t.data_ptr())
+        d.num_blocks = self.num_blocks
+        d.heads = self.heads
+        d.bits = self.bits
+        d.cap = self.cap
+        d.n_chunks = self.n_chunks
+        return d
+
+    def all_entries(self) -> torch.Tensor:
+        """Every page-head's entry slots in order, (NB, H, 2048) int32 on the
+        device: the cap inline ones, then the overflow chunk's (zeros where a
+        page-head has none).  The first min(ocnt, stored) are live."""
+        full = torch.zeros((self.num_blocks, self.heads, PAGE_ELEMS), dtype=torch.int32,
+                           device=self.codes.device)
+        full[:, :, : self.cap] = self.oent
+        if self.ovf is not None:
+            m = self.ovf >= 0
+            full[:, :, self.cap:][m] = self.ovf_ent[self.ovf[m].long()]
+        return full
+
+    def entries(self, block: int, head: int) -> torch.Tensor:
+        """The page-head's stored outlier entries in order (host read)."""
+        n = int(self.ocnt[block, head])
+        inline = self.oent[block, head, : min(n, self.cap)]
+        if n <= self.cap or self.ovf is None or int(self.ovf[block, head]) < 0:
+            return inline
+        rest = self.ovf_ent[int(self.ovf[block, head]), : n - self.cap]
+        return torch.cat([inline, rest])
 
 
 def paged_write(side: PagedSide, values: torch.Tensor, t: NuqLayerTables, slot_mapping: torch.Tensor,
@@ -93,11 +149,8 @@ def paged_write(side: PagedSide, values: torch.Tensor, t: NuqLayerTables, slot_m
             raise AssertionError("positions must have one entry per token")
     if T == 0:
         return
-    s = t.struct(pos)
-    st = N.lib().hkv_paged_write(
-        N.ptr(values), T, H, HEAD_DIM, side.bits, s, N.ptr(slots), side.num_blocks, PAGE,
-        N.ptr(side.codes), N.ptr(side.ocnt), N.ptr(side.oent), side.cap, N.ptr(side.kmin),
-        N.ptr(side.kmax), N.ptr(side.status), N.stream_of(values))
+    st = N.lib().hkv_paged_write(N.ptr(values), T, t.struct(pos), N.ptr(slots), side.desc(),
+                                 N.stream_of(values))
     N.check(st, "hkv_paged_write", AssertionError)
 
 
@@ -122,9 +175,8 @@ def paged_gather(side: PagedSide, t: NuqLayerTables, block_ids: torch.Tensor,
             raise AssertionError("one first position per kept block")
     if NK == 0:
         return out
-    st = N.lib().hkv_paged_gather(
-        N.ptr(side.codes), N.ptr(side.ocnt), N.ptr(side.oent), side.cap, side.num_blocks, PAGE, H,
-        HEAD_DIM, side.bits, t.struct(), N.ptr(ids), N.ptr(fp), NK, N.ptr(out), N.stream_of(out))
+    st = N.lib().hkv_paged_gather(side.desc(), t.struct(), N.ptr(ids), N.ptr(fp), NK, N.ptr(out),
+                                  N.stream_of(out))
     N.check(st, "hkv_paged_gather", AssertionError)
     return out
 
@@ -164,9 +216,8 @@ def paged_select(query: torch.Tensor, kside: PagedSide, block_table: torch.Tenso
     n_out = N._i64(0)
     ws = N.workspace("quest_select", int(N.lib().hkv_quest_select_workspace_bytes(P, H)), q.device)
     st = N.lib().hkv_quest_select_paged(
-        N.ptr(q), N.dtype_code(q), Hq, N.ptr(kside.kmin), N.ptr(kside.kmax), N.DT_F16,
-        kside.num_blocks, N.ptr(bt), P, H, HEAD_DIM, int(k), int(sink_pages), N.ptr(scores),
-        N.ptr(out), n_out, N.ptr(ws), ws.numel(), N.stream_of(q))
+        N.ptr(q), N.dtype_code(q), Hq, kside.desc(), N.ptr(bt), P, int(k), int(sink_pages),
+        N.ptr(scores), N.ptr(out), n_out, N.ptr(ws), ws.numel(), N.stream_of(q))
     N.check(st, "hkv_quest_select_paged", ValueError)
     return out, scores
 
@@ -211,13 +262,9 @@ def paged_decode_attention(query: torch.Tensor, kside: PagedSide, kt: NuqLayerTa
     ws = N.workspace("decode", nb, q.device)
     sc = float(scale) if scale is not None else HEAD_DIM ** -0.5
     st = N.lib().hkv_paged_decode_attn(
-        N.ptr(q), Hq, H, HEAD_DIM, T, N.ptr(bt), kside.num_blocks,
-        N.ptr(kside.codes), N.ptr(kside.ocnt), N.ptr(kside.oent), kside.cap, kside.bits,
-        N.ptr(kt.ensure_tables()),
-        N.ptr(vside.codes), N.ptr(vside.ocnt), N.ptr(vside.oent), vside.cap, vside.bits,
-        N.ptr(vt.ensure_tables()), vt.rows,
-        N.ptr(s), nsel, pps, sc, N.ptr(out), N.dtype_code(out), N.ptr(ws), ws.numel(),
-        N.stream_of(q))
+        N.ptr(q), Hq, T, N.ptr(bt), kside.desc(), N.ptr(kt.ensure_tables()), vside.desc(),
+        N.ptr(vt.ensure_tables()), vt.rows, N.ptr(s), nsel, pps, sc, N.ptr(out), N.dtype_code(out),
+        N.ptr(ws), ws.numel(), N.stream_of(q))
     N.check(st, "hkv_paged_decode_attn", AssertionError)
     return out
 

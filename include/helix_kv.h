@@ -205,82 +205,98 @@ int hkv_pool_gather(const void *codes, const void *outlier_v, const void *outlie
                     const int64_t *first_pos, int64_t NK, void *staging, void *stream);
 
 /*
- * Paged compact pool, one layer and side (K or V), D = 128, block_size 16:
- *   codes (num_blocks, H, 16, D*bits/8) u8 -- page-head blocks, slot rows in
- *     order, codes little-endian within a byte (nuq4: byte j = c[2j] |
+ * Paged compact pool: one layer and side (K or V) of a paged KV cache, head
+ * dim 128, 16 slots per block, described by hkv_paged_side:
+ *   codes (num_blocks, heads, 16, 128*bits/8) u8 -- page-head blocks, slot
+ *     rows in order, codes little-endian within a byte (nuq4: byte j = c[2j] |
  *     c[2j+1] << 4; nuq2: c[4j] in the low bits);
- *   ocnt (num_blocks, H) int32 -- outliers recorded for the page-head;
- *   oent (num_blocks, H, cap) u32 -- the first min(ocnt, cap) of them,
- *     (slot, channel) ascending, as fp16 value | channel << 16 | slot << 24;
- *   kmin / kmax (num_blocks, H, D) fp16 -- K only: min / max over the written
- *     slots of the dequantised values (outlier value, else fp16 pole), a zero
- *     stored as +0;
- *   status (1) int32 -- bit 0 set once a page-head's outliers exceed cap.
+ *   ocnt (num_blocks, heads) int32 -- outliers of the page-head;
+ *   oent (num_blocks, heads, cap) u32 -- its first cap outliers, (slot,
+ *     channel) ascending, as fp16 value | channel << 16 | slot << 24;
+ *   ovf (num_blocks, heads) int32 -- the page-head's overflow chunk (-1: none),
+ *     holding its entries cap.. in ovf_ent (n_chunks, 2048 - cap) u32; chunks
+ *     are handed out from ovf_next on first need and stay with the page-head.
+ *     ovf NULL: no arena (entries past cap are dropped);
+ *   kmin / kmax (num_blocks, heads, 128) fp16 -- K only (else NULL): min / max
+ *     over the written slots of the dequantised values (outlier value, else
+ *     fp16 pole), a zero stored as +0;
+ *   status (1) int32 -- bit 0 set once outliers were dropped (no room left).
  * The reference's pool is byte-per-code with dense outliers
  * (src/kvquant/compact_pool.py:398-446); this is its planned bit-packed
  * layout with outliers kept per block (compact_pool.py:11-12,
  * src/kvquant/vllm_integration.md:51-55), page-head contiguous.
- *
- * hkv_paged_write replaces CompactKVPool.write_kv (compact_pool.py:447-489,
- * kernels :160-287): token t of values (T,H,128) fp16 goes to slot
- * slot_mapping[t] (block slot / 16, row slot % 16; slots < 0 or past the pool
- * are skipped).  A run -- consecutive tokens with consecutive slots in one
- * block -- starting at row w0 keeps the block's outliers of rows < w0 and
- * replaces the rest; kmin / kmax (K: both given, or both NULL for no
- * statistics; V: NULL) restart at w0 = 0 and otherwise fold in.  The tokens
- * of one call that fall in one block must form one run.  V: per-token scales
- * with scales->positions = absolute positions (row min(pos, rows - 1)).
- * values / codes / kmin / kmax 16-byte aligned.
- *
- * hkv_paged_gather replaces CompactKVPool.unpack_to_staging
- * (compact_pool.py:492-537, kernels :292-395): staging (NK, 16, H, 128) fp16
- * row k = block block_ids[k] dequantised (ids outside the pool give zeros);
- * V row p of kept block k uses scale row min(first_pos[k] + p, rows - 1).
- * H <= 16.
  */
-int hkv_paged_write(const void *values, int64_t T, int H, int D, int bits,
-                    const hkv_nuq_scales *scales, const int64_t *slot_mapping, int64_t num_blocks,
-                    int block_size, uint8_t *codes, int32_t *ocnt, uint32_t *oent, int cap,
-                    uint16_t *kmin, uint16_t *kmax, int32_t *status, void *stream);
-int hkv_paged_gather(const uint8_t *codes, const int32_t *ocnt, const uint32_t *oent, int cap,
-                     int64_t num_blocks, int block_size, int H, int D, int bits,
-                     const hkv_nuq_scales *scales, const int64_t *block_ids,
-                     const int64_t *first_pos, int64_t NK, void *staging, void *stream);
+typedef struct hkv_paged_side {
+  uint8_t *codes;
+  int32_t *ocnt;
+  uint32_t *oent;
+  int32_t *ovf;
+  uint32_t *ovf_ent;
+  int32_t *ovf_next;
+  uint16_t *kmin;
+  uint16_t *kmax;
+  int32_t *status;
+  int64_t num_blocks;
+  int32_t heads;    /* <= 16 */
+  int32_t bits;     /* 2 or 4 */
+  int32_t cap;      /* 0..2048 */
+  int32_t n_chunks;
+} hkv_paged_side;
 
 /*
- * Quest selection over a paged pool's K statistics: as hkv_quest_select, with
- * logical page p's statistics at block block_table[p] of kmin / kmax
- * (num_blocks, H, D); a block id outside [0, num_blocks) gets bound -inf.
- * The selection (sinks + k_eff, H) holds logical pages, the sinks being the
- * first logical pages: the block positions follow from the block table
- * rather than from the block ids (src/kvquant/quest_selector.py:38-90 takes
- * the first used block ids as sinks and id * block_size as positions,
- * :85-89).  Same workspace as hkv_quest_select.
+ * hkv_paged_write replaces CompactKVPool.write_kv (compact_pool.py:447-489,
+ * kernels :160-287): token t of values (T, heads, 128) fp16 goes to slot
+ * slot_mapping[t] (block slot / 16, row slot % 16; slots < 0 or past the pool
+ * are skipped).  A run -- consecutive tokens with consecutive slots in one
+ * block -- starting at row w0 keeps the page-head's outliers of rows < w0
+ * and replaces the rest; kmin / kmax restart at w0 = 0 and otherwise fold in.
+ * The tokens of one call that fall in one block must form one run.  V:
+ * per-token scales with scales->positions = absolute positions (row
+ * min(pos, rows - 1)).  values / codes / kmin / kmax 16-byte aligned.
+ *
+ * hkv_paged_gather replaces CompactKVPool.unpack_to_staging
+ * (compact_pool.py:492-537, kernels :292-395): staging (NK, 16, heads, 128)
+ * fp16 row k = block block_ids[k] dequantised (ids outside the pool give
+ * zeros); V row p of kept block k uses scale row min(first_pos[k] + p,
+ * rows - 1).
  */
-int hkv_quest_select_paged(const void *q, int q_dtype, int Hq, const void *kmin, const void *kmax,
-                           int k_dtype, int64_t num_blocks, const int64_t *block_table, int64_t P,
-                           int H, int D, int64_t k, int64_t sink_pages, float *scores, int64_t *out,
-                           int64_t *n_out, void *workspace, size_t workspace_bytes, void *stream);
+int hkv_paged_write(const void *values, int64_t T, const hkv_nuq_scales *scales,
+                    const int64_t *slot_mapping, const hkv_paged_side *side, void *stream);
+int hkv_paged_gather(const hkv_paged_side *side, const hkv_nuq_scales *scales,
+                     const int64_t *block_ids, const int64_t *first_pos, int64_t NK, void *staging,
+                     void *stream);
+
+/*
+ * Quest selection over a paged pool's K statistics (kside->kmin / kmax): as
+ * hkv_quest_select with the group-summed bound, logical page p's statistics
+ * at block block_table[p] (P logical pages); a block outside the pool gets
+ * bound -inf.  The selection (sinks + k_eff, heads) holds logical pages, the
+ * sinks being the first logical pages: positions follow from the block
+ * table, not from block ids (src/kvquant/quest_selector.py:38-90 takes the
+ * first used block ids as sinks and id * block_size as positions, :85-89).
+ * Same workspace as hkv_quest_select.
+ */
+int hkv_quest_select_paged(const void *q, int q_dtype, int Hq, const hkv_paged_side *kside,
+                           const int64_t *block_table, int64_t P, int64_t k, int64_t sink_pages,
+                           float *scores, int64_t *out, int64_t *n_out, void *workspace,
+                           size_t workspace_bytes, void *stream);
 
 /*
  * Fused dequant + sparse decode attention over a paged pool (batch 1, head
  * dim 128): hkv_decode_attn with logical page p of the sequence (tokens
  * [16p, 16p+16), tokens >= T masked) read from block block_table[p] of the
- * paged K / V (hkv_paged_write's layout, the entries of each page-head patched
- * over its codes); sel (nsel, H) holds logical pages, ids outside
- * [0, ceil(T/16)) or whose block is outside the pool are skipped; V rows
- * min(16p + slot, v_rows - 1).  The counterpart of the compact backend's
- * forward over its block table (src/kvquant/compact_backend.py:194-299).
- * Workspace: hkv_decode_workspace_bytes(nsel, Hq, pages_per_split).
+ * paged K / V (the page-head's outliers patched over its codes); sel (nsel,
+ * heads) holds logical pages, ids outside [0, ceil(T/16)) or whose block is
+ * outside the pool are skipped; V rows min(16p + slot, v_rows - 1).  The
+ * counterpart of the compact backend's forward over its block table
+ * (src/kvquant/compact_backend.py:194-299).  Hq / heads <= 16.  Workspace:
+ * hkv_decode_workspace_bytes(nsel, Hq, pages_per_split).
  */
-int hkv_paged_decode_attn(const void *q, int Hq, int H, int D, int64_t T, const int64_t *block_table,
-                          int64_t num_blocks, const uint8_t *k_codes, const int32_t *k_ocnt,
-                          const uint32_t *k_oent, int k_cap, int k_bits, const void *k_tables,
-                          const uint8_t *v_codes, const int32_t *v_ocnt, const uint32_t *v_oent,
-                          int v_cap, int v_bits, const void *v_tables, int64_t v_rows,
-                          const int64_t *sel, int64_t nsel, int pages_per_split, float scale,
-                          void *out, int out_dtype, void *workspace, size_t workspace_bytes,
-                          void *stream);
+int hkv_paged_decode_attn(const void *q, int Hq, int64_t T, const int64_t *block_table,
+                          const hkv_paged_side *k, const void *k_tables, const hkv_paged_side *v,
+                          const void *v_tables, int64_t v_rows, const int64_t *sel, int64_t nsel,
+                          int pages_per_split, float scale, void *out, int out_dtype,
+                          void *workspace, size_t workspace_bytes, void *stream);
 
 /*
  * Quest page statistics: K_pages (P,S,H,D) -> kmin, kmax (P,H,D), same dtype

@@ -592,12 +592,15 @@ def kmeans_inertia(values, centers) -> float:
 PAGE = 16
 
 
-def paged_empty(NB: int, H: int, D: int, bits: int, cap: int, stats: bool) -> dict:
+def paged_empty(NB: int, H: int, D: int, bits: int, cap: int, stats: bool, arena: bool = True) -> dict:
     """An empty paged pool side (numpy): codes (NB,H,16,D*bits/8) u8, ocnt
-    (NB,H) int64, oent (NB,H,cap) u32, kmin / kmax (NB,H,D) fp16 bits (K only;
-    +inf / -inf), status int."""
+    (NB,H) int64, oent (NB,H,room) u32 -- each page-head's entries in order,
+    room = 16*D when an overflow arena takes the entries past cap (the device
+    keeps the first cap inline and the rest in the page-head's chunk), else
+    cap; kmin / kmax (NB,H,D) fp16 bits (K only; +inf / -inf), status int."""
+    room = PAGE * D if arena else cap
     p = dict(codes=np.zeros((NB, H, PAGE, D * bits // 8), np.uint8), ocnt=np.zeros((NB, H), np.int64),
-             oent=np.zeros((NB, H, cap), np.uint32), bits=bits, cap=cap, status=0)
+             oent=np.zeros((NB, H, room), np.uint32), bits=bits, cap=cap, room=room, status=0)
     if stats:
         p["kmin"] = np.full((NB, H, D), 0x7C00, np.uint16)
         p["kmax"] = np.full((NB, H, D), 0xFC00, np.uint16)
@@ -639,13 +642,13 @@ def paged_write(pool: dict, values, slot_mapping, scale, per_token: bool, positi
     its rows' codes (the K / V pack of pack_k / pack_v) into rows w0.. of its
     page for every head; the page-head keeps the outliers of rows < w0 (all of
     them, counted, when every stored one is below w0) and appends the run's
-    outliers in (row, channel) order, storing the first cap; K statistics are
+    outliers in (row, channel) order, storing the first room; K statistics are
     the min / max of the dequantised values over the run's rows (a zero as
     +0), replacing the page's at w0 = 0 and folded in otherwise.  scale =
     (poles, upper, lower) float32 arrays; V rows min(positions[t], rows - 1)."""
     x = _h16(values)
     T, H, D = x.shape
-    bits, cap = pool["bits"], pool["cap"]
+    bits, cap = pool["bits"], pool["room"]
     NB = pool["codes"].shape[0]
     pos = np.arange(T, dtype=np.int64) if positions is None else np.asarray(positions, np.int64)
     if per_token:
@@ -689,7 +692,7 @@ def paged_gather(pool: dict, block_ids, first_pos, poles, per_token: bool, D: in
     (src/kvquant/compact_pool.py:492-537) over the paged layout."""
     ids = np.asarray(block_ids, np.int64)
     NB, H = pool["codes"].shape[:2]
-    bits, cap = pool["bits"], pool["cap"]
+    bits, cap = pool["bits"], pool["room"]
     NK = ids.size
     out = np.zeros((NK, PAGE, H, D), np.uint16)
     for k, b in enumerate(ids):

@@ -40,12 +40,26 @@ def _diff(a, b) -> int:
     return int((a != b).sum())
 
 
+def logical_entries(side) -> np.ndarray:
+    """Every page-head's stored entries in order, (NB, H, 2048) u32: the
+    first cap inline, the rest from the page-head's overflow chunk."""
+    NB, Hh, cap = side.num_blocks, side.heads, side.cap
+    full = np.zeros((NB, Hh, PS * D), np.uint32)
+    full[:, :, :cap] = side.oent.cpu().numpy().view(np.uint32)
+    if side.ovf is not None:
+        idx = side.ovf.cpu().numpy()
+        m = idx >= 0
+        full[m, cap:] = side.ovf_ent.cpu().numpy().view(np.uint32)[idx[m]]
+    return full
+
+
 def _check(side, want, cap):
     assert _diff(side.codes.cpu().numpy(), want["codes"]) == 0
     cnt = side.ocnt.cpu().numpy()
     assert _diff(cnt, want["ocnt"]) == 0
-    ent = side.oent.cpu().numpy().view(np.uint32)
-    live = np.arange(cap)[None, None, :] < np.minimum(cnt, cap)[..., None]
+    room = want["room"]
+    ent = logical_entries(side)[:, :, :room]
+    live = np.arange(room)[None, None, :] < np.minimum(cnt, room)[..., None]
     assert _diff(np.where(live, ent, 0), np.where(live, want["oent"], 0)) == 0
     if "kmin" in want:
         assert _diff(side.kmin.cpu().view(torch.int16).numpy().view(np.uint16), want["kmin"]) == 0
@@ -68,12 +82,15 @@ def _slot_mapping(T, NB, kind):
     raise ValueError(kind)
 
 
-@pytest.mark.parametrize("per_token,L,kind,T,cap", [
-    (False, 16, "aligned", 1024, 256), (False, 4, "offset", 777, 256), (True, 16, "offset", 500, 256),
-    (True, 4, "aligned", 1024, 256), (False, 16, "batch", 40, 256), (True, 16, "batch", 40, 64),
-    (False, 4, "aligned", 256, 8),   # capacity overflow: status set, the first 8 kept
+@pytest.mark.parametrize("per_token,L,kind,T,cap,arena", [
+    (False, 16, "aligned", 1024, 256, True), (False, 4, "offset", 777, 256, True),
+    (True, 16, "offset", 500, 256, True), (True, 4, "aligned", 1024, 256, True),
+    (False, 16, "batch", 40, 256, True), (True, 16, "batch", 40, 64, True),
+    (False, 4, "aligned", 256, 8, True),    # every page-head past cap: entries in overflow chunks
+    (True, 16, "offset", 700, 40, True),    # overflow with mid-page starts
+    (False, 4, "aligned", 256, 8, False),   # no arena: status set, the first 8 kept
 ])
-def test_paged_write_vs_oracle(dev, per_token, L, kind, T, cap):
+def test_paged_write_vs_oracle(dev, per_token, L, kind, T, cap, arena):
     from helix_kv.paged import PagedSide, paged_write
 
     NB, bits = 128, 2 if L <= 4 else 4
@@ -83,14 +100,16 @@ def test_paged_write_vs_oracle(dev, per_token, L, kind, T, cap):
     x = (RNG.standard_t(3, (T, H, D)) * 0.8).astype(np.float16)
     slots = _slot_mapping(T, NB, kind)
     pos = RNG.integers(0, 2 * rows, T) if per_token else None
-    side = PagedSide.empty(NB, H, bits, cap, dev, stats=not per_token)
+    side = PagedSide.empty(NB, H, bits, cap, dev, stats=not per_token,
+                           n_chunks=NB * H if arena else 0)
     paged_write(side, _t(x, dev), t, _t(slots, dev), None if pos is None else _t(pos, dev))
-    want = O.paged_empty(NB, H, D, bits, cap, stats=not per_token)
+    want = O.paged_empty(NB, H, D, bits, cap, stats=not per_token, arena=arena)
     O.paged_write(want, x, slots, [a.astype(np.float32) for a in sc], per_token, positions=pos)
     torch.cuda.synchronize()
     _check(side, want, cap)
     if cap == 8:
-        assert want["status"] == 1
+        assert int(want["ocnt"].max()) > cap
+        assert want["status"] == (0 if arena else 1)
 
 
 @pytest.mark.parametrize("per_token,L", [(False, 16), (False, 4), (True, 16), (True, 4)])
@@ -109,8 +128,8 @@ def test_prefill_then_appends_equals_one_write(dev, per_token, L):
     table = RNG.permutation(NB)[: -(-T // PS)]
     slots = table[np.arange(T) // PS] * PS + np.arange(T) % PS
     pos = np.arange(T)
-    one = PagedSide.empty(NB, H, bits, cap, dev, stats=not per_token)
-    inc = PagedSide.empty(NB, H, bits, cap, dev, stats=not per_token)
+    one = PagedSide.empty(NB, H, bits, cap, dev, stats=not per_token, n_chunks=NB * H)
+    inc = PagedSide.empty(NB, H, bits, cap, dev, stats=not per_token, n_chunks=NB * H)
     xd, sd, pd = _t(x, dev), _t(slots, dev), _t(pos, dev)
     paged_write(one, xd, t, sd, pd if per_token else None)
     paged_write(inc, xd[:T0].contiguous(), t, sd[:T0], pd[:T0] if per_token else None)
@@ -165,7 +184,7 @@ def test_paged_gather_vs_oracle(dev, per_token, L):
     x = (RNG.standard_t(3, (T, H, D)) * 0.8).astype(np.float16)
     slots = _slot_mapping(T, NB, "offset")
     pos = np.arange(T)
-    side = PagedSide.empty(NB, H, bits, cap, dev, stats=False)
+    side = PagedSide.empty(NB, H, bits, cap, dev, stats=False, n_chunks=NB * H)
     paged_write(side, _t(x, dev), t, _t(slots, dev), _t(pos, dev) if per_token else None)
     want = O.paged_empty(NB, H, D, bits, cap, stats=False)
     O.paged_write(want, x, slots, [a.astype(np.float32) for a in sc], per_token,
@@ -188,10 +207,43 @@ def test_paged_write_full_layer(dev):
     t = _tables(dev, sc, False)
     x = RNG.standard_t(3, (T, H, D)).astype(np.float16)
     slots = _slot_mapping(T, NB, "aligned")
-    side = PagedSide.empty(NB, H, 4, cap, dev, stats=True)
-    paged_write(side, _t(x, dev), t, _t(slots, dev))
     want = O.paged_empty(NB, H, D, 4, cap, stats=True)
     O.paged_write(want, x, slots, [a.astype(np.float32) for a in sc], False)
+    over = int((want["ocnt"] > cap).sum())     # arena sized as a caller would: one chunk per
+    side = PagedSide.empty(NB, H, 4, cap, dev, stats=True, n_chunks=over)   # overflowing page-head
+    paged_write(side, _t(x, dev), t, _t(slots, dev))
     torch.cuda.synchronize()
     assert 0.02 < want["ocnt"].sum() / x.size < 0.2
+    assert over > 0 and int(side.ovf_next.item()) == over
     _check(side, want, cap)
+
+
+def test_paged_write_arena_used_up(dev):
+    """With fewer overflow chunks than overflowing page-heads, the chunks go
+    to some of them (first come, first served), every page-head keeps its
+    counts and first cap entries, those with a chunk keep all of theirs, and
+    status flags the loss."""
+    from helix_kv.paged import PagedSide, paged_write
+
+    NB, bits, cap, T, chunks = 64, 4, 64, 1024, 10
+    sc = _scales(False, 16)
+    t = _tables(dev, sc, False)
+    x = (RNG.standard_t(3, (T, H, D)) * 0.8).astype(np.float16)
+    slots = _slot_mapping(T, NB, "aligned")
+    side = PagedSide.empty(NB, H, bits, cap, dev, stats=True, n_chunks=chunks)
+    paged_write(side, _t(x, dev), t, _t(slots, dev))
+    want = O.paged_empty(NB, H, D, bits, cap, stats=True)
+    O.paged_write(want, x, slots, [a.astype(np.float32) for a in sc], False)
+    torch.cuda.synchronize()
+    assert int((want["ocnt"] > cap).sum()) > chunks
+    assert _diff(side.codes.cpu().numpy(), want["codes"]) == 0
+    cnt = side.ocnt.cpu().numpy()
+    assert _diff(cnt, want["ocnt"]) == 0
+    ovf = side.ovf.cpu().numpy()
+    owned = ovf >= 0
+    assert owned.sum() == chunks and np.array_equal(np.sort(ovf[owned]), np.arange(chunks))
+    ent, ref = logical_entries(side), want["oent"]
+    live = np.arange(PS * D)[None, None, :] < np.where(owned, cnt, np.minimum(cnt, cap))[..., None]
+    assert _diff(np.where(live, ent, 0), np.where(live, ref, 0)) == 0
+    assert _diff(side.kmin.cpu().view(torch.int16).numpy().view(np.uint16), want["kmin"]) == 0
+    assert int(side.status.item()) == 1

@@ -45,8 +45,8 @@ def _sequence(dev, T, Lk, Lv, NB, rows=2048, cap=256):
     kt = NuqLayerTables(*(_t(a, dev) for a in ks), per_token=False)
     vt = NuqLayerTables(*(_t(a, dev) for a in vs), per_token=True)
     kb, vb = (2 if Lk <= 4 else 4), (2 if Lv <= 4 else 4)
-    kside = PagedSide.empty(NB, H, kb, cap, dev, stats=True)
-    vside = PagedSide.empty(NB, H, vb, cap, dev)
+    kside = PagedSide.empty(NB, H, kb, cap, dev, stats=True, n_chunks=NB * H)
+    vside = PagedSide.empty(NB, H, vb, cap, dev, n_chunks=NB * H)
     pos = np.arange(T)
     paged_write(kside, _t(k, dev), kt, _t(slots, dev))
     paged_write(vside, _t(v, dev), vt, _t(slots, dev), _t(pos, dev))
@@ -123,6 +123,26 @@ def test_paged_decode_vs_oracle(dev, T, group, Lk, Lv, frac, pps):
                                 lambda h: h // group, num_tokens=T)
     got = paged_decode_attention(_t(q, dev), S["kside"], S["kt"], S["vside"], S["vt"], S["btd"], T,
                                  _t(bad, dev), pages_per_split=pps, out_dtype=torch.float32)
+    _check(got, want)
+
+
+@pytest.mark.parametrize("cap", [24, 300])
+def test_paged_decode_overflow_chunks(dev, cap):
+    """Page-heads whose outliers pass the inline capacity keep the rest in
+    overflow chunks (cap 24: nearly every page-head; 300: beyond the 256
+    entries held in registers), and the decode patches them all."""
+    from helix_kv.paged import paged_decode_attention
+
+    T, group = 2500, 7
+    S = _sequence(dev, T, 16, 16, NB=200, cap=cap)
+    assert int(S["kside"].ovf_next.item()) > 0 or cap > 256
+    P = S["P"]
+    sel = np.stack([np.sort(RNG.permutation(P)[: P // 2]) for _ in range(H)], 1).astype(np.int64)
+    q = RNG.standard_normal((H * group, D)).astype(np.float16)
+    want = O.selected_attention(q.astype(np.float64), S["kpages"], S["vpages"], sel,
+                                lambda h: h // group, num_tokens=T)
+    got = paged_decode_attention(_t(q, dev), S["kside"], S["kt"], S["vside"], S["vt"], S["btd"], T,
+                                 _t(sel, dev), pages_per_split=12, out_dtype=torch.float32)
     _check(got, want)
 
 
