@@ -8,17 +8,15 @@
 //   CSR outliers over rows r = t*H + h: row_ptr (T*H+1) int32, col u8 = d,
 //   val fp16 = the original value; (row, col) ascending.
 //
-// Pack runs as two kernels.  pack_stage_kernel streams the fp16 input once;
-// its unit of work is a wave tile (PASSES passes of 64/G rows, G = D/8 lanes
-// per row), handled by one wave on its own: no block-level barrier.  A wave
-// writes the packed codes, each row's outlier offset within its wave tile
-// (into row_ptr), the tile's outliers into the tile's own staging region, and
-// the tile's outlier count.  copy_kernel turns the counts into offsets, adds
-// them to row_ptr and copies the staged outliers into the dense col/val
-// arrays.  No block ever waits on another: on gfx950 the eight XCDs' L2
-// caches are not coherent, so a single-pass scan whose tiles wait on their
-// predecessors pays a memory round trip per step.
+// Pack is one kernel (pack_fused_kernel): waves take chunks of rows from a
+// work counter, write the packed codes as they go, hold the chunk's outliers
+// in LDS, and place them (and row_ptr) once a decoupled look-back over the
+// chunks' published counts has given the chunk's offset.  One launch packs up
+// to kPackItems tensors of the same kernel variant (a layer's K, or the K of
+// many layers), so a whole prefill step takes a few launches.
 #include "nuq_core.h"
+
+#include <vector>
 
 namespace {
 
@@ -30,16 +28,46 @@ constexpr int kThreads = 256;
 // 48.1 -> 42.8, V nuq4 64.8 -> 59.3).
 __host__ __device__ constexpr int pack_passes(bool per_token, int nb) { return (!per_token && nb < 4) ? 8 : 4; }
 
-// Workspace: header, per-wave-tile counts, a region of (ntiles + 1) words
-// kept so the workspace size stays what earlier versions asked for, then the
-// staged entries (u32: value | column << 16), each region 256-byte aligned.  Staging holds a
-// whole wave tile per wave tile, so no input can overflow it.
-struct PackLayout {
-  int64_t ntiles, tile_rows, tile_elems;
-  size_t cnt_off, base_off, ent_off, bytes;
+constexpr int kPackItems = 16;                 // tensors per fused pack launch
+constexpr int kPackWaveRows = 128;             // least rows a wave packs per chunk
+constexpr uint32_t kPackSpinLimit = 1u << 20;  // look-back rounds without progress before giving up
+constexpr int kPackLookWindows = 16;           // look-back windows of 64 chunks read at once
+constexpr size_t kPackHeader = 256;            // workspace header bytes
+
+// One tensor of a fused pack launch (kernel argument, by value).
+struct PackItem {
+  const uint16_t* x;
+  uint8_t* packed;
+  int32_t* row_ptr;
+  uint8_t* col;
+  uint16_t* val;
+  hkv_nuq_scales sc;
+  int64_t nrows;
+  uint32_t chunk0;  // number of the item's first chunk
+  uint32_t cap;     // col / val capacity
+};
+struct PackBatch {
+  PackItem it[kPackItems];
+  int32_t n;
+  int32_t H;  // heads (the same for every item of a launch)
+  uint32_t nchunks;
 };
 
-__host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+// Rows a wave packs per chunk: whole wave tiles, at least kPackWaveRows.  A
+// chunk is NW such parts, one per wave of a block.
+__host__ __device__ constexpr int pack_tile_rows(int G, int passes) { return (64 / G) * passes; }
+__host__ __device__ constexpr int pack_wave_rows(int G, int passes) {
+  return pack_tile_rows(G, passes) >= kPackWaveRows ? pack_tile_rows(G, passes) : kPackWaveRows;
+}
+__host__ __device__ constexpr int pack_chunk_rows(int G, int passes) {
+  return (kThreads / 64) * pack_wave_rows(G, passes);
+}
+// Outliers of its part of a chunk a wave holds in LDS: one in ten elements
+// (per-token scales: one in thirteen, so four blocks fit a CU's LDS); a part
+// with more writes the rest when its chunk is flushed (pack_redo_rows).
+__host__ __device__ constexpr int pack_ent_cap(int G, int passes, bool per_token) {
+  return (pack_wave_rows(G, passes) * 8 * G / (per_token ? 13 : 10) + 63) & ~63;
+}
 
 HKV_DEV void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -47,18 +75,126 @@ HKV_DEV void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+HKV_DEV uint32_t wave_sum(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += (uint32_t)__shfl_xor((int)v, o, 64);
+  return v;
+}
+
+// v, hidden from the optimiser: item fields loaded through it are loaded
+// again where they are used instead of being kept in scalar registers
+// across the packing loop.
+HKV_DEV int opaque_s(int v) {
+  v = __builtin_amdgcn_readfirstlane(v);
+  asm volatile("" : "+s"(v));
+  return v;
+}
+
+// Chunk status words: epoch (24 bits) | flags (8 bits) | count (32 bits).
+// kStAgg: the chunk's own outlier count; kStInc: the count of the tensor's
+// chunks up to and including this one.  A word whose epoch is not the
+// launch's (left by an earlier launch, or zero) counts as not yet written.
+constexpr uint64_t kStAgg = 1, kStInc = 2;
+HKV_DEV uint64_t st_word(uint32_t epoch, uint64_t flag, uint32_t v) {
+  return ((uint64_t)(epoch & 0xffffffu) << 40) | (flag << 32) | v;
+}
+HKV_DEV void st_publish(uint64_t* p, uint64_t w) {
+  __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The outliers of a chunk at chunk positions >= ecap (more than its wave's
+// LDS holds; rare), found again from the input with the defining fp32
+// threshold compare (v > upper || v < lower, as slow_one) and written at
+// their final places.  Row r's outliers start at chunk position roff[r]; a
+// row's lanes take two channels each, in channel order, so a ballot gives
+// each outlier's rank within the row.
+template <int D>
+HKV_DEV void pack_redo_rows(const PackItem& it, int H, int64_t rbeg, int nrc, const uint16_t* roff,
+                            uint32_t run, uint32_t base, uint32_t ecap, int lane) {
+  const hkv_nuq_scales& sc = it.sc;
+  const SlowInfo si = slow_info(sc);
+#pragma unroll 1
+  for (int rr = 0; rr < nrc; ++rr) {
+    const uint32_t end = rr + 1 < nrc ? roff[rr + 1] : run;
+    if (end <= ecap) continue;  // all of the row's entries were kept
+    const int64_t r = rbeg + rr;
+    const int64_t t = r / H;
+    const int h = (int)(r - t * H);
+    const int64_t trow = sc.per_token ? (int64_t)h * sc.rows + clamp_row(token_pos(sc, t), sc.rows) : 0;
+    uint32_t o = roff[rr];
+#pragma unroll 1
+    for (int d0 = 0; d0 < D; d0 += 128) {
+      const int d = d0 + 2 * lane;
+      uint32_t xw = 0;
+      int f0 = 0, f1 = 0;
+      if (d < D) {
+        xw = *reinterpret_cast<const uint32_t*>(it.x + r * D + d);
+        const int64_t ta = sc.per_token ? trow : (int64_t)h * D + d;
+        const int64_t tb = sc.per_token ? trow : ta + 1;
+        const float v0 = h2f((uint16_t)(xw & 0xffffu)), v1 = h2f((uint16_t)(xw >> 16));
+        f0 = (v0 > load_scale(si.upper, si.tdt, ta)) || (v0 < load_scale(si.lower, si.tdt, ta));
+        f1 = (v1 > load_scale(si.upper, si.tdt, tb)) || (v1 < load_scale(si.lower, si.tdt, tb));
+      }
+      const uint64_t b0 = __ballot(f0), b1 = __ballot(f1);
+      const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
+      // elements before lane's first: both elements of every lower lane
+      uint32_t q = o + (uint32_t)__popcll(b0 & below) + (uint32_t)__popcll(b1 & below);
+      if (f0) {
+        if (q >= ecap && base + q < it.cap) {
+          it.col[base + q] = (uint8_t)d;
+          it.val[base + q] = (uint16_t)(xw & 0xffffu);
+        }
+        ++q;
+      }
+      if (f1 && q >= ecap && base + q < it.cap) {
+        it.col[base + q] = (uint8_t)(d + 1);
+        it.val[base + q] = (uint16_t)(xw >> 16);
+      }
+      o += (uint32_t)__popcll(b0) + (uint32_t)__popcll(b1);
+    }
+  }
+}
+
+// Fused pack.  A launch packs up to kPackItems tensors of one kernel variant.
+// Their rows are cut into chunks of CR rows, numbered consecutively over the
+// tensors.  A block takes the next chunk number from the work counter (one
+// device-scope atomic per chunk: those on one address serialise at about
+// 11 ns each on MI355X, so a chunk is large, NW * WR rows); each wave packs
+// its WR rows (codes straight to HBM, outliers and each row's offset within
+// the wave's part into its LDS).  After a block barrier wave 0 publishes the
+// chunk's count and takes the next number; the chunk's offset (the outliers
+// of the tensor's earlier chunks) is found one chunk later, by a decoupled
+// look-back over the status words once the block has packed its next chunk,
+// so the earlier chunks, which were packed concurrently, have published their
+// counts by then and the look-back rarely waits; every wave then writes the
+// held chunk's row_ptr and outliers at their final places (its LDS holds two
+// chunks).  Chunk numbers are handed out in increasing order, a chunk's count
+// is published as soon as it is packed, and a look-back waits only for counts
+// of lower chunks, held by running blocks: the scheme cannot deadlock.  The
+// status words and the counters are accessed with device-scope relaxed
+// atomics only (they carry the counts themselves; no other data crosses
+// blocks), so no cache write-back is needed across the eight XCDs' L2s.
+//
+// The header holds the work counter, a count of finished blocks and the
+// epoch; the last block to finish resets the counters and advances the epoch,
+// so a zero-filled workspace serves any number of later launches in stream
+// order.
+//
 // KFIX: the rows of one pass of a wave (RW = 64/G) are a multiple of H, so a
 // lane's head is fixed (rw % H) and its token advances by RW / H per pass.
 template <int NB, bool PT, int G, int BITS, bool KFIX, int PASSES>
-__global__ void __launch_bounds__(kThreads)
-pack_stage_kernel(const uint16_t* __restrict__ x, int64_t nrows, int H, hkv_nuq_scales sc,
-                  uint8_t* __restrict__ packed, int32_t* __restrict__ row_ptr,
-                  uint32_t* __restrict__ sent, uint32_t* __restrict__ wt_cnt, int64_t nwt) {
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(PT ? 4 : 3)))
+pack_fused_kernel(const PackBatch B, uint32_t* __restrict__ hdr, uint64_t* __restrict__ status) {
   constexpr int RW = 64 / G;        // rows per wave per pass
   constexpr int WT = RW * PASSES;  // rows per wave tile
   constexpr int D = 8 * G;
   constexpr int RB = D * BITS / 8;  // packed bytes per row
   constexpr int NW = kThreads / 64;
+  constexpr int WR = pack_wave_rows(G, PASSES);  // rows of a wave's part of a chunk
+  constexpr int CR = NW * WR;
+  constexpr int CT = WR / WT;                     // wave tiles per part
+  constexpr int ECAP = pack_ent_cap(G, PASSES, PT);
+  static_assert(WR % WT == 0 && CR == pack_chunk_rows(G, PASSES), "a part is whole wave tiles");
   // Per-token tables of a wave tile's rows are staged in the wave's LDS slice
   // when they fit in 4 KiB (D >= 128), already in search form (each
   // breakpoint and threshold duplicated into both 16-bit halves: words 0..14
@@ -70,286 +206,321 @@ pack_stage_kernel(const uint16_t* __restrict__ x, int64_t nrows, int H, hkv_nuq_
   // each lane's current 8 values, read back by element index in the
   // outlier loop (one 16-byte slot per lane)
   __shared__ __align__(16) uint4 s_x[NW * 64];
+  // two chunks per wave: the one being packed and the one held for its offset
+  __shared__ uint16_t s_val[2][NW][ECAP];  // a wave's outliers, in (row, col) order
+  __shared__ uint8_t s_col[2][NW][ECAP];
+  __shared__ uint16_t s_roff[2][NW][WR];   // each row's first outlier within the wave's part
+  __shared__ uint32_t s_wtot[3][NW];       // each wave's outliers (by chunk number mod 3)
+  __shared__ uint32_t s_next, s_base;
 
   // the wave index through readfirstlane: tile bases are then uniform and
   // stay in scalar registers, addressed with 32-bit lane offsets
   const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int cg = lane % G, rw = lane / G;
   uint32_t* wtab = s_tab + (STAGE ? wv * WT * TW : 0);
-  const hkv_table_t* tabs = (const hkv_table_t*)sc.tables;
-  const SlowInfo si = slow_info(sc);
-  const int hfix = KFIX ? rw % H : 0;
+  const int hfix = KFIX ? rw % B.H : 0;
+  const uint32_t epoch = __hip_atomic_load(hdr + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint32_t nchunks = B.nchunks;
+
+  // Outliers of the tensor's chunks [first, c), by wave 0: lane i of window q
+  // examines chunk hi - 1 - i - 64 q, kPackLookWindows windows requested
+  // together (predecessors publish their inclusive counts one chunk late,
+  // so the nearest is typically a few hundred chunks back).  The nearest
+  // inclusive word ends the walk; every word before it must be at least an
+  // aggregate, else the walk reads again from there.  A walk that makes no
+  // progress for kPackSpinLimit rounds gives up and sets the error word (a
+  // bug guard: it never waits forever).
+  auto lookback = [&](uint32_t c, uint32_t first) -> uint32_t {
+    uint32_t acc = 0, hi = c, spins = 0;
+#pragma unroll 1
+    for (;;) {
+      uint64_t w[kPackLookWindows];
+#pragma unroll
+      for (int q = 0; q < kPackLookWindows; ++q) {
+        const int64_t i = (int64_t)hi - 1 - lane - 64 * q;
+        w[q] = st_word(epoch, kStInc, 0u);  // before the tensor's first chunk: nothing
+        if (i >= (int64_t)first) w[q] = __hip_atomic_load(status + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      bool stop = false, found = false;
+#pragma unroll
+      for (int q = 0; q < kPackLookWindows; ++q) {
+        if (!stop) {
+          const uint32_t fl = (uint32_t)(w[q] >> 32) & 0xffu;
+          const bool ok = (uint32_t)(w[q] >> 40) == (epoch & 0xffffffu) && fl != 0u;
+          const uint64_t incm = __ballot(ok && (fl & kStInc));
+          const uint64_t badm = __ballot(!ok);
+          const int fp = incm ? __builtin_ctzll(incm) : 64;
+          const uint64_t need = fp >= 63 ? ~0ull : ((2ull << fp) - 1ull);
+          if (badm & need) {
+            stop = true;  // a predecessor has not published yet: read again from hi
+          } else {
+            acc += wave_sum(lane <= fp ? (uint32_t)w[q] : 0u);
+            if (fp < 64) {
+              stop = found = true;
+            } else {
+              hi -= 64;
+              spins = 0;
+            }
+          }
+        }
+      }
+      if (found) return acc;
+      if (stop) {
+        if (++spins > kPackSpinLimit) {
+          if (lane == 0) __hip_atomic_store(hdr + 3, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          return acc;
+        }
+        __builtin_amdgcn_s_sleep(2);
+      }
+    }
+  };
 
   Search2<NB> S[PT ? 1 : 4];
-  if constexpr (!PT && KFIX) {
-    const int64_t tab0 = (int64_t)hfix * D + 8 * cg;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      load_search_pair<NB>(tabs + tab0 + 2 * j, tabs + tab0 + 2 * j + 1, S[j]);
-  }
   uint32_t xmin = 0;  // KFIX: the lane's smallest fast-path bound
-  if constexpr (!PT && KFIX) xmin = xsafe_min<NB>(S);
+  int cur = -1;       // item whose per-channel tables S holds
 
-  for (int64_t wt = (int64_t)blockIdx.x * NW + wv; wt < nwt; wt += (int64_t)gridDim.x * NW) {
-    const int64_t r0 = wt * WT;
-    const int64_t t0 = KFIX ? r0 / H : 0;  // token of row r0 (H divides r0)
-    const int nv = nrows - r0 < WT ? (int)(nrows - r0) : WT;  // rows of this tile
-    const uint16_t* xt = x + r0 * D;
-    uint8_t* pt = packed + r0 * RB;
-    int32_t* rpt = row_ptr + r0;
-    uint32_t xs[PASSES][4];
+  if (tid == 0) s_next = __hip_atomic_fetch_add(hdr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  uint32_t c = s_next;
+  // the held chunk (packed, offset not yet known)
+  bool held = false;
+  uint32_t hc = 0, hk = 0;
+  int hj = 0, hbuf = 0, hpar = 0;
+  int64_t hwbeg = 0;
+  int hnrw = 0;
+  uint32_t hrun = 0;
+  int buf = 0, par = 0;
+
+  // Resolve the held chunk's offset (wave 0), then every wave writes its part.
+  auto flush_held = [&]() {
+    if (wv == 0) {
+      const PackItem& ih = B.it[opaque_s(hj)];
+      uint32_t tot = 0;
 #pragma unroll
-    for (int p = 0; p < PASSES; ++p) {
-      const int rr = p * RW + rw;
-      uint4 v = make_uint4(0u, 0u, 0u, 0u);
-      if (rr < nv) v = *reinterpret_cast<const uint4*>(xt + (uint32_t)(rr * D + 8 * cg));
-      xs[p][0] = v.x; xs[p][1] = v.y; xs[p][2] = v.z; xs[p][3] = v.w;
+      for (int w = 0; w < NW; ++w) tot += s_wtot[hpar][w];
+      uint32_t base = 0;  // outliers of the tensor's earlier chunks
+      if (hk != 0) {
+        base = lookback(hc, ih.chunk0);
+        if (lane == 0) st_publish(status + hc, st_word(epoch, kStInc, base + tot));
+      }
+      if (lane == 0) s_base = base;
     }
-    if constexpr (STAGE) {
-      // three 16-byte parts of each row's record: breakpoints 0-7, 8-14, and
-      // the thresholds (the poles are not needed here)
-      for (int i = lane; i < WT * 3; i += 64) {
-        const int rr = i / 3, q = i - rr * 3;
+    __syncthreads();
+    const PackItem& ih = B.it[opaque_s(hj)];
+    uint32_t base = s_base;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) base += w < wv ? s_wtot[hpar][w] : 0u;
+    const uint16_t* wval = s_val[hbuf][wv];
+    const uint8_t* wcol = s_col[hbuf][wv];
+    const uint16_t* wroff = s_roff[hbuf][wv];
+    const uint32_t kept = hrun < (uint32_t)ECAP ? hrun : (uint32_t)ECAP;
+#pragma unroll 1
+    for (uint32_t i = lane; i < kept; i += 64) {
+      const uint32_t o = base + i;
+      if (o < ih.cap) {
+        ih.col[o] = wcol[i];
+        ih.val[o] = wval[i];
+      }
+    }
+#pragma unroll 1
+    for (int i = lane; i < hnrw; i += 64) ih.row_ptr[hwbeg + i] = (int32_t)(base + wroff[i]);
+    if (hnrw > 0 && hwbeg + hnrw == ih.nrows && lane == 0) ih.row_ptr[ih.nrows] = (int32_t)(base + hrun);
+    if (wv == 0 && hk == 0 && ih.nrows == 0 && lane == 0) ih.row_ptr[0] = 0;  // an empty tensor
+    if (hrun > (uint32_t)ECAP) pack_redo_rows<D>(ih, B.H, hwbeg, hnrw, wroff, hrun, base, (uint32_t)ECAP, lane);
+    wave_sync();
+  };
+
+  while (c < nchunks) {
+    int j = 0;
+    while (j + 1 < B.n && c >= B.it[j + 1].chunk0) ++j;
+    const PackItem& it = B.it[j];
+    const hkv_nuq_scales sc = it.sc;
+    const hkv_table_t* tabs = (const hkv_table_t*)sc.tables;
+    const SlowInfo si = slow_info(sc);
+    const int H = B.H;
+    const int64_t nrows = it.nrows;
+    const uint32_t k = c - it.chunk0;
+    const int64_t wbeg = (int64_t)k * CR + (int64_t)wv * WR;  // first row of the wave's part
+    const int64_t wrest = nrows - wbeg;
+    const int nrw = wrest <= 0 ? 0 : (wrest < WR ? (int)wrest : WR);  // rows of the wave's part
+    if constexpr (!PT && KFIX) {
+      if (j != cur) {
+        const int64_t tab0 = (int64_t)hfix * D + 8 * cg;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          load_search_pair<NB>(tabs + tab0 + 2 * q, tabs + tab0 + 2 * q + 1, S[q]);
+        xmin = xsafe_min<NB>(S);
+        cur = j;
+      }
+    }
+    uint32_t run = 0;  // the wave's outliers so far
+    uint16_t* wval = s_val[buf][wv];
+    uint8_t* wcol = s_col[buf][wv];
+    uint16_t* wroff = s_roff[buf][wv];
+#pragma unroll 1
+    for (int tt = 0; tt < CT; ++tt) {
+      const int64_t r0 = wbeg + tt * WT;
+      const int nv = nrw - tt * WT < WT ? nrw - tt * WT : WT;  // rows of this tile
+      if (nv <= 0) break;
+      const int64_t t0 = KFIX ? r0 / H : 0;  // token of row r0 (H divides r0)
+      const uint16_t* xt = it.x + r0 * D;
+      uint8_t* pt = it.packed + r0 * RB;
+      uint32_t xs[PASSES][4];
+#pragma unroll
+      for (int p = 0; p < PASSES; ++p) {
+        const int rr = p * RW + rw;
+        uint4 v = make_uint4(0u, 0u, 0u, 0u);
+        if (rr < nv) v = *reinterpret_cast<const uint4*>(xt + (uint32_t)(rr * D + 8 * cg));
+        xs[p][0] = v.x; xs[p][1] = v.y; xs[p][2] = v.z; xs[p][3] = v.w;
+      }
+      if constexpr (STAGE) {
+        // three 16-byte parts of each row's record: breakpoints 0-7, 8-14, and
+        // the thresholds (the poles are not needed here)
+        for (int i = lane; i < WT * 3; i += 64) {
+          const int rr = i / 3, q = i - rr * 3;
+          if (rr < nv) {
+            int64_t t;
+            int h;
+            if constexpr (KFIX) {  // H divides r0: the row's token and head from rr
+              const int kk = rr / H;
+              t = t0 + kk;
+              h = rr - kk * H;
+            } else {
+              const int64_t r = r0 + rr;
+              t = r / H;
+              h = (int)(r - t * H);
+            }
+            const int64_t tab = (int64_t)h * sc.rows + clamp_row(token_pos(sc, t), sc.rows);
+            const uint4 v = reinterpret_cast<const uint4*>(tabs + tab)[q == 2 ? 4 : q];
+            uint32_t* dw = wtab + rr * TW;
+            if (q < 2) {
+              const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+              for (int e = 0; e < 8; ++e) {
+                const uint32_t hh = (w[e >> 1] >> (16 * (e & 1))) & 0xffffu;
+                if (8 * q + e < 15) dw[8 * q + e] = hh | (hh << 16);
+              }
+            } else {
+              const uint32_t lo = v.x & 0xffffu, up = v.x >> 16;
+              const uint32_t xsf = ((v.y >> 16) & 1u) ? (v.y & 0xffffu) : 0xffffu;
+              dw[15] = lo | (lo << 16);
+              dw[16] = up | (up << 16);
+              dw[17] = xsf | (xsf << 16);
+            }
+          }
+        }
+        wave_sync();
+      }
+
+#pragma unroll
+      for (int p = 0; p < PASSES; ++p) {
+        const int rr = p * RW + rw;
+        const int64_t r = r0 + rr;
+        uint32_t m = 0;
         if (rr < nv) {
           int64_t t;
           int h;
-          if constexpr (KFIX) {  // H divides r0: the row's token and head from rr
-            const int k = rr / H;
-            t = t0 + k;
-            h = rr - k * H;
+          if constexpr (KFIX) {
+            t = t0 + p * (RW / H) + rw / H;
+            h = hfix;
           } else {
-            const int64_t r = r0 + rr;
             t = r / H;
             h = (int)(r - t * H);
           }
-          const int64_t tab = (int64_t)h * sc.rows + clamp_row(token_pos(sc, t), sc.rows);
-          const uint4 v = reinterpret_cast<const uint4*>(tabs + tab)[q == 2 ? 4 : q];
-          uint32_t* dw = wtab + rr * TW;
-          if (q < 2) {
-            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+          const uint4 xv = make_uint4(xs[p][0], xs[p][1], xs[p][2], xs[p][3]);
+          s_x[wv * 64 + lane] = xv;
+          uint32_t pk;
+          if constexpr (PT) {
+            const RowTabAt tab{sc.rows, sc.positions, sc.pos_offset, h, t};  // for the exact scan only
+            if constexpr (STAGE) {
+              const uint32_t* tw = wtab + rr * TW;
 #pragma unroll
-            for (int k = 0; k < 8; ++k) {
-              const uint32_t hh = (w[k >> 1] >> (16 * (k & 1))) & 0xffffu;
-              if (8 * q + k < 15) dw[8 * q + k] = hh | (hh << 16);
+              for (int i = 0; i < (1 << NB) - 1; ++i) S[0].bp[i] = tw[i];
+              S[0].lo = tw[15];
+              S[0].up = tw[16];
+              S[0].xsafe = tw[17];
+            } else {
+              load_search_bcast<NB>(tabs + tab(0), S[0]);
             }
+            quant8_packed<NB, PT, BITS>(xv, S, si, tab, &pk, &m);
           } else {
-            const uint32_t lo = v.x & 0xffffu, up = v.x >> 16;
-            const uint32_t xsf = ((v.y >> 16) & 1u) ? (v.y & 0xffffu) : 0xffffu;
-            dw[15] = lo | (lo << 16);
-            dw[16] = up | (up << 16);
-            dw[17] = xsf | (xsf << 16);
+            const int64_t tab0 = (int64_t)h * D + 8 * cg;
+            if constexpr (!KFIX) {
+#pragma unroll
+              for (int q = 0; q < 4; ++q)
+                load_search_pair<NB>(tabs + tab0 + 2 * q, tabs + tab0 + 2 * q + 1, S[q]);
+            }
+            if constexpr (KFIX) quant8_packed<NB, PT, BITS, ChanTab, true>(xv, S, si, ChanTab{tab0}, &pk, &m, xmin);
+            else quant8_packed<NB, PT, BITS>(xv, S, si, ChanTab{tab0}, &pk, &m);
           }
-        }
-      }
-      wave_sync();
-    }
-
-    uint32_t* st = sent + r0 * D;  // the wave tile's staging region
-    uint32_t run = 0;              // outliers of the tile's earlier passes
-#pragma unroll
-    for (int p = 0; p < PASSES; ++p) {
-      const int rr = p * RW + rw;
-      const int64_t r = r0 + rr;
-      uint32_t m = 0;
-      if (rr < nv) {
-        int64_t t;
-        int h;
-        if constexpr (KFIX) {
-          t = t0 + p * (RW / H) + rw / H;
-          h = hfix;
-        } else {
-          t = r / H;
-          h = (int)(r - t * H);
-        }
-        const uint4 xv = make_uint4(xs[p][0], xs[p][1], xs[p][2], xs[p][3]);
-        s_x[wv * 64 + lane] = xv;
-        uint32_t pk;
-        if constexpr (PT) {
-          const RowTabAt tab{sc.rows, sc.positions, sc.pos_offset, h, t};  // for the exact scan only
-          if constexpr (STAGE) {
-            const uint32_t* tw = wtab + rr * TW;
-#pragma unroll
-            for (int i = 0; i < (1 << NB) - 1; ++i) S[0].bp[i] = tw[i];
-            S[0].lo = tw[15];
-            S[0].up = tw[16];
-            S[0].xsafe = tw[17];
+          if constexpr (BITS == 4) {
+            store_stream(reinterpret_cast<uint32_t*>(pt + (uint32_t)(rr * RB + 4 * cg)), pk);
           } else {
-            load_search_bcast<NB>(tabs + tab(0), S[0]);
+            store_stream(reinterpret_cast<uint16_t*>(pt + (uint32_t)(rr * RB + 2 * cg)), (uint16_t)pk);
           }
-          quant8_packed<NB, PT, BITS>(xv, S, si, tab, &pk, &m);
-        } else {
-          const int64_t tab0 = (int64_t)h * D + 8 * cg;
-          if constexpr (!KFIX) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-              load_search_pair<NB>(tabs + tab0 + 2 * j, tabs + tab0 + 2 * j + 1, S[j]);
+        }
+        // lanes are in (row, channel) order, so the wave's exclusive count is
+        // the position in (row, col) order
+        uint32_t tot;
+        const uint32_t pos = run + wave_excl_count_fused(__builtin_popcount(m), &tot);
+        if (rr < nv && cg == 0) wroff[tt * WT + rr] = (uint16_t)pos;
+        run += tot;
+        // entries at positions >= ECAP are not kept: the chunk's epilogue
+        // finds them again from the input
+        const uint16_t* xl = reinterpret_cast<const uint16_t*>(s_x + wv * 64 + lane);
+        const uint32_t c8 = 8u * cg;
+        uint32_t o = pos;
+        while (m) {
+          const int e = __builtin_ctz(m);
+          m &= m - 1u;
+          if (o < (uint32_t)ECAP) {
+            wval[o] = xl[e];
+            wcol[o] = (uint8_t)(c8 + e);
           }
-          if constexpr (KFIX) quant8_packed<NB, PT, BITS, ChanTab, true>(xv, S, si, ChanTab{tab0}, &pk, &m, xmin);
-          else quant8_packed<NB, PT, BITS>(xv, S, si, ChanTab{tab0}, &pk, &m);
-        }
-        if constexpr (BITS == 4) {
-          store_stream(reinterpret_cast<uint32_t*>(pt + (uint32_t)(rr * RB + 4 * cg)), pk);
-        } else {
-          store_stream(reinterpret_cast<uint16_t*>(pt + (uint32_t)(rr * RB + 2 * cg)), (uint16_t)pk);
+          ++o;
         }
       }
-      // lanes are in (row, channel) order, so the wave's exclusive count is
-      // the position in (row, col) order
-      uint32_t tot;
-      uint32_t pos = run + wave_excl_count_fused(__builtin_popcount(m), &tot);
-      run += tot;
-      if (rr < nv && cg == 0)
-        *reinterpret_cast<int32_t*>(reinterpret_cast<char*>(rpt) + 4u * (uint32_t)rr) = (int32_t)pos;
-      // pos counts the tile's outliers before this one, so pos < WT * D: every
-      // entry stays inside the tile's staging region
-      const uint16_t* xl = reinterpret_cast<const uint16_t*>(s_x + wv * 64 + lane);
-      const uint32_t colb = (uint32_t)(8 * cg) << 16;
-      uint32_t off = 4u * pos;
-      while (m) {
-        const int e = __builtin_ctz(m);
-        m &= m - 1u;
-        *reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(st) + off) =
-            (uint32_t)xl[e] | (colb + ((uint32_t)e << 16));
-        off += 4u;
-      }
+      if constexpr (STAGE) wave_sync();  // the slice is refilled for the next tile
     }
-    if (lane == 0) wt_cnt[wt] = run;
-    if constexpr (STAGE) wave_sync();  // the slice is refilled for the next tile
-  }
-}
 
-// The dense CSR, in one kernel after the stage kernel.  Block b owns the
-// wave tiles [b * tpb, (b + 1) * tpb) (tpb: a power of two from 32 to 256,
-// the smallest that keeps the grid within kCopyBlocks blocks, or 256).  Its
-// base is the sum of the counts of all earlier tiles, which it reads itself
-// (at most nwt counts, from L2: no separate scan kernel and no inter-block
-// waiting); its tiles' offsets are a block scan of their counts, one tile per
-// thread.  Each wave then copies a run of the block's tiles, requesting the
-// staged entries of several tiles (and the block's row_ptr entries) before
-// storing any, so a block waits on few memory round trips.  The last block
-// writes row_ptr[nrows] = nnz.
-constexpr int kCopyBlocks = 256;
-constexpr int kCopyThreads = 1024;
-constexpr int kCopyMaxTPB = 256;
-constexpr int kCopyU = 4;   // loads in flight per thread: prefix counts, row_ptr
-constexpr int kCopyTW = 4;  // tiles per wave and batch of staged-entry loads
-constexpr int kCopyUT = 4;  // staged-entry loads per lane and tile in a batch
+    // publish the chunk's count and take the next chunk (wave 0), then
+    // resolve and write the chunk held from the previous round
+    if (lane == 0) s_wtot[par][wv] = run;
+    __syncthreads();
+    if (wv == 0) {
+      uint32_t tot = 0;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) tot += s_wtot[par][w];
+      if (lane == 0) {
+        st_publish(status + c, st_word(epoch, k == 0 ? kStInc : kStAgg, tot));
+        s_next = __hip_atomic_fetch_add(hdr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    if (held) flush_held();  // its barrier also orders s_next
+    else __syncthreads();
+    held = true;
+    hc = c;
+    hk = k;
+    hj = j;
+    hbuf = buf;
+    hpar = par;
+    hwbeg = wbeg;
+    hnrw = nrw;
+    hrun = run;
+    c = s_next;
+    buf ^= 1;
+    par = par == 2 ? 0 : par + 1;
+  }
+  if (held) flush_held();
 
-HKV_DEV uint32_t wave_sum(uint32_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += (uint32_t)__shfl_xor((int)v, o, 64);
-  return v;
-}
-
-__global__ void __launch_bounds__(kCopyThreads)
-copy_kernel(const uint32_t* __restrict__ cnt, int64_t nwt, int tpb, int64_t WT, int64_t D,
-            int64_t nrows, const uint32_t* __restrict__ sent, int32_t* __restrict__ row_ptr,
-            uint8_t* __restrict__ col, uint16_t* __restrict__ val, uint32_t cap) {
-  constexpr int NW = kCopyThreads / 64;
-  __shared__ uint32_t s_off[kCopyMaxTPB + 1];
-  __shared__ uint32_t s_pre[NW], s_run[NW];
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int64_t t0 = (int64_t)blockIdx.x * tpb;
-  const int nt = (int)min<int64_t>(tpb, nwt - t0);
-  const uint32_t region = (uint32_t)(WT * D);  // staging capacity of a tile
-  // this block's tiles, one per thread, and the counts of all earlier tiles
-  // (t0 is a multiple of 4: whole 16-byte groups), all requested together
-  const uint32_t own = tid < nt ? min(cnt[t0 + tid], region) : 0u;
-  uint32_t pre = 0;
-  const uint4* c4 = reinterpret_cast<const uint4*>(cnt);
-  for (int64_t i0 = tid; i0 < t0 / 4; i0 += (int64_t)kCopyThreads * kCopyU) {
-    uint4 v[kCopyU];
-#pragma unroll
-    for (int u = 0; u < kCopyU; ++u) {
-      const int64_t i = i0 + (int64_t)u * kCopyThreads;
-      v[u] = i < t0 / 4 ? c4[i] : make_uint4(0u, 0u, 0u, 0u);
-    }
-#pragma unroll
-    for (int u = 0; u < kCopyU; ++u) pre += v[u].x + v[u].y + v[u].z + v[u].w;
-  }
-  pre = wave_sum(pre);
-  const uint32_t inc = wave_incl_sum_fused(own);
-  if (lane == 63) s_run[wv] = inc;
-  if (lane == 0) s_pre[wv] = pre;
-  __syncthreads();
-  uint32_t base = 0, before = inc - own;
-#pragma unroll
-  for (int w = 0; w < NW; ++w) {
-    base += s_pre[w];
-    before += w < wv ? s_run[w] : 0u;
-  }
-  if (tid < tpb) s_off[tid] = before;
-  if (tid == kCopyThreads - 1) s_off[tpb] = before + own;  // the block's total (tiles < tpb <= 256)
-  __syncthreads();
-  const uint32_t total = s_off[tpb];
-  const int64_t r0 = t0 * WT;
-  const uint32_t nr = (uint32_t)min<int64_t>(nrows - r0, (int64_t)nt * WT);
-  const uint32_t wt32 = (uint32_t)WT;
-  const uint32_t* src = sent + r0 * D;
-  auto put = [&](uint32_t o, uint32_t e) {
-    if (o < cap) {
-      col[o] = (uint8_t)(e >> 16);
-      val[o] = (uint16_t)e;
-    }
-  };
-  // row_ptr: the first kCopyU rows per thread are requested together with
-  // the first batch of entries; larger blocks loop over the rest
-  int32_t rv[kCopyU];
-#pragma unroll
-  for (int u = 0; u < kCopyU; ++u) {
-    const uint32_t i = tid + u * kCopyThreads;
-    rv[u] = i < nr ? row_ptr[r0 + i] : 0;
-  }
-  // entries: wave wv copies tiles [wv * tpw, (wv + 1) * tpw), kCopyTW tiles
-  // per batch, kCopyUT entries per lane and tile requested before any store
-  // (a tile with more entries finishes in a loop after the batch)
-  const int tpw = tpb / NW;  // 2 to 16
-  for (int m0 = 0; m0 < tpw; m0 += kCopyTW) {
-    uint32_t e[kCopyTW][kCopyUT];
-#pragma unroll
-    for (int m = 0; m < kCopyTW; ++m) {
-      const int j = wv * tpw + m0 + m;
-      const uint32_t n = (m0 + m < tpw && j < nt) ? s_off[j + 1] - s_off[j] : 0u;
-#pragma unroll
-      for (int u = 0; u < kCopyUT; ++u) {
-        const uint32_t i = lane + 64u * u;
-        e[m][u] = i < n ? src[(int64_t)j * region + i] : 0u;
-      }
-    }
-    if (m0 == 0) {
-#pragma unroll
-      for (int u = 0; u < kCopyU; ++u) {
-        const uint32_t i = tid + u * kCopyThreads;
-        if (i < nr) row_ptr[r0 + i] = rv[u] + (int32_t)(base + s_off[i / wt32]);
-      }
-    }
-#pragma unroll
-    for (int m = 0; m < kCopyTW; ++m) {
-      const int j = wv * tpw + m0 + m;
-      const bool own_tile = m0 + m < tpw && j < nt;
-      const uint32_t n = own_tile ? s_off[j + 1] - s_off[j] : 0u;
-      const uint32_t o0 = base + (own_tile ? s_off[j] : 0u);
-#pragma unroll
-      for (int u = 0; u < kCopyUT; ++u) {
-        const uint32_t i = lane + 64u * u;
-        if (i < n) put(o0 + i, e[m][u]);
-      }
-      for (uint32_t i = lane + 64u * kCopyUT; i < n; i += 64u) put(o0 + i, src[(int64_t)j * region + i]);
+  if (tid == 0) {
+    const uint32_t done = __hip_atomic_fetch_add(hdr + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (done == gridDim.x - 1u) {  // every block has taken its last chunk number
+      __hip_atomic_store(hdr + 0, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(hdr + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(hdr + 2, epoch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
-  for (uint32_t i0 = tid + kCopyU * kCopyThreads; i0 < nr; i0 += kCopyThreads * kCopyU) {
-#pragma unroll
-    for (int u = 0; u < kCopyU; ++u) {
-      const uint32_t i = i0 + u * kCopyThreads;
-      rv[u] = i < nr ? row_ptr[r0 + i] : 0;
-    }
-#pragma unroll
-    for (int u = 0; u < kCopyU; ++u) {
-      const uint32_t i = i0 + u * kCopyThreads;
-      if (i < nr) row_ptr[r0 + i] = rv[u] + (int32_t)(base + s_off[i / wt32]);
-    }
-  }
-  if (t0 + nt == nwt && tid == 0) row_ptr[nrows] = (int32_t)(base + total);
 }
 
 // Compact unpack.  Each wave owns a private LDS segment of kUPasses * RW
@@ -703,21 +874,7 @@ unpack_d128_kernel(const uint8_t* __restrict__ packed, const int32_t* __restrict
   }
 }
 
-__global__ void write_zero_rowptr(int32_t* row_ptr) { row_ptr[0] = 0; }
-
 bool pow2_G(int D) { return D % 8 == 0 && D >= 8 && D <= 256 && ((D / 8) & (D / 8 - 1)) == 0; }
-
-PackLayout pack_layout(int64_t nrows, int D, int passes) {
-  PackLayout L;
-  L.tile_rows = (int64_t)(64 / (D / 8)) * passes;
-  L.ntiles = (nrows + L.tile_rows - 1) / L.tile_rows;
-  L.tile_elems = L.tile_rows * D;
-  L.cnt_off = 256;
-  L.base_off = L.cnt_off + align256(sizeof(uint32_t) * (size_t)L.ntiles);
-  L.ent_off = L.base_off + align256(sizeof(uint32_t) * (size_t)(L.ntiles + 1));
-  L.bytes = L.ent_off + sizeof(uint32_t) * (size_t)(L.ntiles * L.tile_elems);
-  return L;
-}
 
 int num_cus() {
   static int n = 0;
@@ -741,55 +898,89 @@ unsigned resident_grid(K kernel, int64_t nblocks, size_t lds = 0) {
   return (unsigned)std::min<int64_t>(nblocks, (int64_t)per_cu * num_cus());
 }
 
-struct PackArgs {
-  const uint16_t* x;
-  int64_t nrows;
-  int H;
-  hkv_nuq_scales sc;
-  uint8_t* pk;
-  int32_t* rp;
-  uint32_t* sent;
-  uint32_t* cnt;
-  int64_t ntiles;  // wave tiles
+struct PackLaunch {
   hipStream_t s;
+  uint32_t* hdr;
+  uint64_t* status;
 };
 
 template <int NB, bool PT, int G, int BITS, bool KFIX>
-void launch_stage(const PackArgs& a) {
-  auto k = pack_stage_kernel<NB, PT, G, BITS, KFIX, pack_passes(PT, NB)>;
-  const int64_t nblocks = (a.ntiles + kThreads / 64 - 1) / (kThreads / 64);
-  hipLaunchKernelGGL(k, dim3(resident_grid(k, nblocks)), dim3(kThreads), 0, a.s, a.x, a.nrows,
-                     a.H, a.sc, a.pk, a.rp, a.sent, a.cnt, a.ntiles);
+void launch_fused(const PackBatch& b, const PackLaunch& l) {
+  auto k = pack_fused_kernel<NB, PT, G, BITS, KFIX, pack_passes(PT, NB)>;
+  hipLaunchKernelGGL(k, dim3(resident_grid(k, (int64_t)b.nchunks)), dim3(kThreads), 0, l.s, b, l.hdr,
+                     l.status);
 }
 
 template <int NB, bool PT, int BITS, bool KFIX>
-void launch_stage_g(int G, const PackArgs& a) {
+void launch_fused_g(int G, const PackBatch& b, const PackLaunch& l) {
   switch (G) {
-    case 1: launch_stage<NB, PT, 1, BITS, KFIX>(a); break;
-    case 2: launch_stage<NB, PT, 2, BITS, KFIX>(a); break;
-    case 4: launch_stage<NB, PT, 4, BITS, KFIX>(a); break;
-    case 8: launch_stage<NB, PT, 8, BITS, KFIX>(a); break;
-    case 16: launch_stage<NB, PT, 16, BITS, KFIX>(a); break;
-    default: launch_stage<NB, PT, 32, BITS, KFIX>(a); break;
+    case 1: launch_fused<NB, PT, 1, BITS, KFIX>(b, l); break;
+    case 2: launch_fused<NB, PT, 2, BITS, KFIX>(b, l); break;
+    case 4: launch_fused<NB, PT, 4, BITS, KFIX>(b, l); break;
+    case 8: launch_fused<NB, PT, 8, BITS, KFIX>(b, l); break;
+    case 16: launch_fused<NB, PT, 16, BITS, KFIX>(b, l); break;
+    default: launch_fused<NB, PT, 32, BITS, KFIX>(b, l); break;
   }
 }
 
 template <int NB, bool PT, int BITS>
-void launch_stage_k(bool kfix, int G, const PackArgs& a) {
-  if (kfix) launch_stage_g<NB, PT, BITS, true>(G, a);
-  else launch_stage_g<NB, PT, BITS, false>(G, a);
+void launch_fused_k(bool kfix, int G, const PackBatch& b, const PackLaunch& l) {
+  if (kfix) launch_fused_g<NB, PT, BITS, true>(G, b, l);
+  else launch_fused_g<NB, PT, BITS, false>(G, b, l);
 }
 
 template <bool PT, int BITS>
-void launch_stage_nb(int nb, bool kfix, int G, const PackArgs& a) {
+void launch_fused_nb(int nb, bool kfix, int G, const PackBatch& b, const PackLaunch& l) {
   switch (nb) {
-    case 0: launch_stage_k<0, PT, BITS>(kfix, G, a); break;
-    case 1: launch_stage_k<1, PT, BITS>(kfix, G, a); break;
-    case 2: launch_stage_k<2, PT, BITS>(kfix, G, a); break;
-    case 3: if constexpr (BITS == 4) launch_stage_k<3, PT, BITS>(kfix, G, a); break;
-    default: if constexpr (BITS == 4) launch_stage_k<4, PT, BITS>(kfix, G, a); break;
+    case 0: launch_fused_k<0, PT, BITS>(kfix, G, b, l); break;
+    case 1: launch_fused_k<1, PT, BITS>(kfix, G, b, l); break;
+    case 2: launch_fused_k<2, PT, BITS>(kfix, G, b, l); break;
+    case 3: if constexpr (BITS == 4) launch_fused_k<3, PT, BITS>(kfix, G, b, l); break;
+    default: if constexpr (BITS == 4) launch_fused_k<4, PT, BITS>(kfix, G, b, l); break;
   }
 }
+
+// The kernel variant of one item; items of equal keys share launches.
+struct PackKey {
+  int nb, pt, bits, G, kfix, H;
+  bool operator==(const PackKey& o) const {
+    return nb == o.nb && pt == o.pt && bits == o.bits && G == o.G && kfix == o.kfix && H == o.H;
+  }
+};
+
+int check_pack_item(const hkv_pack_item& a) {
+  const hkv_nuq_scales* sc = &a.scales;
+  if (!sc->tables || !sc->poles || !sc->upper || !sc->lower) return HKV_ERR_ARG;
+  if (a.bits != 2 && a.bits != 4) return HKV_ERR_ARG;
+  if (sc->levels < 1 || sc->levels > (1 << a.bits)) return HKV_ERR_ARG;
+  if (sc->per_token && sc->rows < 1) return HKV_ERR_SHAPE;
+  if (a.T < 0 || a.H < 1 || !pow2_G(a.D)) return HKV_ERR_SHAPE;
+  if (a.T * a.H * a.D >= ((int64_t)1 << 31)) return HKV_ERR_SHAPE;  // int32 row_ptr
+  if (a.capacity < 0) return HKV_ERR_ARG;
+  if (!a.row_ptr) return HKV_ERR_ARG;
+  if (a.T > 0) {
+    if (!a.values || !a.packed || (a.capacity > 0 && (!a.col || !a.val))) return HKV_ERR_ARG;
+    if (((uintptr_t)a.values & 15u) || ((uintptr_t)a.packed & 3u)) return HKV_ERR_ARG;
+  }
+  return HKV_OK;
+}
+
+PackKey pack_key(const hkv_pack_item& a) {
+  const int G = a.D / 8;
+  return PackKey{nb_for_levels_host(a.scales.levels), a.scales.per_token != 0, a.bits, G,
+                 (64 / G) % a.H == 0, a.H};
+}
+
+// Chunks of one item (at least one, so an empty tensor still gets row_ptr[0]).
+int64_t pack_item_chunks(const hkv_pack_item& a) {
+  const PackKey k = pack_key(a);
+  const int64_t cr = pack_chunk_rows(k.G, pack_passes(k.pt, k.nb));
+  const int64_t n = (a.T * a.H + cr - 1) / cr;
+  return n > 0 ? n : 1;
+}
+
+// Workspace bound: every chunk of every item (launches reuse the status words).
+size_t pack_ws_bytes(int64_t chunks) { return kPackHeader + 8 * (size_t)chunks; }
 
 template <bool PT, int BITS, bool KLDS>
 void launch_unpack_g(int G, unsigned grid, size_t lds, hipStream_t s, const uint8_t* pk,
@@ -811,66 +1002,99 @@ void launch_unpack_g(int G, unsigned grid, size_t lds, hipStream_t s, const uint
 
 extern "C" size_t hkv_nuq_pack_compact_workspace_bytes(int64_t T, int H, int D) {
   if (T < 0 || H < 1 || !pow2_G(D)) return 0;
-  // the larger of the two tilings (more tiles: more counts)
-  return std::max(pack_layout(T * H, D, 4).bytes, pack_layout(T * H, D, 8).bytes);
+  // every variant's chunks are at least NW * kPackWaveRows rows
+  const int64_t cr = (int64_t)(kThreads / 64) * kPackWaveRows;
+  const int64_t n = (T * H + cr - 1) / cr;
+  return pack_ws_bytes(n > 0 ? n : 1);
+}
+
+extern "C" size_t hkv_nuq_pack_compact_batch_workspace_bytes(const hkv_pack_item* items, int n) {
+  if (!items || n < 0) return 0;
+  int64_t chunks = 0;
+  for (int i = 0; i < n; ++i) {
+    if (items[i].T < 0 || items[i].H < 1 || !pow2_G(items[i].D)) return 0;
+    chunks += pack_item_chunks(items[i]);
+  }
+  return pack_ws_bytes(chunks > 0 ? chunks : 1);
+}
+
+extern "C" int hkv_nuq_pack_compact_batch(const hkv_pack_item* items, int n, void* workspace,
+                                          size_t workspace_bytes, void* stream) {
+  if (n < 0 || (n > 0 && !items)) return HKV_ERR_ARG;
+  if (n == 0) return HKV_OK;
+  for (int i = 0; i < n; ++i) {
+    const int st = check_pack_item(items[i]);
+    if (st != HKV_OK) return st;
+  }
+  if (!workspace || ((uintptr_t)workspace & 255u) ||
+      workspace_bytes < hkv_nuq_pack_compact_batch_workspace_bytes(items, n))
+    return HKV_ERR_WORKSPACE;
+  PackLaunch l;
+  l.s = (hipStream_t)stream;
+  l.hdr = (uint32_t*)workspace;
+  l.status = (uint64_t*)((char*)workspace + kPackHeader);
+  std::vector<char> done((size_t)n, 0);
+  for (int i0 = 0; i0 < n; ++i0) {
+    if (done[i0]) continue;
+    const PackKey key = pack_key(items[i0]);
+    // the items of this variant, in order, kPackItems per launch
+    PackBatch b;
+    b.n = 0;
+    b.H = key.H;
+    b.nchunks = 0;
+    for (int i = i0; i <= n; ++i) {
+      const bool take = i < n && !done[i] && pack_key(items[i]) == key;
+      if (take) {
+        const hkv_pack_item& a = items[i];
+        PackItem& p = b.it[b.n++];
+        p.x = (const uint16_t*)a.values;
+        p.packed = (uint8_t*)a.packed;
+        p.row_ptr = a.row_ptr;
+        p.col = a.col;
+        p.val = a.val;
+        p.sc = a.scales;
+        p.nrows = a.T * a.H;
+        p.chunk0 = b.nchunks;
+        p.cap = (uint32_t)std::min<int64_t>(a.capacity, 0x7fffffff);
+        b.nchunks += (uint32_t)pack_item_chunks(a);
+        done[i] = 1;
+      }
+      if (b.n > 0 && (b.n == kPackItems || i == n)) {
+        if (key.bits == 4) {
+          if (key.pt) launch_fused_nb<true, 4>(key.nb, key.kfix, key.G, b, l);
+          else launch_fused_nb<false, 4>(key.nb, key.kfix, key.G, b, l);
+        } else {
+          if (key.pt) launch_fused_nb<true, 2>(key.nb, key.kfix, key.G, b, l);
+          else launch_fused_nb<false, 2>(key.nb, key.kfix, key.G, b, l);
+        }
+        HKV_CHECK_LAUNCH();
+        b.n = 0;
+        b.nchunks = 0;
+      }
+    }
+  }
+  return HKV_OK;
 }
 
 extern "C" int hkv_nuq_pack_compact(const void* values, int64_t T, int H, int D, int bits,
                                     const hkv_nuq_scales* scales, void* packed, int32_t* row_ptr,
                                     uint8_t* col, uint16_t* val, int64_t capacity, void* workspace,
                                     size_t workspace_bytes, void* stream) {
-  if (!scales || !scales->tables || !scales->poles || !scales->upper || !scales->lower)
-    return HKV_ERR_ARG;
-  if (bits != 2 && bits != 4) return HKV_ERR_ARG;
-  if (scales->levels < 1 || scales->levels > (1 << bits)) return HKV_ERR_ARG;
-  if (scales->per_token && scales->rows < 1) return HKV_ERR_SHAPE;
-  if (T < 0 || H < 1 || !pow2_G(D)) return HKV_ERR_SHAPE;
-  if (T * H * D >= ((int64_t)1 << 31)) return HKV_ERR_SHAPE;  // int32 row_ptr
-  if (capacity < 0) return HKV_ERR_ARG;
-  if (!row_ptr) return HKV_ERR_ARG;
-  hipStream_t s = (hipStream_t)stream;
-  const int64_t nrows = T * H;
-  if (nrows == 0) {
-    hipLaunchKernelGGL(write_zero_rowptr, dim3(1), dim3(1), 0, s, row_ptr);
-    HKV_CHECK_LAUNCH();
-    return HKV_OK;
-  }
-  if (!values || !packed || (capacity > 0 && (!col || !val))) return HKV_ERR_ARG;
-  if (((uintptr_t)values & 15u) || ((uintptr_t)packed & 3u)) return HKV_ERR_ARG;
-  const PackLayout lay = pack_layout(nrows, D, pack_passes(scales->per_token != 0, nb_for_levels_host(scales->levels)));
-  if (!workspace || workspace_bytes < lay.bytes || ((uintptr_t)workspace & 255u))
-    return HKV_ERR_WORKSPACE;
-  const int G = D / 8, RW = 64 / G;
-  char* ws = (char*)workspace;
-  PackArgs a;
-  a.x = (const uint16_t*)values;
-  a.nrows = nrows;
+  if (!scales) return HKV_ERR_ARG;
+  hkv_pack_item a;
+  a.values = values;
+  a.T = T;
   a.H = H;
-  a.sc = *scales;
-  a.pk = (uint8_t*)packed;
-  a.rp = row_ptr;
-  a.sent = (uint32_t*)(ws + lay.ent_off);
-  a.cnt = (uint32_t*)(ws + lay.cnt_off);
-  a.ntiles = lay.ntiles;
-  a.s = s;
-  const bool kfix = (RW % H) == 0;
-  const int nb = nb_for_levels_host(a.sc.levels);
-  if (bits == 4) {
-    if (a.sc.per_token) launch_stage_nb<true, 4>(nb, kfix, G, a);
-    else launch_stage_nb<false, 4>(nb, kfix, G, a);
-  } else {
-    if (a.sc.per_token) launch_stage_nb<true, 2>(nb, kfix, G, a);
-    else launch_stage_nb<false, 2>(nb, kfix, G, a);
-  }
-  HKV_CHECK_LAUNCH();
-  const uint32_t cap = (uint32_t)std::min<int64_t>(capacity, 0x7fffffff);
-  int tpb = 32;
-  while (tpb < kCopyMaxTPB && (a.ntiles + tpb - 1) / tpb > kCopyBlocks) tpb *= 2;
-  const unsigned cgrid = (unsigned)((a.ntiles + tpb - 1) / tpb);
-  hipLaunchKernelGGL(copy_kernel, dim3(cgrid), dim3(kCopyThreads), 0, s, a.cnt, a.ntiles, tpb,
-                     lay.tile_rows, (int64_t)D, nrows, a.sent, row_ptr, col, val, cap);
-  HKV_CHECK_LAUNCH();
-  return HKV_OK;
+  a.D = D;
+  a.bits = bits;
+  a.reserved = 0;
+  a.scales = *scales;
+  a.packed = packed;
+  a.row_ptr = row_ptr;
+  a.col = col;
+  a.val = val;
+  a.capacity = capacity;
+  return hkv_nuq_pack_compact_batch(&a, 1, workspace, workspace_bytes, stream);
 }
 
 extern "C" int hkv_nuq_unpack_compact(const void* packed, const int32_t* row_ptr,

@@ -46,6 +46,16 @@ class NuqScales(ctypes.Structure):
     ]
 
 
+class PackItem(ctypes.Structure):
+    """Mirror of ``hkv_pack_item``."""
+
+    _fields_ = [
+        ("values", _p), ("T", _i64), ("H", ctypes.c_int32), ("D", ctypes.c_int32),
+        ("bits", ctypes.c_int32), ("reserved", ctypes.c_int32), ("scales", NuqScales),
+        ("packed", _p), ("row_ptr", _p), ("col", _p), ("val", _p), ("capacity", _i64),
+    ]
+
+
 class PagedSideDesc(ctypes.Structure):
     """Mirror of ``hkv_paged_side``."""
 
@@ -73,6 +83,8 @@ _SIGS = {
     "hkv_nuq_pack_compact_workspace_bytes": ([_i64, _i32, _i32], _sz),
     "hkv_nuq_pack_compact": ([_p, _i64, _i32, _i32, _i32, ctypes.POINTER(NuqScales), _p, _p, _p,
                               _p, _i64, _p, _sz, _p], _i32),
+    "hkv_nuq_pack_compact_batch_workspace_bytes": ([ctypes.POINTER(PackItem), _i32], _sz),
+    "hkv_nuq_pack_compact_batch": ([ctypes.POINTER(PackItem), _i32, _p, _sz, _p], _i32),
     "hkv_nuq_unpack_compact": ([_p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32,
                                 ctypes.POINTER(NuqScales), _p, _p], _i32),
     "hkv_nuq_quantize_generic": ([_i32, ctypes.POINTER(_i64), ctypes.POINTER(TensorDesc),

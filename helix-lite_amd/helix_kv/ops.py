@@ -251,6 +251,70 @@ def nuq_pack_compact(values: torch.Tensor, t: NuqLayerTables, bits: int, *,
                         val=out.val[:nnz], bits=bits, nnz=nnz)
 
 
+class CompactPackBatch:
+    """A prepared batch of compact packs (a prefill step: every layer's K and
+    V), launched by calling it: as few launches as the tensors' kernel
+    variants allow, each result identical to its own :func:`nuq_pack_compact`
+    call.  ``jobs`` is a sequence of (values, tables, bits, out) or (values,
+    tables, bits, out, positions, pos_offset) with caller-allocated ``out``
+    CompactCodes.  Nothing is read back (the caller compares each
+    out.row_ptr[-1] with its capacity when it next synchronises), so a call
+    can be captured in a HIP graph.  The tensors must stay alive while the
+    batch is in use."""
+
+    def __init__(self, jobs) -> None:
+        self.jobs = list(jobs)
+        self.n = len(self.jobs)
+        self.items = (N.PackItem * max(1, self.n))()
+        self._keep = []
+        dev = None
+        for i, job in enumerate(self.jobs):
+            values, t, bits, out = job[:4]
+            positions = job[4] if len(job) > 4 else None
+            pos_offset = job[5] if len(job) > 5 else 0
+            H, D = _HD(t, values)
+            _check_values(values, H, D)
+            if bits not in (2, 4):
+                raise AssertionError("bits must be 2 or 4")
+            if t.levels > (1 << bits):
+                raise AssertionError(f"{t.levels} levels do not fit in {bits} bits")
+            T = int(values.shape[0])
+            if out is None or out.shape != (T, H, D) or out.bits != bits or \
+                    out.row_ptr.numel() != T * H + 1:
+                raise AssertionError(f"job {i}: out must be CompactCodes of {(T, H, D)} at {bits} bits")
+            if dev is None:
+                dev = values.device
+            elif values.device != dev:
+                raise AssertionError("all tensors of a batch must be on one device")
+            pos = _positions(positions, T, values.device)
+            self._keep.append(pos)
+            it = self.items[i]
+            it.values = values.data_ptr()
+            it.T, it.H, it.D, it.bits = T, H, D, bits
+            it.scales = t.struct(pos, pos_offset)
+            it.packed = out.packed.data_ptr()
+            it.row_ptr = out.row_ptr.data_ptr()
+            it.col = out.col.data_ptr()
+            it.val = out.val.data_ptr()
+            it.capacity = min(int(out.col.numel()), int(out.val.numel()))
+        self.device = dev
+        self.ws_bytes = int(N.lib().hkv_nuq_pack_compact_batch_workspace_bytes(self.items, self.n)) \
+            if self.n else 0
+
+    def __call__(self) -> list[CompactCodes]:
+        if self.n:
+            ws = N.workspace("nuq_pack", self.ws_bytes, self.device)
+            st = N.lib().hkv_nuq_pack_compact_batch(self.items, self.n, N.ptr(ws), ws.numel(),
+                                                    N.stream_of(self.jobs[0][0]))
+            N.check(st, "hkv_nuq_pack_compact_batch", AssertionError)
+        return [job[3] for job in self.jobs]
+
+
+def nuq_pack_compact_batch(jobs) -> list[CompactCodes]:
+    """Prepare and launch a :class:`CompactPackBatch` once."""
+    return CompactPackBatch(jobs)()
+
+
 def nuq_unpack_compact(cc: CompactCodes, t: NuqLayerTables, *, positions=None, pos_offset: int = 0,
                        out: torch.Tensor | None = None) -> torch.Tensor:
     N.require_gpu(cc.packed, cc.row_ptr)

@@ -124,19 +124,47 @@ int hkv_nuq_unpack_dense(const void *codes, const void *outlier_v, const void *o
  * cannot know it).  bits = 2 or 4 (levels <= 2^bits).  Requires
  * scales->tables, D % 8 == 0, D <= 256.  The planned format of
  * src/kvquant/triton_kernels.py:7-18 and src/kvquant/compact_pool.py:11-12
- * (the reference never implemented it).  Two kernels on `stream`: a stage
- * kernel (codes, per-tile outlier counts, outliers staged per tile) and a
- * copy kernel that turns the counts into offsets and copies the staged
- * outliers into col/val.  `workspace` (256-byte aligned, no initialisation
- * needed) holds the counts and staged outliers:
- * hkv_nuq_pack_compact_workspace_bytes(T, H, D) bytes; calls that may overlap
- * must not share it.
+ * (the reference never implemented it).  One kernel on `stream`.
+ * `workspace` (256-byte aligned) holds a work counter and per-chunk status
+ * words: hkv_nuq_pack_compact_workspace_bytes(T, H, D) bytes, ZERO-FILLED
+ * before its first use and then passed unchanged to later calls (each call
+ * leaves its counters ready for the next; a workspace serves calls of any
+ * size up to the one it was sized for).  Word 3 of the workspace (uint32)
+ * becomes nonzero if a chunk ever gave up waiting for its predecessors'
+ * counts (a bounded wait that guards against a stalled device; not expected
+ * to happen).  Calls that may overlap must not share a workspace.
  */
 size_t hkv_nuq_pack_compact_workspace_bytes(int64_t T, int H, int D);
 int hkv_nuq_pack_compact(const void *values, int64_t T, int H, int D, int bits,
                          const hkv_nuq_scales *scales, void *packed, int32_t *row_ptr,
                          uint8_t *col, uint16_t *val, int64_t capacity, void *workspace,
                          size_t workspace_bytes, void *stream);
+
+/* One tensor of a batched compact pack: the arguments of hkv_nuq_pack_compact. */
+typedef struct hkv_pack_item {
+  const void *values;   /* (T,H,D) fp16 */
+  int64_t T;
+  int32_t H, D, bits, reserved;
+  hkv_nuq_scales scales;
+  void *packed;         /* (T,H,D*bits/8) u8 */
+  int32_t *row_ptr;     /* (T*H+1) */
+  uint8_t *col;
+  uint16_t *val;
+  int64_t capacity;
+} hkv_pack_item;
+
+/*
+ * Batched compact pack: n independent hkv_nuq_pack_compact calls (a prefill
+ * step: every layer's K and V) in as few launches as their kernel variants
+ * allow (one per variant and 16 tensors), each tensor's result identical to
+ * its own call.  Same workspace contract, sized by
+ * hkv_nuq_pack_compact_batch_workspace_bytes(items, n).  The batch form of
+ * the per-layer pack calls of the reference's prefill
+ * (src/kvquant/compact_pool.py:447-489, called per layer).
+ */
+size_t hkv_nuq_pack_compact_batch_workspace_bytes(const hkv_pack_item *items, int n);
+int hkv_nuq_pack_compact_batch(const hkv_pack_item *items, int n, void *workspace,
+                               size_t workspace_bytes, void *stream);
 
 /*
  * Compact unpack: packed codes + CSR -> out (T,H,D) fp16.  Inverse of

@@ -36,16 +36,11 @@ def test_host_only_entry_points():
     assert b"gfx950" in L.hkv_version()
     assert L.hkv_status_string(0) == b"ok"
     assert L.hkv_status_string(4) == b"output capacity too small"
-    # 256-byte header, one u32 count and one u32 base per wave tile (D = 128:
-    # sized for the smaller, 16-row tiles of per-channel 16-level tables; plus
-    # the final base), then a 4-byte staging entry per element, each region
-    # 256-aligned
-    ntiles = 131072 * 4 // 16
-    assert L.hkv_nuq_pack_compact_workspace_bytes(131072, 4, 128) == \
-        256 + 4 * ntiles + (4 * ntiles + 256) + 131072 * 4 * 128 * 4
-    # 40 rows = 2 wave tiles: header, counts and bases (each padded to 256),
-    # staging for 64 x 128
-    assert L.hkv_nuq_pack_compact_workspace_bytes(10, 4, 128) == 256 + 256 + 256 + 64 * 128 * 4
+    # 256-byte header (work counter, finished waves, epoch, error word), then
+    # one 8-byte status word per chunk (four waves of at least 128 rows)
+    assert L.hkv_nuq_pack_compact_workspace_bytes(131072, 4, 128) == 256 + 8 * (131072 * 4 // 512)
+    assert L.hkv_nuq_pack_compact_workspace_bytes(10, 4, 128) == 256 + 8
+    assert L.hkv_nuq_pack_compact_workspace_bytes(0, 4, 128) == 256 + 8
     assert L.hkv_nuq_pack_compact_workspace_bytes(10, 4, 100) == 0  # unsupported D
     assert L.hkv_quest_topk_workspace_bytes(65536, 4) >= 64
 
@@ -55,6 +50,9 @@ def test_struct_layouts_match_header():
 
     assert ctypes.sizeof(_native.NuqScales) == 4 * 8 + 4 * 4 + 8 + 8 + 8
     assert ctypes.sizeof(_native.TensorDesc) == 8 + 4 + 4 + 6 * 8
+    # hkv_pack_item: values, T, H/D/bits/reserved, scales, 4 pointers, capacity
+    assert ctypes.sizeof(_native.PackItem) == 8 + 8 + 16 + ctypes.sizeof(_native.NuqScales) + 32 + 8
+    assert _native.PackItem.scales.offset == 32
     assert "#define HKV_TABLE_BYTES 80" in HEADER.read_text()
     assert _native.TABLE_BYTES == 80
 

@@ -311,6 +311,85 @@ def test_compact_full_size_vs_oracle(dev, per_token, L, T):
     assert np.array_equal(_bits(cc.val), val)
 
 
+@pytest.mark.parametrize("per_token,L,thr", [(False, 16, 0.3), (True, 16, 0.3), (False, 4, 0.1),
+                                             (True, 4, 0.6)])
+def test_compact_dense_outliers_vs_oracle(dev, per_token, L, thr):
+    """Thresholds so tight that 30-90% of the elements are outliers: every
+    64-row chunk holds more outliers than its wave keeps in LDS, so the
+    entries past that are found again from the input after the chunk's
+    offset is known.  Every byte against the oracle, and the workspace's
+    error word stays zero."""
+    from helix_kv import _native as N
+    from helix_kv.ops import NuqLayerTables, nuq_pack_compact, pack_workspace
+
+    T, H, D = 3000, 4, 128
+    bits = 2 if L <= 4 else 4
+    x = RNG.standard_t(3, (T, H, D)).astype(np.float16)
+    rows = D if not per_token else 512
+    poles = np.sort(RNG.standard_normal((H, rows, L)), axis=-1).astype(np.float16)
+    up = RNG.uniform(thr, 2 * thr, (H, rows)).astype(np.float16)
+    t = NuqLayerTables(_t(poles, dev), _t(up, dev), _t(-up, dev), per_token=per_token)
+    cc = nuq_pack_compact(_t(x, dev), t, bits, capacity=T * H * D)
+    f32 = [a.astype(np.float32) for a in (poles, up, -up)]
+    if per_token:
+        wc, wv, wm = O.pack_v(x, *f32, positions=np.arange(T))
+    else:
+        wc, wv, wm = O.pack_k(x, *f32)
+    pk, rp, col, val = O.pack_compact(wc, wv, wm, bits)
+    assert cc.nnz == len(col) and cc.nnz / x.size > 0.25
+    assert np.array_equal(cc.row_ptr.cpu().numpy(), rp)
+    assert np.array_equal(cc.packed.cpu().numpy(), pk)
+    assert np.array_equal(cc.col.cpu().numpy(), col)
+    assert np.array_equal(_bits(cc.val), val)
+    ws = pack_workspace(T, H, D, dev)
+    assert int(ws[12:16].view(torch.int32).item()) == 0  # no look-back gave up
+
+
+def test_compact_batch_equals_single_calls(dev):
+    """One hkv_nuq_pack_compact_batch over tensors of all four kernel
+    variants, several heads counts and sizes (including an empty tensor and
+    more tensors of one variant than a launch takes): each result is
+    identical to its own hkv_nuq_pack_compact call; two against the oracle."""
+    from helix_kv.ops import CompactCodes, NuqLayerTables, nuq_pack_compact, nuq_pack_compact_batch
+
+    rng = np.random.default_rng(5)
+    D = 128
+    specs = [(False, 16, 4, 3000), (True, 4, 4, 2000), (False, 4, 4, 1), (True, 16, 4, 0),
+             (False, 16, 2, 700), (True, 16, 4, 1500)] + [(False, 4, 4, 100 + 37 * i) for i in range(18)]
+    jobs, singles, host = [], [], []
+    for per_token, L, H, T in specs:
+        bits = 2 if L <= 4 else 4
+        x = rng.standard_t(3, (T, H, D)).astype(np.float16)
+        rows = D if not per_token else 1024
+        poles = np.sort(rng.standard_normal((H, rows, L)), axis=-1).astype(np.float16)
+        up = rng.uniform(1.2, 2.5, (H, rows)).astype(np.float16)
+        t = NuqLayerTables(_t(poles, dev), _t(up, dev), _t(-up, dev), per_token=per_token)
+        xd = _t(x, dev)
+        cap = max(64, T * H * D // 4)
+        jobs.append((xd, t, bits, CompactCodes.empty(T, H, D, bits, cap, dev)))
+        singles.append(nuq_pack_compact(xd, t, bits, capacity=cap))
+        host.append((x, poles, up, per_token, bits))
+    outs = nuq_pack_compact_batch(jobs)
+    torch.cuda.synchronize()
+    for cc, ref in zip(outs, singles):
+        n = int(cc.row_ptr[-1].item())
+        assert n == ref.nnz
+        assert torch.equal(cc.packed, ref.packed) and torch.equal(cc.row_ptr, ref.row_ptr)
+        assert torch.equal(cc.col[:n], ref.col[:n]) and torch.equal(cc.val[:n], ref.val[:n])
+    for i in (0, 1):
+        x, poles, up, per_token, bits = host[i]
+        f32 = [a.astype(np.float32) for a in (poles, up, -up)]
+        if per_token:
+            wc, wv, wm = O.pack_v(x, *f32, positions=np.arange(x.shape[0]))
+        else:
+            wc, wv, wm = O.pack_k(x, *f32)
+        pk, rp, col, val = O.pack_compact(wc, wv, wm, bits)
+        cc = outs[i]
+        assert np.array_equal(cc.packed.cpu().numpy(), pk) and np.array_equal(cc.row_ptr.cpu().numpy(), rp)
+        n = len(col)
+        assert np.array_equal(cc.col[:n].cpu().numpy(), col) and np.array_equal(_bits(cc.val[:n]), val)
+
+
 @pytest.mark.parametrize("H,per_token,L,T", [(1, False, 16, 257), (2, False, 4, 129), (8, False, 16, 333),
                                           (8, True, 16, 333), (16, True, 4, 77), (2, True, 16, 5)])
 def test_compact_unpack_heads_and_positions(dev, H, per_token, L, T):
