@@ -29,9 +29,9 @@ constexpr int kThreads = 256;
 __host__ __device__ constexpr int pack_passes(bool per_token, int nb) { return (!per_token && nb < 4) ? 8 : 4; }
 
 constexpr int kPackItems = 16;                 // tensors per fused pack launch
-constexpr int kPackWaveRows = 128;             // least rows a wave packs per chunk
+constexpr int kPackWaveRows = 128;             // least rows a wave packs per chunk (per-token: half)
 constexpr uint32_t kPackSpinLimit = 1u << 20;  // look-back rounds without progress before giving up
-constexpr int kPackLookWindows = 16;           // look-back windows of 64 chunks read at once
+constexpr int kPackLookWindows = 8;            // look-back windows of 64 chunks read at once
 constexpr size_t kPackHeader = 256;            // workspace header bytes
 
 // One tensor of a fused pack launch (kernel argument, by value).
@@ -53,20 +53,23 @@ struct PackBatch {
   uint32_t nchunks;
 };
 
-// Rows a wave packs per chunk: whole wave tiles, at least kPackWaveRows.  A
-// chunk is NW such parts, one per wave of a block.
+// Rows a wave packs per chunk: whole wave tiles, at least kPackWaveRows
+// (per-token scales: half as many, so the two chunks' outliers a wave holds
+// leave room for five blocks per CU).  A chunk is NW such parts, one per wave
+// of a block.
 __host__ __device__ constexpr int pack_tile_rows(int G, int passes) { return (64 / G) * passes; }
-__host__ __device__ constexpr int pack_wave_rows(int G, int passes) {
-  return pack_tile_rows(G, passes) >= kPackWaveRows ? pack_tile_rows(G, passes) : kPackWaveRows;
+__host__ __device__ constexpr int pack_wave_rows(int G, int passes, bool per_token) {
+  return pack_tile_rows(G, passes) >= (per_token ? kPackWaveRows / 2 : kPackWaveRows)
+             ? pack_tile_rows(G, passes)
+             : (per_token ? kPackWaveRows / 2 : kPackWaveRows);
 }
-__host__ __device__ constexpr int pack_chunk_rows(int G, int passes) {
-  return (kThreads / 64) * pack_wave_rows(G, passes);
+__host__ __device__ constexpr int pack_chunk_rows(int G, int passes, bool per_token) {
+  return (kThreads / 64) * pack_wave_rows(G, passes, per_token);
 }
-// Outliers of its part of a chunk a wave holds in LDS: one in ten elements
-// (per-token scales: one in thirteen, so four blocks fit a CU's LDS); a part
-// with more writes the rest when its chunk is flushed (pack_redo_rows).
+// Outliers of its part of a chunk a wave holds in LDS (one in ten elements);
+// a part with more writes the rest when its chunk is flushed (pack_redo_rows).
 __host__ __device__ constexpr int pack_ent_cap(int G, int passes, bool per_token) {
-  return (pack_wave_rows(G, passes) * 8 * G / (per_token ? 13 : 10) + 63) & ~63;
+  return (pack_wave_rows(G, passes, per_token) * 8 * G / 10 + 63) & ~63;
 }
 
 HKV_DEV void wave_sync() {
@@ -155,6 +158,14 @@ HKV_DEV void pack_redo_rows(const PackItem& it, int H, int64_t rbeg, int nrc, co
   }
 }
 
+// The exact-scan inputs of a batch item, loaded where the rare exact scan
+// needs them.
+struct ItemSlow {
+  const PackBatch* b;
+  int j;
+  HKV_DEV SlowInfo get() const { return slow_info(b->it[opaque_s(j)].sc); }
+};
+
 // Fused pack.  A launch packs up to kPackItems tensors of one kernel variant.
 // Their rows are cut into chunks of CR rows, numbered consecutively over the
 // tensors.  A block takes the next chunk number from the work counter (one
@@ -190,11 +201,11 @@ pack_fused_kernel(const PackBatch B, uint32_t* __restrict__ hdr, uint64_t* __res
   constexpr int D = 8 * G;
   constexpr int RB = D * BITS / 8;  // packed bytes per row
   constexpr int NW = kThreads / 64;
-  constexpr int WR = pack_wave_rows(G, PASSES);  // rows of a wave's part of a chunk
+  constexpr int WR = pack_wave_rows(G, PASSES, PT);  // rows of a wave's part of a chunk
   constexpr int CR = NW * WR;
   constexpr int CT = WR / WT;                     // wave tiles per part
   constexpr int ECAP = pack_ent_cap(G, PASSES, PT);
-  static_assert(WR % WT == 0 && CR == pack_chunk_rows(G, PASSES), "a part is whole wave tiles");
+  static_assert(WR % WT == 0 && CR == pack_chunk_rows(G, PASSES, PT), "a part is whole wave tiles");
   // Per-token tables of a wave tile's rows are staged in the wave's LDS slice
   // when they fit in 4 KiB (D >= 128), already in search form (each
   // breakpoint and threshold duplicated into both 16-bit halves: words 0..14
@@ -282,19 +293,21 @@ pack_fused_kernel(const PackBatch B, uint32_t* __restrict__ hdr, uint64_t* __res
   if (tid == 0) s_next = __hip_atomic_fetch_add(hdr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
   uint32_t c = s_next;
-  // the held chunk (packed, offset not yet known)
+  // the held chunk (packed, offset not yet known): its number; it sits in
+  // LDS buffer buf ^ 1 and its wave counts in s_wtot[(par + 2) % 3]
   bool held = false;
-  uint32_t hc = 0, hk = 0;
-  int hj = 0, hbuf = 0, hpar = 0;
-  int64_t hwbeg = 0;
-  int hnrw = 0;
-  uint32_t hrun = 0;
+  uint32_t hc = 0;
   int buf = 0, par = 0;
 
   // Resolve the held chunk's offset (wave 0), then every wave writes its part.
   auto flush_held = [&]() {
+    const int hbuf = buf ^ 1, hpar = par == 0 ? 2 : par - 1;
+    int hj = 0;
+    while (hj + 1 < B.n && hc >= B.it[hj + 1].chunk0) ++hj;
+    hj = opaque_s(hj);
+    const PackItem& ih = B.it[hj];
+    const uint32_t hk = hc - ih.chunk0;
     if (wv == 0) {
-      const PackItem& ih = B.it[opaque_s(hj)];
       uint32_t tot = 0;
 #pragma unroll
       for (int w = 0; w < NW; ++w) tot += s_wtot[hpar][w];
@@ -306,7 +319,10 @@ pack_fused_kernel(const PackBatch B, uint32_t* __restrict__ hdr, uint64_t* __res
       if (lane == 0) s_base = base;
     }
     __syncthreads();
-    const PackItem& ih = B.it[opaque_s(hj)];
+    const int64_t hwbeg = (int64_t)hk * CR + (int64_t)wv * WR;
+    const int64_t hrest = ih.nrows - hwbeg;
+    const int hnrw = hrest <= 0 ? 0 : (hrest < WR ? (int)hrest : WR);
+    const uint32_t hrun = s_wtot[hpar][wv];
     uint32_t base = s_base;
 #pragma unroll
     for (int w = 0; w < NW; ++w) base += w < wv ? s_wtot[hpar][w] : 0u;
@@ -336,7 +352,7 @@ pack_fused_kernel(const PackBatch B, uint32_t* __restrict__ hdr, uint64_t* __res
     const PackItem& it = B.it[j];
     const hkv_nuq_scales sc = it.sc;
     const hkv_table_t* tabs = (const hkv_table_t*)sc.tables;
-    const SlowInfo si = slow_info(sc);
+    const ItemSlow si{&B, j};
     const int H = B.H;
     const int64_t nrows = it.nrows;
     const uint32_t k = c - it.chunk0;
@@ -442,7 +458,7 @@ pack_fused_kernel(const PackBatch B, uint32_t* __restrict__ hdr, uint64_t* __res
             } else {
               load_search_bcast<NB>(tabs + tab(0), S[0]);
             }
-            quant8_packed<NB, PT, BITS>(xv, S, si, tab, &pk, &m);
+            quant8_packed<NB, PT, BITS, RowTabAt, false, ItemSlow>(xv, S, si, tab, &pk, &m);
           } else {
             const int64_t tab0 = (int64_t)h * D + 8 * cg;
             if constexpr (!KFIX) {
@@ -450,8 +466,8 @@ pack_fused_kernel(const PackBatch B, uint32_t* __restrict__ hdr, uint64_t* __res
               for (int q = 0; q < 4; ++q)
                 load_search_pair<NB>(tabs + tab0 + 2 * q, tabs + tab0 + 2 * q + 1, S[q]);
             }
-            if constexpr (KFIX) quant8_packed<NB, PT, BITS, ChanTab, true>(xv, S, si, ChanTab{tab0}, &pk, &m, xmin);
-            else quant8_packed<NB, PT, BITS>(xv, S, si, ChanTab{tab0}, &pk, &m);
+            if constexpr (KFIX) quant8_packed<NB, PT, BITS, ChanTab, true, ItemSlow>(xv, S, si, ChanTab{tab0}, &pk, &m, xmin);
+            else quant8_packed<NB, PT, BITS, ChanTab, false, ItemSlow>(xv, S, si, ChanTab{tab0}, &pk, &m);
           }
           if constexpr (BITS == 4) {
             store_stream(reinterpret_cast<uint32_t*>(pt + (uint32_t)(rr * RB + 4 * cg)), pk);
@@ -500,13 +516,6 @@ pack_fused_kernel(const PackBatch B, uint32_t* __restrict__ hdr, uint64_t* __res
     else __syncthreads();
     held = true;
     hc = c;
-    hk = k;
-    hj = j;
-    hbuf = buf;
-    hpar = par;
-    hwbeg = wbeg;
-    hnrw = nrw;
-    hrun = run;
     c = s_next;
     buf ^= 1;
     par = par == 2 ? 0 : par + 1;
@@ -974,7 +983,7 @@ PackKey pack_key(const hkv_pack_item& a) {
 // Chunks of one item (at least one, so an empty tensor still gets row_ptr[0]).
 int64_t pack_item_chunks(const hkv_pack_item& a) {
   const PackKey k = pack_key(a);
-  const int64_t cr = pack_chunk_rows(k.G, pack_passes(k.pt, k.nb));
+  const int64_t cr = pack_chunk_rows(k.G, pack_passes(k.pt, k.nb), k.pt);
   const int64_t n = (a.T * a.H + cr - 1) / cr;
   return n > 0 ? n : 1;
 }
@@ -1002,8 +1011,8 @@ void launch_unpack_g(int G, unsigned grid, size_t lds, hipStream_t s, const uint
 
 extern "C" size_t hkv_nuq_pack_compact_workspace_bytes(int64_t T, int H, int D) {
   if (T < 0 || H < 1 || !pow2_G(D)) return 0;
-  // every variant's chunks are at least NW * kPackWaveRows rows
-  const int64_t cr = (int64_t)(kThreads / 64) * kPackWaveRows;
+  // every variant's chunks are at least NW * kPackWaveRows / 2 rows
+  const int64_t cr = (int64_t)(kThreads / 64) * (kPackWaveRows / 2);
   const int64_t n = (T * H + cr - 1) / cr;
   return pack_ws_bytes(n > 0 ? n : 1);
 }

@@ -21,6 +21,15 @@ HKV_DEV SlowInfo slow_info(const hkv_nuq_scales& s) {
   return SlowInfo{s.poles, s.upper, s.lower, s.poles_dtype, s.thr_dtype, s.levels};
 }
 
+// The exact-scan inputs of a call site: a SlowInfo itself, or an object
+// whose get() loads them where the rare exact scan needs them (so they are
+// not held in registers across a kernel's main loop).
+HKV_DEV const SlowInfo& slow_get(const SlowInfo& s) { return s; }
+template <typename L>
+HKV_DEV SlowInfo slow_get(const L& l) {
+  return l.get();
+}
+
 HKV_DEV int64_t clamp_row(int64_t pos, int64_t rows) {
   return pos > rows - 1 ? rows - 1 : (pos < 0 ? 0 : pos);
 }
@@ -203,8 +212,8 @@ HKV_DEV constexpr uint32_t posm(int j) { return (1u << (2 * j)) | (1u << (16 + 2
 // the 8 elements is within xmin, the smallest bound of the 8 tables (see
 // xsafe_min), instead of comparing each pair with its own bounds.  Never less
 // exact: the scan decides whatever the fast path does not.
-template <int NB, bool PT, int BITS, typename TabFn, bool XMIN = false>
-HKV_DEV void quant8_packed(const uint4 xv, const Search2<NB>* S, const SlowInfo& si, TabFn tab,
+template <int NB, bool PT, int BITS, typename TabFn, bool XMIN = false, typename SI = SlowInfo>
+HKV_DEV void quant8_packed(const uint4 xv, const Search2<NB>* S, const SI& slow, TabFn tab,
                            uint32_t* packed, uint32_t* mask8, uint32_t xmin = 0) {
   const uint32_t x[4] = {xv.x, xv.y, xv.z, xv.w};
   uint32_t uns = 0;
@@ -252,6 +261,7 @@ HKV_DEV void quant8_packed(const uint4 xv, const Search2<NB>* S, const SlowInfo&
       *packed = BITS == 4 ? pack_nibbles(c) : pack_crumbs(c);
     }
   } else {
+    const SlowInfo si = slow_get(slow);
     uint32_t c[4], om[4];
 #pragma unroll 1
     for (int j = 0; j < 4; ++j) {
