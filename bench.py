@@ -280,8 +280,8 @@ def cpu_baseline(dev, layers=(0, 16), chunks: int = 3) -> dict:
 
 
 def bench_nuq(args, dev):
-    from helix_kv.ops import (CompactCodes, CompactPackBatch, NuqLayerTables, nuq_pack_compact,
-                              nuq_unpack_compact)
+    from helix_kv.ops import (CompactCodes, CompactPackBatch, CompactUnpackBatch, NuqLayerTables,
+                              nuq_pack_compact, nuq_unpack_compact)
 
     log(f"[bench] generating {LAYERS} layers of K/V ({T_TOK}x{H}x{D} fp16)")
     layers = []
@@ -310,6 +310,13 @@ def bench_nuq(args, dev):
     packs = pack_launches()
     batch = CompactPackBatch([(Ld[x], Ld[t], Ld["bits"], Ld[c]) for Ld in layers
                               for x, t, c in (("K", "kt", "ck"), ("V", "vt", "cv"))])
+    # the same step as its four launches, one per kernel variant, each timed
+    # on its own (the roofline unit)
+    variants = {}
+    for Ld in layers:
+        for name, x, t, c in (("K", "K", "kt", "ck"), ("V", "V", "vt", "cv")):
+            variants.setdefault(f"{name} nuq{Ld['bits']}", []).append((Ld[x], Ld[t], Ld["bits"], Ld[c]))
+    vbatches = {k: CompactPackBatch(v) for k, v in variants.items()}
 
     def step_single():
         for f in packs:
@@ -336,6 +343,22 @@ def bench_nuq(args, dev):
     ms = time_events(step, args.steps)
     pack_gbs = algo / (ms * 1e-3) / 1e9
     single_ms = time_events(step_single, args.steps)
+    # per-launch durations: each variant's launch event-timed on its own, the
+    # mean over args.steps rounds
+    vms = {k: 0.0 for k in vbatches}
+    for _ in range(args.steps):
+        for k, d in zip(vbatches, per_launch_ms(list(vbatches.values()))):
+            vms[k] += d / args.steps
+    vbytes = {}
+    for k, jobs in variants.items():
+        n = sum(x.numel() for x, _, _, _ in jobs)
+        b = jobs[0][2]
+        rows = sum(x.shape[0] * x.shape[1] for x, _, _, _ in jobs)
+        vnnz = sum(int(c.row_ptr[-1].item()) for _, _, _, c in jobs)
+        sb = sum(scale_bytes((t.poles, t.upper, t.lower)) for _, t, _, _ in jobs)
+        vbytes[k] = n * 2 + n * b // 8 + (rows + len(jobs)) * 4 + 3 * vnnz + sb
+    log("[bench] pack launches: " + ", ".join(
+        f"{k} {vms[k] * 1e3:.0f} us ({vbytes[k] / (vms[k] * 1e-3) / 1e9:.0f} GB/s)" for k in vms))
     durs = per_launch_ms(packs)
     kern_ms = sum(durs)
     log(f"[bench] pack: {ms:.3f} ms/step, {pack_gbs:.0f} GB/s (one batched call); 56 single calls "
@@ -347,9 +370,15 @@ def bench_nuq(args, dev):
         unpacks.append(lambda Ld=Ld, ok=ok: nuq_unpack_compact(Ld["ck"], Ld["kt"], out=ok))
         unpacks.append(lambda Ld=Ld, ov=ov: nuq_unpack_compact(Ld["cv"], Ld["vt"], out=ov))
 
-    def ustep():
+    ubatch = CompactUnpackBatch([(Ld[c], Ld[t], o) for Ld, oo in zip(layers, outs)
+                                 for (c, t), o in zip((("ck", "kt"), ("cv", "vt")), oo)])
+
+    def ustep_single():
         for f in unpacks:
             f()
+
+    def ustep():
+        ubatch()
 
     for _ in range(max(1, args.warmup)):
         ustep()
@@ -367,12 +396,24 @@ def bench_nuq(args, dev):
                 raise RuntimeError(f"round trip of layer {li} {name}: {bad} elements differ")
     ums = time_events(ustep, args.steps)
     unpack_gbs = algo / (ums * 1e-3) / 1e9
+    # ceilings on the same GPU for comparison: torch's fill of an fp16 tensor
+    # the size of one layer's K (write only) and its copy (read + write)
+    buf = torch.empty_like(layers[0]["K"])
+    fill_ms = time_events(lambda: buf.zero_(), 20)
+    copy_ms = time_events(lambda: buf.copy_(layers[0]["K"]), 20)
+    ceil = dict(fill_GBps=buf.numel() * 2 / (fill_ms * 1e-3) / 1e9,
+                copy_GBps=buf.numel() * 4 / (copy_ms * 1e-3) / 1e9)
+    del buf
+    log(f"[bench] ceilings: fill {ceil['fill_GBps']:.0f} GB/s, copy {ceil['copy_GBps']:.0f} GB/s (read + write)")
+    ums_single = time_events(ustep_single, args.steps)
     udurs = per_launch_ms(unpacks)
-    log(f"[bench] unpack: {ums:.3f} ms/step, {unpack_gbs:.0f} GB/s; kernels {sum(udurs):.3f} ms")
+    log(f"[bench] unpack: {ums:.3f} ms/step, {unpack_gbs:.0f} GB/s (one batched call); 56 single calls "
+        f"{ums_single:.3f} ms/step, kernels {sum(udurs):.3f} ms")
     del outs
     return dict(pack_ms=ms, pack_gbs=pack_gbs, pack_kernel_ms=kern_ms, algo_bytes=algo, nnz=nnz,
                 unpack_ms=ums, unpack_gbs=unpack_gbs, unpack_kernel_ms=sum(udurs),
-                launches=len(packs))
+                launches=len(packs), single_ms=single_ms, variant_ms=vms, variant_bytes=vbytes,
+                unpack_single_ms=ums_single, ceilings=ceil)
 
 
 def bench_quest(args, dev):
@@ -1075,19 +1116,30 @@ def main() -> None:
                    "nuq2_layers": CUT, "t_cal": T_CAL},
     }
     if "pack_gbs" in res:
-        n_l = res["launches"]
-        ach = res["algo_bytes"] / (res["pack_kernel_ms"] * 1e-3)
+        vms, vb = res["variant_ms"], res["variant_bytes"]
+        n_l = len(vms)
+        launch_ms = sum(vms.values()) / n_l
+        ach = sum(vb.values()) / (sum(vms.values()) * 1e-3)
         line["roofline"] = {"bound": "hbm", "achieved": round(ach / 1e9, 1), "peak": HBM_PEAK / 1e9,
                             "unit": "GB/s", "frac": round(ach / HBM_PEAK, 4),
                             "traffic": profiled_traffic(PACK_PROFILE),
-                            "kernel": "hkv_nuq_pack_compact call (stage + copy kernels), "
-                                      f"{n_l} calls per step, event-timed one by one",
-                            "algorithmic_bytes_per_launch": round(res["algo_bytes"] / n_l),
-                            "launch_us": round(res["pack_kernel_ms"] * 1e3 / n_l, 2),
+                            "kernel": "pack_fused_kernel: one launch per kernel variant (K / V at "
+                                      f"nuq2 / nuq4) over its layers, {n_l} launches per step, each "
+                                      "event-timed on its own",
+                            "algorithmic_bytes_per_launch": round(sum(vb.values()) / n_l),
+                            "launch_us": round(launch_ms * 1e3, 2),
+                            "launches": {k: {"us": round(vms[k] * 1e3, 1),
+                                             "GBps": round(vb[k] / (vms[k] * 1e-3) / 1e9, 1)} for k in vms},
                             "traffic_source": PACK_PROFILE}
-        uach = res["algo_bytes"] / (res["unpack_kernel_ms"] * 1e-3)
+        line["pack_single_calls_ms_per_step"] = round(res["single_ms"], 4)
         line["unpack"] = {"GBps": round(res["unpack_gbs"], 2), "ms_per_step": round(res["unpack_ms"], 4),
-                          "kernel_GBps": round(uach / 1e9, 1), "frac": round(uach / HBM_PEAK, 4)}
+                          "frac": round(res["unpack_gbs"] * 1e9 / HBM_PEAK, 4),
+                          "single_calls_ms_per_step": round(res["unpack_single_ms"], 4),
+                          "write_ceiling_GBps": round(res["ceilings"]["fill_GBps"], 1),
+                          "copy_ceiling_GBps": round(res["ceilings"]["copy_GBps"], 1),
+                          "vs_write_ceiling": round(res["unpack_gbs"] / res["ceilings"]["fill_GBps"], 4),
+                          "rate": "algorithmic bytes of the step's 56 unpacks / the event-timed duration "
+                                  "of one batched call (4 launches)"}
         line["outliers_nnz"] = res["nnz"]
     if "quest_us" in res:
         qach = res["quest_algo_bytes"] / (res["quest_us"] * 1e-6)

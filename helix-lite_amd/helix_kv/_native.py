@@ -56,6 +56,16 @@ class PackItem(ctypes.Structure):
     ]
 
 
+class UnpackItem(ctypes.Structure):
+    """Mirror of ``hkv_unpack_item``."""
+
+    _fields_ = [
+        ("packed", _p), ("row_ptr", _p), ("col", _p), ("val", _p), ("capacity", _i64), ("T", _i64),
+        ("H", ctypes.c_int32), ("D", ctypes.c_int32), ("bits", ctypes.c_int32),
+        ("reserved", ctypes.c_int32), ("scales", NuqScales), ("out", _p),
+    ]
+
+
 class PagedSideDesc(ctypes.Structure):
     """Mirror of ``hkv_paged_side``."""
 
@@ -85,6 +95,7 @@ _SIGS = {
                               _p, _i64, _p, _sz, _p], _i32),
     "hkv_nuq_pack_compact_batch_workspace_bytes": ([ctypes.POINTER(PackItem), _i32], _sz),
     "hkv_nuq_pack_compact_batch": ([ctypes.POINTER(PackItem), _i32, _p, _sz, _p], _i32),
+    "hkv_nuq_unpack_compact_batch": ([ctypes.POINTER(UnpackItem), _i32, _p], _i32),
     "hkv_nuq_unpack_compact": ([_p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32,
                                 ctypes.POINTER(NuqScales), _p, _p], _i32),
     "hkv_nuq_quantize_generic": ([_i32, ctypes.POINTER(_i64), ctypes.POINTER(TensorDesc),

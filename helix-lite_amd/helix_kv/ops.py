@@ -333,6 +333,47 @@ def nuq_unpack_compact(cc: CompactCodes, t: NuqLayerTables, *, positions=None, p
     return out
 
 
+class CompactUnpackBatch:
+    """A prepared batch of compact unpacks, launched by calling it: as few
+    launches as the tensors' kernel variants allow, each result identical to
+    its own :func:`nuq_unpack_compact` call.  ``jobs`` is a sequence of
+    (cc, tables, out) or (cc, tables, out, positions, pos_offset) with
+    caller-allocated fp16 ``out`` (T,H,D).  The tensors must stay alive while
+    the batch is in use."""
+
+    def __init__(self, jobs) -> None:
+        self.jobs = list(jobs)
+        self.n = len(self.jobs)
+        self.items = (N.UnpackItem * max(1, self.n))()
+        self._keep = []
+        for i, job in enumerate(self.jobs):
+            cc, t, out = job[:3]
+            positions = job[3] if len(job) > 3 else None
+            pos_offset = job[4] if len(job) > 4 else 0
+            N.require_gpu(cc.packed, cc.row_ptr, out)
+            T, H, D = cc.shape
+            if tuple(out.shape) != (T, H, D) or out.dtype != torch.float16 or not out.is_contiguous():
+                raise AssertionError(f"job {i}: out must be contiguous fp16 {(T, H, D)}")
+            pos = _positions(positions, T, cc.packed.device)
+            self._keep.append(pos)
+            it = self.items[i]
+            it.packed = cc.packed.data_ptr()
+            it.row_ptr = cc.row_ptr.data_ptr()
+            it.col = cc.col.data_ptr()
+            it.val = cc.val.data_ptr()
+            it.capacity = min(int(cc.col.numel()), int(cc.val.numel()))
+            it.T, it.H, it.D, it.bits = T, H, D, cc.bits
+            it.scales = t.struct(pos, pos_offset)
+            it.out = out.data_ptr()
+
+    def __call__(self) -> list[torch.Tensor]:
+        if self.n:
+            st = N.lib().hkv_nuq_unpack_compact_batch(self.items, self.n,
+                                                      N.stream_of(self.jobs[0][2]))
+            N.check(st, "hkv_nuq_unpack_compact_batch", AssertionError)
+        return [job[2] for job in self.jobs]
+
+
 # ------------------------------------------------------------------ Quest
 
 def _fdt(t: torch.Tensor) -> int:

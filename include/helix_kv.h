@@ -176,6 +176,29 @@ int hkv_nuq_unpack_compact(const void *packed, const int32_t *row_ptr, const uin
                            const uint16_t *val, int64_t capacity, int64_t T, int H, int D,
                            int bits, const hkv_nuq_scales *scales, void *out, void *stream);
 
+/* One tensor of a batched compact unpack: the arguments of hkv_nuq_unpack_compact. */
+typedef struct hkv_unpack_item {
+  const void *packed;
+  const int32_t *row_ptr;
+  const uint8_t *col;
+  const uint16_t *val;
+  int64_t capacity;
+  int64_t T;
+  int32_t H, D, bits, reserved;
+  hkv_nuq_scales scales;
+  void *out;            /* (T,H,D) fp16 */
+} hkv_unpack_item;
+
+/*
+ * Batched compact unpack: n independent hkv_nuq_unpack_compact calls in as
+ * few launches as their kernel variants allow (one per variant and 16
+ * tensors; the launch's blocks are shared among the tensors in proportion to
+ * their rows), each result identical to its own call.  No workspace.  The
+ * batch form of the per-layer dequantisation the reference runs for every
+ * layer (src/kvquant/triton_batched.py:151-171, :306-326).
+ */
+int hkv_nuq_unpack_compact_batch(const hkv_unpack_item *items, int n, void *stream);
+
 /*
  * Broadcasting quantise with the CPU spec's dtype semantics: over a shape of
  * up to 6 dims, code = first argmin_l |round_cdt(v - pole_l)| (NaN differences

@@ -376,6 +376,12 @@ def test_compact_batch_equals_single_calls(dev):
         assert n == ref.nnz
         assert torch.equal(cc.packed, ref.packed) and torch.equal(cc.row_ptr, ref.row_ptr)
         assert torch.equal(cc.col[:n], ref.col[:n]) and torch.equal(cc.val[:n], ref.val[:n])
+    # the batched unpack of the same tensors equals the single-tensor unpack
+    from helix_kv.ops import CompactUnpackBatch, nuq_unpack_compact
+    ujobs = [(cc, job[1], torch.empty_like(job[0])) for cc, job in zip(outs, jobs)]
+    CompactUnpackBatch(ujobs)()
+    for (cc, t, out), job in zip(ujobs, jobs):
+        assert torch.equal(out.view(torch.int16), nuq_unpack_compact(cc, t).view(torch.int16))
     for i in (0, 1):
         x, poles, up, per_token, bits = host[i]
         f32 = [a.astype(np.float32) for a in (poles, up, -up)]
