@@ -518,7 +518,11 @@ extern "C" int hkv_nuq_unpack_compact_batch(const hkv_unpack_item* items, int n,
   for (int i0 = 0; i0 < n; ++i0) {
     if (done[i0]) continue;
     const hkv_unpack_item& a0 = items[i0];
-    if (!batchable(a0)) {  // the single-tensor path
+    // the single-tensor path: shapes the batched kernel does not take, and
+    // per-token tensors, whose pole rows are read through L2 (the rows of a
+    // whole batch in flight at once overflow it: 46 us a tensor batched
+    // against 42.7 us alone for V nuq2 at 131072 x 4 x 128)
+    if (!batchable(a0) || a0.scales.per_token) {
       done[i0] = 1;
       const int st = hkv_nuq_unpack_compact(a0.packed, a0.row_ptr, a0.col, a0.val, a0.capacity, a0.T,
                                             a0.H, a0.D, a0.bits, &a0.scales, a0.out, stream);
@@ -528,7 +532,7 @@ extern "C" int hkv_nuq_unpack_compact_batch(const hkv_unpack_item* items, int n,
     const int pt = a0.scales.per_token != 0, bits = a0.bits, H = a0.H;
     std::vector<int> grp;
     for (int i = i0; i < n; ++i)
-      if (!done[i] && batchable(items[i]) && (items[i].scales.per_token != 0) == pt &&
+      if (!done[i] && batchable(items[i]) && !items[i].scales.per_token &&
           items[i].bits == bits && items[i].H == H) {
         grp.push_back(i);
         done[i] = 1;

@@ -190,10 +190,11 @@ typedef struct hkv_unpack_item {
 } hkv_unpack_item;
 
 /*
- * Batched compact unpack: n independent hkv_nuq_unpack_compact calls in as
- * few launches as their kernel variants allow (one per variant and 16
- * tensors; the launch's blocks are shared among the tensors in proportion to
- * their rows), each result identical to its own call.  No workspace.  The
+ * Batched compact unpack: n independent hkv_nuq_unpack_compact calls, each
+ * result identical to its own call.  Per-channel (K) tensors share launches
+ * (one per variant and 16 tensors; the launch's blocks are split among the
+ * tensors in proportion to their rows); per-token (V) tensors are launched
+ * one by one, since their pole rows are read through L2.  No workspace.  The
  * batch form of the per-layer dequantisation the reference runs for every
  * layer (src/kvquant/triton_batched.py:151-171, :306-326).
  */
