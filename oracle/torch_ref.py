@@ -147,3 +147,24 @@ def topk_pages_with_sinks(bound, k: int, sink_pages: int = 1):
     top = torch.topk(masked, k=k_eff, dim=0)
     selected = torch.cat([sink_idx, top.indices], dim=0)
     return selected.sort(dim=0).values
+
+
+def selected_attention(query, K_pages, V_pages, page_indices):
+    """Per head h: scores = (K_h @ q_h) * D^-0.5 in the query's dtype, fp32
+    softmax cast back to the query's dtype, then attn @ V_{h % H_v}.
+    src/quest/reference.py:136-168 (same op sequence, same dtypes)."""
+    import math
+
+    P, page_size, H, D = K_pages.shape
+    Hv, Dv = V_pages.shape[2], V_pages.shape[3]
+    n = page_indices.shape[0]
+    out = torch.zeros(H, Dv, dtype=query.dtype)
+    scale = 1.0 / math.sqrt(D)
+    for h in range(H):
+        idx = page_indices[:, h]
+        Kh = K_pages[idx, :, h, :].reshape(n * page_size, D)
+        Vh = V_pages[idx, :, h % Hv, :].reshape(n * page_size, Dv)
+        scores = (Kh @ query[h]) * scale
+        attn = torch.softmax(scores.float(), dim=0).to(query.dtype)
+        out[h] = attn @ Vh
+    return out
