@@ -670,8 +670,8 @@ def bench_calibration(args, dev):
     (src/kvquant/calibration.py:45-59): K from 32 prompts x 4096 tokens
     (131072 x 4 x 128), V (32, 4096, 4, 128), nuq2 and nuq4, 0.5 % outlier
     thresholds, 5000-value subsample; 512 + 16384 fits per layer, all on the
-    GPU (sorted quantiles, device compaction, one hkv_kmeans_1d launch per
-    side).  Beside it, the reference's own fit (sklearn KMeans, n_init=3,
+    GPU (sorted quantiles, device compaction, one hkv_kmeans_1d_optimal launch
+    per side: the exact k-means optimum of each subsample).  Beside it, the reference's own fit (sklearn KMeans, n_init=3,
     max_iter=20, calibration.py:106-123) timed on a sample of the same
     problems on the host, one problem at a time as the reference runs them."""
     import time
@@ -682,7 +682,7 @@ def bench_calibration(args, dev):
     t3 = torch.distributions.StudentT(torch.tensor(3.0, device=dev))
     K = (t3.sample((32 * 4096, H, D)) * torch.exp(0.5 * torch.randn((1, H, D), device=dev))).half()
     V = t3.sample((32, 4096, H, D)).half()
-    out, poles = {}, {}
+    out, poles, thr = {}, {}, {}
     for bits in (2, 4):
         cfg = CalibrationConfig(num_bits=bits)
         calibrate_keys(K, cfg)   # first use at these sizes: sort and allocator set-up
@@ -696,6 +696,8 @@ def bench_calibration(args, dev):
         assert torch.isfinite(ks.poles).all() and torch.isfinite(vs.poles).all()
         poles[bits] = ([ks.poles[0, d].cpu().numpy() for d in range(8)] +
                        [vs.poles[0, t].cpu().numpy() for t in range(24)])
+        thr[bits] = ([(float(ks.lower_threshold[0, d]), float(ks.upper_threshold[0, d])) for d in range(8)] +
+                     [(float(vs.lower_threshold[0, t]), float(vs.upper_threshold[0, t])) for t in range(24)])
     # the reference's fit on a sample of problems: 8 K channels and 24 V positions
     from sklearn.cluster import KMeans
 
@@ -707,7 +709,7 @@ def bench_calibration(args, dev):
     for t in range(24):
         sample.append(Vc[:, t, :].reshape(-1))
     rng = np.random.default_rng(0)
-    fit_s, ratio = {}, {}
+    fit_s, ratio, same = {}, {}, {}
 
     def inertia(x, c):
         return float(np.min((x.astype(np.float64)[:, None] - np.asarray(c, np.float64)[None, :]) ** 2,
@@ -731,14 +733,28 @@ def bench_calibration(args, dev):
             m = x[(x >= lo) & (x <= up)]
             r.append(inertia(m, ours) / inertia(m, ref))
         ratio[bits] = (float(np.mean(r)), float(np.max(r)))
+        # the same comparison on the values the GPU fit saw (the calibration's
+        # seeded permutation, the first 5000 in-threshold values): sklearn
+        # fitted on exactly those, both scored on them
+        r2 = []
+        for i, (x, ours) in enumerate(zip(sample, poles[bits])):
+            perm = torch.randperm(x.size, generator=torch.Generator().manual_seed(0)).numpy()
+            lo, up = thr[bits][i]
+            xp = x[perm]
+            sub = xp[(xp >= lo) & (xp <= up)][:5000]
+            km = KMeans(n_clusters=2 ** bits, n_init=3, max_iter=20, random_state=0)
+            ref = km.fit(sub.reshape(-1, 1)).cluster_centers_.ravel()
+            r2.append(inertia(sub, ours) / inertia(sub, ref))
+        same[bits] = (float(np.mean(r2)), float(np.max(r2)))
     log(f"[bench] calibration per layer: GPU nuq2 {out[2]:.1f} ms, nuq4 {out[4]:.1f} ms; "
         f"reference fit on the host (estimated from {len(sample)} problems) "
         f"{fit_s[2]:.0f} s / {fit_s[4]:.0f} s; inertia GPU / sklearn mean (max) "
-        f"nuq2 {ratio[2][0]:.3f} ({ratio[2][1]:.3f}), nuq4 {ratio[4][0]:.3f} ({ratio[4][1]:.3f})")
+        f"nuq2 {ratio[2][0]:.3f} ({ratio[2][1]:.3f}), nuq4 {ratio[4][0]:.3f} ({ratio[4][1]:.3f}); "
+        f"on the same values nuq2 {same[2][0]:.4f} ({same[2][1]:.4f}), nuq4 {same[4][0]:.4f} ({same[4][1]:.4f})")
     del K, V
     torch.cuda.empty_cache()
     return dict(cal_ms={b: out[b] for b in out}, cal_cpu_s=fit_s, cal_sample=len(sample),
-                cal_ratio=ratio)
+                cal_ratio=ratio, cal_ratio_same=same)
 
 
 def bench_roundtrip(args, dev):
@@ -1182,10 +1198,13 @@ def main() -> None:
             "cpu_sample_problems": res["cal_sample"],
             "inertia_vs_reference_fit": {f"nuq{b}": {"mean": round(v[0], 4), "max": round(v[1], 4)}
                                          for b, v in res["cal_ratio"].items()},
+            "inertia_vs_reference_fit_same_values": {
+                f"nuq{b}": {"mean": round(v[0], 5), "max": round(v[1], 5)}
+                for b, v in res["cal_ratio_same"].items()},
             "config": "one layer at the reference's default calibration config: K (131072, 4, "
                       "128) and V (32, 4096, 4, 128) fp16 Student-t(3), 0.5% thresholds, "
                       "5000-value subsample, 512 + 16384 fits; GPU: quantiles, compaction "
-                      "and hkv_kmeans_1d (order-statistic start, 50 Lloyd steps); host: "
+                      "and hkv_kmeans_1d_optimal (exact 1-D k-means by dynamic programming); host: "
                       "sklearn KMeans(n_init=3, max_iter=20) per problem as the reference "
                       "runs it, timed on a sample and scaled to the layer's problems"}
     if "dec_step_us" in res:

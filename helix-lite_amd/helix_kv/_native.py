@@ -145,6 +145,8 @@ _SIGS = {
                               ctypes.POINTER(NuqScales), _i32, _i32, ctypes.POINTER(_i64),
                               ctypes.POINTER(_i64), _p, _p, _p], _i32),
     "hkv_kmeans_1d": ([_p, _p, _i64, _i32, _i32, _p, _p], _i32),
+    "hkv_kmeans_1d_optimal_workspace_bytes": ([], _sz),
+    "hkv_kmeans_1d_optimal": ([_p, _p, _i64, _i32, _p, _p, _sz, _p], _i32),
     "hkv_selected_attention_workspace_bytes": ([_i64, _i32, _i32, _i32], _sz),
     "hkv_selected_attention": ([_p, _i32, _i32, _i32, _p, _p, _i32, _i64, _i32, _i32, _i32, _i32,
                                 _p, _i64, _i32, _i32, ctypes.c_float, _p, _i32, _p, _sz, _p], _i32),

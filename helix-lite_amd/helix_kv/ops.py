@@ -851,3 +851,24 @@ def kmeans_1d(values: torch.Tensor, offsets: torch.Tensor, k: int, iters: int = 
                                N.stream_of(v))
     N.check(st, "hkv_kmeans_1d", ValueError)
     return centers
+
+
+def kmeans_1d_optimal(values: torch.Tensor, offsets: torch.Tensor, k: int) -> torch.Tensor:
+    """Batched optimal 1-D k-means (hkv_kmeans_1d_optimal): the problems of
+    :func:`kmeans_1d`, each solved exactly by dynamic programming over its
+    sorted values (at most 6144 values a problem; larger ones give NaN).
+    Returns (n, k) fp32 centres sorted ascending."""
+    N.require_gpu(values, offsets)
+    if values.dim() != 1 or offsets.dim() != 1 or offsets.numel() < 1:
+        raise ValueError("values must be (N,) and offsets (n + 1,)")
+    v = values.to(torch.float32).contiguous()
+    if v.numel() == 0:
+        v = torch.zeros(1, dtype=torch.float32, device=values.device)
+    off = offsets.to(torch.int64).contiguous()
+    n = int(off.numel()) - 1
+    centers = torch.empty((n, int(k)), dtype=torch.float32, device=values.device)
+    ws = N.workspace("kmeans_dp", int(N.lib().hkv_kmeans_1d_optimal_workspace_bytes()), v.device)
+    st = N.lib().hkv_kmeans_1d_optimal(N.ptr(v), N.ptr(off), n, int(k), N.ptr(centers), N.ptr(ws),
+                                       ws.numel(), N.stream_of(v))
+    N.check(st, "hkv_kmeans_1d_optimal", ValueError)
+    return centers

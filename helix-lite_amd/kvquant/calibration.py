@@ -18,8 +18,11 @@ steps are this build's own and differ from the reference's:
   - the subsample keeps, per problem, the first kmeans_subsample in-threshold
     values in one seeded permutation of the sample axis (the reference draws
     rng.choice per problem);
-  - the fit starts at order statistics and takes kmeans_iters Lloyd steps
-    (hkv_kmeans_1d), where sklearn runs k-means++ with 3 restarts.
+  - the fit is the exact optimum of the k-means objective on the subsample
+    (hkv_kmeans_1d_optimal: dynamic programming over the sorted values), so
+    its inertia is never above that of sklearn's k-means++ with 3 restarts;
+    kmeans_fit="lloyd" (or a subsample above 6144) takes kmeans_iters Lloyd
+    steps from order statistics instead (hkv_kmeans_1d).
 Model loading and the dataset (run_calibration) need network access and are
 not part of this build.
 """
@@ -29,15 +32,20 @@ from dataclasses import dataclass
 
 import torch
 
-from helix_kv.ops import kmeans_1d
+from helix_kv.ops import kmeans_1d, kmeans_1d_optimal
 
 from .scales import PerChannelScale, PerTokenScale
+
+
+OPTIMAL_MAX = 6144  # the largest problem the exact fit takes
 
 
 @dataclass
 class CalibrationConfig:
     """The reference's fields (src/kvquant/calibration.py:45-59) plus the
-    number of Lloyd steps of the GPU fit."""
+    GPU fit: "optimal" (exact 1-D k-means by dynamic programming,
+    hkv_kmeans_1d_optimal, for kmeans_subsample <= 6144) or "lloyd"
+    (kmeans_iters Lloyd steps from order statistics, hkv_kmeans_1d)."""
 
     model_name: str = "Qwen/Qwen2.5-7B-Instruct-1M"
     num_prompts: int = 32
@@ -54,6 +62,7 @@ class CalibrationConfig:
     log_every_n_layers: int = 1
     progress_log_path: str | None = None
     kmeans_iters: int = 50
+    kmeans_fit: str = "optimal"
 
 
 def row_quantiles(X: torch.Tensor, q: float) -> torch.Tensor:
@@ -94,7 +103,13 @@ def _fit_rows(X: torch.Tensor, cfg: CalibrationConfig):
     offsets = torch.zeros(R + 1, dtype=torch.int64, device=X.device)
     offsets[1:] = torch.cumsum(counts, dim=0)
     values = Xp[keep]
-    poles = kmeans_1d(values, offsets, 2 ** int(cfg.num_bits), int(cfg.kmeans_iters))
+    k = 2 ** int(cfg.num_bits)
+    if cfg.kmeans_fit == "optimal" and int(cfg.kmeans_subsample) <= OPTIMAL_MAX:
+        poles = kmeans_1d_optimal(values, offsets, k)
+    elif cfg.kmeans_fit in ("optimal", "lloyd"):
+        poles = kmeans_1d(values, offsets, k, int(cfg.kmeans_iters))
+    else:
+        raise ValueError(f"kmeans_fit must be 'optimal' or 'lloyd', got {cfg.kmeans_fit!r}")
     return poles, up, lo
 
 

@@ -585,6 +585,22 @@ int hkv_selected_attention(const void *q, int q_dtype, int Hq, int D, const void
 int hkv_kmeans_1d(const float *values, const int64_t *offsets, int64_t n_problems, int k,
                   int iters, float *centers, void *stream);
 
+/*
+ * Optimal batched 1-D k-means: the same problems and output as
+ * hkv_kmeans_1d, solved exactly by dynamic programming over the sorted values
+ * (least within-cluster sum of squares; partial costs rounded to fp32 per DP
+ * row, the leftmost split wins ties), so the fit is never worse than any
+ * k-means run, the reference's sklearn fit included (src/kvquant/
+ * calibration.py:106-123).  Problems of at most 6144 values (the calibration
+ * subsample is 5000); larger ones get NaN centres.  `workspace` holds each
+ * resident block's split table: hkv_kmeans_1d_optimal_workspace_bytes()
+ * bytes for a full grid (less runs fewer blocks at once; at least one
+ * block's 184,320 bytes).
+ */
+size_t hkv_kmeans_1d_optimal_workspace_bytes(void);
+int hkv_kmeans_1d_optimal(const float *values, const int64_t *offsets, int64_t n_problems, int k,
+                          float *centers, void *workspace, size_t workspace_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -66,6 +66,8 @@ def _declare(L: ctypes.CDLL) -> None:
     L.orc_page_bound_group.argtypes = [_p, _p, _p, _i64, _i32, _i32, _i32, _p]
     L.orc_topk_sinks.argtypes = [_p, _i64, _i32, _i64, _i64, _p]
     L.orc_topk_sinks.restype = _i64
+    L.orc_kmeans_dp.argtypes = [_p, _i64, _i32, _p]
+    L.orc_kmeans_dp.restype = _i32
 
 
 def _ptr(a: np.ndarray | None):
@@ -578,6 +580,17 @@ def kmeans_1d(values, k: int, iters: int):
         m = np.bincount(idx, minlength=k)
         c = np.where(m > 0, (s / np.maximum(m, 1)).astype(np.float32), c).astype(np.float32)
     return np.sort(c)
+
+
+def kmeans_optimal(values, k: int) -> np.ndarray:
+    """One 1-D k-means problem solved exactly (orc_kmeans_dp: dynamic
+    programming over every split of the sorted values) -> k fp32 centres,
+    ascending.  The objective of sklearn's KMeans in
+    src/kvquant/calibration.py:106-123, minimised globally."""
+    v = np.ascontiguousarray(np.asarray(values, np.float32).reshape(-1))
+    out = np.empty(k, np.float32)
+    lib().orc_kmeans_dp(v.ctypes.data if v.size else None, v.size, k, out.ctypes.data)
+    return out
 
 
 def kmeans_inertia(values, centers) -> float:

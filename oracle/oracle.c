@@ -527,3 +527,104 @@ int64_t orc_topk_sinks(const float *bound, int64_t P, int H, int64_t k,
     free(sel);
     return s + keff;
 }
+
+/* Optimal 1-D k-means of n fp32 values into k clusters (the calibration fit
+ * of the f4 row, solving the objective sklearn's KMeans approximates in
+ * src/kvquant/calibration.py:106-123).  Dynamic programming over the sorted
+ * values (Wang & Song 2011): D[0][i] = cost(0, i), D[m][i] = min over
+ * m <= j <= i of D[m-1][j-1] + cost(j, i), with cost(j, i) the sum of squared
+ * deviations of x[j..i] from their mean, from fp64 prefix sums.  Every
+ * candidate j is tried (no monotone-argmin shortcut); D rows are rounded to
+ * fp32, the leftmost minimum wins, rows m < k-1 cover i up to n-1-(k-1-m)
+ * and the last row only i = n-1.  The prefix sums follow the device's order:
+ * the sorted values cut into 256 chunks of ceil(n / 256), each chunk summed
+ * in order from the sum of the earlier chunks' totals (themselves summed in
+ * order).  centers: the clusters' means, fl32(fp64 sum / count), ascending.
+ * n < k: the values and k - n zeros, sorted (calibration.py:116-119).
+ * Returns 0, or -1 for n > 6144 (centres NaN). */
+static int cmp_f32(const void *a, const void *b)
+{
+    float x = *(const float *)a, y = *(const float *)b;
+    return (x > y) - (x < y);
+}
+
+int orc_kmeans_dp(const float *values, int64_t n64, int k, float *centers)
+{
+    if (n64 > 6144) {
+        for (int l = 0; l < k; l++) centers[l] = NAN;
+        return -1;
+    }
+    int n = (int)n64;
+    float *x = malloc(sizeof(float) * (size_t)(n > k ? n : k));
+    for (int i = 0; i < n; i++) x[i] = values[i];
+    if (n < k) {
+        for (int i = n; i < k; i++) x[i] = 0.0f;
+        qsort(x, (size_t)k, sizeof(float), cmp_f32);
+        for (int l = 0; l < k; l++) centers[l] = x[l];
+        free(x);
+        return 0;
+    }
+    qsort(x, (size_t)n, sizeof(float), cmp_f32);
+    double *S1 = malloc(sizeof(double) * (size_t)(n + 1));
+    double *S2 = malloc(sizeof(double) * (size_t)(n + 1));
+    int per = (n + 255) / 256;
+    double b1 = 0.0, b2 = 0.0;  /* totals of the earlier chunks */
+    S1[0] = 0.0;
+    S2[0] = 0.0;
+    for (int t = 0; t < 256; t++) {
+        int i0 = t * per, i1 = i0 + per < n ? i0 + per : n;
+        double c1 = b1, c2 = b2, a1 = 0.0, a2 = 0.0;
+        for (int i = i0; i < i1; i++) {
+            double v = (double)x[i];
+            c1 += v;
+            c2 += v * v;
+            a1 += v;
+            a2 += v * v;
+            S1[i + 1] = c1;
+            S2[i + 1] = c2;
+        }
+        b1 += a1;
+        b2 += a2;
+    }
+    float *Dp = malloc(sizeof(float) * (size_t)n), *Dc = malloc(sizeof(float) * (size_t)n);
+    int *opt = malloc(sizeof(int) * (size_t)k * (size_t)n);
+    for (int i = 0; i < n; i++) {
+        double s = S1[i + 1], q = S2[i + 1];
+        Dp[i] = (float)(q - s * s / (double)(i + 1));
+    }
+    int last = k - 1;
+    for (int m = 1; m <= last; m++) {
+        int ilo = m == last ? n - 1 : m, ihi = n - 1 - (last - m);
+        for (int i = ilo; i <= ihi; i++) {
+            double best = INFINITY;
+            int bj = -1;
+            for (int j = m; j <= i; j++) {
+                double s = S1[i + 1] - S1[j], q = S2[i + 1] - S2[j];
+                double c = (double)Dp[j - 1] + (q - s * s / (double)(i - j + 1));
+                if (c < best) {
+                    best = c;
+                    bj = j;
+                }
+            }
+            Dc[i] = (float)best;
+            opt[(size_t)m * (size_t)n + (size_t)i] = bj;
+        }
+        float *t = Dp;
+        Dp = Dc;
+        Dc = t;
+    }
+    int i = n - 1;
+    for (int m = last; m >= 1; m--) {
+        int j = opt[(size_t)m * (size_t)n + (size_t)i];
+        centers[m] = (float)((S1[i + 1] - S1[j]) / (double)(i - j + 1));
+        i = j - 1;
+    }
+    centers[0] = (float)(S1[i + 1] / (double)(i + 1));
+    free(x);
+    free(S1);
+    free(S2);
+    free(Dp);
+    free(Dc);
+    free(opt);
+    return 0;
+}

@@ -42,6 +42,30 @@ def test_kmeans_vs_oracle(dev, k, iters, dist):
         assert np.array_equal(got[i], O.kmeans_1d(p, k, iters)), (i, sizes[i])
 
 
+@pytest.mark.parametrize("k,dist", [(4, "normal"), (16, "t3"), (1, "t3"), (3, "normal"), (16, "normal")])
+def test_kmeans_optimal_vs_oracle(dev, k, dist):
+    """hkv_kmeans_1d_optimal against the oracle's exhaustive DP: bit-exact
+    centres for problems of every size class (empty, fewer than k, exactly k,
+    up to the 6144-value limit, and past it: NaN), and values with ties."""
+    from helix_kv.ops import kmeans_1d_optimal
+
+    sizes = [0, 1, k - 1 if k > 1 else 0, k, 17, 100, 2000, 5000, 6144, 6145, 4096]
+    parts, vals, off = _ragged(sizes, dist)
+    # a problem with many ties: values on a coarse grid
+    tie = (np.round(RNG.standard_normal(1500) * 4) / 4).astype(np.float32)
+    parts.append(tie)
+    vals = np.concatenate([vals, tie])
+    off = np.concatenate([off, [off[-1] + tie.size]]).astype(np.int64)
+    got = kmeans_1d_optimal(torch.from_numpy(vals).to(dev), torch.from_numpy(off).to(dev), k)
+    got = got.cpu().numpy()
+    for i, p in enumerate(parts):
+        want = O.kmeans_optimal(p, k)
+        if p.size > 6144:
+            assert np.isnan(got[i]).all(), i
+        else:
+            assert np.array_equal(got[i], want), (i, p.size, got[i], want)
+
+
 def _oracle_rows(X, cfg):
     n = X.shape[1]
     up = np.quantile(X, 1 - cfg.outlier_pct, axis=1)   # float32 rows, as the reference
@@ -51,7 +75,10 @@ def _oracle_rows(X, cfg):
     for r in range(X.shape[0]):
         x = X[r, perm]
         inside = x[(x >= lo[r]) & (x <= up[r])][: cfg.kmeans_subsample]
-        poles.append(O.kmeans_1d(inside, 2 ** cfg.num_bits, cfg.kmeans_iters))
+        if cfg.kmeans_fit == "optimal":
+            poles.append(O.kmeans_optimal(inside, 2 ** cfg.num_bits))
+        else:
+            poles.append(O.kmeans_1d(inside, 2 ** cfg.num_bits, cfg.kmeans_iters))
     return np.stack(poles), up, lo
 
 

@@ -78,3 +78,70 @@ def test_row_quantiles_match_numpy():
             want = np.quantile(X, q, axis=1)
             assert want.dtype == np.float32
             assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (n, q)
+
+
+# ------------------------------------------------- the optimal fit (default)
+
+def _sse(v: np.ndarray, labels: np.ndarray, k: int) -> float:
+    s = 0.0
+    for l in range(k):
+        m = v[labels == l].astype(np.float64)
+        if m.size:
+            s += float(((m - m.mean()) ** 2).sum())
+    return s
+
+
+@pytest.mark.parametrize("n,k,seed", [(7, 2, 0), (8, 3, 1), (9, 3, 2), (6, 4, 3)])
+def test_optimal_equals_brute_force_over_all_assignments(n, k, seed):
+    """Every assignment of n values to k labels (k^n of them, no contiguity
+    assumed): the least sum of squared deviations equals the oracle fit's
+    inertia."""
+    import itertools
+
+    rng = np.random.default_rng(seed)
+    v = rng.standard_normal(n).astype(np.float32)
+    best = min(_sse(v, np.array(lab), k) for lab in itertools.product(range(k), repeat=n)
+               if len(set(lab)) == k)
+    got = O.kmeans_inertia(v, O.kmeans_optimal(v, k))
+    assert abs(got - best) <= 1e-6 * max(1.0, best)
+
+
+@pytest.mark.parametrize("dist,k", [("normal", 4), ("normal", 16), ("t3clip", 4), ("t3clip", 16)])
+def test_optimal_never_worse_than_sklearn_or_lloyd(dist, k):
+    """The calibration's problems (5000 in-threshold values): the optimal fit
+    is at most sklearn's KMeans(n_init=3, max_iter=20) inertia (the
+    reference's fit, calibration.py:121) and at most the Lloyd fit's."""
+    from sklearn.cluster import KMeans
+
+    for rep in range(3):
+        x = RNG.standard_normal(5000) if dist == "normal" else RNG.standard_t(3, 5000)
+        if dist == "t3clip":
+            lo, up = np.quantile(x, [0.005, 0.995])
+            x = x[(x >= lo) & (x <= up)]
+        x = x.astype(np.float32)
+        opt = O.kmeans_inertia(x, O.kmeans_optimal(x, k))
+        sk = KMeans(n_clusters=k, n_init=3, max_iter=20, random_state=rep).fit(x.reshape(-1, 1))
+        assert opt <= O.kmeans_inertia(x, sk.cluster_centers_.ravel()) * (1 + 1e-6)
+        assert opt <= O.kmeans_inertia(x, O.kmeans_1d(x, k, 50)) * (1 + 1e-6)
+
+
+def test_optimal_known_answers():
+    # separated clusters: their means; padding as the reference; k = 1: the mean
+    parts = [c + RNG.uniform(-0.01, 0.01, 300) for c in (-10.0, 0.0, 10.0)]
+    v = np.concatenate(parts).astype(np.float32)
+    want = np.array([np.float32(np.sort(p.astype(np.float32)).astype(np.float64).sum() / p.size)
+                     for p in parts])
+    got = O.kmeans_optimal(RNG.permutation(v), 3)
+    assert np.allclose(got, want, rtol=0, atol=1e-6)
+    assert np.array_equal(O.kmeans_optimal(np.array([3.0, -1.0], np.float32), 4),
+                          np.array([-1.0, 0.0, 0.0, 3.0], np.float32))
+    w = RNG.standard_normal(1000).astype(np.float32)
+    assert abs(O.kmeans_optimal(w, 1)[0] - w.astype(np.float64).mean()) < 1e-6
+    # the optimal partition of sorted values is contiguous: each centre is the
+    # mean of the values nearest to it (a Lloyd fixed point)
+    c = O.kmeans_optimal(w, 8)
+    near = np.argmin(np.abs(w[:, None].astype(np.float64) - c[None, :]), axis=1)
+    for l in range(8):
+        assert abs(c[l] - w[near == l].astype(np.float64).mean()) < 1e-5
+    # more than 6144 values: not solved
+    assert np.isnan(O.kmeans_optimal(np.zeros(6145, np.float32), 4)).all()
