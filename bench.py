@@ -502,15 +502,21 @@ def bench_quest(args, dev):
 DEC_TOK, HQ = 1 << 20, 28
 
 
-def build_decode_layers(dev, layers):
+def build_decode_layers(dev, layers, paged: bool = False):
     """The decode workload's compact pool: for each layer, K and V of
     1,048,576 tokens packed to the compact format (nuq2 below layer 16, nuq4
     from it), the fp16 page min / max of the reconstructed K (the statistics
-    the pool keeps), and the layer's decode query (28, 128) fp16."""
+    the pool keeps), and the layer's decode query (28, 128) fp16.  With
+    paged=True the same K and V are also written into the paged pool (page
+    p of the sequence at block bt[p] of a random permutation, per page-head
+    outlier lists, K page statistics kept by the pool)."""
     from helix_kv.ops import NuqLayerTables, nuq_pack_compact, nuq_unpack_compact, quest_page_stats
+    from helix_kv.paged import PagedSide, paged_write
 
     P = DEC_TOK // 16
     gq = torch.Generator(device=dev).manual_seed(5)
+    bt = torch.randperm(P, generator=torch.Generator().manual_seed(8)).to(dev)
+    slots = bt[torch.arange(DEC_TOK, device=dev) // 16] * 16 + torch.arange(DEC_TOK, device=dev) % 16
     out = []
     for l in layers:
         K, V, ks, vs, L = make_layer(l, dev, T=DEC_TOK, seed_base=5000)
@@ -520,12 +526,18 @@ def build_decode_layers(dev, layers):
         cap = DEC_TOK * H * D // 10
         ck = nuq_pack_compact(K, kt, bits, capacity=cap)
         cv = nuq_pack_compact(V, vt, bits, capacity=cap)
+        Ld = dict(layer=l, ck=ck, cv=cv, kt=kt, vt=vt, bits=bits, bt=bt)
+        if paged:
+            Ld["pk"] = PagedSide.empty(P, H, bits, PAGED_CAP, dev, stats=True)
+            Ld["pv"] = PagedSide.empty(P, H, bits, PAGED_CAP, dev)
+            paged_write(Ld["pk"], K, kt, slots)
+            paged_write(Ld["pv"], V, vt, slots)
         del K, V
         kr = nuq_unpack_compact(ck, kt)
-        kmin, kmax = quest_page_stats(kr.view(P, 16, H, D))
+        Ld["kmin"], Ld["kmax"] = quest_page_stats(kr.view(P, 16, H, D))
         del kr
-        q = torch.randn((HQ, D), generator=gq, device=dev).half()
-        out.append(dict(layer=l, ck=ck, cv=cv, kt=kt, vt=vt, bits=bits, kmin=kmin, kmax=kmax, q=q))
+        Ld["q"] = torch.randn((HQ, D), generator=gq, device=dev).half()
+        out.append(Ld)
     torch.cuda.synchronize()
     return out
 
@@ -563,7 +575,7 @@ def bench_decode(args, dev):
     k, s = P // 4, 4
     nsel = k + s
     log(f"[bench] decode: building the {LAYERS}-layer compact pool at {DEC_TOK} tokens")
-    layers = build_decode_layers(dev, range(LAYERS))
+    layers = build_decode_layers(dev, range(LAYERS), paged=True)
     log(f"[bench] decode pool ready, {torch.cuda.memory_allocated() / 2**30:.1f} GiB allocated")
     pps = decode_pages_per_split(nsel, H)
     scores = torch.empty((H, P), dtype=torch.float32, device=dev)
@@ -642,6 +654,83 @@ def bench_decode(args, dev):
     union_pages = int(upages.numel())
     log(f"[bench] decode step, union of heads' pages: {union_us:.1f} us; layer {LAYERS - 1}: "
         f"{union_pages} of {P} pages, check rel err {uworst:.2e}")
+    # compact u8 page metadata (half the statistics' bytes): the same per-head
+    # step with the selection read from it, and how far it moves the result
+    from helix_kv.ops import quest_page_stats_u8, quest_select_u8
+    from helix_kv.paged import paged_decode_attention, paged_decode_step, paged_select
+
+    for Ld in layers:
+        Ld["u8"] = quest_page_stats_u8(Ld["kmin"], Ld["kmax"])
+        Ld["sel8"] = torch.empty_like(Ld["sel"])
+        Ld["out8"] = torch.empty_like(Ld["out"])
+
+    def step_u8():
+        for Ld in layers:
+            quest_select_u8(Ld["q"], Ld["u8"], k, s, scores=scores, out=Ld["sel8"])
+            decode_attention(Ld["q"], Ld["ck"], Ld["kt"], Ld["cv"], Ld["vt"], Ld["sel8"],
+                             pages_per_split=pps, out=Ld["out8"])
+
+    u8_us = graph_us(step_u8, stream, iters)
+    ov, rd = [], []
+    for Ld in layers:
+        a, b8 = Ld["sel"][s:], Ld["sel8"][s:]
+        for g in range(H):
+            ov.append(float(torch.isin(b8[:, g], a[:, g]).float().mean().item()))
+        r = (Ld["out8"].float() - Ld["out"].float()).norm(dim=-1) / Ld["out"].float().norm(dim=-1)
+        rd.append(float(r.max().item()))
+    log(f"[bench] decode step over u8 page metadata: {u8_us:.1f} us; page-set overlap with the fp16 "
+        f"selection mean {np.mean(ov):.4f} min {np.min(ov):.4f}; output change vs fp16 selection "
+        f"max {np.max(rd):.2e} mean {np.mean(rd):.2e}")
+    # the paged pool (page-head blocks of codes, per page-head outlier lists,
+    # a random block table): the same per-head step, and the reference's
+    # union step, read from it
+    for Ld in layers:
+        Ld["psel"] = torch.empty_like(Ld["sel"])
+        Ld["pout"] = torch.empty_like(Ld["out"])
+        Ld["pout_u"] = torch.empty_like(Ld["out"])
+
+    def paged_select_all():
+        for Ld in layers:
+            paged_select(Ld["q"], Ld["pk"], Ld["bt"], DEC_TOK, k, s, scores=scores, out=Ld["psel"])
+
+    def paged_decode_all():
+        for Ld in layers:
+            paged_decode_attention(Ld["q"], Ld["pk"], Ld["kt"], Ld["pv"], Ld["vt"], Ld["bt"], DEC_TOK,
+                                   Ld["psel"], pages_per_split=pps, out=Ld["pout"])
+
+    def paged_step():
+        paged_select_all()
+        paged_decode_all()
+
+    def paged_union():
+        for Ld in layers:
+            paged_decode_step(Ld["q"], Ld["pk"], Ld["kt"], Ld["pv"], Ld["vt"], Ld["bt"], DEC_TOK, k, s,
+                              gqa="mean", select="union", out=Ld["pout_u"])
+
+    p_step_us = graph_us(paged_step, stream, iters)
+    p_sel_us = graph_us(paged_select_all, stream, iters)
+    p_dec_us = graph_us(paged_decode_all, stream, iters)
+    p_union_us = graph_us(paged_union, stream, iters)
+    prel = 0.0
+    for Ld in layers:
+        if not torch.equal(Ld["psel"], Ld["sel"]):
+            raise RuntimeError(f"paged selection of layer {Ld['layer']} differs from the compact one")
+        prel = max(prel, float(((Ld["pout"].float() - Ld["out"].float()).norm(dim=-1)
+                                / Ld["out"].float().norm(dim=-1)).max().item()))
+        prel = max(prel, float(((Ld["pout_u"].float() - Ld["out_u"].float()).norm(dim=-1)
+                                / Ld["out_u"].float().norm(dim=-1)).max().item()))
+    if prel > 1e-3:
+        raise RuntimeError(f"paged decode differs from the compact decode: rel {prel:.2e}")
+    p_bytes = 0
+    for Ld in layers:
+        b = Ld["bits"]
+        ent = 0
+        for side in (Ld["pk"], Ld["pv"]):
+            ent += int(torch.gather(side.ocnt[Ld["bt"]].long(), 0, Ld["sel"]).sum().item())
+        p_bytes += nsel * H * (8 + 2 * 4 + 2 * 16 * D * b // 8) + 4 * ent + HQ * D * 2 * 2 + P * 8
+    p_sel_bytes = LAYERS * (2 * P * H * D * 2 + P * 8 + HQ * D * 2 + nsel * H * 8)
+    log(f"[bench] paged pool decode step: {p_step_us:.1f} us (select {p_sel_us:.1f}, decode {p_dec_us:.1f}); "
+        f"union step {p_union_us:.1f} us; equal to the compact path (rel {prel:.1e})")
     # algorithmic bytes
     sel_bytes = LAYERS * (2 * P * H * D * 2 + HQ * D * 2 + nsel * H * 8)
     dec_bytes = 0
@@ -662,7 +751,12 @@ def bench_decode(args, dev):
     return dict(dec_step_us=step_us, dec_select_us=sel_us, dec_attn_us=dec_us,
                 dec_sel_bytes=sel_bytes, dec_attn_bytes=dec_bytes, dec_rel_err=worst,
                 dec_pps=pps, dec_sel_outliers=sel_out, dec_union_us=union_us,
-                dec_union_pages=union_pages, dec_union_rel_err=uworst)
+                dec_union_pages=union_pages, dec_union_rel_err=uworst,
+                dec_u8_us=u8_us, dec_u8_overlap=(float(np.mean(ov)), float(np.min(ov))),
+                dec_u8_out_change=(float(np.max(rd)), float(np.mean(rd))),
+                dec_paged_us=p_step_us, dec_paged_sel_us=p_sel_us, dec_paged_attn_us=p_dec_us,
+                dec_paged_union_us=p_union_us, dec_paged_attn_bytes=p_bytes,
+                dec_paged_sel_bytes=p_sel_bytes)
 
 
 def bench_calibration(args, dev):
@@ -1228,6 +1322,26 @@ def main() -> None:
                           "group's queries selects top 16384 + 4 sink pages per KV head, and "
                           "every query head attends to the union of the KV heads' pages; "
                           "decode_step (no host reads), one HIP graph per step"},
+            "u8_metadata": {
+                "us_per_step": round(res["dec_u8_us"], 1),
+                "page_overlap_with_fp16_selection": {"mean": round(res["dec_u8_overlap"][0], 4),
+                                                     "min": round(res["dec_u8_overlap"][1], 4)},
+                "output_change_vs_fp16_selection": {"max": float(f"{res['dec_u8_out_change'][0]:.3g}"),
+                                                    "mean": float(f"{res['dec_u8_out_change'][1]:.3g}")},
+                "config": "the same step with each layer's selection read from the compact u8 page "
+                          "metadata (conservatively rounded: every bound >= the fp16 one); overlap = "
+                          "the fraction of the u8-selected non-sink pages the fp16 selection also "
+                          "holds, per KV head and layer; output change = relative L2 per query head"},
+            "paged_pool": {
+                "us_per_step": round(res["dec_paged_us"], 1),
+                "select_us": round(res["dec_paged_sel_us"], 1),
+                "attn_us": round(res["dec_paged_attn_us"], 1),
+                "attn_GBps": round(res["dec_paged_attn_bytes"] / (res["dec_paged_attn_us"] * 1e-6) / 1e9, 1),
+                "union_mean_q_us_per_step": round(res["dec_paged_union_us"], 1),
+                "config": "the same sequence written into the paged pool (page-head blocks of codes, "
+                          "per page-head outlier lists, pages at a random permutation of blocks): "
+                          "selection through the block table, fused decode reading page-head "
+                          "blocks; equal to the compact path's selection and output"},
             "config": f"Qwen2.5-7B shapes: {LAYERS} layers, 28 q heads, 4 KV heads, 128; "
                       f"{DEC_TOK} tokens in the mixed nuq2/nuq4 compact pool (~5% CSR "
                       "outliers); per layer Quest top 16384 + 4 sink pages per KV head, then "

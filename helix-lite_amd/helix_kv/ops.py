@@ -611,11 +611,12 @@ def decode_attention(query: torch.Tensor, k: CompactCodes, kt: NuqLayerTables, v
 
 
 def decode_step(query: torch.Tensor, k: CompactCodes, kt: NuqLayerTables, v: CompactCodes,
-                vt: NuqLayerTables, K_min: torch.Tensor, K_max: torch.Tensor, top_k: int,
-                sink_pages: int = 4, *, gqa: str = "mean", select: str = "union",
+                vt: NuqLayerTables, K_min: torch.Tensor | None, K_max: torch.Tensor | None,
+                top_k: int, sink_pages: int = 4, *, gqa: str = "mean", select: str = "union",
                 scale: float | None = None, out: torch.Tensor | None = None,
                 out_dtype: torch.dtype = torch.float16,
-                pages_per_split: int | None = None) -> torch.Tensor:
+                pages_per_split: int | None = None,
+                stats_u8: "QuestStatsU8 | None" = None) -> torch.Tensor:
     """One decode step of one sequence held in the compact format: Quest page
     selection from the page statistics, then the fused dequant + attention over
     the selected pages.  Every size is known on the host, so the step reads
@@ -634,13 +635,22 @@ def decode_step(query: torch.Tensor, k: CompactCodes, kt: NuqLayerTables, v: Com
       - The sequence is the k.shape[0] tokens of k / v; the last page may be
         partial and its missing slots are masked (compact_backend.py:253-262).
     query (Hq, 128) fp16; K_min / K_max (ceil(T / 16), H, 128) page statistics
-    of the sequence's K.  Returns (Hq, 128).
+    of the sequence's K, or stats_u8 (their compact u8 form, quest_page_stats_u8:
+    half the bytes, every bound at least the fp16 one) with K_min / K_max None.
+    Returns (Hq, 128).
     """
-    N.require_gpu(query, K_min, K_max)
     T, H, D = k.shape
     P = -(-T // 16)
-    if K_min.dim() != 3 or tuple(K_min.shape) != (P, H, D) or K_max.shape != K_min.shape:
-        raise ValueError(f"K_min/K_max should be ({P}, {H}, {D}), got {tuple(K_min.shape)}")
+    if stats_u8 is not None:
+        N.require_gpu(query, stats_u8.qmin)
+        if tuple(stats_u8.qmin.shape) != (P, H, D):
+            raise ValueError(f"stats_u8 should be ({P}, {H}, {D}), got {tuple(stats_u8.qmin.shape)}")
+    else:
+        if K_min is None or K_max is None:
+            raise ValueError("decode_step needs K_min / K_max or stats_u8")
+        N.require_gpu(query, K_min, K_max)
+        if K_min.dim() != 3 or tuple(K_min.shape) != (P, H, D) or K_max.shape != K_min.shape:
+            raise ValueError(f"K_min/K_max should be ({P}, {H}, {D}), got {tuple(K_min.shape)}")
     if query.dim() != 2 or int(query.shape[0]) % H or int(query.shape[1]) != D:
         raise ValueError(f"query {tuple(query.shape)} incompatible with (T, H, D) = {(T, H, D)}")
     Hq = int(query.shape[0])
@@ -650,7 +660,10 @@ def decode_step(query: torch.Tensor, k: CompactCodes, kt: NuqLayerTables, v: Com
         qs = query
     else:
         raise ValueError(f"gqa must be 'mean' or 'sum', got {gqa!r}")
-    sel, _ = quest_select(qs, K_min, K_max, top_k, sink_pages)
+    if stats_u8 is not None:
+        sel, _ = quest_select_u8(qs, stats_u8, top_k, sink_pages)
+    else:
+        sel, _ = quest_select(qs, K_min, K_max, top_k, sink_pages)
     if select == "union":
         # the union's pages ascending at the front, -1 after them: the decode
         # kernel's splits past the union's end find no valid page and return

@@ -234,6 +234,39 @@ def test_decode_step_vs_oracle(dev, gqa, select):
     _check(got, want)
 
 
+@pytest.mark.parametrize("gqa,select", [("mean", "union"), ("sum", "per_head")])
+def test_decode_step_u8_metadata_vs_oracle(dev, gqa, select):
+    """decode_step over the compact u8 page metadata: the selection is the
+    oracle's top-K over the bound of the dequantised u8 statistics (every
+    bound at least the fp16 one), the attention as in the fp16 case."""
+    from helix_kv.ops import decode_step, quest_page_stats_u8
+
+    T, H, group, top_k, sinks = 3000, 4, 7, 40, 4
+    kc, kt, kd, vc, vt, vd = _problem(dev, T, H, 16, 4, 2048)
+    P = kd.shape[0]
+    k16 = kd.reshape(-1, H, 128)[:T].astype(np.float16)
+    kmin, kmax = _stats(k16, T, H)
+    qmin, qmax, lo, st = O.page_stats_u8(kmin, kmax)
+    dmn, dmx = O.page_stats_u8_deq(qmin, qmax, lo, st)
+    q = RNG.standard_normal((H * group, 128)).astype(np.float16)
+    qd = _t(q, dev)
+    if gqa == "mean":
+        qs = qd.reshape(H, group, 128).mean(dim=1).to(torch.float16).cpu().numpy()
+        bound = O.page_bound(qs, dmn, dmx)
+    else:
+        bound = O.page_bound_group(q, dmn, dmx, group)
+    sel = O.topk_sinks(bound, min(top_k, P - sinks), sinks)
+    if select == "union":
+        ids = np.unique(sel.reshape(-1))
+        sel = np.repeat(ids[:, None], H, axis=1)
+    want = O.selected_attention(q.astype(np.float64), kd, vd, sel, lambda h: h // group,
+                                num_tokens=T)
+    u8 = quest_page_stats_u8(_t(kmin, dev), _t(kmax, dev))
+    got = decode_step(qd, kc, kt, vc, vt, None, None, top_k, sinks, gqa=gqa, select=select,
+                      out_dtype=torch.float32, stats_u8=u8)
+    _check(got, want)
+
+
 def test_decode_step_graph_replay(dev):
     """The step reads nothing back to the host, so it records into a HIP graph;
     three replays, with eager steps between them, equal the eager result."""
