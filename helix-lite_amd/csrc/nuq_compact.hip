@@ -188,7 +188,7 @@ struct ItemSlow {
 // KFIX: the rows of one pass of a wave (RW = 64/G) are a multiple of H, so a
 // lane's head is fixed (rw % H) and its token advances by RW / H per pass.
 template <int NB, bool PT, int G, int BITS, bool KFIX, int PASSES>
-__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(PT ? 4 : 3)))
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(PT ? 5 : 3)))
 pack_fused_kernel(const PackBatch B, uint32_t* __restrict__ hdr, uint64_t* __restrict__ status) {
   constexpr int RW = 64 / G;        // rows per wave per pass
   constexpr int WT = RW * PASSES;  // rows per wave tile
