@@ -319,7 +319,23 @@ bound_kernel(const void* q, int qdt, int group, const KT* __restrict__ kmin,
 }
 
 constexpr int kMaxMMHeads = 64;  // heads with per-block key ranges (multi-block top-K)
-constexpr int kBoundUnrollF16 = 4;  // row groups per step (two steps of loads in flight)
+constexpr int kBoundUnrollF16 = 2;  // row groups per step (two steps of loads in flight)
+
+// A lane's statistics (read once, never again by this kernel): non-temporal
+// loads keep the 128 MiB stream from displacing the cached query, scores and
+// key ranges (44.9 against 48.0 us per 1M-token selection, which also
+// measured 2 row groups per step against 4 at 4 blocks per CU).
+template <typename LT>
+HKV_DEV LT load_stream(const LT* p) {
+  if constexpr (sizeof(LT) == 16) {
+    typedef uint32_t v4n __attribute__((ext_vector_type(4)));
+    return __builtin_bit_cast(LT, __builtin_nontemporal_load(reinterpret_cast<const v4n*>(p)));
+  } else {
+    static_assert(sizeof(LT) == 8, "8 or 16 bytes");
+    typedef uint32_t v2n __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(LT, __builtin_nontemporal_load(reinterpret_cast<const v2n*>(p)));
+  }
+}
 
 // fp16 stats with D = 8*G (G a power of two, G <= 64): lane c of a row owns
 // channels [8c, 8c+8) and loads them with one 128-bit load per array.  HFIX:
@@ -388,8 +404,8 @@ HKV_DEV void bound_f16_rows(const void* q, int qdt, int group, const void* kmin_
           r = (int)bk * H + rl % H;
         }
       }
-      a[u] = reinterpret_cast<const LT*>(kmin + (uint32_t)r * D)[c];
-      b[u] = reinterpret_cast<const LT*>(kmax + (uint32_t)r * D)[c];
+      a[u] = load_stream(reinterpret_cast<const LT*>(kmin + (uint32_t)r * D) + c);
+      b[u] = load_stream(reinterpret_cast<const LT*>(kmax + (uint32_t)r * D) + c);
     }
   };
   int r0 = bx * span;
@@ -993,6 +1009,7 @@ constexpr int kMBWin = 1024;     // window keys stored per slice
 
 struct MBWork {
   uint32_t* ctr;     // [H] arrival counters (zero between calls)
+  uint32_t* leave;   // [H] departure counters of the fused form (zero between calls)
   const uint2* mm;   // [H][nmm] (min key, max key) of the bound kernel's blocks
   int nmm;
   uint32_t* hist;    // [H][NB][kMBBins / 2] u16 counts, bin 2i in the low half of word i
@@ -1076,7 +1093,83 @@ HKV_DEV uint4 mb_excl_scan4(uint4 v, uint4* red) {
 // back to memory before this wave's stores have reached L2.
 HKV_DEV void wait_stores() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
+constexpr uint32_t kMBStage = 8192;     // pages staged in LDS per round of the ordered write
+constexpr int kMBSpinLimit = 1 << 22;   // polls of the fused form's wait for a head's slices
+
+// Block j's part of the output: the selected pages of slice j -- every key
+// > T and, of the keys == T, those whose rank among the head's T-equal keys
+// is below need_eq -- in page order from output row `first` (eqb0 T-equal
+// keys of the head lie in slices before j).  Positions come from one block
+// scan of the per-thread counts, (== T) << 16 | (> T) (at most kMBThreads *
+// KPT each).  The pages are staged in LDS in output order and written by
+// consecutive threads: the column of head h is strided by H, so each
+// 128-byte line is written with one request instead of one per page.
+// kv: the thread's keys, candidates j * slice + i * kMBThreads + tid when
+// the stage holds the slice (they are transposed through it so that the
+// thread holds candidates c0 .. c0 + KPT - 1), else c0 + i directly.
 template <int KPT>
+HKV_DEV void mb_write_slice(float (&kv)[KPT], int n, int64_t s, int64_t* out, int H, int h, int j,
+                            uint32_t T, uint32_t need_eq, uint32_t row_end, uint32_t first,
+                            uint32_t eqb0, uint32_t* stage, uint32_t* red) {
+  const int tid = threadIdx.x;
+  const int c0 = j * (kMBThreads * KPT) + tid * KPT;
+  if constexpr (kMBThreads * KPT <= (int)kMBStage) {
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) stage[i * kMBThreads + tid] = __float_as_uint(kv[i]);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) kv[i] = __uint_as_float(stage[tid * KPT + i]);
+  }
+  auto taken = [&](uint32_t eqs) { return eqs < need_eq ? eqs : need_eq; };
+  uint32_t key[KPT];
+  uint32_t gt = 0, eq = 0;
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) {
+    key[i] = c0 + i < n ? ukey(kv[i]) : 0u;  // 0: below every real key
+    gt += key[i] > T ? 1u : 0u;
+    eq += (c0 + i < n && key[i] == T) ? 1u : 0u;
+  }
+  uint32_t tot;
+  const uint32_t pre = mb_excl_scan(gt | (eq << 16), red, tot);  // its barriers order the stage
+  const uint32_t nsel = (tot & 0xffffu) + taken(eqb0 + (tot >> 16)) - taken(eqb0);
+  const uint32_t rel0 = (pre & 0xffffu) + taken(eqb0 + (pre >> 16)) - taken(eqb0);
+  for (uint32_t sub = 0; sub < nsel; sub += kMBStage) {
+    uint32_t rel = rel0, eqr = eqb0 + (pre >> 16);
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      const bool is_eq = c0 + i < n && key[i] == T;
+      const bool sel = key[i] > T || (is_eq && eqr < need_eq);
+      eqr += is_eq ? 1u : 0u;
+      if (sel && rel - sub < kMBStage) stage[rel - sub] = (uint32_t)(s + c0 + i);
+      rel += sel ? 1u : 0u;
+    }
+    __syncthreads();
+    const uint32_t cnt = nsel - sub < kMBStage ? nsel - sub : kMBStage;
+    for (uint32_t i = tid; i < cnt; i += kMBThreads) {
+      const uint32_t r = first + sub + i;
+      if (r < row_end) out[(int64_t)r * H + h] = (int64_t)stage[i];
+    }
+    __syncthreads();
+  }
+}
+
+// Fused form: a block leaves once it is done with the head's shared state;
+// the last of the head's NB blocks to leave zeroes both counters for the next
+// call (every block has passed its wait by then).
+HKV_DEV void mb_leave(const MBWork& w, int h, int NB) {
+  if (threadIdx.x == 0 && atomicAdd(&w.leave[h], 1u) == (uint32_t)(NB - 1)) {
+    atomicExch(&w.ctr[h], 0u);
+    atomicExch(&w.leave[h], 0u);
+  }
+}
+
+// FUSED: every block of the head computes the threshold itself once all NB
+// slices have arrived, then writes its own slice (no second kernel, the keys
+// stay in registers).  Blocks wait for one another, so the host uses this
+// form only when the whole grid is resident at once (at most one block per
+// CU); else the last block to arrive computes the threshold for
+// topk_mb_write.
+template <int KPT, bool FUSED>
 __global__ void __launch_bounds__(kMBThreads)
 topk_mb_hist(const float* scores, int64_t P, int64_t s, int64_t keff, int64_t* out, int H,
                MBWork w) {
@@ -1212,19 +1305,37 @@ topk_mb_hist(const float* scores, int64_t P, int64_t s, int64_t keff, int64_t* o
   }
   wait_stores();
   __syncthreads();
-  if (tid == 0) {
-    __threadfence();  // release this slice's histogram and window
-    s_last = atomicAdd(&w.ctr[h], 1u) == (uint32_t)(NB - 1);
+  if constexpr (FUSED) {
+    if (tid == 0) {
+      __threadfence();  // release this slice's histogram and window
+      uint32_t a = atomicAdd(&w.ctr[h], 1u) + 1u;
+      int it = 0;
+      while (a < (uint32_t)NB && it < kMBSpinLimit) {
+        __builtin_amdgcn_s_sleep(2);
+        a = __hip_atomic_load(&w.ctr[h], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ++it;
+      }
+      s_last = a >= (uint32_t)NB;
+      __threadfence();  // acquire every slice's histogram (one cache invalidation for the block)
+      if (!s_last) w.thr[h * 4 + 2] = 2u;  // gave up waiting: this slice's pages are not written
+    }
+    __syncthreads();
+    if (!s_last) return;
+  } else {
+    if (tid == 0) {
+      __threadfence();  // release this slice's histogram and window
+      s_last = atomicAdd(&w.ctr[h], 1u) == (uint32_t)(NB - 1);
+    }
+    __syncthreads();
+    if (!s_last) return;
+    if (tid == 0) {
+      __threadfence();  // acquire every slice's histogram (one cache invalidation for the block)
+      atomicExch(&w.ctr[h], 0u);  // every slice has arrived: ready for the next call
+    }
+    __syncthreads();
   }
-  __syncthreads();
-  if (!s_last) return;
-  if (tid == 0) {
-    __threadfence();  // acquire every slice's histogram (one cache invalidation for the block)
-    atomicExch(&w.ctr[h], 0u);  // every slice has arrived: ready for the next call
-  }
-  __syncthreads();
 
-  // ---- last block of head h: the threshold
+  // ---- every block (FUSED) or the last block of head h: the threshold
   // Thread t owns bins 4 * ch .. 4 * ch + 3, ch = 1023 - t (bins high to low
   // over the threads; its k-th bin from the top is field 3 - k), one 8-byte
   // chunk of every slice's u16 histogram.  Per group of 8 slices a packed
@@ -1386,11 +1497,13 @@ topk_mb_hist(const float* scores, int64_t P, int64_t s, int64_t keff, int64_t* o
   const uint64_t hi1w = (uint64_t)lo1 + ((1ull << sh1) - 1ull);
   const uint32_t hi1 = hi1w > 0xffffffffull ? 0xffffffffu : (uint32_t)hi1w;
   if (cnt1 > (uint32_t)kMBCand) {
-    // a huge bin: the single-block selector over the whole column
+    // a huge bin: the single-block selector over the whole column (block 0
+    // of the head in the fused form)
     __shared__ SelShared ssh;
     ColumnF32 cc{scores + (int64_t)h * P, 1, 0};
-    select_column(cc, P, s, keff, out + h, H, ssh);
-    if (tid == 0) w.thr[h * 4 + 2] = 1u;
+    if (!FUSED || j == 0) select_column(cc, P, s, keff, out + h, H, ssh);
+    if constexpr (FUSED) mb_leave(w, h, NB);
+    else if (tid == 0) w.thr[h * 4 + 2] = 1u;
     return;
   }
   if (tid == 0) {
@@ -1537,50 +1650,68 @@ topk_mb_hist(const float* scores, int64_t P, int64_t s, int64_t keff, int64_t* o
     else if (k == T) atomicAdd(&sh.sl_eq[jj], 1);
   }
   __syncthreads();
-  if (tid == 0) {
-    int outp = (int)s, eqb = 0;
-    for (int jj = 0; jj < NB; ++jj) {
-      w.meta[((int64_t)h * NB + jj) * 2] = outp;
-      w.meta[((int64_t)h * NB + jj) * 2 + 1] = eqb;
-      const int e = sh.sl_eq[jj];
-      const int take = eqb >= (int)need_eq ? 0 : ((int)need_eq - eqb < e ? (int)need_eq - eqb : e);
-      outp += sh.sl_gt[jj] + take;
-      eqb += e;
+  if constexpr (FUSED) {
+    // this slice's first output row and the T-equal keys before it, then its pages
+    if (tid == 0) {
+      int outp = (int)s, eqb = 0;
+      for (int jj = 0; jj < j; ++jj) {
+        const int e = sh.sl_eq[jj];
+        const int take = eqb >= (int)need_eq ? 0 : ((int)need_eq - eqb < e ? (int)need_eq - eqb : e);
+        outp += sh.sl_gt[jj] + take;
+        eqb += e;
+      }
+      sh.bc[0] = (uint32_t)outp;
+      sh.bc[1] = (uint32_t)eqb;
     }
-    w.thr[h * 4] = T;
-    w.thr[h * 4 + 1] = need_eq;
-    w.thr[h * 4 + 2] = 0u;
-    w.thr[h * 4 + 3] = (uint32_t)(s + keff);
+    if (j == 0)
+      for (int64_t i = tid; i < s; i += kMBThreads) out[i * H + h] = i;
+    __syncthreads();
+    const uint32_t first = sh.bc[0], eqb0 = sh.bc[1];
+    if constexpr (kMBThreads * KPT > (int)kMBStage) {
+      // the stage cannot transpose the slice: the thread's consecutive keys, read again
+      const int cd = j * slice + tid * KPT;
+#pragma unroll
+      for (int i = 0; i < KPT; ++i) kv[i] = col[cd + i < n ? cd + i : n - 1];
+    }
+    mb_write_slice<KPT>(kv, n, s, out, H, h, j, T, need_eq, (uint32_t)(s + keff), first, eqb0,
+                        reinterpret_cast<uint32_t*>(sh.cand), sh.red[0]);
+    mb_leave(w, h, NB);
+  } else {
+    if (tid == 0) {
+      int outp = (int)s, eqb = 0;
+      for (int jj = 0; jj < NB; ++jj) {
+        w.meta[((int64_t)h * NB + jj) * 2] = outp;
+        w.meta[((int64_t)h * NB + jj) * 2 + 1] = eqb;
+        const int e = sh.sl_eq[jj];
+        const int take = eqb >= (int)need_eq ? 0 : ((int)need_eq - eqb < e ? (int)need_eq - eqb : e);
+        outp += sh.sl_gt[jj] + take;
+        eqb += e;
+      }
+      w.thr[h * 4] = T;
+      w.thr[h * 4 + 1] = need_eq;
+      w.thr[h * 4 + 2] = 0u;
+      w.thr[h * 4 + 3] = (uint32_t)(s + keff);
+    }
   }
 }
 
-// Block j writes the selected pages of slice j: every key > T and, of the
-// keys == T, those whose rank among the head's T-equal keys is below the
-// number taken.  Positions come from one block scan of the per-thread counts,
-// (== T) << 16 | (> T) (at most kMBThreads * KPT each).  The pages are staged
-// in LDS in output order and written by consecutive threads: the column of
-// head h is strided by H, so each 128-byte line is written with one request
-// instead of one per page.
+// Two-kernel form: block j writes the selected pages of slice j from the
+// threshold and offsets the last block of topk_mb_hist left.
 template <int KPT>
 __global__ void __launch_bounds__(kMBThreads)
 topk_mb_write(const float* scores, int64_t P, int64_t s, int64_t* out, int H, MBWork w) {
-  constexpr uint32_t kStage = 8192;
   __shared__ uint32_t red[kMBWaves];
-  __shared__ uint32_t stage[kStage];
+  __shared__ uint32_t stage[kMBStage];
   const int j = blockIdx.x, h = blockIdx.y, NB = gridDim.x, tid = threadIdx.x;
   const int n = (int)(P - s);
   const float* col = scores + (int64_t)h * P + s;
-  const int c0 = j * (kMBThreads * KPT) + tid * KPT;
-  // the keys, the threshold and the slice's offsets are requested together.
-  // Where the stage holds the slice, load i reads candidates
-  // j * slice + i * kMBThreads + [0, kMBThreads) (consecutive words across
-  // the block) and the stage transposes them so that the thread holds
-  // candidates c0 .. c0 + KPT - 1; else the thread reads those directly.
-  constexpr bool kTranspose = kMBThreads * KPT <= kStage;
+  // the keys, the threshold and the slice's offsets are requested together,
+  // in the layout mb_write_slice takes
+  constexpr bool kTranspose = kMBThreads * KPT <= (int)kMBStage;
   float kv[KPT];
 #pragma unroll
   for (int i = 0; i < KPT; ++i) {
-    const int c = kTranspose ? j * (kMBThreads * KPT) + i * kMBThreads + tid : c0 + i;
+    const int c = kTranspose ? j * (kMBThreads * KPT) + i * kMBThreads + tid : j * (kMBThreads * KPT) + tid * KPT + i;
     kv[i] = col[c < n ? c : n - 1];
   }
   const uint4 th = *reinterpret_cast<const uint4*>(w.thr + h * 4);
@@ -1588,46 +1719,8 @@ topk_mb_write(const float* scores, int64_t P, int64_t s, int64_t* out, int H, MB
   if (j == 0)
     for (int64_t i = tid; i < s; i += kMBThreads) out[i * H + h] = i;
   if (th.z) return;  // written by the fallback
-  if constexpr (kTranspose) {
-#pragma unroll
-    for (int i = 0; i < KPT; ++i) stage[i * kMBThreads + tid] = __float_as_uint(kv[i]);
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < KPT; ++i) kv[i] = __uint_as_float(stage[tid * KPT + i]);
-  }
-  const uint32_t T = th.x, need_eq = th.y, row_end = th.w;
-  auto taken = [&](uint32_t eqs) { return eqs < need_eq ? eqs : need_eq; };
-  uint32_t key[KPT];
-  uint32_t gt = 0, eq = 0;
-#pragma unroll
-  for (int i = 0; i < KPT; ++i) {
-    key[i] = c0 + i < n ? ukey(kv[i]) : 0u;  // 0: below every real key
-    gt += key[i] > T ? 1u : 0u;
-    eq += (c0 + i < n && key[i] == T) ? 1u : 0u;
-  }
-  uint32_t tot;
-  const uint32_t pre = mb_excl_scan(gt | (eq << 16), red, tot);
-  const uint32_t eqb0 = (uint32_t)me.y;
-  const uint32_t nsel = (tot & 0xffffu) + taken(eqb0 + (tot >> 16)) - taken(eqb0);
-  const uint32_t rel0 = (pre & 0xffffu) + taken(eqb0 + (pre >> 16)) - taken(eqb0);
-  for (uint32_t sub = 0; sub < nsel; sub += kStage) {
-    uint32_t rel = rel0, eqr = eqb0 + (pre >> 16);
-#pragma unroll
-    for (int i = 0; i < KPT; ++i) {
-      const bool is_eq = c0 + i < n && key[i] == T;
-      const bool sel = key[i] > T || (is_eq && eqr < need_eq);
-      eqr += is_eq ? 1u : 0u;
-      if (sel && rel - sub < kStage) stage[rel - sub] = (uint32_t)(s + c0 + i);
-      rel += sel ? 1u : 0u;
-    }
-    __syncthreads();
-    const uint32_t cnt = nsel - sub < kStage ? nsel - sub : kStage;
-    for (uint32_t i = tid; i < cnt; i += kMBThreads) {
-      const uint32_t r = (uint32_t)me.x + sub + i;
-      if (r < row_end) out[(int64_t)r * H + h] = (int64_t)stage[i];
-    }
-    __syncthreads();
-  }
+  mb_write_slice<KPT>(kv, n, s, out, H, h, j, th.x, th.y, th.w, (uint32_t)me.x, (uint32_t)me.y, stage,
+                      red);
 }
 
 int num_cus() {
@@ -2066,7 +2159,7 @@ SelectWs select_ws_layout(int64_t P, int H) {
   l.NB = (int)nb;
   l.kpt = kpt;
   l.ctr_off = 0;
-  l.thr_off = al(sizeof(uint32_t) * H);
+  l.thr_off = al(sizeof(uint32_t) * 2 * H);  // arrival, then departure counters
   l.mm_off = l.thr_off + al(sizeof(uint32_t) * 4 * H);
   l.hist_off = l.mm_off + al(sizeof(uint2) * (size_t)num_cus() * 4 * H);
   l.meta_off = l.hist_off + al(sizeof(uint32_t) * (size_t)H * nb * (kMBBins / 2));
@@ -2194,6 +2287,7 @@ int select_after_bound(const float* scores, int64_t P, int H, int64_t k, int64_t
   if (!mb || nmm == 0) return topk(scores, HKV_DT_F32, P, H, 1, P, k, sink_pages, out, nullptr, st);
   MBWork w;
   w.ctr = (uint32_t*)(ws + lay.ctr_off);
+  w.leave = w.ctr + H;
   w.mm = (const uint2*)(ws + lay.mm_off);
   w.nmm = nmm;
   w.hist = (uint32_t*)(ws + lay.hist_off);
@@ -2202,14 +2296,25 @@ int select_after_bound(const float* scores, int64_t P, int H, int64_t k, int64_t
   w.wcand = (uint32_t*)(ws + lay.wcand_off);
   w.wmeta = (int*)(ws + lay.wmeta_off);
   const dim3 grid((unsigned)lay.NB, (unsigned)H);
+  // the fused form's blocks wait for one another: only where every block of
+  // the grid has a CU of its own
+  const bool fused = (int64_t)lay.NB * H <= (int64_t)num_cus();
   if (lay.kpt == 8) {
-    hipLaunchKernelGGL((topk_mb_hist<8>), grid, dim3(kMBThreads), 0, st, scores, P, s, keff, out, H, w);
-    HKV_CHECK_LAUNCH();
-    hipLaunchKernelGGL((topk_mb_write<8>), grid, dim3(kMBThreads), 0, st, scores, P, s, out, H, w);
+    if (fused) {
+      hipLaunchKernelGGL((topk_mb_hist<8, true>), grid, dim3(kMBThreads), 0, st, scores, P, s, keff, out, H, w);
+    } else {
+      hipLaunchKernelGGL((topk_mb_hist<8, false>), grid, dim3(kMBThreads), 0, st, scores, P, s, keff, out, H, w);
+      HKV_CHECK_LAUNCH();
+      hipLaunchKernelGGL((topk_mb_write<8>), grid, dim3(kMBThreads), 0, st, scores, P, s, out, H, w);
+    }
   } else {
-    hipLaunchKernelGGL((topk_mb_hist<32>), grid, dim3(kMBThreads), 0, st, scores, P, s, keff, out, H, w);
-    HKV_CHECK_LAUNCH();
-    hipLaunchKernelGGL((topk_mb_write<32>), grid, dim3(kMBThreads), 0, st, scores, P, s, out, H, w);
+    if (fused) {
+      hipLaunchKernelGGL((topk_mb_hist<32, true>), grid, dim3(kMBThreads), 0, st, scores, P, s, keff, out, H, w);
+    } else {
+      hipLaunchKernelGGL((topk_mb_hist<32, false>), grid, dim3(kMBThreads), 0, st, scores, P, s, keff, out, H, w);
+      HKV_CHECK_LAUNCH();
+      hipLaunchKernelGGL((topk_mb_write<32>), grid, dim3(kMBThreads), 0, st, scores, P, s, out, H, w);
+    }
   }
   HKV_CHECK_LAUNCH();
   return HKV_OK;

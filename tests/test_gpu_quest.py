@@ -144,7 +144,7 @@ def test_fused_select_small_and_per_kv_head(dev):
         assert np.array_equal(idx.cpu().numpy(), O.topk_sinks(wb, k, s))
 
 
-@pytest.mark.parametrize("P,H,g,k,s,mode", [
+@pytest.mark.parametrize("P,H,g,k,s,mode,D", [(*c, 128) if len(c) == 6 else c for c in [
     (40000, 4, 7, 10000, 4, "normal"),     # five slices, the last one partial
     (65536, 2, 7, 1, 0, "normal"),         # a single page besides no sinks
     (65536, 4, 1, 65532, 4, "normal"),     # every candidate
@@ -154,13 +154,17 @@ def test_fused_select_small_and_per_kv_head(dev):
     (600000, 2, 7, 150000, 4, "normal"),   # many slices (KPT 32)
     (65536, 2, 7, 100, 4, "nan"),          # NaN ranks highest: the threshold in the top bin
     (65536, 2, 7, 5000, 1, "nan"),         # NaN present (coarse bins), one sink: unaligned column
-])
-def test_multiblock_select_vs_oracle(dev, P, H, g, k, s, mode):
+    # more slice blocks than CUs: the two-kernel form (threshold by the last block, then a write kernel)
+    (40960, 64, 1, 10240, 4, "normal", 8),     # 5 slices x 64 heads
+    (540000, 16, 2, 135000, 4, "normal", 32),  # 17 slices of 32768 x 16 heads (KPT 32)
+]])
+def test_multiblock_select_vs_oracle(dev, P, H, g, k, s, mode, D):
     """The multi-block top-K (fp16 statistics, large columns) against the
-    oracle, including repeated calls on the same workspace."""
+    oracle, including repeated calls on the same workspace.  Up to one slice
+    block per CU every block of a head computes the threshold and writes its
+    own slice (fused form); beyond that the two-kernel form runs."""
     from helix_kv.ops import quest_select
 
-    D = 128
     if mode == "equal":
         mn = np.zeros((P, H, D), np.float16)
         mx = np.ones((P, H, D), np.float16)
