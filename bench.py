@@ -1155,11 +1155,18 @@ def profile_pass(what: str, dev) -> None:
     elif what == "ragged":
         bench_ragged(argparse.Namespace(steps=1), dev)
     elif what == "decode":
+        from helix_kv.paged import paged_decode_attention, paged_select
+
         P = DEC_TOK // 16
-        for Ld in build_decode_layers(dev, (0, CUT)):
+        for Ld in build_decode_layers(dev, (0, CUT), paged=True):
             sel, _ = quest_select(Ld["q"], Ld["kmin"], Ld["kmax"], P // 4, 4)
             for _ in range(3):
                 decode_attention(Ld["q"], Ld["ck"], Ld["kt"], Ld["cv"], Ld["vt"], sel)
+            # the same selection read from the paged pool (page-head blocks)
+            psel, _ = paged_select(Ld["q"], Ld["pk"], Ld["bt"], DEC_TOK, P // 4, 4)
+            for _ in range(3):
+                paged_decode_attention(Ld["q"], Ld["pk"], Ld["kt"], Ld["pv"], Ld["vt"], Ld["bt"], DEC_TOK,
+                                       psel)
     torch.cuda.synchronize()
     log(f"[bench] profile pass {what} done")
 

@@ -158,17 +158,20 @@ HKV_DEV int csr_slot(int a, int sub, int s, int cap) {
   return i < cap ? i : cap - 1;
 }
 
-// PG: lane l holds entries l + 64 s (s < kSlots) of the page-head (index
-// clamped into [0, cap)) in kval[s] / vval[s].
+// PG: lane l holds entries l + 64 s (s < kSlots) of the page-head in
+// kval[s] / vval[s], the index clamped to the page-head's last entry (or 0):
+// the loads stay unconditional, and those past the count read a line
+// already fetched, so only the entries' own lines come from HBM.
 template <int KB, int VB, bool PG>
 HKV_DEV void load_outl(const DecodeArgs& A, const PageLoad<KB, VB>& L, int lane, PageOutl& O) {
   const int kcap = (int)A.k.cap, vcap = (int)A.v.cap;
   if constexpr (PG) {
+    const int kl = (L.kr.x < kcap ? L.kr.x : kcap) - 1, vl = (L.vr.x < vcap ? L.vr.x : vcap) - 1;
 #pragma unroll
     for (int s = 0; s < kSlots; ++s) {
       const int i = lane + 64 * s;
-      if (kcap > 0) O.kval[s] = A.k.oent[(int64_t)L.kr.y * kcap + (i < kcap ? i : kcap - 1)];
-      if (vcap > 0) O.vval[s] = A.v.oent[(int64_t)L.vr.y * vcap + (i < vcap ? i : vcap - 1)];
+      if (kcap > 0) O.kval[s] = A.k.oent[(int64_t)L.kr.y * kcap + (i < kl ? i : (kl > 0 ? kl : 0))];
+      if (vcap > 0) O.vval[s] = A.v.oent[(int64_t)L.vr.y * vcap + (i < vl ? i : (vl > 0 ? vl : 0))];
     }
     return;
   }

@@ -97,6 +97,23 @@ HKV_DEV void store_stream(void* p, uint4 v) {
 HKV_DEV void store_stream(uint32_t* p, uint32_t v) { __builtin_nontemporal_store(v, p); }
 HKV_DEV void store_stream(uint16_t* p, uint16_t v) { __builtin_nontemporal_store(v, p); }
 
+// Streaming (non-temporal) loads for inputs read once: a large stream does
+// not displace the kernel's small re-read working set (tables, counters).
+template <typename LT>
+HKV_DEV LT load_stream(const LT* p) {
+  if constexpr (sizeof(LT) == 16) {
+    return __builtin_bit_cast(LT, __builtin_nontemporal_load(reinterpret_cast<const hkv_v4u*>(p)));
+  } else if constexpr (sizeof(LT) == 8) {
+    typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(LT, __builtin_nontemporal_load(reinterpret_cast<const v2u*>(p)));
+  } else if constexpr (sizeof(LT) == 4) {
+    return __builtin_bit_cast(LT, __builtin_nontemporal_load(reinterpret_cast<const unsigned int*>(p)));
+  } else {
+    static_assert(sizeof(LT) == 2, "2, 4, 8 or 16 bytes");
+    return __builtin_bit_cast(LT, __builtin_nontemporal_load(reinterpret_cast<const unsigned short*>(p)));
+  }
+}
+
 // Pack the low halves of a and b into one register (a -> lane 0, b -> lane 1).
 HKV_DEV uint32_t pack_lo(uint32_t a, uint32_t b) { return (a & 0xffffu) | (b << 16); }
 

@@ -380,7 +380,7 @@ pack_fused_kernel(const PackBatch B, uint32_t* __restrict__ hdr, uint64_t* __res
       for (int p = 0; p < PASSES; ++p) {
         const int rr = p * RW + rw;
         uint4 v = make_uint4(0u, 0u, 0u, 0u);
-        if (rr < nv) v = *reinterpret_cast<const uint4*>(xt + (uint32_t)(rr * D + 8 * cg));
+        if (rr < nv) v = load_stream(reinterpret_cast<const uint4*>(xt + (uint32_t)(rr * D + 8 * cg)));
         xs[p][0] = v.x; xs[p][1] = v.y; xs[p][2] = v.z; xs[p][3] = v.w;
       }
       if constexpr (STAGE) {

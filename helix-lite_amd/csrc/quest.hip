@@ -321,21 +321,10 @@ bound_kernel(const void* q, int qdt, int group, const KT* __restrict__ kmin,
 constexpr int kMaxMMHeads = 64;  // heads with per-block key ranges (multi-block top-K)
 constexpr int kBoundUnrollF16 = 2;  // row groups per step (two steps of loads in flight)
 
-// A lane's statistics (read once, never again by this kernel): non-temporal
-// loads keep the 128 MiB stream from displacing the cached query, scores and
-// key ranges (44.9 against 48.0 us per 1M-token selection, which also
-// measured 2 row groups per step against 4 at 4 blocks per CU).
-template <typename LT>
-HKV_DEV LT load_stream(const LT* p) {
-  if constexpr (sizeof(LT) == 16) {
-    typedef uint32_t v4n __attribute__((ext_vector_type(4)));
-    return __builtin_bit_cast(LT, __builtin_nontemporal_load(reinterpret_cast<const v4n*>(p)));
-  } else {
-    static_assert(sizeof(LT) == 8, "8 or 16 bytes");
-    typedef uint32_t v2n __attribute__((ext_vector_type(2)));
-    return __builtin_bit_cast(LT, __builtin_nontemporal_load(reinterpret_cast<const v2n*>(p)));
-  }
-}
+// A lane's statistics are read once: load_stream keeps the 128 MiB stream
+// from displacing the cached query, scores and key ranges (44.9 against
+// 48.0 us per 1M-token selection, which also measured 2 row groups per step
+// against 4 at 4 blocks per CU).
 
 // fp16 stats with D = 8*G (G a power of two, G <= 64): lane c of a row owns
 // channels [8c, 8c+8) and loads them with one 128-bit load per array.  HFIX:
