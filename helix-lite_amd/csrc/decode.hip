@@ -243,9 +243,10 @@ HKV_DEV void patch_rest_paged(const Side& sd, int2 cr, int lane, uint16_t* tile,
   }
 }
 
+// One block: split `split` of the selection (pages split * pps ..) for KV
+// head blockIdx.y.
 template <int KB, int VB, bool PG>
-__global__ void __launch_bounds__(kDT) __attribute__((amdgpu_waves_per_eu(3, 3)))
-decode_kernel(DecodeArgs A) {
+HKV_DEV void decode_body(const DecodeArgs& A, int64_t split) {
   __shared__ __align__(16) uint16_t s_klut[kKLut];
   __shared__ __align__(16) uint16_t s_vlut[kW][kPS * 16];   // [row][level] of the wave's page
   __shared__ __align__(16) uint16_t s_tiles[kW][2][kPS * kTS];
@@ -253,7 +254,7 @@ decode_kernel(DecodeArgs A) {
 
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int g = blockIdx.y, H = A.H, group = A.group;
-  const int64_t j0 = (int64_t)blockIdx.x * A.pps;
+  const int64_t j0 = split * A.pps;
   const int64_t j1 = j0 + A.pps < A.nsel ? j0 + A.pps : A.nsel;
 
   for (int i = tid; i < kHD * 16; i += kDT) {
@@ -442,7 +443,6 @@ decode_kernel(DecodeArgs A) {
     for (int r = 0; r < 4; ++r) s_o[(wv * 16 + qh) * kHD + 16 * t + 4 * kg + r] = o[t][r];
   __syncthreads();
   const int Hq = H * group;
-  const int64_t split = blockIdx.x;
   for (int i = tid; i < group * kHD; i += kDT) {
     const int hh = i / kHD, d = i % kHD;
     float M = -__builtin_inff();
@@ -462,6 +462,124 @@ decode_kernel(DecodeArgs A) {
       A.part_l[split * Hq + hq] = L;
     }
   }
+}
+
+template <int KB, int VB, bool PG>
+__global__ void __launch_bounds__(kDT) __attribute__((amdgpu_waves_per_eu(3, 3)))
+decode_kernel(DecodeArgs A) {
+  decode_body<KB, VB, PG>(A, blockIdx.x);
+}
+
+// Batched form: B sequences of one compact-format tensor (or of one paged
+// pool), each with its own query, length, selection rows and splits.
+// Sequence b owns the kernel's blocks [split0[b], split0[b+1]); base[b] is
+// its first token in the compact tensor (a multiple of 16) or its first
+// block-table entry in the paged form.
+constexpr int kMaxDecSeqs = 64;
+struct DecSegs {
+  int64_t split0[kMaxDecSeqs + 1];
+  int64_t base[kMaxDecSeqs];
+  int64_t T[kMaxDecSeqs];
+  int64_t sel0[kMaxDecSeqs];
+  int64_t nsel[kMaxDecSeqs];
+  int nseg;
+};
+
+template <int KB, int VB, bool PG>
+__global__ void __launch_bounds__(kDT) __attribute__((amdgpu_waves_per_eu(3, 3)))
+decode_batch_kernel(DecodeArgs A, DecSegs S) {
+  int b = 0;
+  while (b + 1 < S.nseg && S.split0[b + 1] <= (int64_t)blockIdx.x) ++b;
+  // the sequence's view: its query, tokens, selection and partials
+  DecodeArgs a = A;
+  const int Hq = A.H * A.group;
+  a.q = A.q + (int64_t)b * Hq * kHD;
+  a.T = S.T[b];
+  a.npages = (S.T[b] + kPS - 1) / kPS;
+  a.sel = A.sel + S.sel0[b] * A.H;
+  a.nsel = S.nsel[b];
+  if constexpr (PG) {
+    a.bt = A.bt + S.base[b];
+  } else {
+    const int64_t r0 = S.base[b] * A.H;  // first row of the sequence
+    a.k.packed = A.k.packed + r0 * (kHD * KB / 8);
+    a.k.row_ptr = A.k.row_ptr + r0;
+    a.v.packed = A.v.packed + r0 * (kHD * VB / 8);
+    a.v.row_ptr = A.v.row_ptr + r0;
+  }
+  a.part_m = A.part_m + S.split0[b] * Hq;
+  a.part_l = A.part_l + S.split0[b] * Hq;
+  a.part_o = A.part_o + S.split0[b] * Hq * kHD;
+  decode_body<KB, VB, PG>(a, (int64_t)blockIdx.x - S.split0[b]);
+}
+
+// Union of the heads' selected pages per sequence (the reference's decode
+// attends every query head over it: src/kvquant/quest_selector.py:80, then
+// all heads of each kept block, src/kvquant/compact_pool.py:492-537).
+// Sequence b's selection is rows row0[b] .. row0[b+1]-1 of sel (rows, H),
+// page ids local to the sequence; its union goes to rows page0[b] .. of out
+// (all H columns), ascending, -1 after it.  flags (one byte per page of all
+// sequences) is zero on entry and left zero.
+struct UnionSegs {
+  int64_t row0[kMaxDecSeqs + 1];
+  int64_t page0[kMaxDecSeqs + 1];
+  int nseg;
+};
+
+__global__ void __launch_bounds__(256)
+union_mark_kernel(const int64_t* __restrict__ sel, int H, UnionSegs S, uint8_t* __restrict__ flags) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= S.row0[S.nseg] * H) return;
+  const int64_t r = i / H;
+  int b = 0;
+  while (b + 1 < S.nseg && S.row0[b + 1] <= r) ++b;
+  const int64_t p = sel[i], P = S.page0[b + 1] - S.page0[b];
+  if (p >= 0 && p < P) flags[S.page0[b] + p] = 1;
+}
+
+constexpr int kUnionThreads = 1024;
+constexpr int kUnionPer = 16;  // consecutive pages per thread and round
+
+__global__ void __launch_bounds__(kUnionThreads)
+union_compact_kernel(uint8_t* __restrict__ flags, UnionSegs S, int H, int64_t* __restrict__ out) {
+  __shared__ uint32_t red[kUnionThreads / 64];
+  const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int64_t p0 = S.page0[b], P = S.page0[b + 1] - p0;
+  int64_t done = 0;  // union pages written so far
+  for (int64_t c = 0; c < P; c += (int64_t)kUnionThreads * kUnionPer) {
+    const int64_t q0 = c + (int64_t)tid * kUnionPer;
+    uint32_t m = 0;
+#pragma unroll
+    for (int i = 0; i < kUnionPer; ++i)
+      if (q0 + i < P && flags[p0 + q0 + i]) m |= 1u << i;
+    // exclusive prefix of the threads' counts, in thread (= page) order
+    const uint32_t cnt = (uint32_t)__builtin_popcount(m);
+    uint32_t x = cnt;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t y = __shfl_up(x, o, 64);
+      if (lane >= o) x += y;
+    }
+    if (lane == 63) red[wv] = x;
+    __syncthreads();
+    uint32_t before = 0, tot = 0;
+    for (int w = 0; w < kUnionThreads / 64; ++w) {
+      before += w < wv ? red[w] : 0u;
+      tot += red[w];
+    }
+    int64_t o = done + before + x - cnt;
+    for (int i = 0; i < kUnionPer; ++i) {
+      if ((m >> i) & 1u) {
+        for (int h = 0; h < H; ++h) out[(p0 + o) * H + h] = q0 + i;
+        flags[p0 + q0 + i] = 0;
+        ++o;
+      }
+    }
+    done += tot;
+    __syncthreads();  // red is rewritten by the next round
+  }
+  for (int64_t r = done + tid; r < P; r += kUnionThreads)
+    for (int h = 0; h < H; ++h) out[(p0 + r) * H + h] = -1;
 }
 
 // ------------------------------------------------ dense pages (any dtype)
@@ -561,9 +679,8 @@ dense_attn_kernel(DenseArgs A) {
 constexpr int kMergeCh = 16;
 constexpr int kMergeSub = kDT / kMergeCh;
 
-__global__ void __launch_bounds__(kDT)
-merge_kernel(const float* __restrict__ pm, const float* __restrict__ pl,
-             const float* __restrict__ po, int64_t splits, int Hq, int Dv, void* out, int odt) {
+HKV_DEV void merge_body(const float* __restrict__ pm, const float* __restrict__ pl,
+                       const float* __restrict__ po, int64_t splits, int Hq, int Dv, void* out, int odt) {
   __shared__ float s_red[kW];
   __shared__ float s_acc[kDT];
   const int hq = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -613,6 +730,28 @@ merge_kernel(const float* __restrict__ pm, const float* __restrict__ pl,
   }
 }
 
+__global__ void __launch_bounds__(kDT)
+merge_kernel(const float* __restrict__ pm, const float* __restrict__ pl,
+             const float* __restrict__ po, int64_t splits, int Hq, int Dv, void* out, int odt) {
+  merge_body(pm, pl, po, splits, Hq, Dv, out, odt);
+}
+
+// Batched: blockIdx.z = sequence b merges its splits [split0[b], split0[b+1])
+// into out + b * Hq * Dv.
+struct MergeSegs {
+  int64_t split0[kMaxDecSeqs + 1];
+};
+
+__global__ void __launch_bounds__(kDT)
+merge_batch_kernel(const float* __restrict__ pm, const float* __restrict__ pl,
+                   const float* __restrict__ po, MergeSegs S, int Hq, int Dv, void* out, int odt) {
+  const int b = blockIdx.z;
+  const int64_t s0 = S.split0[b];
+  const size_t esz = odt == HKV_DT_F32 ? 4 : 2;
+  merge_body(pm + s0 * Hq, pl + s0 * Hq, po + s0 * Hq * Dv, S.split0[b + 1] - s0, Hq, Dv,
+             static_cast<char*>(out) + (size_t)b * Hq * Dv * esz, odt);
+}
+
 void launch_merge(const float* pm, const float* pl, const float* po, int64_t splits, int Hq, int Dv,
                   void* out, int odt, hipStream_t s) {
   hipLaunchKernelGGL(merge_kernel, dim3((unsigned)Hq, (unsigned)((Dv + kMergeCh - 1) / kMergeCh)),
@@ -625,6 +764,12 @@ template <int KB, int VB, bool PG = false>
 void launch_decode(const DecodeArgs& a, int64_t splits, hipStream_t s) {
   hipLaunchKernelGGL((decode_kernel<KB, VB, PG>), dim3((unsigned)splits, (unsigned)a.H), dim3(kDT),
                      0, s, a);
+}
+
+template <int KB, int VB, bool PG = false>
+void launch_decode_batch(const DecodeArgs& a, const DecSegs& sg, hipStream_t s) {
+  hipLaunchKernelGGL((decode_batch_kernel<KB, VB, PG>), dim3((unsigned)sg.split0[sg.nseg], (unsigned)a.H),
+                     dim3(kDT), 0, s, a, sg);
 }
 
 }  // namespace
@@ -757,6 +902,132 @@ extern "C" int hkv_decode_attn(const void* q, int Hq, int H, int D, int64_t T,
   else launch_decode<2, 2>(a, splits, s);
   HKV_CHECK_LAUNCH();
   launch_merge(pm, pl, po, splits, Hq, kHD, out, out_dtype, s);
+  HKV_CHECK_LAUNCH();
+  return HKV_OK;
+}
+
+extern "C" size_t hkv_decode_batch_workspace_bytes(int B, const int64_t* sel_offsets, int Hq,
+                                                   int pages_per_split) {
+  if (B < 1 || B > kMaxDecSeqs || !sel_offsets || Hq < 1 || pages_per_split < 1) return 0;
+  int64_t splits = 0;
+  for (int b = 0; b < B; ++b) {
+    const int64_t n = sel_offsets[b + 1] - sel_offsets[b];
+    if (n < 0) return 0;
+    splits += n_splits(n, pages_per_split);
+  }
+  return sizeof(float) * (size_t)splits * Hq * (2 + kHD);
+}
+
+extern "C" int hkv_decode_attn_batch(const void* q, int B, int Hq, int H, int D, int64_t T,
+                                     const int64_t* tok_offsets, const int64_t* seq_lens,
+                                     const void* k_packed, const int32_t* k_row_ptr,
+                                     const uint8_t* k_col, const uint16_t* k_val, int64_t k_cap,
+                                     int k_bits, const void* k_tables,
+                                     const void* v_packed, const int32_t* v_row_ptr,
+                                     const uint8_t* v_col, const uint16_t* v_val, int64_t v_cap,
+                                     int v_bits, const void* v_tables, int64_t v_rows,
+                                     const int64_t* sel, const int64_t* sel_offsets,
+                                     int pages_per_split, float scale, void* out, int out_dtype,
+                                     void* workspace, size_t workspace_bytes, void* stream) {
+  if (D != kHD) return HKV_ERR_SHAPE;
+  if (B < 1 || B > kMaxDecSeqs) return HKV_ERR_SHAPE;
+  if (H < 1 || H > 65535 || Hq < H || Hq % H || Hq / H > 16 || T < 1) return HKV_ERR_SHAPE;
+  if (pages_per_split < 1 || pages_per_split > kMaxPPS) return HKV_ERR_ARG;
+  if ((k_bits != 2 && k_bits != 4) || (v_bits != 2 && v_bits != 4)) return HKV_ERR_ARG;
+  if (out_dtype != HKV_DT_F16 && out_dtype != HKV_DT_F32) return HKV_ERR_DTYPE;
+  if (v_rows < 1 || k_cap < 0 || v_cap < 0) return HKV_ERR_ARG;
+  if (T * H * D >= ((int64_t)1 << 31) || (int64_t)H * v_rows >= ((int64_t)1 << 31))
+    return HKV_ERR_SHAPE;
+  if (!q || !k_packed || !k_row_ptr || !k_tables || !v_packed || !v_row_ptr || !v_tables || !out ||
+      !tok_offsets || !seq_lens || !sel_offsets)
+    return HKV_ERR_ARG;
+  if ((k_cap > 0 && (!k_col || !k_val)) || (v_cap > 0 && (!v_col || !v_val))) return HKV_ERR_ARG;
+  if ((((uintptr_t)k_packed | (uintptr_t)v_packed) & 15u) || ((uintptr_t)q & 7u))
+    return HKV_ERR_ARG;
+  DecSegs sg;
+  sg.nseg = B;
+  sg.split0[0] = 0;
+  if (sel_offsets[0] < 0) return HKV_ERR_ARG;
+  for (int b = 0; b < B; ++b) {
+    const int64_t t0 = tok_offsets[b], n = seq_lens[b], ns = sel_offsets[b + 1] - sel_offsets[b];
+    if (t0 < 0 || t0 % kPS || n < 1 || t0 + n > T || ns < 0) return HKV_ERR_ARG;
+    if (ns > 0 && !sel) return HKV_ERR_ARG;
+    sg.base[b] = t0;
+    sg.T[b] = n;
+    sg.sel0[b] = sel_offsets[b];
+    sg.nsel[b] = ns;
+    sg.split0[b + 1] = sg.split0[b] + n_splits(ns, pages_per_split);
+  }
+  const int64_t splits = sg.split0[B];
+  if (splits > 0x7fffffff) return HKV_ERR_SHAPE;
+  const size_t need = hkv_decode_batch_workspace_bytes(B, sel_offsets, Hq, pages_per_split);
+  if (!workspace || workspace_bytes < need) return HKV_ERR_WORKSPACE;
+  hipStream_t s = (hipStream_t)stream;
+  float* pm = (float*)workspace;
+  float* pl = pm + splits * Hq;
+  float* po = pl + splits * Hq;
+  DecodeArgs a;
+  a.q = (const uint16_t*)q;
+  a.k = Side{(const uint8_t*)k_packed, k_row_ptr, k_col, k_val, k_cap, (const hkv_table_t*)k_tables, 0,
+             nullptr, nullptr};
+  a.v = Side{(const uint8_t*)v_packed, v_row_ptr, v_col, v_val, v_cap, (const hkv_table_t*)v_tables,
+             v_rows, nullptr, nullptr};
+  a.bt = nullptr;
+  a.nblocks = 0;
+  a.H = H;
+  a.group = Hq / H;
+  a.T = T;
+  a.npages = (T + kPS - 1) / kPS;
+  a.sel = sel;
+  a.nsel = 0;
+  a.pps = pages_per_split;
+  a.scale = scale;
+  a.part_m = pm;
+  a.part_l = pl;
+  a.part_o = po;
+  if (k_bits == 4 && v_bits == 4) launch_decode_batch<4, 4>(a, sg, s);
+  else if (k_bits == 4) launch_decode_batch<4, 2>(a, sg, s);
+  else if (v_bits == 4) launch_decode_batch<2, 4>(a, sg, s);
+  else launch_decode_batch<2, 2>(a, sg, s);
+  HKV_CHECK_LAUNCH();
+  MergeSegs ms;
+  for (int b = 0; b <= B; ++b) ms.split0[b] = sg.split0[b];
+  hipLaunchKernelGGL(merge_batch_kernel, dim3((unsigned)Hq, (unsigned)((kHD + kMergeCh - 1) / kMergeCh), (unsigned)B),
+                     dim3(kDT), 0, s, pm, pl, po, ms, Hq, kHD, out, out_dtype);
+  HKV_CHECK_LAUNCH();
+  return HKV_OK;
+}
+
+extern "C" size_t hkv_union_pages_workspace_bytes(int64_t total_pages) {
+  if (total_pages < 0) return 0;
+  return ((size_t)total_pages + 255) & ~(size_t)255;
+}
+
+extern "C" int hkv_union_pages_ragged(const int64_t* sel, int H, int B, const int64_t* row_offsets,
+                                      const int64_t* page_offsets, int64_t* out, void* flags,
+                                      size_t flags_bytes, void* stream) {
+  if (B < 1 || B > kMaxDecSeqs || H < 1) return HKV_ERR_SHAPE;
+  if (!row_offsets || !page_offsets || !out || !flags) return HKV_ERR_ARG;
+  UnionSegs sg;
+  sg.nseg = B;
+  if (row_offsets[0] != 0 || page_offsets[0] != 0) return HKV_ERR_ARG;
+  for (int b = 0; b <= B; ++b) {
+    if (b > 0 && (row_offsets[b] < row_offsets[b - 1] || page_offsets[b] < page_offsets[b - 1]))
+      return HKV_ERR_ARG;
+    sg.row0[b] = row_offsets[b];
+    sg.page0[b] = page_offsets[b];
+  }
+  if (sg.row0[B] > 0 && !sel) return HKV_ERR_ARG;
+  if (flags_bytes < (size_t)sg.page0[B]) return HKV_ERR_WORKSPACE;
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t n = sg.row0[B] * H;
+  if (n > 0) {
+    hipLaunchKernelGGL(union_mark_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, sel, H, sg,
+                       (uint8_t*)flags);
+    HKV_CHECK_LAUNCH();
+  }
+  hipLaunchKernelGGL(union_compact_kernel, dim3((unsigned)B), dim3(kUnionThreads), 0, s, (uint8_t*)flags,
+                     sg, H, out);
   HKV_CHECK_LAUNCH();
   return HKV_OK;
 }

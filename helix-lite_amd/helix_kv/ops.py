@@ -696,14 +696,24 @@ def decode_step_batch(queries: torch.Tensor, k: CompactCodes, kt: NuqLayerTables
                       seq_starts, seq_lens, top_k: int, sink_pages: int = 4, *, gqa: str = "mean",
                       select: str = "union", scale: float | None = None,
                       out: torch.Tensor | None = None,
-                      out_dtype: torch.dtype = torch.float16) -> torch.Tensor:
+                      out_dtype: torch.dtype = torch.float16,
+                      pages_per_split: int | None = None) -> torch.Tensor:
     """decode_step for B sequences held in one compact-format tensor, still
     without host reads.  Sequence b is tokens [seq_starts[b], seq_starts[b] +
     seq_lens[b]) of k / v (starts are multiples of the 16-token page; V was
     packed with positions counted from each sequence's start), its page
     statistics are K_min / K_max rows [seq_starts[b] / 16, ...).  The reference
     forward handles batch 1 only (src/kvquant/compact_backend.py:184-203).
+
+    When the sequences lie back to back (each starts on the page after the
+    previous one's last) and B <= 64, the step is one ragged Quest selection
+    (hkv_quest_select_ragged), the per-sequence union of the heads' pages for
+    select="union" (hkv_union_pages_ragged) and one batched decode + merge
+    (hkv_decode_attn_batch); each sequence's result equals decode_step's with
+    the same pages_per_split.  Otherwise decode_step runs per sequence.
     queries (B, Hq, 128) fp16; returns (B, Hq, 128)."""
+    import ctypes
+
     N.require_gpu(queries, K_min, K_max)
     starts = [int(s) for s in seq_starts]
     lens = [int(n) for n in seq_lens]
@@ -712,13 +722,68 @@ def decode_step_batch(queries: torch.Tensor, k: CompactCodes, kt: NuqLayerTables
         raise ValueError(f"queries {tuple(queries.shape)} do not match {B} sequences")
     if any(s % 16 for s in starts) or any(n < 1 for n in lens):
         raise ValueError("sequence starts must be multiples of 16 and lengths positive")
+    if gqa not in ("mean", "sum"):
+        raise ValueError(f"gqa must be 'mean' or 'sum', got {gqa!r}")
+    if select not in ("union", "per_head"):
+        raise ValueError(f"select must be 'union' or 'per_head', got {select!r}")
     if out is None:
         out = torch.empty(tuple(queries.shape), dtype=out_dtype, device=queries.device)
-    for b, (t0, n) in enumerate(zip(starts, lens)):
-        p0, p1 = t0 // 16, (t0 + n + 15) // 16
-        decode_step(queries[b], compact_view(k, t0, t0 + n), kt, compact_view(v, t0, t0 + n), vt,
-                    K_min[p0:p1], K_max[p0:p1], top_k, sink_pages, gqa=gqa, select=select,
-                    scale=scale, out=out[b])
+    T, H, D = k.shape
+    pages = [-(-n // 16) for n in lens]
+    back_to_back = all(starts[b + 1] == starts[b] + 16 * pages[b] for b in range(B - 1))
+    if B > 64 or not back_to_back or starts[-1] + lens[-1] > T or v.shape != (T, H, D):
+        for b, (t0, n) in enumerate(zip(starts, lens)):
+            p0, p1 = t0 // 16, (t0 + n + 15) // 16
+            decode_step(queries[b], compact_view(k, t0, t0 + n), kt, compact_view(v, t0, t0 + n), vt,
+                        K_min[p0:p1], K_max[p0:p1], top_k, sink_pages, gqa=gqa, select=select,
+                        scale=scale, out=out[b], pages_per_split=pages_per_split)
+        return out
+    Hq = int(queries.shape[1])
+    if Hq % H or int(queries.shape[2]) != D or queries.dtype != torch.float16:
+        raise ValueError(f"queries {tuple(queries.shape)} incompatible with (T, H, D) = {(T, H, D)}")
+    if tuple(out.shape) != (B, Hq, D) or out.dtype not in (torch.float16, torch.float32) or \
+            not out.is_contiguous():
+        raise AssertionError(f"out must be contiguous ({B}, {Hq}, {D}) fp16 or fp32")
+    if kt.per_token or not vt.per_token:
+        raise AssertionError("K scales are per-channel, V scales per-token")
+    p0 = starts[0] // 16
+    ptot = sum(pages)
+    offs = [0]
+    for n in pages:
+        offs.append(offs[-1] + n)
+    qs = queries.reshape(B, H, Hq // H, D).mean(dim=2).to(torch.float16) if gqa == "mean" else queries
+    sel, rows, _ = quest_select_ragged(qs, K_min[p0:p0 + ptot], K_max[p0:p0 + ptot], offs, top_k,
+                                       sink_pages)
+    dev = queries.device
+    if select == "union":
+        c_rows = (ctypes.c_int64 * (B + 1))(*rows)
+        c_pages = (ctypes.c_int64 * (B + 1))(*offs)
+        flags = N.workspace("union_flags", int(N.lib().hkv_union_pages_workspace_bytes(ptot)), dev)
+        union = torch.empty((max(ptot, 1), H), dtype=torch.int64, device=dev)
+        st = N.lib().hkv_union_pages_ragged(N.ptr(sel), H, B, c_rows, c_pages, N.ptr(union), N.ptr(flags),
+                                            flags.numel(), N.stream_of(qs))
+        N.check(st, "hkv_union_pages_ragged", ValueError)
+        sel, sel_offs = union, offs
+    else:
+        sel_offs = rows
+    nsel_all = sel_offs[-1]
+    pps = int(pages_per_split) if pages_per_split else decode_pages_per_split(nsel_all, H)
+    c_sel = (ctypes.c_int64 * (B + 1))(*sel_offs)
+    c_tok = (ctypes.c_int64 * B)(*starts)
+    c_len = (ctypes.c_int64 * B)(*lens)
+    q = queries.contiguous()
+    nb = int(N.lib().hkv_decode_batch_workspace_bytes(B, c_sel, Hq, pps))
+    ws = N.workspace("decode", nb, dev)
+    sc = float(scale) if scale is not None else D ** -0.5
+    st = N.lib().hkv_decode_attn_batch(
+        N.ptr(q), B, Hq, H, D, T, c_tok, c_len,
+        N.ptr(k.packed), N.ptr(k.row_ptr), N.ptr(k.col), N.ptr(k.val),
+        min(int(k.col.numel()), int(k.val.numel())), k.bits, N.ptr(kt.ensure_tables()),
+        N.ptr(v.packed), N.ptr(v.row_ptr), N.ptr(v.col), N.ptr(v.val),
+        min(int(v.col.numel()), int(v.val.numel())), v.bits, N.ptr(vt.ensure_tables()), vt.rows,
+        N.ptr(sel), c_sel, pps, sc, N.ptr(out), N.dtype_code(out), N.ptr(ws), ws.numel(),
+        N.stream_of(q))
+    N.check(st, "hkv_decode_attn_batch", AssertionError)
     return out
 
 

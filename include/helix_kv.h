@@ -509,6 +509,52 @@ int hkv_decode_attn(const void *q, int Hq, int H, int D, int64_t T,
                     size_t workspace_bytes, void *stream);
 
 /*
+ * Batched decode: hkv_decode_attn for B <= 64 sequences held in one
+ * compact-format K / V of T tokens, in one decode launch and one merge
+ * launch (the reference decodes one sequence per forward,
+ * src/kvquant/compact_backend.py:184-203; its per-sequence path is
+ * :194-299).  Sequence b is tokens [tok_offsets[b], tok_offsets[b] +
+ * seq_lens[b]) (tok_offsets multiples of 16), with query q[b] (q (B, Hq,
+ * 128) fp16) and selection rows sel_offsets[b] .. sel_offsets[b+1]-1 of sel
+ * (rows, H) int64, page ids local to the sequence (ids outside its pages are
+ * skipped); V per-token tables are indexed by the position within the
+ * sequence, row min(t, v_rows - 1).  out (B, Hq, 128) fp16 or fp32.
+ * tok_offsets, seq_lens (B) and sel_offsets (B+1) are HOST arrays.  Each
+ * sequence's result equals hkv_decode_attn over its view with the same
+ * pages_per_split.  Workspace: hkv_decode_batch_workspace_bytes (no zeroing).
+ */
+size_t hkv_decode_batch_workspace_bytes(int B, const int64_t *sel_offsets, int Hq,
+                                        int pages_per_split);
+int hkv_decode_attn_batch(const void *q, int B, int Hq, int H, int D, int64_t T,
+                          const int64_t *tok_offsets, const int64_t *seq_lens,
+                          const void *k_packed, const int32_t *k_row_ptr, const uint8_t *k_col,
+                          const uint16_t *k_val, int64_t k_cap, int k_bits, const void *k_tables,
+                          const void *v_packed, const int32_t *v_row_ptr, const uint8_t *v_col,
+                          const uint16_t *v_val, int64_t v_cap, int v_bits, const void *v_tables,
+                          int64_t v_rows, const int64_t *sel, const int64_t *sel_offsets,
+                          int pages_per_split, float scale, void *out, int out_dtype,
+                          void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * Per-sequence union of the KV heads' selected pages, the page set the
+ * reference's decode attends for every query head
+ * (src/kvquant/quest_selector.py:80, then all heads of each kept block,
+ * src/kvquant/compact_pool.py:492-537).  Sequence b (B <= 64) owns rows
+ * row_offsets[b] .. row_offsets[b+1]-1 of sel (rows, H) int64 (page ids local
+ * to the sequence, as hkv_quest_select_ragged writes them) and pages
+ * [0, page_offsets[b+1] - page_offsets[b]); its union goes, ascending, to rows
+ * page_offsets[b] .. of out (page_offsets[B], H) int64, every column alike,
+ * with -1 in the rows after it.  row_offsets / page_offsets (B+1, first entry
+ * 0) are HOST arrays.  flags: hkv_union_pages_workspace_bytes(page_offsets[B])
+ * bytes, zero-filled before the first call; each call leaves it zero.  Two
+ * launches, no host reads.
+ */
+size_t hkv_union_pages_workspace_bytes(int64_t total_pages);
+int hkv_union_pages_ragged(const int64_t *sel, int H, int B, const int64_t *row_offsets,
+                           const int64_t *page_offsets, int64_t *out, void *flags,
+                           size_t flags_bytes, void *stream);
+
+/*
  * Ragged batched Quest selection: B <= 64 sequences, sequence b owning pages
  * [page_offsets[b], page_offsets[b+1]) of the concatenated statistics kmin /
  * kmax (P_total, H, D) fp16 (D % 8 == 0, D/8 a power of two), with its own

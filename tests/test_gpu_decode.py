@@ -340,10 +340,13 @@ def test_graph_survives_workspace_growth(dev):
     assert all(bool((f == 7).all()) for f in fillers)
 
 
-def test_decode_step_batch_vs_oracle(dev):
+@pytest.mark.parametrize("select,gqa", [("union", "mean"), ("per_head", "sum"), ("per_head", "mean"),
+                                        ("union", "sum")])
+def test_decode_step_batch_vs_oracle(dev, select, gqa):
     """Three sequences in one compact tensor (page-aligned starts, V packed with
-    positions from each sequence's start): decode_step_batch equals the oracle
-    pipeline per sequence, union and mean-q as the reference forward."""
+    positions from each sequence's start): decode_step_batch (one ragged
+    selection, the per-sequence union, one batched decode) equals the oracle
+    pipeline per sequence; union and mean-q are the reference forward's."""
     from helix_kv.ops import NuqLayerTables, decode_step_batch, nuq_pack_compact
 
     H, group, D, top_k, sinks = 4, 7, 128, 12, 4
@@ -380,17 +383,83 @@ def test_decode_step_batch_vs_oracle(dev):
     q = RNG.standard_normal((len(lens), H * group, D)).astype(np.float16)
     qd = _t(q, dev)
     got = decode_step_batch(qd, kc, kt, vc, vt, _t(kmin, dev), _t(kmax, dev), starts, lens,
-                            top_k, sinks, out_dtype=torch.float32)
+                            top_k, sinks, gqa=gqa, select=select, out_dtype=torch.float32)
     for b, (s0, n) in enumerate(zip(starts, lens)):
         P = -(-n // PS)
         pad = P * PS - n
         kb = np.concatenate([kd[s0:s0 + n], np.zeros((pad, H, D))]).reshape(P, PS, H, D)
         vb = np.concatenate([vd[s0:s0 + n], np.zeros((pad, H, D))]).reshape(P, PS, H, D)
-        qs = qd[b].reshape(H, group, D).mean(dim=1).to(torch.float16).cpu().numpy()
-        bound = O.page_bound(qs, stats[b][0], stats[b][1])
+        if gqa == "mean":
+            qs = qd[b].reshape(H, group, D).mean(dim=1).to(torch.float16).cpu().numpy()
+            bound = O.page_bound(qs, stats[b][0], stats[b][1])
+        else:
+            bound = O.page_bound_group(q[b], stats[b][0].astype(np.float32),
+                                       stats[b][1].astype(np.float32), group)
         sel = O.topk_sinks(bound, min(top_k, P - sinks), sinks)
-        ids = np.unique(sel.reshape(-1))
-        want = O.selected_attention(q[b].astype(np.float64), kb, vb,
-                                    np.repeat(ids[:, None], H, axis=1), lambda h: h // group,
+        if select == "union":
+            ids = np.unique(sel.reshape(-1))
+            sel = np.repeat(ids[:, None], H, axis=1)
+        want = O.selected_attention(q[b].astype(np.float64), kb, vb, sel, lambda h: h // group,
                                     num_tokens=n)
         _check(got[b], want)
+
+
+@pytest.mark.parametrize("layout", ["back_to_back", "gapped"])
+def test_decode_step_batch_equals_single_steps(dev, layout):
+    """The batched step (one ragged selection, one union, one decode launch;
+    the gapped layout takes the per-sequence path) equals decode_step on each
+    sequence's view with the same pages_per_split, bit for bit, in both select
+    modes; and a HIP graph of the batched step replays it exactly."""
+    from helix_kv.ops import (NuqLayerTables, compact_view, decode_step, decode_step_batch,
+                              nuq_pack_compact)
+
+    H, group, D, top_k, sinks, pps = 4, 7, 128, 20, 4, 8
+    lens = [700, 1601, 40, 2100, 16]
+    gap = 0 if layout == "back_to_back" else 32
+    starts = [0]
+    for n in lens[:-1]:
+        starts.append(starts[-1] + -(-n // PS) * PS + gap)
+    T = starts[-1] + -(-lens[-1] // PS) * PS
+    pos = np.zeros(T, np.int64)
+    for s0, n in zip(starts, lens):
+        pos[s0:s0 + -(-n // PS) * PS] = np.arange(-(-n // PS) * PS)
+    k = (RNG.standard_t(3, (T, H, D)) * 0.7).astype(np.float16)
+    v = (RNG.standard_t(3, (T, H, D)) * 0.7).astype(np.float16)
+    kp, ku, kl = _scales(H, D, 4, 1.2)
+    vp, vu, vl = _scales(H, 1024, 16, 1.2)
+    kt = NuqLayerTables(_t(kp, dev), _t(ku, dev), _t(kl, dev), per_token=False)
+    vt = NuqLayerTables(_t(vp, dev), _t(vu, dev), _t(vl, dev), per_token=True)
+    kc = nuq_pack_compact(_t(k, dev), kt, 2)
+    vc = nuq_pack_compact(_t(v, dev), vt, 4, positions=torch.from_numpy(pos))
+    kmin, kmax = _stats(k, T, H)
+    kmin_d, kmax_d = _t(kmin, dev), _t(kmax, dev)
+    qd = _t(RNG.standard_normal((len(lens), H * group, D)).astype(np.float16), dev)
+    for select in ("union", "per_head"):
+        got = decode_step_batch(qd, kc, kt, vc, vt, kmin_d, kmax_d, starts, lens, top_k, sinks,
+                                select=select, pages_per_split=pps)
+        for b, (t0, n) in enumerate(zip(starts, lens)):
+            p0, p1 = t0 // PS, (t0 + n + PS - 1) // PS
+            one = decode_step(qd[b], compact_view(kc, t0, t0 + n), kt, compact_view(vc, t0, t0 + n), vt,
+                              kmin_d[p0:p1], kmax_d[p0:p1], top_k, sinks, select=select,
+                              pages_per_split=pps)
+            assert torch.equal(got[b].view(torch.int16), one.view(torch.int16)), (layout, select, b)
+    if layout != "back_to_back":
+        return
+    out = torch.empty_like(got)
+    st = torch.cuda.Stream()
+    with torch.cuda.stream(st):
+        decode_step_batch(qd, kc, kt, vc, vt, kmin_d, kmax_d, starts, lens, top_k, sinks,
+                          pages_per_split=pps, out=out)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=st):
+            decode_step_batch(qd, kc, kt, vc, vt, kmin_d, kmax_d, starts, lens, top_k, sinks,
+                              pages_per_split=pps, out=out)
+    torch.cuda.synchronize()
+    want = decode_step_batch(qd, kc, kt, vc, vt, kmin_d, kmax_d, starts, lens, top_k, sinks,
+                             pages_per_split=pps)
+    for _ in range(3):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), want.view(torch.int16))
