@@ -977,8 +977,36 @@ def bench_ragged(args, dev):
     del kd
     log(f"[bench] ragged select + gather: {us:.1f} us/step, {rows} rows x {H} heads, "
         f"{(sel_bytes + gather_bytes) / (us * 1e-6) / 1e9:.0f} GB/s")
+    # the fused decode step of the 8 sequences (same selections, per-head
+    # pages; and the reference's mean-q union of the heads' pages): one
+    # batched step against decode_step per sequence
+    from helix_kv.ops import compact_view, decode_step, decode_step_batch
+
+    starts = [int(o) * 16 for o in offs[:-1]]
+    tlens = [int(n) * 16 for n in lens]
+    dout = torch.empty((len(lens), HQ, D), dtype=torch.float16, device=dev)
+    lout = torch.empty_like(dout)
+    dec = {}
+    for mode, gqa in (("per_head", "sum"), ("union", "mean")):
+        def batched():
+            decode_step_batch(q, ck, kt, cv, vt, kmin, kmax, starts, tlens, ks, 4, gqa=gqa,
+                              select=mode, out=dout)
+
+        def looped():
+            for b, (t0, n) in enumerate(zip(starts, tlens)):
+                p0, p1 = t0 // 16, (t0 + n) // 16
+                decode_step(q[b], compact_view(ck, t0, t0 + n), kt, compact_view(cv, t0, t0 + n), vt,
+                            kmin[p0:p1], kmax[p0:p1], ks[b], 4, gqa=gqa, select=mode, out=lout[b])
+
+        dec[mode] = (graph_us(batched, stream, iters), graph_us(looped, stream, iters))
+        rel = float(((dout.float() - lout.float()).norm(dim=-1) / lout.float().norm(dim=-1)).max().item())
+        if rel > 1e-3:
+            raise RuntimeError(f"batched decode step differs from the per-sequence steps: {rel:.2e}")
+    log(f"[bench] ragged decode step, 8 sequences: per-head pages {dec['per_head'][0]:.1f} us batched "
+        f"({dec['per_head'][1]:.1f} us as 8 decode_step calls); mean-q union "
+        f"{dec['union'][0]:.1f} us batched ({dec['union'][1]:.1f} us as 8 calls)")
     return dict(rag_us=us, rag_bytes=sel_bytes + gather_bytes, rag_rows=rows, rag_pages=Ptot,
-                rag_sel_bytes=sel_bytes, rag_gather_bytes=gather_bytes)
+                rag_sel_bytes=sel_bytes, rag_gather_bytes=gather_bytes, rag_dec=dec)
 
 
 PAGED_CAP = 256  # outlier entries per page-head (12.5% of its 2048 elements)
@@ -1282,6 +1310,11 @@ def main() -> None:
                                     "concatenated nuq4 compact pool, 4 KV heads x 128, q (8, 28, 128); "
                                     "per sequence top 25% + 4 sinks per KV head, then per-head "
                                     "gather + dequant of K and V into fp16 staging; one HIP graph"}
+        if "rag_dec" in res:
+            d = res["rag_dec"]
+            line["ragged"]["decode_step_us"] = {
+                "per_head_batched": round(d["per_head"][0], 1), "per_head_8_calls": round(d["per_head"][1], 1),
+                "union_mean_q_batched": round(d["union"][0], 1), "union_mean_q_8_calls": round(d["union"][1], 1)}
     if "rt_us" in res:
         line["roundtrip_4096"] = {
             "us_per_round_trip": round(res["rt_us"], 2),

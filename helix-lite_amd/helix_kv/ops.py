@@ -693,7 +693,7 @@ def compact_view(c: CompactCodes, t0: int, t1: int) -> CompactCodes:
 
 def decode_step_batch(queries: torch.Tensor, k: CompactCodes, kt: NuqLayerTables, v: CompactCodes,
                       vt: NuqLayerTables, K_min: torch.Tensor, K_max: torch.Tensor,
-                      seq_starts, seq_lens, top_k: int, sink_pages: int = 4, *, gqa: str = "mean",
+                      seq_starts, seq_lens, top_k, sink_pages: int = 4, *, gqa: str = "mean",
                       select: str = "union", scale: float | None = None,
                       out: torch.Tensor | None = None,
                       out_dtype: torch.dtype = torch.float16,
@@ -711,7 +711,8 @@ def decode_step_batch(queries: torch.Tensor, k: CompactCodes, kt: NuqLayerTables
     select="union" (hkv_union_pages_ragged) and one batched decode + merge
     (hkv_decode_attn_batch); each sequence's result equals decode_step's with
     the same pages_per_split.  Otherwise decode_step runs per sequence.
-    queries (B, Hq, 128) fp16; returns (B, Hq, 128)."""
+    top_k: one int, or one per sequence.  queries (B, Hq, 128) fp16; returns
+    (B, Hq, 128)."""
     import ctypes
 
     N.require_gpu(queries, K_min, K_max)
@@ -722,6 +723,9 @@ def decode_step_batch(queries: torch.Tensor, k: CompactCodes, kt: NuqLayerTables
         raise ValueError(f"queries {tuple(queries.shape)} do not match {B} sequences")
     if any(s % 16 for s in starts) or any(n < 1 for n in lens):
         raise ValueError("sequence starts must be multiples of 16 and lengths positive")
+    ks = [int(top_k)] * B if not hasattr(top_k, '__len__') else [int(x) for x in top_k]
+    if len(ks) != B:
+        raise ValueError("one top_k per sequence")
     if gqa not in ("mean", "sum"):
         raise ValueError(f"gqa must be 'mean' or 'sum', got {gqa!r}")
     if select not in ("union", "per_head"):
@@ -735,7 +739,7 @@ def decode_step_batch(queries: torch.Tensor, k: CompactCodes, kt: NuqLayerTables
         for b, (t0, n) in enumerate(zip(starts, lens)):
             p0, p1 = t0 // 16, (t0 + n + 15) // 16
             decode_step(queries[b], compact_view(k, t0, t0 + n), kt, compact_view(v, t0, t0 + n), vt,
-                        K_min[p0:p1], K_max[p0:p1], top_k, sink_pages, gqa=gqa, select=select,
+                        K_min[p0:p1], K_max[p0:p1], ks[b], sink_pages, gqa=gqa, select=select,
                         scale=scale, out=out[b], pages_per_split=pages_per_split)
         return out
     Hq = int(queries.shape[1])
@@ -752,7 +756,7 @@ def decode_step_batch(queries: torch.Tensor, k: CompactCodes, kt: NuqLayerTables
     for n in pages:
         offs.append(offs[-1] + n)
     qs = queries.reshape(B, H, Hq // H, D).mean(dim=2).to(torch.float16) if gqa == "mean" else queries
-    sel, rows, _ = quest_select_ragged(qs, K_min[p0:p0 + ptot], K_max[p0:p0 + ptot], offs, top_k,
+    sel, rows, _ = quest_select_ragged(qs, K_min[p0:p0 + ptot], K_max[p0:p0 + ptot], offs, ks,
                                        sink_pages)
     dev = queries.device
     if select == "union":
