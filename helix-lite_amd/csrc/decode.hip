@@ -518,11 +518,19 @@ decode_batch_kernel(DecodeArgs A, DecSegs S) {
 // all heads of each kept block, src/kvquant/compact_pool.py:492-537).
 // Sequence b's selection is rows row0[b] .. row0[b+1]-1 of sel (rows, H),
 // page ids local to the sequence; its union goes to rows page0[b] .. of out
-// (all H columns), ascending, -1 after it.  flags (one byte per page of all
-// sequences) is zero on entry and left zero.
+// (all H columns), ascending, -1 after it.  Three launches over the whole
+// batch: mark (a flag byte per selected page), count (set flags per chunk of
+// kUnionChunk pages), write (each chunk's pages at the offset its sequence's
+// earlier chunks give, through LDS so the rows are written coalesced; the
+// chunk's rows past the union get -1; the flags are cleared).  The flags
+// (one byte per page of all sequences) are zero on entry and left zero.
+constexpr int kUnionThreads = 256;
+constexpr int kUnionPer = 8;                                 // pages per thread
+constexpr int kUnionChunk = kUnionThreads * kUnionPer;       // pages per block
 struct UnionSegs {
   int64_t row0[kMaxDecSeqs + 1];
   int64_t page0[kMaxDecSeqs + 1];
+  int64_t chunk0[kMaxDecSeqs + 1];  // sequence b's chunks are chunk0[b] .. chunk0[b+1]-1
   int nseg;
 };
 
@@ -537,49 +545,98 @@ union_mark_kernel(const int64_t* __restrict__ sel, int H, UnionSegs S, uint8_t* 
   if (p >= 0 && p < P) flags[S.page0[b] + p] = 1;
 }
 
-constexpr int kUnionThreads = 1024;
-constexpr int kUnionPer = 16;  // consecutive pages per thread and round
+// Block = chunk c of sequence b: its pages [q0, q1) of the sequence and the
+// thread's flag mask (page q0 + kUnionPer * tid + i at bit i).
+struct UnionChunk {
+  int b;
+  int64_t p0, P, q0, q1;
+};
+HKV_DEV UnionChunk union_chunk(const UnionSegs& S) {
+  UnionChunk u;
+  u.b = 0;
+  while (u.b + 1 < S.nseg && S.chunk0[u.b + 1] <= (int64_t)blockIdx.x) ++u.b;
+  u.p0 = S.page0[u.b];
+  u.P = S.page0[u.b + 1] - u.p0;
+  u.q0 = ((int64_t)blockIdx.x - S.chunk0[u.b]) * kUnionChunk;
+  u.q1 = u.q0 + kUnionChunk < u.P ? u.q0 + kUnionChunk : u.P;
+  return u;
+}
+HKV_DEV uint32_t union_mask(const uint8_t* flags, const UnionChunk& u) {
+  const int64_t t0 = u.q0 + (int64_t)kUnionPer * threadIdx.x;
+  uint32_t m = 0;
+#pragma unroll
+  for (int i = 0; i < kUnionPer; ++i)
+    if (t0 + i < u.q1 && flags[u.p0 + t0 + i]) m |= 1u << i;
+  return m;
+}
+HKV_DEV uint32_t union_block_sum(uint32_t v, uint32_t* red) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  __syncthreads();
+  if (lane == 0) red[wv] = v;
+  __syncthreads();
+  uint32_t t = 0;
+  for (int w = 0; w < kUnionThreads / 64; ++w) t += red[w];
+  return t;
+}
 
 __global__ void __launch_bounds__(kUnionThreads)
-union_compact_kernel(uint8_t* __restrict__ flags, UnionSegs S, int H, int64_t* __restrict__ out) {
+union_count_kernel(const uint8_t* __restrict__ flags, UnionSegs S, uint32_t* __restrict__ cnt) {
   __shared__ uint32_t red[kUnionThreads / 64];
-  const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int64_t p0 = S.page0[b], P = S.page0[b + 1] - p0;
-  int64_t done = 0;  // union pages written so far
-  for (int64_t c = 0; c < P; c += (int64_t)kUnionThreads * kUnionPer) {
-    const int64_t q0 = c + (int64_t)tid * kUnionPer;
-    uint32_t m = 0;
-#pragma unroll
-    for (int i = 0; i < kUnionPer; ++i)
-      if (q0 + i < P && flags[p0 + q0 + i]) m |= 1u << i;
-    // exclusive prefix of the threads' counts, in thread (= page) order
-    const uint32_t cnt = (uint32_t)__builtin_popcount(m);
-    uint32_t x = cnt;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const uint32_t y = __shfl_up(x, o, 64);
-      if (lane >= o) x += y;
-    }
-    if (lane == 63) red[wv] = x;
-    __syncthreads();
-    uint32_t before = 0, tot = 0;
-    for (int w = 0; w < kUnionThreads / 64; ++w) {
-      before += w < wv ? red[w] : 0u;
-      tot += red[w];
-    }
-    int64_t o = done + before + x - cnt;
-    for (int i = 0; i < kUnionPer; ++i) {
-      if ((m >> i) & 1u) {
-        for (int h = 0; h < H; ++h) out[(p0 + o) * H + h] = q0 + i;
-        flags[p0 + q0 + i] = 0;
-        ++o;
-      }
-    }
-    done += tot;
-    __syncthreads();  // red is rewritten by the next round
+  const UnionChunk u = union_chunk(S);
+  const uint32_t t = union_block_sum((uint32_t)__builtin_popcount(union_mask(flags, u)), red);
+  if (threadIdx.x == 0) cnt[blockIdx.x] = t;
+}
+
+__global__ void __launch_bounds__(kUnionThreads)
+union_write_kernel(uint8_t* __restrict__ flags, UnionSegs S, const uint32_t* __restrict__ cnt, int H,
+                   int64_t* __restrict__ out) {
+  __shared__ uint32_t red[kUnionThreads / 64];
+  __shared__ uint32_t lst[kUnionChunk];  // the chunk's union pages, in order
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const UnionChunk u = union_chunk(S);
+  // pages of the sequence's earlier chunks, and of all its chunks
+  const int64_t c0 = S.chunk0[u.b], c = (int64_t)blockIdx.x;
+  uint32_t before = 0, all = 0;
+  for (int64_t i = c0 + tid; i < S.chunk0[u.b + 1]; i += kUnionThreads) {
+    before += i < c ? cnt[i] : 0u;
+    all += cnt[i];
   }
-  for (int64_t r = done + tid; r < P; r += kUnionThreads)
-    for (int h = 0; h < H; ++h) out[(p0 + r) * H + h] = -1;
+  before = union_block_sum(before, red);
+  all = union_block_sum(all, red);
+  // the chunk's pages in order: exclusive scan of the threads' counts
+  const uint32_t m = union_mask(flags, u);
+  const uint32_t k = (uint32_t)__builtin_popcount(m);
+  uint32_t x = k;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  __syncthreads();
+  if (lane == 63) red[wv] = x;
+  __syncthreads();
+  uint32_t pre = x - k, tot = 0;
+  for (int w = 0; w < kUnionThreads / 64; ++w) {
+    pre += w < wv ? red[w] : 0u;
+    tot += red[w];
+  }
+  const int64_t t0 = u.q0 + (int64_t)kUnionPer * tid;
+#pragma unroll
+  for (int i = 0; i < kUnionPer; ++i) {
+    if ((m >> i) & 1u) {
+      lst[pre++] = (uint32_t)(t0 + i);
+      flags[u.p0 + t0 + i] = 0;
+    }
+  }
+  __syncthreads();
+  // rows before + j of the sequence, every column, written consecutively
+  int64_t* o = out + (u.p0 + (int64_t)before) * H;
+  for (int64_t e = tid; e < (int64_t)tot * H; e += kUnionThreads) o[e] = (int64_t)lst[e / H];
+  // this chunk's share of the rows after the union: [q0, q1) past `all`
+  const int64_t r0 = u.q0 > (int64_t)all ? u.q0 : (int64_t)all;
+  for (int64_t e = r0 * H + tid; e < u.q1 * H; e += kUnionThreads) out[u.p0 * H + e] = -1;
 }
 
 // ------------------------------------------------ dense pages (any dtype)
@@ -998,9 +1055,18 @@ extern "C" int hkv_decode_attn_batch(const void* q, int B, int Hq, int H, int D,
   return HKV_OK;
 }
 
+// Workspace: the flags (one byte per page) at its start, the per-chunk
+// counts (at most total_pages / kUnionChunk + kMaxDecSeqs + 1 chunks) at its
+// end.  A buffer reused by calls over different page counts keeps every
+// call's counts past every call's flags: a call over P pages needs its size
+// W >= align256(P) + 4 n(P) with n growing with P, so the flags of any call
+// end below W - 4 n(P) for every P it can hold.
+static size_t union_counts(int64_t total_pages) { return (size_t)total_pages / kUnionChunk + kMaxDecSeqs + 1; }
+
 extern "C" size_t hkv_union_pages_workspace_bytes(int64_t total_pages) {
   if (total_pages < 0) return 0;
-  return ((size_t)total_pages + 255) & ~(size_t)255;
+  const size_t f = ((size_t)total_pages + 255) & ~(size_t)255;
+  return f + sizeof(uint32_t) * union_counts(total_pages);
 }
 
 extern "C" int hkv_union_pages_ragged(const int64_t* sel, int H, int B, const int64_t* row_offsets,
@@ -1011,24 +1077,33 @@ extern "C" int hkv_union_pages_ragged(const int64_t* sel, int H, int B, const in
   UnionSegs sg;
   sg.nseg = B;
   if (row_offsets[0] != 0 || page_offsets[0] != 0) return HKV_ERR_ARG;
+  sg.chunk0[0] = 0;
   for (int b = 0; b <= B; ++b) {
     if (b > 0 && (row_offsets[b] < row_offsets[b - 1] || page_offsets[b] < page_offsets[b - 1]))
       return HKV_ERR_ARG;
     sg.row0[b] = row_offsets[b];
     sg.page0[b] = page_offsets[b];
+    if (b > 0)
+      sg.chunk0[b] = sg.chunk0[b - 1] + (page_offsets[b] - page_offsets[b - 1] + kUnionChunk - 1) / kUnionChunk;
   }
   if (sg.row0[B] > 0 && !sel) return HKV_ERR_ARG;
-  if (flags_bytes < (size_t)sg.page0[B]) return HKV_ERR_WORKSPACE;
+  if (flags_bytes < hkv_union_pages_workspace_bytes(sg.page0[B])) return HKV_ERR_WORKSPACE;
+  const int64_t chunks = sg.chunk0[B];
+  if (chunks > 0x7fffffff) return HKV_ERR_SHAPE;
   hipStream_t s = (hipStream_t)stream;
+  uint8_t* fl = (uint8_t*)flags;
+  uint32_t* cnt = (uint32_t*)(fl + ((flags_bytes - sizeof(uint32_t) * union_counts(sg.page0[B])) & ~(size_t)3));
   const int64_t n = sg.row0[B] * H;
   if (n > 0) {
-    hipLaunchKernelGGL(union_mark_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, sel, H, sg,
-                       (uint8_t*)flags);
+    hipLaunchKernelGGL(union_mark_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, sel, H, sg, fl);
     HKV_CHECK_LAUNCH();
   }
-  hipLaunchKernelGGL(union_compact_kernel, dim3((unsigned)B), dim3(kUnionThreads), 0, s, (uint8_t*)flags,
-                     sg, H, out);
-  HKV_CHECK_LAUNCH();
+  if (chunks > 0) {
+    hipLaunchKernelGGL(union_count_kernel, dim3((unsigned)chunks), dim3(kUnionThreads), 0, s, fl, sg, cnt);
+    HKV_CHECK_LAUNCH();
+    hipLaunchKernelGGL(union_write_kernel, dim3((unsigned)chunks), dim3(kUnionThreads), 0, s, fl, sg, cnt, H, out);
+    HKV_CHECK_LAUNCH();
+  }
   return HKV_OK;
 }
 

@@ -667,17 +667,31 @@ def decode_step(query: torch.Tensor, k: CompactCodes, kt: NuqLayerTables, v: Com
     if select == "union":
         # the union's pages ascending at the front, -1 after them: the decode
         # kernel's splits past the union's end find no valid page and return
-        flags = torch.zeros(P, dtype=torch.bool, device=query.device)
-        flags.index_fill_(0, sel.reshape(-1), True)
-        pages = torch.arange(P, dtype=torch.int64, device=query.device)
-        dest = torch.where(flags, torch.cumsum(flags, 0) - 1, torch.full_like(pages, P))
-        union = torch.full((P + 1,), -1, dtype=torch.int64, device=query.device)
-        union.scatter_(0, dest, torch.where(flags, pages, torch.full_like(pages, -1)))
-        sel = union[:P].view(P, 1).expand(P, H).contiguous()
+        sel = union_pages(sel, P)
     elif select != "per_head":
         raise ValueError(f"select must be 'union' or 'per_head', got {select!r}")
     return decode_attention(query, k, kt, v, vt, sel, scale=scale, out=out, out_dtype=out_dtype,
                             pages_per_split=pages_per_split)
+
+
+def union_pages(sel: torch.Tensor, P: int) -> torch.Tensor:
+    """The union over KV heads of one sequence's selection (n, H) of pages in
+    [0, P), as a (P, H) list of the union's pages ascending, every column
+    alike, followed by -1 (hkv_union_pages_ragged: three launches, no read-back).
+    src/kvquant/quest_selector.py:80."""
+    import ctypes
+
+    N.require_gpu(sel)
+    n, H = (int(x) for x in sel.shape)
+    s = sel.to(torch.int64).contiguous()
+    out = torch.empty((max(P, 1), H), dtype=torch.int64, device=sel.device)
+    flags = N.workspace("union_flags", int(N.lib().hkv_union_pages_workspace_bytes(P)), sel.device)
+    c_rows = (ctypes.c_int64 * 2)(0, n)
+    c_pages = (ctypes.c_int64 * 2)(0, P)
+    st = N.lib().hkv_union_pages_ragged(N.ptr(s), H, 1, c_rows, c_pages, N.ptr(out), N.ptr(flags),
+                                        flags.numel(), N.stream_of(s))
+    N.check(st, "hkv_union_pages_ragged", ValueError)
+    return out[:P]
 
 
 def compact_view(c: CompactCodes, t0: int, t1: int) -> CompactCodes:

@@ -19,7 +19,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _native as N
-from .ops import NuqLayerTables
+from .ops import NuqLayerTables, union_pages
 
 PAGE = 16
 HEAD_DIM = 128
@@ -267,20 +267,6 @@ def paged_decode_attention(query: torch.Tensor, kside: PagedSide, kt: NuqLayerTa
         N.ptr(ws), ws.numel(), N.stream_of(q))
     N.check(st, "hkv_paged_decode_attn", AssertionError)
     return out
-
-
-def union_pages(sel: torch.Tensor, P: int) -> torch.Tensor:
-    """The union over KV heads of a selection (n, H), as a (P, H) list of the
-    union's pages ascending followed by -1 (every size known on the host: no
-    read-back).  src/kvquant/quest_selector.py:80."""
-    H = int(sel.shape[1])
-    flags = torch.zeros(P, dtype=torch.bool, device=sel.device)
-    flags.index_fill_(0, sel.reshape(-1), True)
-    pages = torch.arange(P, dtype=torch.int64, device=sel.device)
-    dest = torch.where(flags, torch.cumsum(flags, 0) - 1, torch.full_like(pages, P))
-    union = torch.full((P + 1,), -1, dtype=torch.int64, device=sel.device)
-    union.scatter_(0, dest, torch.where(flags, pages, torch.full_like(pages, -1)))
-    return union[:P].view(P, 1).expand(P, H).contiguous()
 
 
 def paged_decode_step(query: torch.Tensor, kside: PagedSide, kt: NuqLayerTables, vside: PagedSide,

@@ -546,8 +546,8 @@ int hkv_decode_attn_batch(const void *q, int B, int Hq, int H, int D, int64_t T,
  * page_offsets[b] .. of out (page_offsets[B], H) int64, every column alike,
  * with -1 in the rows after it.  row_offsets / page_offsets (B+1, first entry
  * 0) are HOST arrays.  flags: hkv_union_pages_workspace_bytes(page_offsets[B])
- * bytes, zero-filled before the first call; each call leaves it zero.  Two
- * launches, no host reads.
+ * bytes, zero-filled before the first call; each call leaves it zero.  Three
+ * launches over the whole batch, no host reads.
  */
 size_t hkv_union_pages_workspace_bytes(int64_t total_pages);
 int hkv_union_pages_ragged(const int64_t *sel, int H, int B, const int64_t *row_offsets,

@@ -404,6 +404,22 @@ def test_decode_step_batch_vs_oracle(dev, select, gqa):
         _check(got[b], want)
 
 
+def test_union_pages_vs_numpy_on_a_reused_workspace(dev):
+    """The union of the heads' pages (hkv_union_pages_ragged) against numpy,
+    over calls of growing and shrinking page counts on one workspace: each
+    call must leave the flags zero for the next, whatever its size."""
+    from helix_kv.ops import union_pages
+
+    for P, n, H in [(5000, 1250, 4), (300, 80, 2), (70000, 17500, 4), (100, 100, 4), (70000, 20, 1),
+                    (40, 10, 4), (2048, 600, 3), (2049, 600, 3)]:
+        sel = np.stack([RNG.choice(P, n, replace=False) for _ in range(H)], axis=1).astype(np.int64)
+        got = union_pages(_t(sel, dev), P).cpu().numpy()
+        u = np.unique(sel)
+        want = np.full((P, H), -1, np.int64)
+        want[: len(u)] = u[:, None]
+        assert np.array_equal(got, want), (P, n, H)
+
+
 @pytest.mark.parametrize("layout", ["back_to_back", "gapped"])
 def test_decode_step_batch_equals_single_steps(dev, layout):
     """The batched step (one ragged selection, one union, one decode launch;
