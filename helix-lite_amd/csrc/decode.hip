@@ -192,7 +192,8 @@ HKV_DEV void load_outl(const DecodeArgs& A, const PageLoad<KB, VB>& L, int lane,
 }
 
 // Dequantise the lane's 32 codes into tile row l/4, channels [32(l%4), +32).
-template <int NB, typename Lut>
+// FULL: every row of the page is a token of the context (no masking).
+template <int NB, bool FULL, typename Lut>
 HKV_DEV void dequant_rows(const uint32_t (&w)[NB], bool valid, int lane, uint16_t* tile, Lut lut) {
   const int row = lane >> 2, c0 = 32 * (lane & 3);
 #pragma unroll
@@ -209,7 +210,7 @@ HKV_DEV void dequant_rows(const uint32_t (&w)[NB], bool valid, int lane, uint16_
         else code = (w[e >> 4] >> (2 * (e & 15))) & 3u;
         pr |= (uint32_t)lut(c0 + e, code) << (16 * e2);
       }
-      h[j] = valid ? pr : 0u;  // rows past the context read as zeros
+      h[j] = (FULL || valid) ? pr : 0u;  // rows past the context read as zeros
     }
     *reinterpret_cast<uint4*>(tile + row * kTS + c0 + 8 * k) = make_uint4(h[0], h[1], h[2], h[3]);
   }
@@ -322,17 +323,19 @@ HKV_DEV void decode_body(const DecodeArgs& A, int64_t split) {
     const bool valid = t0 + row < A.T;
     *reinterpret_cast<uint2*>(vl + row * 16 + 4 * (lane & 3)) = L.vtab;
     wave_sync();
-    dequant_rows<KB>(L.kc, valid, lane, kt,
-                     [&](int ch, uint32_t c) { return s_klut[klut_index(ch, (int)c)]; });
-    dequant_rows<VB>(L.vc, valid, lane, vt,
-                     [&](int, uint32_t c) { return vl[row * 16 + (int)c]; });
+    auto klut = [&](int ch, uint32_t c) { return s_klut[klut_index(ch, (int)c)]; };
+    auto vlut = [&](int, uint32_t c) { return vl[row * 16 + (int)c]; };
+    dequant_rows<KB, false>(L.kc, valid, lane, kt, klut);
+    dequant_rows<VB, false>(L.vc, valid, lane, vt, vlut);
     wave_sync();
     if constexpr (PG) {
       // the page-head's entries (rows past the context are masked below)
-      const int kn = L.kr.x < (int)A.k.cap ? L.kr.x : (int)A.k.cap;
-      const int vn = L.vr.x < (int)A.v.cap ? L.vr.x : (int)A.v.cap;
+      // the counts are the same in every lane: slots past them are skipped
+      const int kn = __builtin_amdgcn_readfirstlane(L.kr.x < (int)A.k.cap ? L.kr.x : (int)A.k.cap);
+      const int vn = __builtin_amdgcn_readfirstlane(L.vr.x < (int)A.v.cap ? L.vr.x : (int)A.v.cap);
 #pragma unroll
       for (int s = 0; s < kSlots; ++s) {
+        if (64 * s >= (kn > vn ? kn : vn)) break;
         const int i = lane + 64 * s;
         if (i < kn) {
           const uint32_t e = Ob.kval[s], sl = e >> 24, ch = (e >> 16) & 255u;
