@@ -58,6 +58,18 @@ constexpr float kLog2e = 1.4426950408889634f;
 // q puts the four q groups on disjoint banks (32 or 64 banks).
 HKV_DEV int klut_index(int ch, int c) { return ch * 16 + 16 * (ch >> 5) + c; }
 
+// nuq2 pair tables: one 32-bit word holds the two fp16 values of a pair of
+// adjacent channels' codes, so a lane makes one table read (and one address)
+// per two codes and stores the word as it is.  K: pair p = channels (2p,
+// 2p+1) of the block's KV head, entry x = c0 | c1 << 2 (the pair's 4 code
+// bits) -> pole(2p, c0) | pole(2p+1, c1) << 16, at word kpair_index(p, x)
+// (the 16-word skew per 16 pairs puts the four channel groups of a wave on
+// disjoint banks).  V: per row, entry x -> pole(c0) | pole(c1) << 16 of the
+// row's per-token poles.
+HKV_DEV int kpair_index(int p, int x) { return p * 16 + 16 * (p >> 4) + x; }
+constexpr int kKPair = 64 * 16 + 16 * 4;  // words
+constexpr int kKLutWords = kKPair > kKLut / 2 ? kKPair : kKLut / 2;
+
 struct Side {  // one of K / V in the compact format, or in the paged pool
   const uint8_t* packed;   // compact: (T, H, D*bits/8); paged: (NB, H, 16, D*bits/8)
   const int32_t* row_ptr;  // compact: (T*H + 1)
@@ -150,7 +162,9 @@ HKV_DEV void load_page(const DecodeArgs& A, int p, int b, int g, int lane, PageL
     load_codes<VB>(A.v.packed, r, q, L.vc);
   }
   const int vrow = t < (int)A.v.rows ? t : (int)A.v.rows - 1;
-  L.vtab = *reinterpret_cast<const uint2*>(A.v.tabs[(uint32_t)(g * (int)A.v.rows + vrow)].pf16 + 4 * q);
+  // nuq4: levels 4q..4q+3 of the row; nuq2: its 4 levels, in every lane
+  L.vtab = *reinterpret_cast<const uint2*>(A.v.tabs[(uint32_t)(g * (int)A.v.rows + vrow)].pf16 +
+                                           (VB == 2 ? 0 : 4 * q));
 }
 
 HKV_DEV int csr_slot(int a, int sub, int s, int cap) {
@@ -216,6 +230,26 @@ HKV_DEV void dequant_rows(const uint32_t (&w)[NB], bool valid, int lane, uint16_
   }
 }
 
+// nuq2 through a pair table: the lane's 16 pairs (channels [32(l%4), +32) of
+// row l/4) read lut[pstride * k + x] for pair k with code bits x.
+template <int PSTRIDE>
+HKV_DEV void dequant_pairs(const uint32_t (&w)[2], bool valid, int lane, uint16_t* tile,
+                           const uint32_t* lut) {
+  const int row = lane >> 2, c0 = 32 * (lane & 3);
+#pragma unroll
+  for (int k4 = 0; k4 < 4; ++k4) {  // 8 channels per 128-bit LDS store
+    uint32_t h[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int k = 4 * k4 + j;
+      const uint32_t x = (w[k >> 3] >> (4 * (k & 7))) & 15u;
+      const uint32_t v = lut[PSTRIDE * k + (int)x];
+      h[j] = valid ? v : 0u;  // rows past the context read as zeros
+    }
+    *reinterpret_cast<uint4*>(tile + row * kTS + c0 + 8 * k4) = make_uint4(h[0], h[1], h[2], h[3]);
+  }
+}
+
 // CSR entries beyond the kSlots held in registers (rows with > 4*kSlots
 // outliers): read directly.
 HKV_DEV void patch_rest(const Side& sd, int2 rb, int lane, uint16_t* tile) {
@@ -248,8 +282,11 @@ HKV_DEV void patch_rest_paged(const Side& sd, int2 cr, int lane, uint16_t* tile,
 // head blockIdx.y.
 template <int KB, int VB, bool PG>
 HKV_DEV void decode_body(const DecodeArgs& A, int64_t split) {
-  __shared__ __align__(16) uint16_t s_klut[kKLut];
-  __shared__ __align__(16) uint16_t s_vlut[kW][kPS * 16];   // [row][level] of the wave's page
+  // K: the nuq4 table (halves) or the nuq2 pair table (words); V: the wave's
+  // page, [row][level] halves (nuq4) or [row][pair entry] words (nuq2)
+  __shared__ __align__(16) uint32_t s_klut_w[kKLutWords];
+  __shared__ __align__(16) uint32_t s_vlut_w[kW][kPS * 16];
+  uint16_t* s_klut = reinterpret_cast<uint16_t*>(s_klut_w);
   __shared__ __align__(16) uint16_t s_tiles[kW][2][kPS * kTS];
   __shared__ float s_m[kW][16], s_l[kW][16];
 
@@ -258,9 +295,18 @@ HKV_DEV void decode_body(const DecodeArgs& A, int64_t split) {
   const int64_t j0 = split * A.pps;
   const int64_t j1 = j0 + A.pps < A.nsel ? j0 + A.pps : A.nsel;
 
-  for (int i = tid; i < kHD * 16; i += kDT) {
-    const int d = i >> 4, l = i & 15;
-    s_klut[klut_index(d, l)] = A.k.tabs[(int64_t)g * kHD + d].pf16[l];
+  if constexpr (KB == 2) {
+    for (int i = tid; i < 64 * 16; i += kDT) {
+      const int pp = i >> 4, x = i & 15;
+      const uint32_t lo = A.k.tabs[(int64_t)g * kHD + 2 * pp].pf16[x & 3];
+      const uint32_t hi = A.k.tabs[(int64_t)g * kHD + 2 * pp + 1].pf16[x >> 2];
+      s_klut_w[kpair_index(pp, x)] = lo | hi << 16;
+    }
+  } else {
+    for (int i = tid; i < kHD * 16; i += kDT) {
+      const int d = i >> 4, l = i & 15;
+      s_klut[klut_index(d, l)] = A.k.tabs[(int64_t)g * kHD + d].pf16[l];
+    }
   }
 
   // the wave's page ids, one per lane (-1: none / out of range)
@@ -315,18 +361,35 @@ HKV_DEV void decode_body(const DecodeArgs& A, int64_t split) {
 
   uint16_t* kt = s_tiles[wv][0];
   uint16_t* vt = s_tiles[wv][1];
-  uint16_t* vl = s_vlut[wv];
+  uint16_t* vl = reinterpret_cast<uint16_t*>(s_vlut_w[wv]);
+  uint32_t* vlw = s_vlut_w[wv];
 
   auto compute = [&](const PageLoad<KB, VB>& L, const PageOutl& Ob, int p) {
     const int64_t t0 = (int64_t)p * kPS;
     const int row = lane >> 2;
     const bool valid = t0 + row < A.T;
-    *reinterpret_cast<uint2*>(vl + row * 16 + 4 * (lane & 3)) = L.vtab;
+    const int q = lane & 3;
+    if constexpr (VB == 2) {
+      // the row's pair entries 4q .. 4q + 3 (c1 = q): pole(c0) | pole(q) << 16
+      const uint32_t p01 = L.vtab.x, p23 = L.vtab.y;
+      const uint32_t pq = ((q < 2 ? p01 : p23) >> (16 * (q & 1))) << 16;
+      *reinterpret_cast<uint4*>(vlw + row * 16 + 4 * q) =
+          make_uint4((p01 & 0xffffu) | pq, (p01 >> 16) | pq, (p23 & 0xffffu) | pq, (p23 >> 16) | pq);
+    } else {
+      *reinterpret_cast<uint2*>(vl + row * 16 + 4 * q) = L.vtab;
+    }
     wave_sync();
-    auto klut = [&](int ch, uint32_t c) { return s_klut[klut_index(ch, (int)c)]; };
-    auto vlut = [&](int, uint32_t c) { return vl[row * 16 + (int)c]; };
-    dequant_rows<KB, false>(L.kc, valid, lane, kt, klut);
-    dequant_rows<VB, false>(L.vc, valid, lane, vt, vlut);
+    if constexpr (KB == 2) {
+      dequant_pairs<16>(L.kc, valid, lane, kt, s_klut_w + kpair_index(16 * q, 0));
+    } else {
+      dequant_rows<KB, false>(L.kc, valid, lane, kt,
+                              [&](int ch, uint32_t c) { return s_klut[klut_index(ch, (int)c)]; });
+    }
+    if constexpr (VB == 2) {
+      dequant_pairs<0>(L.vc, valid, lane, vt, vlw + row * 16);
+    } else {
+      dequant_rows<VB, false>(L.vc, valid, lane, vt, [&](int, uint32_t c) { return vl[row * 16 + (int)c]; });
+    }
     wave_sync();
     if constexpr (PG) {
       // the page-head's entries (rows past the context are masked below)
