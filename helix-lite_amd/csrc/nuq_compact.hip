@@ -50,6 +50,7 @@ struct PackBatch {
   int32_t n;
   int32_t H;  // heads (the same for every item of a launch)
   uint32_t nchunks;
+  int32_t wr;  // rows of a wave's part of a chunk: whole wave tiles, at most the variant's WR
 };
 
 // Rows a wave packs per chunk: whole wave tiles, at least kPackWaveRows
@@ -161,11 +162,12 @@ struct ItemSlow {
 };
 
 // Fused pack.  A launch packs up to kPackItems tensors of one kernel variant.
-// Their rows are cut into chunks of CR rows, numbered consecutively over the
-// tensors.  A block takes the next chunk number from the work counter (one
+// Their rows are cut into chunks of NW * wr rows, numbered consecutively over
+// the tensors.  A block takes the next chunk number from the work counter (one
 // device-scope atomic per chunk: those on one address serialise at about
-// 11 ns each on MI355X, so a chunk is large, NW * WR rows); each wave packs
-// its WR rows (codes straight to HBM, outliers and each row's offset within
+// 11 ns each on MI355X, so a chunk is large, wr = WR rows a wave, except in a
+// launch too small to give every CU two such chunks); each wave packs its wr
+// rows (codes straight to HBM, outliers and each row's offset within
 // the wave's part into its LDS).  After a block barrier wave 0 publishes the
 // chunk's count and takes the next number; the chunk's offset (the outliers
 // of the tensor's earlier chunks) is found one chunk later, by a decoupled
@@ -195,11 +197,9 @@ pack_fused_kernel(const PackBatch B, uint32_t* __restrict__ hdr, uint64_t* __res
   constexpr int D = 8 * G;
   constexpr int RB = D * BITS / 8;  // packed bytes per row
   constexpr int NW = kThreads / 64;
-  constexpr int WR = pack_wave_rows(G, PASSES, PT);  // rows of a wave's part of a chunk
-  constexpr int CR = NW * WR;
-  constexpr int CT = WR / WT;                     // wave tiles per part
+  constexpr int WR = pack_wave_rows(G, PASSES, PT);  // most rows of a wave's part of a chunk
   constexpr int ECAP = pack_ent_cap(G, PASSES, PT);
-  static_assert(WR % WT == 0 && CR == pack_chunk_rows(G, PASSES, PT), "a part is whole wave tiles");
+  static_assert(WR % WT == 0 && NW * WR == pack_chunk_rows(G, PASSES, PT), "a part is whole wave tiles");
   // Per-token tables of a wave tile's rows are staged in the wave's LDS slice
   // when they fit in 4 KiB (D >= 128), already in search form (each
   // breakpoint and threshold duplicated into both 16-bit halves: words 0..14
@@ -226,6 +226,9 @@ pack_fused_kernel(const PackBatch B, uint32_t* __restrict__ hdr, uint64_t* __res
   const int hfix = KFIX ? rw % B.H : 0;
   const uint32_t epoch = __hip_atomic_load(hdr + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const uint32_t nchunks = B.nchunks;
+  // this launch's part and chunk rows (WR, or fewer tiles for a small batch)
+  const int wr = B.wr;
+  const int64_t cr = (int64_t)NW * wr;
 
   // Outliers of the tensor's chunks [first, c), by wave 0: lane i of window q
   // examines chunk hi - 1 - i - 64 q, kPackLookWindows windows requested
@@ -313,9 +316,9 @@ pack_fused_kernel(const PackBatch B, uint32_t* __restrict__ hdr, uint64_t* __res
       if (lane == 0) s_base = base;
     }
     __syncthreads();
-    const int64_t hwbeg = (int64_t)hk * CR + (int64_t)wv * WR;
+    const int64_t hwbeg = (int64_t)hk * cr + (int64_t)wv * wr;
     const int64_t hrest = ih.nrows - hwbeg;
-    const int hnrw = hrest <= 0 ? 0 : (hrest < WR ? (int)hrest : WR);
+    const int hnrw = hrest <= 0 ? 0 : (hrest < wr ? (int)hrest : wr);
     const uint32_t hrun = s_wtot[hpar][wv];
     uint32_t base = s_base;
 #pragma unroll
@@ -350,9 +353,9 @@ pack_fused_kernel(const PackBatch B, uint32_t* __restrict__ hdr, uint64_t* __res
     const int H = B.H;
     const int64_t nrows = it.nrows;
     const uint32_t k = c - it.chunk0;
-    const int64_t wbeg = (int64_t)k * CR + (int64_t)wv * WR;  // first row of the wave's part
+    const int64_t wbeg = (int64_t)k * cr + (int64_t)wv * wr;  // first row of the wave's part
     const int64_t wrest = nrows - wbeg;
-    const int nrw = wrest <= 0 ? 0 : (wrest < WR ? (int)wrest : WR);  // rows of the wave's part
+    const int nrw = wrest <= 0 ? 0 : (wrest < wr ? (int)wrest : wr);  // rows of the wave's part
     if constexpr (!PT && KFIX) {
       if (j != cur) {
         const int64_t tab0 = (int64_t)hfix * D + 8 * cg;
@@ -368,7 +371,7 @@ pack_fused_kernel(const PackBatch B, uint32_t* __restrict__ hdr, uint64_t* __res
     uint8_t* wcol = s_col[buf][wv];
     uint16_t* wroff = s_roff[buf][wv];
 #pragma unroll 1
-    for (int tt = 0; tt < CT; ++tt) {
+    for (int tt = 0; tt * WT < wr; ++tt) {
       const int64_t r0 = wbeg + tt * WT;
       const int nv = nrw - tt * WT < WT ? nrw - tt * WT : WT;  // rows of this tile
       if (nv <= 0) break;
@@ -599,22 +602,32 @@ PackKey pack_key(const hkv_pack_item& a) {
                  (64 / G) % a.H == 0, a.H};
 }
 
-// Chunks of one item (at least one, so an empty tensor still gets row_ptr[0]).
-int64_t pack_item_chunks(const hkv_pack_item& a) {
+// Chunks of one item at cr rows a chunk (at least one, so an empty tensor
+// still gets row_ptr[0]); cr = 0: the variant's full chunk.
+int64_t pack_item_chunks(const hkv_pack_item& a, int64_t cr = 0) {
   const PackKey k = pack_key(a);
-  const int64_t cr = pack_chunk_rows(k.G, pack_passes(k.pt, k.nb), k.pt);
+  if (cr <= 0) cr = pack_chunk_rows(k.G, pack_passes(k.pt, k.nb), k.pt);
   const int64_t n = (a.T * a.H + cr - 1) / cr;
   return n > 0 ? n : 1;
 }
 
+// A launch over few full chunks leaves most CUs idle (a 4096-token tensor is
+// 32 chunks of 512 rows): its parts are halved, down to one wave tile, while
+// the launch has fewer than two chunks per CU and stays within
+// kPackSmallChunks chunks.  The workspace holds status words for
+// max(full-chunk count, kPackSmallChunks) chunks.
+constexpr int64_t kPackSmallChunks = 2048;
+
 // Workspace bound: every chunk of every item (launches reuse the status words).
-size_t pack_ws_bytes(int64_t chunks) { return kPackHeader + 8 * (size_t)chunks; }
+size_t pack_ws_bytes(int64_t chunks) {
+  return kPackHeader + 8 * (size_t)(chunks > kPackSmallChunks ? chunks : kPackSmallChunks);
+}
 
 }  // namespace
 
 extern "C" size_t hkv_nuq_pack_compact_workspace_bytes(int64_t T, int H, int D) {
   if (T < 0 || H < 1 || !pow2_G(D)) return 0;
-  // every variant's chunks are at least NW * kPackWaveRows / 2 rows
+  // every variant's full chunks are at least NW * kPackWaveRows / 2 rows
   const int64_t cr = (int64_t)(kThreads / 64) * (kPackWaveRows / 2);
   const int64_t n = (T * H + cr - 1) / cr;
   return pack_ws_bytes(n > 0 ? n : 1);
@@ -649,15 +662,30 @@ extern "C" int hkv_nuq_pack_compact_batch(const hkv_pack_item* items, int n, voi
   for (int i0 = 0; i0 < n; ++i0) {
     if (done[i0]) continue;
     const PackKey key = pack_key(items[i0]);
-    // the items of this variant, in order, kPackItems per launch
-    PackBatch b;
-    b.n = 0;
-    b.H = key.H;
-    b.nchunks = 0;
-    for (int i = i0; i <= n; ++i) {
-      const bool take = i < n && !done[i] && pack_key(items[i]) == key;
-      if (take) {
-        const hkv_pack_item& a = items[i];
+    const int passes = pack_passes(key.pt, key.nb);
+    const int wt = pack_tile_rows(key.G, passes), wfull = pack_wave_rows(key.G, passes, key.pt);
+    // the items of this variant, in order, kPackItems per launch; the part
+    // rows of a launch follow from its items' full-chunk count
+    std::vector<int> mine;
+    for (int i = i0; i < n; ++i)
+      if (!done[i] && pack_key(items[i]) == key) mine.push_back(i);
+    for (size_t m0 = 0; m0 < mine.size(); m0 += kPackItems) {
+      const size_t m1 = std::min(mine.size(), m0 + (size_t)kPackItems);
+      int wr = wfull;
+      auto chunks_at = [&](int w) {
+        int64_t c = 0;
+        for (size_t m = m0; m < m1; ++m) c += pack_item_chunks(items[mine[m]], (int64_t)(kThreads / 64) * w);
+        return c;
+      };
+      while (wr > wt && chunks_at(wr) < 2 * (int64_t)num_cus() && chunks_at(wr / 2) <= kPackSmallChunks)
+        wr /= 2;
+      PackBatch b;
+      b.n = 0;
+      b.H = key.H;
+      b.nchunks = 0;
+      b.wr = wr;
+      for (size_t m = m0; m < m1; ++m) {
+        const hkv_pack_item& a = items[mine[m]];
         PackItem& p = b.it[b.n++];
         p.x = (const uint16_t*)a.values;
         p.packed = (uint8_t*)a.packed;
@@ -668,21 +696,17 @@ extern "C" int hkv_nuq_pack_compact_batch(const hkv_pack_item* items, int n, voi
         p.nrows = a.T * a.H;
         p.chunk0 = b.nchunks;
         p.cap = (uint32_t)std::min<int64_t>(a.capacity, 0x7fffffff);
-        b.nchunks += (uint32_t)pack_item_chunks(a);
-        done[i] = 1;
+        b.nchunks += (uint32_t)pack_item_chunks(a, (int64_t)(kThreads / 64) * wr);
+        done[mine[m]] = 1;
       }
-      if (b.n > 0 && (b.n == kPackItems || i == n)) {
-        if (key.bits == 4) {
-          if (key.pt) launch_fused_nb<true, 4>(key.nb, key.kfix, key.G, b, l);
-          else launch_fused_nb<false, 4>(key.nb, key.kfix, key.G, b, l);
-        } else {
-          if (key.pt) launch_fused_nb<true, 2>(key.nb, key.kfix, key.G, b, l);
-          else launch_fused_nb<false, 2>(key.nb, key.kfix, key.G, b, l);
-        }
-        HKV_CHECK_LAUNCH();
-        b.n = 0;
-        b.nchunks = 0;
+      if (key.bits == 4) {
+        if (key.pt) launch_fused_nb<true, 4>(key.nb, key.kfix, key.G, b, l);
+        else launch_fused_nb<false, 4>(key.nb, key.kfix, key.G, b, l);
+      } else {
+        if (key.pt) launch_fused_nb<true, 2>(key.nb, key.kfix, key.G, b, l);
+        else launch_fused_nb<false, 2>(key.nb, key.kfix, key.G, b, l);
       }
+      HKV_CHECK_LAUNCH();
     }
   }
   return HKV_OK;

@@ -38,9 +38,12 @@ def test_host_only_entry_points():
     assert L.hkv_status_string(4) == b"output capacity too small"
     # 256-byte header (work counter, finished waves, epoch, error word), then
     # one 8-byte status word per chunk (four waves of at least 64 rows)
-    assert L.hkv_nuq_pack_compact_workspace_bytes(131072, 4, 128) == 256 + 8 * (131072 * 4 // 256)
-    assert L.hkv_nuq_pack_compact_workspace_bytes(10, 4, 128) == 256 + 8
-    assert L.hkv_nuq_pack_compact_workspace_bytes(0, 4, 128) == 256 + 8
+    # a 256-byte header and 8 bytes per chunk of 256 rows, for at least 2048
+    # chunks (a small tensor is packed in smaller chunks)
+    assert L.hkv_nuq_pack_compact_workspace_bytes(262144, 4, 128) == 256 + 8 * (262144 * 4 // 256)
+    assert L.hkv_nuq_pack_compact_workspace_bytes(131072, 4, 128) == 256 + 8 * 2048
+    assert L.hkv_nuq_pack_compact_workspace_bytes(10, 4, 128) == 256 + 8 * 2048
+    assert L.hkv_nuq_pack_compact_workspace_bytes(0, 4, 128) == 256 + 8 * 2048
     assert L.hkv_nuq_pack_compact_workspace_bytes(10, 4, 100) == 0  # unsupported D
     assert L.hkv_quest_topk_workspace_bytes(65536, 4) >= 64
 
