@@ -319,6 +319,7 @@ bound_kernel(const void* q, int qdt, int group, const KT* __restrict__ kmin,
 }
 
 constexpr int kMaxMMHeads = 64;  // heads with per-block key ranges (multi-block top-K)
+constexpr int kPidStage = 2048;  // block-table ids a bound block stages in LDS
 constexpr int kBoundUnrollF16 = 2;  // row groups per step (two steps of loads in flight)
 
 // A lane's statistics are read once: load_stream keeps the 128 MiB stream
@@ -378,14 +379,34 @@ HKV_DEV void bound_f16_rows(const void* q, int qdt, int group, const void* kmin_
   // flight.
   // pids (HFIX only): page p's statistics are row pids[p] of (nstat, H, D)
   // -- a block table mapping the logical pages scored here to the pool's
-  // blocks; an id outside [0, nstat) reads block 0.
-  auto load = [&](int r0, LT (&a)[U], LT (&b)[U]) {
+  // blocks; an id outside [0, nstat) reads block 0.  The block's ids (span / H
+  // consecutive pages per step) are staged in LDS first, -1 for an id outside
+  // the statistics, so a step's statistics loads never wait on its id loads
+  // (up to kPidStage ids a block; beyond, each load reads its id itself).
+  __shared__ int s_pid[kPidStage];
+  const int pps = span / H;  // pages per step (H divides RB)
+  const int nsteps = nr > bx * span ? (nr - bx * span + step - 1) / step : 0;
+  const bool pid_lds = HFIX && pids && nsteps * pps <= kPidStage;
+  if (pid_lds) {
+    for (int i = threadIdx.x; i < nsteps * pps; i += 256) {
+      const int st = i / pps;
+      int p = (bx * span + st * step) / H + (i - st * pps);
+      p = p < (int)P ? p : (int)P - 1;
+      const int64_t bk = pids[p];
+      s_pid[i] = (bk < 0 || bk >= nstat) ? -1 : (int)bk;
+    }
+    __syncthreads();
+  }
+  auto load = [&](int r0, int sl, LT (&a)[U], LT (&b)[U]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       int r = r0 + u * RB + rl;
       r = r < nr ? r : nr - 1;
       if constexpr (HFIX) {
-        if (pids) {  // r0 is a multiple of H, and so is RB
+        if (pid_lds) {  // a step past the block's last (clamped rows) reads its last id
+          const int bk = s_pid[sl < nsteps ? sl * pps + u * (RB / H) + rl / H : nsteps * pps - 1];
+          r = (bk < 0 ? 0 : bk) * H + rl % H;
+        } else if (pids) {  // r0 is a multiple of H, and so is RB
           int p = r0 / H + u * (RB / H) + rl / H;
           p = p < (int)P ? p : (int)P - 1;
           int64_t bk = pids[p];
@@ -397,7 +418,7 @@ HKV_DEV void bound_f16_rows(const void* q, int qdt, int group, const void* kmin_
       b[u] = load_stream(reinterpret_cast<const LT*>(kmax + (uint32_t)r * D) + c);
     }
   };
-  int r0 = bx * span;
+  int r0 = bx * span, sl = 0;
   // the block's clamped, group-summed query, [2][H][D] in LDS
   if (q_lds) {
     // raw query chunks first, then two steps of statistics: waiting for the
@@ -411,8 +432,8 @@ HKV_DEV void bound_f16_rows(const void* q, int qdt, int group, const void* kmin_
       const int i = threadIdx.x + 256 * k;
       qc[k] = gq[i < nch ? i : nch - 1];
     }
-    load(r0, a0, b0);
-    load(r0 + step, a1, b1);
+    load(r0, 0, a0, b0);
+    load(r0 + step, 1, a1, b1);
     // unconditional stores (a clamped chunk rewrites the last one with its
     // own value), so the chunk loads stay ahead of the statistics loads
 #pragma unroll
@@ -428,8 +449,8 @@ HKV_DEV void bound_f16_rows(const void* q, int qdt, int group, const void* kmin_
       qs[H * D + i] = qb;
     }
   } else {
-    load(r0, a0, b0);
-    load(r0 + step, a1, b1);
+    load(r0, 0, a0, b0);
+    load(r0 + step, 1, a1, b1);
     for (int i = threadIdx.x; i < H * D; i += 256) {
       float qa, qb;
       group_q(q, qdt, i / D, group, D, i % D, qa, qb);
@@ -457,7 +478,7 @@ HKV_DEV void bound_f16_rows(const void* q, int qdt, int group, const void* kmin_
     }
   }
   uint32_t kmn_t = 0xffffffffu, kmx_t = 0u;  // key range of this thread's rows (HFIX: one head)
-  auto compute = [&](int rs, int pb, const LT (&a)[U], const LT (&b)[U]) {
+  auto compute = [&](int rs, int pb, int sl, const LT (&a)[U], const LT (&b)[U]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int r = rs + u * RB + rl;
@@ -506,7 +527,9 @@ HKV_DEV void bound_f16_rows(const void* q, int qdt, int group, const void* kmin_
       if (r < nr && c == 0) {
         float v = __fadd_rn(__fadd_rn(ps, ns), 0.0f);
         if constexpr (HFIX) {
-          if (pids) {  // a page id outside the statistics gets bound -inf (never preferred)
+          if (pid_lds) {  // a page id outside the statistics gets bound -inf (never preferred)
+            if (s_pid[sl * pps + u * (RB / H) + rl / H] < 0) v = -__builtin_inff();
+          } else if (pids) {
             const int64_t bk = pids[p];
             if (bk < 0 || bk >= nstat) v = -__builtin_inff();
           }
@@ -528,15 +551,17 @@ HKV_DEV void bound_f16_rows(const void* q, int qdt, int group, const void* kmin_
   int pb = HFIX ? r0 / H : 0;
   const int pstep = HFIX ? step / H : 0;
   while (r0 < nr) {
-    compute(r0, pb, a0, b0);
-    load(r0 + 2 * step, a0, b0);
+    compute(r0, pb, sl, a0, b0);
+    load(r0 + 2 * step, sl + 2, a0, b0);
     r0 += step;
     pb += pstep;
+    ++sl;
     if (r0 >= nr) break;
-    compute(r0, pb, a1, b1);
-    load(r0 + 2 * step, a1, b1);
+    compute(r0, pb, sl, a1, b1);
+    load(r0 + 2 * step, sl + 2, a1, b1);
     r0 += step;
     pb += pstep;
+    ++sl;
   }
   if constexpr (HFIX) {
     // per-block key range of each head for the multi-block top-K
