@@ -1173,6 +1173,23 @@ def profile_pass(what: str, dev) -> None:
                         nuq_pack_compact(X, tb, bits, out=cc, sync=False)
                     else:
                         nuq_unpack_compact(cc, tb, out=out)
+    elif what == "pack_step":
+        # the headline step itself: all 28 layers' K and V in one batched call
+        # (four launches, one per kernel variant), three times
+        from helix_kv.ops import CompactPackBatch
+
+        items = []
+        for layer in range(LAYERS):
+            K, V, ks, vs, L = make_layer(layer, dev)
+            bits = 2 if L <= 4 else 4
+            for X, sc, pt in ((K, ks, False), (V, vs, True)):
+                tb = NuqLayerTables(*sc, per_token=pt)
+                tb.ensure_tables()
+                items.append((X, tb, bits, CompactCodes.empty(*X.shape, bits, X.numel() // 10, dev)))
+            log(f"[bench] profile pass pack_step: layer {layer} ready")
+        batch = CompactPackBatch(items)
+        for _ in range(3):
+            batch()
     elif what == "quest":
         P = 65536
         g = torch.Generator(device=dev).manual_seed(3)
@@ -1206,7 +1223,7 @@ def main() -> None:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--only", choices=["all", "nuq", "paged", "quest", "ragged", "decode",
                                        "calibration", "roundtrip"], default="all")
-    ap.add_argument("--profile", choices=["pack", "unpack", "quest", "ragged", "decode"], default=None,
+    ap.add_argument("--profile", choices=["pack", "pack_step", "unpack", "quest", "ragged", "decode"], default=None,
                     help="run a short fixed launch sequence for rocprofv3 counters and exit")
     ap.add_argument("--cpu-layers", default="0,16",
                     help="layers of the workload timed on the CPU baseline")
