@@ -48,7 +48,7 @@ constexpr int kHD = 128;        // head dim of the fused kernel
 constexpr int kPS = 16;         // tokens per page
 constexpr int kTS = kHD + 8;    // padded tile row (halves)
 constexpr int kMaxPPS = 256;    // pages per split: at most 64 per wave
-constexpr int kSlots = 4;       // CSR entries per lane per side kept in registers
+constexpr int kSlots = 3;       // CSR entries per lane per side kept in registers
 constexpr int kKLut = kHD * 16 + 16 * 4;  // halves of the swizzled K LUT
 constexpr float kLog2e = 1.4426950408889634f;
 
