@@ -1121,6 +1121,87 @@ extern "C" int hkv_decode_attn_batch(const void* q, int B, int Hq, int H, int D,
   return HKV_OK;
 }
 
+extern "C" int hkv_paged_decode_attn_batch(const void* q, int B, int Hq, const int64_t* seq_lens,
+                                           const int64_t* block_table, const int64_t* bt_offsets,
+                                           const hkv_paged_side* ks, const void* k_tables,
+                                           const hkv_paged_side* vs, const void* v_tables,
+                                           int64_t v_rows, const int64_t* sel,
+                                           const int64_t* sel_offsets, int pages_per_split,
+                                           float scale, void* out, int out_dtype, void* workspace,
+                                           size_t workspace_bytes, void* stream) {
+  if (!ks || !vs) return HKV_ERR_ARG;
+  const int H = ks->heads;
+  const int64_t num_blocks = ks->num_blocks;
+  const int k_bits = ks->bits, v_bits = vs->bits, k_cap = ks->cap, v_cap = vs->cap;
+  if (B < 1 || B > kMaxDecSeqs) return HKV_ERR_SHAPE;
+  if (vs->heads != H || vs->num_blocks != num_blocks) return HKV_ERR_SHAPE;
+  if (H < 1 || H > 16 || Hq < H || Hq % H || Hq / H > 16 || num_blocks < 1) return HKV_ERR_SHAPE;
+  if (pages_per_split < 1 || pages_per_split > kMaxPPS) return HKV_ERR_ARG;
+  if ((k_bits != 2 && k_bits != 4) || (v_bits != 2 && v_bits != 4)) return HKV_ERR_ARG;
+  if (out_dtype != HKV_DT_F16 && out_dtype != HKV_DT_F32) return HKV_ERR_DTYPE;
+  if (v_rows < 1 || k_cap < 0 || v_cap < 0 || k_cap > kPS * kHD || v_cap > kPS * kHD) return HKV_ERR_ARG;
+  if (num_blocks * H * kPS * kHD >= ((int64_t)1 << 31) || (int64_t)H * v_rows >= ((int64_t)1 << 31))
+    return HKV_ERR_SHAPE;
+  if (!q || !block_table || !ks->codes || !ks->ocnt || !k_tables || !vs->codes || !vs->ocnt ||
+      !v_tables || !out || !seq_lens || !bt_offsets || !sel_offsets)
+    return HKV_ERR_ARG;
+  if ((k_cap > 0 && !ks->oent) || (v_cap > 0 && !vs->oent)) return HKV_ERR_ARG;
+  if ((ks->ovf && !ks->ovf_ent) || (vs->ovf && !vs->ovf_ent)) return HKV_ERR_ARG;
+  if ((((uintptr_t)ks->codes | (uintptr_t)vs->codes) & 15u) || ((uintptr_t)q & 7u)) return HKV_ERR_ARG;
+  DecSegs sg;
+  sg.nseg = B;
+  sg.split0[0] = 0;
+  if (sel_offsets[0] < 0) return HKV_ERR_ARG;
+  for (int b = 0; b < B; ++b) {
+    const int64_t n = seq_lens[b], ns = sel_offsets[b + 1] - sel_offsets[b];
+    if (n < 1 || n >= ((int64_t)1 << 31) - kPS || bt_offsets[b] < 0 || ns < 0) return HKV_ERR_ARG;
+    if (ns > 0 && !sel) return HKV_ERR_ARG;
+    sg.base[b] = bt_offsets[b];
+    sg.T[b] = n;
+    sg.sel0[b] = sel_offsets[b];
+    sg.nsel[b] = ns;
+    sg.split0[b + 1] = sg.split0[b] + n_splits(ns, pages_per_split);
+  }
+  const int64_t splits = sg.split0[B];
+  if (splits > 0x7fffffff) return HKV_ERR_SHAPE;
+  const size_t need = hkv_decode_batch_workspace_bytes(B, sel_offsets, Hq, pages_per_split);
+  if (!workspace || workspace_bytes < need) return HKV_ERR_WORKSPACE;
+  hipStream_t s = (hipStream_t)stream;
+  float* pm = (float*)workspace;
+  float* pl = pm + splits * Hq;
+  float* po = pl + splits * Hq;
+  DecodeArgs a;
+  a.q = (const uint16_t*)q;
+  a.k = Side{ks->codes, nullptr, nullptr, nullptr, k_cap, (const hkv_table_t*)k_tables, 0, ks->ocnt,
+             ks->oent, ks->ovf, ks->ovf_ent};
+  a.v = Side{vs->codes, nullptr, nullptr, nullptr, v_cap, (const hkv_table_t*)v_tables, v_rows,
+             vs->ocnt, vs->oent, vs->ovf, vs->ovf_ent};
+  a.H = H;
+  a.group = Hq / H;
+  a.T = 0;
+  a.npages = 0;
+  a.sel = sel;
+  a.nsel = 0;
+  a.bt = block_table;
+  a.nblocks = num_blocks;
+  a.pps = pages_per_split;
+  a.scale = scale;
+  a.part_m = pm;
+  a.part_l = pl;
+  a.part_o = po;
+  if (k_bits == 4 && v_bits == 4) launch_decode_batch<4, 4, true>(a, sg, s);
+  else if (k_bits == 4) launch_decode_batch<4, 2, true>(a, sg, s);
+  else if (v_bits == 4) launch_decode_batch<2, 4, true>(a, sg, s);
+  else launch_decode_batch<2, 2, true>(a, sg, s);
+  HKV_CHECK_LAUNCH();
+  MergeSegs ms;
+  for (int b = 0; b <= B; ++b) ms.split0[b] = sg.split0[b];
+  hipLaunchKernelGGL(merge_batch_kernel, dim3((unsigned)Hq, (unsigned)((kHD + kMergeCh - 1) / kMergeCh), (unsigned)B),
+                     dim3(kDT), 0, s, pm, pl, po, ms, Hq, kHD, out, out_dtype);
+  HKV_CHECK_LAUNCH();
+  return HKV_OK;
+}
+
 // Workspace: the flags (one byte per page) at its start, the per-chunk
 // counts (at most total_pages / kUnionChunk + kMaxDecSeqs + 1 chunks) at its
 // end.  A buffer reused by calls over different page counts keeps every

@@ -143,6 +143,10 @@ _SIGS = {
                                _p, _p, _p, _p, _i64, _i32, _p,
                                _p, _p, _p, _p, _i64, _i32, _p, _i64,
                                _p, ctypes.POINTER(_i64), _i32, ctypes.c_float, _p, _i32, _p, _sz, _p], _i32),
+    "hkv_paged_decode_attn_batch": ([_p, _i32, _i32, ctypes.POINTER(_i64), _p, ctypes.POINTER(_i64),
+                                     ctypes.POINTER(PagedSideDesc), _p, ctypes.POINTER(PagedSideDesc), _p,
+                                     _i64, _p, ctypes.POINTER(_i64), _i32, ctypes.c_float, _p, _i32, _p,
+                                     _sz, _p], _i32),
     "hkv_union_pages_workspace_bytes": ([_i64], _sz),
     "hkv_union_pages_ragged": ([_p, _i32, _i32, ctypes.POINTER(_i64), ctypes.POINTER(_i64), _p, _p, _sz,
                                 _p], _i32),

@@ -304,3 +304,101 @@ def paged_decode_step(query: torch.Tensor, kside: PagedSide, kt: NuqLayerTables,
         raise ValueError(f"select must be 'union' or 'per_head', got {select!r}")
     return paged_decode_attention(query, kside, kt, vside, vt, block_table, seq_len, sel, scale=scale,
                                   pages_per_split=pages_per_split, out=out, out_dtype=out_dtype)
+
+
+def paged_decode_step_batch(queries: torch.Tensor, kside: PagedSide, kt: NuqLayerTables,
+                            vside: PagedSide, vt: NuqLayerTables, block_tables: torch.Tensor,
+                            seq_lens, top_k, sink_pages: int = 4, *, gqa: str = "mean",
+                            select: str = "union", scale: float | None = None,
+                            out: torch.Tensor | None = None,
+                            out_dtype: torch.dtype = torch.float16,
+                            pages_per_split: int | None = None) -> torch.Tensor:
+    """paged_decode_step for B <= 64 sequences of one pool, with no host reads:
+    sequence b has seq_lens[b] tokens, query queries[b] and its logical page p
+    in block block_tables[b, p] (block_tables (B, M) as the attention
+    metadata's block table, M >= ceil(seq_lens[b] / 16)).  A Quest selection
+    per sequence into one selection, the per-sequence union of the heads'
+    pages for select="union" (hkv_union_pages_ragged), then one batched decode
+    + merge (hkv_paged_decode_attn_batch); each sequence's result equals
+    paged_decode_step's with the same pages_per_split.  The reference forward
+    falls back to dense attention for batches above one
+    (src/kvquant/compact_backend.py:195-203).  top_k: one int, or one per
+    sequence.  queries (B, Hq, 128) fp16; returns (B, Hq, 128)."""
+    import ctypes
+    from .ops import decode_pages_per_split
+
+    N.require_gpu(queries, block_tables)
+    lens = [int(n) for n in seq_lens]
+    B = len(lens)
+    H = kside.heads
+    if queries.dim() != 3 or int(queries.shape[0]) != B or int(queries.shape[2]) != HEAD_DIM:
+        raise ValueError(f"queries {tuple(queries.shape)} do not match {B} sequences x {HEAD_DIM}")
+    Hq = int(queries.shape[1])
+    if Hq % H or queries.dtype != torch.float16:
+        raise ValueError(f"queries {tuple(queries.shape)} {queries.dtype}: fp16 with a multiple of {H} heads")
+    if B < 1 or B > 64:
+        raise ValueError(f"1 to 64 sequences, got {B}")
+    if any(n < 1 for n in lens):
+        raise ValueError("sequence lengths must be positive")
+    ks = [int(top_k)] * B if not hasattr(top_k, '__len__') else [int(x) for x in top_k]
+    if len(ks) != B:
+        raise ValueError("one top_k per sequence")
+    if gqa not in ("mean", "sum"):
+        raise ValueError(f"gqa must be 'mean' or 'sum', got {gqa!r}")
+    if select not in ("union", "per_head"):
+        raise ValueError(f"select must be 'union' or 'per_head', got {select!r}")
+    if kt.per_token or not vt.per_token:
+        raise AssertionError("K scales are per-channel, V scales per-token")
+    if vside.heads != H or vside.num_blocks != kside.num_blocks:
+        raise AssertionError("K and V sides must have the same blocks and heads")
+    pages = [-(-n // PAGE) for n in lens]
+    if block_tables.dim() != 2 or int(block_tables.shape[0]) != B or \
+            int(block_tables.shape[1]) < max(pages):
+        raise ValueError(f"block_tables must be ({B}, >= {max(pages)}), got {tuple(block_tables.shape)}")
+    M = int(block_tables.shape[1])
+    bt = block_tables.to(torch.int64).contiguous()
+    dev = queries.device
+    if out is None:
+        out = torch.empty((B, Hq, HEAD_DIM), dtype=out_dtype, device=dev)
+    if tuple(out.shape) != (B, Hq, HEAD_DIM) or out.dtype not in (torch.float16, torch.float32) or \
+            not out.is_contiguous():
+        raise AssertionError(f"out must be contiguous ({B}, {Hq}, {HEAD_DIM}) fp16 or fp32")
+    q = queries.contiguous()
+    qs = q.reshape(B, H, Hq // H, HEAD_DIM).mean(dim=2).to(torch.float16) if gqa == "mean" else q
+    sp = int(sink_pages)
+    rows = [0]
+    for P, k in zip(pages, ks):
+        s = max(0, min(sp, P))
+        rows.append(rows[-1] + s + max(0, min(k, P - s)))
+    offs = [0]
+    for P in pages:
+        offs.append(offs[-1] + P)
+    sel = torch.empty((max(rows[-1], 1), H), dtype=torch.int64, device=dev)
+    scores = torch.empty((H * max(pages),), dtype=torch.float32, device=dev)
+    for b in range(B):
+        paged_select(qs[b], kside, bt[b], lens[b], ks[b], sp, out=sel[rows[b]:rows[b + 1]],
+                     scores=scores[:H * pages[b]].view(H, pages[b]))
+    if select == "union":
+        c_rows = (ctypes.c_int64 * (B + 1))(*rows)
+        c_pages = (ctypes.c_int64 * (B + 1))(*offs)
+        flags = N.workspace("union_flags", int(N.lib().hkv_union_pages_workspace_bytes(offs[-1])), dev)
+        union = torch.empty((offs[-1], H), dtype=torch.int64, device=dev)
+        st = N.lib().hkv_union_pages_ragged(N.ptr(sel), H, B, c_rows, c_pages, N.ptr(union),
+                                            N.ptr(flags), flags.numel(), N.stream_of(qs))
+        N.check(st, "hkv_union_pages_ragged", ValueError)
+        sel, sel_offs = union, offs
+    else:
+        sel_offs = rows
+    pps = int(pages_per_split) if pages_per_split else decode_pages_per_split(sel_offs[-1], H)
+    c_sel = (ctypes.c_int64 * (B + 1))(*sel_offs)
+    c_len = (ctypes.c_int64 * B)(*lens)
+    c_bt = (ctypes.c_int64 * B)(*[b * M for b in range(B)])
+    nb = int(N.lib().hkv_decode_batch_workspace_bytes(B, c_sel, Hq, pps))
+    ws = N.workspace("decode", nb, dev)
+    sc = float(scale) if scale is not None else HEAD_DIM ** -0.5
+    st = N.lib().hkv_paged_decode_attn_batch(
+        N.ptr(q), B, Hq, c_len, N.ptr(bt), c_bt, kside.desc(), N.ptr(kt.ensure_tables()),
+        vside.desc(), N.ptr(vt.ensure_tables()), vt.rows, N.ptr(sel), c_sel, pps, sc, N.ptr(out),
+        N.dtype_code(out), N.ptr(ws), ws.numel(), N.stream_of(q))
+    N.check(st, "hkv_paged_decode_attn_batch", AssertionError)
+    return out

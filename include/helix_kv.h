@@ -536,6 +536,29 @@ int hkv_decode_attn_batch(const void *q, int B, int Hq, int H, int D, int64_t T,
                           void *workspace, size_t workspace_bytes, void *stream);
 
 /*
+ * Batched decode over a paged pool: hkv_paged_decode_attn for B <= 64
+ * sequences sharing one pool, in one decode launch and one merge launch (the
+ * compact backend's forward over the block tables of a batch,
+ * src/kvquant/compact_backend.py:184-299, which attends one sequence at a
+ * time).  Sequence b has seq_lens[b] tokens, query q[b] (q (B, Hq, 128)
+ * fp16), its logical page p in block block_table[bt_offsets[b] + p]
+ * (block_table a device array holding ceil(seq_lens[b] / 16) entries from
+ * bt_offsets[b] on), and selection rows sel_offsets[b] .. sel_offsets[b+1]-1
+ * of sel (rows, heads), logical page ids of the sequence.  V rows min(16p +
+ * slot, v_rows - 1).  seq_lens, bt_offsets (B) and sel_offsets (B+1) are HOST
+ * arrays.  Each sequence's result equals hkv_paged_decode_attn over its view
+ * with the same pages_per_split.  Workspace: hkv_decode_batch_workspace_bytes
+ * (no zeroing).  out (B, Hq, 128) fp16 or fp32.
+ */
+int hkv_paged_decode_attn_batch(const void *q, int B, int Hq, const int64_t *seq_lens,
+                                const int64_t *block_table, const int64_t *bt_offsets,
+                                const hkv_paged_side *k, const void *k_tables,
+                                const hkv_paged_side *v, const void *v_tables, int64_t v_rows,
+                                const int64_t *sel, const int64_t *sel_offsets,
+                                int pages_per_split, float scale, void *out, int out_dtype,
+                                void *workspace, size_t workspace_bytes, void *stream);
+
+/*
  * Per-sequence union of the KV heads' selected pages, the page set the
  * reference's decode attends for every query head
  * (src/kvquant/quest_selector.py:80, then all heads of each kept block,

@@ -200,3 +200,120 @@ def test_paged_decode_step_graph_replay(dev):
         other = paged_decode_step(*args, select="per_head")
         torch.cuda.synchronize()
         assert not torch.equal(other, eager)
+
+
+def _batch_pool(dev, lens, Lk, Lv, spare=23, cap=256):
+    """Sequences of the given lengths written into one pool, each through its
+    own random blocks; returns the sides, tables and the (B, M) block table
+    (entries past a sequence's pages are -1)."""
+    from helix_kv.ops import NuqLayerTables
+    from helix_kv.paged import PagedSide, paged_write
+
+    pages = [-(-n // PS) for n in lens]
+    NB = sum(pages) + spare
+    perm = RNG.permutation(NB).astype(np.int64)
+    M = max(pages) + 3
+    bt = np.full((len(lens), M), -1, np.int64)
+    ks, vs = _scales(D, Lk), _scales(max(lens), Lv)
+    kt = NuqLayerTables(*(_t(a, dev) for a in ks), per_token=False)
+    vt = NuqLayerTables(*(_t(a, dev) for a in vs), per_token=True)
+    kb, vb = (2 if Lk <= 4 else 4), (2 if Lv <= 4 else 4)
+    kside = PagedSide.empty(NB, H, kb, cap, dev, stats=True, n_chunks=NB * H)
+    vside = PagedSide.empty(NB, H, vb, cap, dev, n_chunks=NB * H)
+    kp = O.paged_empty(NB, H, D, kb, cap, stats=True)
+    vp = O.paged_empty(NB, H, D, vb, cap, stats=False)
+    o = 0
+    for b, (T, P) in enumerate(zip(lens, pages)):
+        bt[b, :P] = perm[o:o + P]
+        o += P
+        slots = bt[b, np.arange(T) // PS] * PS + np.arange(T) % PS
+        k = (RNG.standard_t(3, (T, H, D)) * 0.7).astype(np.float16)
+        v = (RNG.standard_t(3, (T, H, D)) * 0.7).astype(np.float16)
+        paged_write(kside, _t(k, dev), kt, _t(slots, dev))
+        paged_write(vside, _t(v, dev), vt, _t(slots, dev), _t(np.arange(T), dev))
+        O.paged_write(kp, k, slots, [a.astype(np.float32) for a in ks], False)
+        O.paged_write(vp, v, slots, [a.astype(np.float32) for a in vs], True, positions=np.arange(T))
+    oracle_pages = []
+    for b, P in enumerate(pages):
+        first = np.arange(P) * PS
+        oracle_pages.append((O.h2f(O.paged_gather(kp, bt[b, :P], first, ks[0].astype(np.float32), False)),
+                             O.h2f(O.paged_gather(vp, bt[b, :P], first, vs[0].astype(np.float32), True))))
+    return kside, vside, kt, vt, _t(bt, dev), oracle_pages
+
+
+@pytest.mark.parametrize("gqa,select", [("mean", "union"), ("sum", "per_head"), ("mean", "per_head")])
+def test_paged_decode_step_batch_equals_single_steps(dev, gqa, select):
+    """One batched paged step over sequences of one pool equals paged_decode_step
+    per sequence (same pages_per_split) bit for bit, with per-sequence top_k
+    and a sequence shorter than its sinks + top_k; the step records into a
+    HIP graph whose replays give the eager result."""
+    from helix_kv.paged import paged_decode_step, paged_decode_step_batch
+
+    lens = [3000, 700, 16 * 97, 33, 2100]
+    top_k = [40, 12, 30, 50, 25]
+    group, sinks, pps = 7, 4, 9
+    kside, vside, kt, vt, btd, _ = _batch_pool(dev, lens, 16, 4)
+    q = _t(RNG.standard_normal((len(lens), H * group, D)).astype(np.float16), dev)
+    got = paged_decode_step_batch(q, kside, kt, vside, vt, btd, lens, top_k, sinks, gqa=gqa,
+                                  select=select, pages_per_split=pps)
+    for b, T in enumerate(lens):
+        P = -(-T // PS)
+        want = paged_decode_step(q[b], kside, kt, vside, vt, btd[b, :P], T, top_k[b], sinks,
+                                 gqa=gqa, select=select, pages_per_split=pps)
+        assert torch.equal(got[b], want), b
+    out = torch.empty_like(got)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        paged_decode_step_batch(q, kside, kt, vside, vt, btd, lens, top_k, sinks, gqa=gqa,
+                                select=select, pages_per_split=pps)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        paged_decode_step_batch(q, kside, kt, vside, vt, btd, lens, top_k, sinks, gqa=gqa,
+                                select=select, pages_per_split=pps, out=out)
+    for _ in range(3):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, got)
+        paged_decode_step(q[0], kside, kt, vside, vt, btd[0], lens[0], 5, 1)
+        torch.cuda.synchronize()
+
+
+def test_paged_decode_attention_batch_vs_oracle(dev):
+    """The batched paged decode (hkv_paged_decode_attn_batch) over given
+    selections, nuq2 K / nuq4 V, against the oracle's float64 attention over
+    each sequence's pages gathered from the pool bytes."""
+    import ctypes
+
+    from helix_kv import _native as N
+
+    lens, group, pps = [900, 1601, 40], 4, 5
+    B = len(lens)
+    kside, vside, kt, vt, btd, opages = _batch_pool(dev, lens, 4, 16, spare=5)
+    q = RNG.standard_normal((B, H * group, D)).astype(np.float16)
+    sels, offs = [], [0]
+    for T in lens:
+        P = -(-T // PS)
+        n = max(1, P // 3)
+        sels.append(np.stack([np.sort(RNG.permutation(P)[:n]) for _ in range(H)], 1).astype(np.int64))
+        offs.append(offs[-1] + n)
+    sel = np.concatenate(sels)
+    qd, seld = _t(q, dev), _t(sel, dev)
+    out = torch.empty((B, H * group, D), dtype=torch.float32, device=dev)
+    c_sel = (ctypes.c_int64 * (B + 1))(*offs)
+    M = int(btd.shape[1])
+    ws = torch.empty(int(N.lib().hkv_decode_batch_workspace_bytes(B, c_sel, H * group, pps)),
+                     dtype=torch.uint8, device=dev)
+    st = N.lib().hkv_paged_decode_attn_batch(
+        N.ptr(qd), B, H * group, (ctypes.c_int64 * B)(*lens), N.ptr(btd),
+        (ctypes.c_int64 * B)(*[b * M for b in range(B)]), kside.desc(), N.ptr(kt.ensure_tables()),
+        vside.desc(), N.ptr(vt.ensure_tables()), vt.rows, N.ptr(seld), c_sel, pps, D ** -0.5,
+        N.ptr(out), N.dtype_code(out), N.ptr(ws), ws.numel(), N.stream_of(qd))
+    assert st == 0
+    torch.cuda.synchronize()
+    for b, T in enumerate(lens):
+        want = O.selected_attention(q[b].astype(np.float64), *opages[b], sels[b], lambda h: h // group,
+                                    num_tokens=T)
+        _check(out[b], want)
