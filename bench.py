@@ -1005,8 +1005,50 @@ def bench_ragged(args, dev):
     log(f"[bench] ragged decode step, 8 sequences: per-head pages {dec['per_head'][0]:.1f} us batched "
         f"({dec['per_head'][1]:.1f} us as 8 decode_step calls); mean-q union "
         f"{dec['union'][0]:.1f} us batched ({dec['union'][1]:.1f} us as 8 calls)")
+    # the same 8 sequences in one paged pool (each page at a random block,
+    # the block table (8, max pages) as the attention metadata holds it):
+    # paged_decode_step_batch against paged_decode_step per sequence
+    from helix_kv.paged import PagedSide, paged_decode_step, paged_decode_step_batch, paged_write
+
+    g = torch.Generator(device=dev).manual_seed(4)
+    K = torch.randn((T, H, D), generator=g, device=dev).half()
+    V = torch.randn((T, H, D), generator=g, device=dev).half()
+    perm = torch.randperm(Ptot, generator=torch.Generator().manual_seed(5)).to(dev)
+    tok = torch.arange(T, device=dev)
+    slots = perm[tok // 16] * 16 + tok % 16
+    bt = torch.full((len(lens), int(max(lens))), -1, dtype=torch.int64, device=dev)
+    for b in range(len(lens)):
+        bt[b, :int(lens[b])] = perm[int(offs[b]):int(offs[b + 1])]
+    pk = PagedSide.empty(Ptot, H, 4, PAGED_CAP, dev, stats=True)
+    pv = PagedSide.empty(Ptot, H, 4, PAGED_CAP, dev)
+    paged_write(pk, K, kt, slots)
+    paged_write(pv, V, vt, slots, W["pos"])
+    del K, V, tok, slots
+    pdec = {}
+    for mode, gqa in (("per_head", "sum"), ("union", "mean")):
+        decode_step_batch(q, ck, kt, cv, vt, kmin, kmax, starts, tlens, ks, 4, gqa=gqa, select=mode,
+                          out=dout)
+
+        def pbatched():
+            paged_decode_step_batch(q, pk, kt, pv, vt, bt, tlens, ks, 4, gqa=gqa, select=mode, out=lout)
+
+        def plooped():
+            for b, n in enumerate(tlens):
+                paged_decode_step(q[b], pk, kt, pv, vt, bt[b], n, ks[b], 4, gqa=gqa, select=mode,
+                                  out=lout[b])
+
+        pdec[mode] = (graph_us(pbatched, stream, iters), graph_us(plooped, stream, iters))
+        pbatched()
+        rel = float(((dout.float() - lout.float()).norm(dim=-1) / dout.float().norm(dim=-1)).max().item())
+        if rel > 1e-3:
+            raise RuntimeError(f"paged batched decode differs from the compact one: {rel:.2e}")
+    log(f"[bench] ragged paged decode step, 8 sequences: per-head pages {pdec['per_head'][0]:.1f} us "
+        f"batched ({pdec['per_head'][1]:.1f} us as 8 paged_decode_step calls); mean-q union "
+        f"{pdec['union'][0]:.1f} us batched ({pdec['union'][1]:.1f} us as 8 calls); equal to the "
+        f"compact batch (rel {rel:.1e})")
+    del pk, pv
     return dict(rag_us=us, rag_bytes=sel_bytes + gather_bytes, rag_rows=rows, rag_pages=Ptot,
-                rag_sel_bytes=sel_bytes, rag_gather_bytes=gather_bytes, rag_dec=dec)
+                rag_sel_bytes=sel_bytes, rag_gather_bytes=gather_bytes, rag_dec=dec, rag_pdec=pdec)
 
 
 PAGED_CAP = 256  # outlier entries per page-head (12.5% of its 2048 elements)
@@ -1330,6 +1372,11 @@ def main() -> None:
         if "rag_dec" in res:
             d = res["rag_dec"]
             line["ragged"]["decode_step_us"] = {
+                "per_head_batched": round(d["per_head"][0], 1), "per_head_8_calls": round(d["per_head"][1], 1),
+                "union_mean_q_batched": round(d["union"][0], 1), "union_mean_q_8_calls": round(d["union"][1], 1)}
+        if "rag_pdec" in res:
+            d = res["rag_pdec"]
+            line["ragged"]["paged_decode_step_us"] = {
                 "per_head_batched": round(d["per_head"][0], 1), "per_head_8_calls": round(d["per_head"][1], 1),
                 "union_mean_q_batched": round(d["union"][0], 1), "union_mean_q_8_calls": round(d["union"][1], 1)}
     if "rt_us" in res:

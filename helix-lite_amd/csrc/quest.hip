@@ -593,10 +593,13 @@ bound_f16_kernel(const void* q, int qdt, int group, const uint16_t* __restrict__
 // [blk[s], blk[s+1]), the top-K kernel's blockIdx.y = s); scores head-major
 // over the concatenated page axis, (H, off[nseg]).
 constexpr int kMaxSeqs = 64;
+// Paged (bt non-null, HFIX only): sequence s's logical page p has its
+// statistics at row bt[bt0[s] + p] of the pool's (nstat, H, D) statistics.
 struct Segs {
   int64_t off[kMaxSeqs + 1];
   int64_t k[kMaxSeqs];
   int64_t out_off[kMaxSeqs + 1];
+  int64_t bt0[kMaxSeqs];
   int blk[kMaxSeqs + 1];  // the bound kernel's blocks of sequence b: [blk[b], blk[b+1])
   int nseg;
 };
@@ -605,15 +608,21 @@ template <int G, bool HFIX>
 __global__ void __launch_bounds__(256)
 bound_f16_ragged_kernel(const char* q, int64_t q_bytes, int qdt, int group,
                         const uint16_t* __restrict__ kmin, const uint16_t* __restrict__ kmax, int H,
-                        float* out, const Segs segs, int q_lds) {
+                        float* out, const Segs segs, int q_lds, const int64_t* bt, int64_t nstat) {
   // blocks are given to the sequences in proportion to their pages
   int sq = 0;
   while (sq + 1 < segs.nseg && segs.blk[sq + 1] <= (int)blockIdx.x) ++sq;
   const int bx = (int)blockIdx.x - segs.blk[sq], gx = segs.blk[sq + 1] - segs.blk[sq];
   const int64_t o0 = segs.off[sq], P = segs.off[sq + 1] - o0;
-  bound_f16_rows<G, HFIX>(q + sq * q_bytes, qdt, group, kmin + o0 * H * (8 * G),
-                          kmax + o0 * H * (8 * G), P, H, out, HKV_DT_F32, 1, segs.off[segs.nseg], o0,
-                          bx, gx, nullptr, q_lds);
+  if (HFIX && bt) {
+    bound_f16_rows<G, HFIX>(q + sq * q_bytes, qdt, group, kmin, kmax, P, H, out, HKV_DT_F32, 1,
+                            segs.off[segs.nseg], o0, bx, gx, nullptr, q_lds, nullptr, nullptr,
+                            bt + segs.bt0[sq], nstat);
+  } else {
+    bound_f16_rows<G, HFIX>(q + sq * q_bytes, qdt, group, kmin + o0 * H * (8 * G),
+                            kmax + o0 * H * (8 * G), P, H, out, HKV_DT_F32, 1, segs.off[segs.nseg],
+                            o0, bx, gx, nullptr, q_lds);
+  }
 }
 
 // --------------------------------------------------------- a10: top-K
@@ -2418,13 +2427,18 @@ extern "C" int hkv_quest_select_blocks(const void* q, int q_dtype, int H, const 
   return HKV_OK;
 }
 
-extern "C" int hkv_quest_select_ragged(const void* q, int q_dtype, int B, int Hq, const void* kmin,
-                                       const void* kmax, int k_dtype, int H, int D,
-                                       const int64_t* page_offsets, const int64_t* top_k,
-                                       int64_t sink_pages, float* scores, int64_t* out,
-                                       int64_t* out_offsets, void* stream) {
+namespace {
+
+// The ragged selection of both layouts: compact (bt NULL: sequence b's
+// statistics are rows page_offsets[b].. of kmin / kmax) or paged (logical
+// page p of sequence b at row bt[bt_offsets[b] + p] of the pool's nstat
+// blocks; a lane's head must be fixed).
+int select_ragged(const void* q, int q_dtype, int B, int Hq, const void* kmin, const void* kmax,
+                  int k_dtype, int H, int D, const int64_t* page_offsets, const int64_t* top_k,
+                  int64_t sink_pages, float* scores, int64_t* out, int64_t* out_offsets,
+                  const int64_t* bt, const int64_t* bt_offsets, int64_t nstat, hipStream_t st) {
   if (B < 1 || B > kMaxSeqs) return HKV_ERR_SHAPE;
-  if (!page_offsets || !top_k || !out_offsets) return HKV_ERR_ARG;
+  if (!page_offsets || !top_k || !out_offsets || (bt && !bt_offsets)) return HKV_ERR_ARG;
   if (q_dtype != HKV_DT_F16 && q_dtype != HKV_DT_F32 && q_dtype != HKV_DT_BF16) return HKV_ERR_DTYPE;
   if (k_dtype != HKV_DT_F16) return HKV_ERR_DTYPE;
   if (H < 1 || Hq < H || Hq % H || D < 8 || D % 8 || D > 512) return HKV_ERR_SHAPE;
@@ -2440,6 +2454,8 @@ extern "C" int hkv_quest_select_ragged(const void* q, int q_dtype, int B, int Hq
     if (P < 0) return HKV_ERR_ARG;
     sg.off[b] = page_offsets[b];
     sg.k[b] = top_k[b];
+    sg.bt0[b] = bt ? bt_offsets[b] : 0;
+    if (sg.bt0[b] < 0) return HKV_ERR_ARG;
     const int64_t s = sink_pages < 0 ? 0 : (sink_pages > P ? P : sink_pages);
     const int64_t keff = top_k[b] < 0 ? 0 : (top_k[b] > P - s ? P - s : top_k[b]);
     out_offsets[b + 1] = out_offsets[b] + s + keff;
@@ -2449,10 +2465,11 @@ extern "C" int hkv_quest_select_ragged(const void* q, int q_dtype, int B, int Hq
   for (int b = 0; b <= B; ++b) sg.out_off[b] = out_offsets[b];
   const int64_t Ptot = page_offsets[B];
   if (Ptot * H >= ((int64_t)1 << 31) || Ptot * H * D >= ((int64_t)1 << 32)) return HKV_ERR_SHAPE;
+  // paged: the pool's statistics rows are addressed in 32 bits, a lane's head fixed
+  if (bt && (nstat < 1 || nstat * H * D >= ((int64_t)1 << 31) || (64 / G) % H)) return HKV_ERR_SHAPE;
   if (Ptot == 0) return HKV_OK;
   if (!q || !kmin || !kmax || !scores || (out_offsets[B] > 0 && !out)) return HKV_ERR_ARG;
   if (((uintptr_t)kmin | (uintptr_t)kmax) & 15u) return HKV_ERR_ARG;
-  hipStream_t st = (hipStream_t)stream;
   const size_t lds = sizeof(float) * 2 * H * D;
   if (lds > 64 * 1024) return HKV_ERR_SHAPE;
   // blocks per sequence: num_cus * 4 in all, shared in proportion to the
@@ -2483,10 +2500,12 @@ extern "C" int hkv_quest_select_ragged(const void* q, int q_dtype, int B, int Hq
 #define HKV_RB(GG)                                                                                \
   if (hfix)                                                                                       \
     hipLaunchKernelGGL((bound_f16_ragged_kernel<GG, true>), dim3(gx), dim3(256), ldsq, st,        \
-                       (const char*)q, q_bytes, q_dtype, group, mn, mx, H, scores, sg, qlds);     \
+                       (const char*)q, q_bytes, q_dtype, group, mn, mx, H, scores, sg, qlds, bt,  \
+                       nstat);                                                                    \
   else                                                                                            \
     hipLaunchKernelGGL((bound_f16_ragged_kernel<GG, false>), dim3(gx), dim3(256), ldsq, st,       \
-                       (const char*)q, q_bytes, q_dtype, group, mn, mx, H, scores, sg, qlds);
+                       (const char*)q, q_bytes, q_dtype, group, mn, mx, H, scores, sg, qlds,     \
+                       nullptr, 0);
   switch (G) {
     case 1: HKV_RB(1) break;
     case 2: HKV_RB(2) break;
@@ -2508,6 +2527,29 @@ extern "C" int hkv_quest_select_ragged(const void* q, int q_dtype, int B, int Hq
   }
   HKV_CHECK_LAUNCH();
   return HKV_OK;
+}
+
+}  // namespace
+
+extern "C" int hkv_quest_select_ragged(const void* q, int q_dtype, int B, int Hq, const void* kmin,
+                                       const void* kmax, int k_dtype, int H, int D,
+                                       const int64_t* page_offsets, const int64_t* top_k,
+                                       int64_t sink_pages, float* scores, int64_t* out,
+                                       int64_t* out_offsets, void* stream) {
+  return select_ragged(q, q_dtype, B, Hq, kmin, kmax, k_dtype, H, D, page_offsets, top_k, sink_pages,
+                       scores, out, out_offsets, nullptr, nullptr, 0, (hipStream_t)stream);
+}
+
+extern "C" int hkv_quest_select_paged_ragged(const void* q, int q_dtype, int B, int Hq,
+                                             const hkv_paged_side* kside, const int64_t* block_table,
+                                             const int64_t* bt_offsets, const int64_t* page_offsets,
+                                             const int64_t* top_k, int64_t sink_pages, float* scores,
+                                             int64_t* out, int64_t* out_offsets, void* stream) {
+  if (!kside || !block_table) return HKV_ERR_ARG;
+  if (kside->heads < 1 || kside->heads > 16) return HKV_ERR_SHAPE;
+  return select_ragged(q, q_dtype, B, Hq, kside->kmin, kside->kmax, HKV_DT_F16, kside->heads, 128,
+                       page_offsets, top_k, sink_pages, scores, out, out_offsets, block_table,
+                       bt_offsets, kside->num_blocks, (hipStream_t)stream);
 }
 
 // ------------------------------------------------ allocation-free selection

@@ -153,6 +153,9 @@ _SIGS = {
     "hkv_quest_select_ragged": ([_p, _i32, _i32, _i32, _p, _p, _i32, _i32, _i32,
                                  ctypes.POINTER(_i64), ctypes.POINTER(_i64), _i64, _p, _p,
                                  ctypes.POINTER(_i64), _p], _i32),
+    "hkv_quest_select_paged_ragged": ([_p, _i32, _i32, _i32, ctypes.POINTER(PagedSideDesc), _p,
+                                       ctypes.POINTER(_i64), ctypes.POINTER(_i64), ctypes.POINTER(_i64),
+                                       _i64, _p, _p, ctypes.POINTER(_i64), _p], _i32),
     "hkv_nuq_gather_pages": ([_p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32,
                               ctypes.POINTER(NuqScales), _i32, _i32, ctypes.POINTER(_i64),
                               ctypes.POINTER(_i64), _p, _p, _p], _i32),

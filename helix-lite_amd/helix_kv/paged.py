@@ -222,6 +222,59 @@ def paged_select(query: torch.Tensor, kside: PagedSide, block_table: torch.Tenso
     return out, scores
 
 
+def paged_select_ragged(queries: torch.Tensor, kside: PagedSide, block_tables: torch.Tensor,
+                        seq_lens, top_k, sink_pages: int, *, scores: torch.Tensor | None = None):
+    """paged_select for B <= 64 sequences of one pool in one bound launch and
+    one top-K launch (hkv_quest_select_paged_ragged): sequence b has
+    seq_lens[b] tokens, query queries[b] (Hq, 128) and its logical page p at
+    block block_tables[b, p].  The pool's KV heads must divide 4.  Returns
+    (sel (rows, H) int64 logical pages, ascending per sequence and head;
+    out_offsets (B+1 ints), the rows of sequence b; scores (H, total pages)
+    fp32, sequence b's at columns out of the running page count)."""
+    import ctypes
+    from .ops import _ragged_rows
+
+    N.require_gpu(queries, block_tables)
+    if kside.kmin is None:
+        raise ValueError("the side holds no page statistics (K written with stats)")
+    lens = [int(n) for n in seq_lens]
+    B = len(lens)
+    H = kside.heads
+    if queries.dim() != 3 or int(queries.shape[0]) != B or int(queries.shape[2]) != HEAD_DIM or \
+            int(queries.shape[1]) % H:
+        raise ValueError(f"queries {tuple(queries.shape)} incompatible with {B} sequences, {H} KV heads")
+    if 4 % H:
+        raise ValueError(f"the ragged paged selection needs 1, 2 or 4 KV heads, not {H}")
+    pages = [-(-n // PAGE) for n in lens]
+    if block_tables.dim() != 2 or int(block_tables.shape[0]) != B or \
+            int(block_tables.shape[1]) < max(pages, default=0):
+        raise ValueError(f"block_tables must be ({B}, >= {max(pages, default=0)}), got "
+                         f"{tuple(block_tables.shape)}")
+    M = int(block_tables.shape[1])
+    bt = block_tables.to(torch.int64).contiguous()
+    offs = [0]
+    for P in pages:
+        offs.append(offs[-1] + P)
+    ks = [int(top_k)] * B if not hasattr(top_k, '__len__') else [int(x) for x in top_k]
+    if len(ks) != B:
+        raise ValueError("one top_k per sequence")
+    rows = _ragged_rows(offs, ks, sink_pages)
+    q = queries.contiguous()
+    out = torch.empty((max(rows[-1], 1), H), dtype=torch.int64, device=q.device)
+    if scores is None:
+        scores = torch.empty((H, max(offs[-1], 1)), dtype=torch.float32, device=q.device)
+    c_off = (ctypes.c_int64 * (B + 1))(*offs)
+    c_k = (ctypes.c_int64 * B)(*ks)
+    c_bt = (ctypes.c_int64 * B)(*[b * M for b in range(B)])
+    c_out = (ctypes.c_int64 * (B + 1))()
+    st = N.lib().hkv_quest_select_paged_ragged(
+        N.ptr(q), N.dtype_code(q), B, int(q.shape[1]), kside.desc(), N.ptr(bt), c_bt, c_off, c_k,
+        int(sink_pages), N.ptr(scores), N.ptr(out), c_out, N.stream_of(q))
+    N.check(st, "hkv_quest_select_paged_ragged", ValueError)
+    assert list(c_out) == rows
+    return out[: rows[-1]], rows, scores[:, : offs[-1]]
+
+
 def paged_decode_attention(query: torch.Tensor, kside: PagedSide, kt: NuqLayerTables,
                            vside: PagedSide, vt: NuqLayerTables, block_table: torch.Tensor,
                            seq_len: int, sel: torch.Tensor, *, scale: float | None = None,
@@ -316,10 +369,11 @@ def paged_decode_step_batch(queries: torch.Tensor, kside: PagedSide, kt: NuqLaye
     """paged_decode_step for B <= 64 sequences of one pool, with no host reads:
     sequence b has seq_lens[b] tokens, query queries[b] and its logical page p
     in block block_tables[b, p] (block_tables (B, M) as the attention
-    metadata's block table, M >= ceil(seq_lens[b] / 16)).  A Quest selection
-    per sequence into one selection, the per-sequence union of the heads'
-    pages for select="union" (hkv_union_pages_ragged), then one batched decode
-    + merge (hkv_paged_decode_attn_batch); each sequence's result equals
+    metadata's block table, M >= ceil(seq_lens[b] / 16)).  One ragged Quest
+    selection (hkv_quest_select_paged_ragged; one paged selection per sequence
+    where the pool has more than 4 KV heads), the per-sequence union of the
+    heads' pages for select="union" (hkv_union_pages_ragged), then one batched
+    decode + merge (hkv_paged_decode_attn_batch); each sequence's result equals
     paged_decode_step's with the same pages_per_split.  The reference forward
     falls back to dense attention for batches above one
     (src/kvquant/compact_backend.py:195-203).  top_k: one int, or one per
@@ -366,18 +420,20 @@ def paged_decode_step_batch(queries: torch.Tensor, kside: PagedSide, kt: NuqLaye
     q = queries.contiguous()
     qs = q.reshape(B, H, Hq // H, HEAD_DIM).mean(dim=2).to(torch.float16) if gqa == "mean" else q
     sp = int(sink_pages)
-    rows = [0]
-    for P, k in zip(pages, ks):
-        s = max(0, min(sp, P))
-        rows.append(rows[-1] + s + max(0, min(k, P - s)))
     offs = [0]
     for P in pages:
         offs.append(offs[-1] + P)
-    sel = torch.empty((max(rows[-1], 1), H), dtype=torch.int64, device=dev)
-    scores = torch.empty((H * max(pages),), dtype=torch.float32, device=dev)
-    for b in range(B):
-        paged_select(qs[b], kside, bt[b], lens[b], ks[b], sp, out=sel[rows[b]:rows[b + 1]],
-                     scores=scores[:H * pages[b]].view(H, pages[b]))
+    if 4 % H == 0:
+        sel, rows, _ = paged_select_ragged(qs, kside, bt, lens, ks, sp)
+    else:  # a bound lane cannot hold a fixed head: one selection per sequence
+        from .ops import _ragged_rows
+
+        rows = _ragged_rows(offs, ks, sp)
+        sel = torch.empty((max(rows[-1], 1), H), dtype=torch.int64, device=dev)
+        scores = torch.empty((H * max(pages),), dtype=torch.float32, device=dev)
+        for b in range(B):
+            paged_select(qs[b], kside, bt[b], lens[b], ks[b], sp, out=sel[rows[b]:rows[b + 1]],
+                         scores=scores[:H * pages[b]].view(H, pages[b]))
     if select == "union":
         c_rows = (ctypes.c_int64 * (B + 1))(*rows)
         c_pages = (ctypes.c_int64 * (B + 1))(*offs)

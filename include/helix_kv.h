@@ -597,6 +597,22 @@ int hkv_quest_select_ragged(const void *q, int q_dtype, int B, int Hq, const voi
                             float *scores, int64_t *out, int64_t *out_offsets, void *stream);
 
 /*
+ * hkv_quest_select_ragged over a paged pool's K statistics (kside->kmin /
+ * kmax, D = 128): sequence b has page_offsets[b+1] - page_offsets[b] logical
+ * pages, logical page p's statistics at block block_table[bt_offsets[b] + p]
+ * (a block outside the pool gets bound -inf), as hkv_quest_select_paged per
+ * sequence (src/kvquant/quest_selector.py:38-90 per sequence).  scores (H,
+ * page_offsets[B]) fp32.  bt_offsets (B) is a HOST array, block_table a
+ * device array.  kside->heads must divide 4 (1, 2 or 4: a bound lane's KV
+ * head is fixed); HKV_ERR_SHAPE otherwise.
+ */
+int hkv_quest_select_paged_ragged(const void *q, int q_dtype, int B, int Hq,
+                                  const hkv_paged_side *kside, const int64_t *block_table,
+                                  const int64_t *bt_offsets, const int64_t *page_offsets,
+                                  const int64_t *top_k, int64_t sink_pages, float *scores,
+                                  int64_t *out, int64_t *out_offsets, void *stream);
+
+/*
  * Gather + dequantise the selected pages of a compact-format K or V (as
  * hkv_nuq_pack_compact writes it over the concatenated tokens of B <= 64
  * sequences; page p = tokens [16p, 16p+16)) into staging (rows, 16, H, 128)

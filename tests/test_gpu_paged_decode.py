@@ -233,12 +233,13 @@ def _batch_pool(dev, lens, Lk, Lv, spare=23, cap=256):
         paged_write(vside, _t(v, dev), vt, _t(slots, dev), _t(np.arange(T), dev))
         O.paged_write(kp, k, slots, [a.astype(np.float32) for a in ks], False)
         O.paged_write(vp, v, slots, [a.astype(np.float32) for a in vs], True, positions=np.arange(T))
-    oracle_pages = []
+    oracle_pages, stats = [], []
     for b, P in enumerate(pages):
         first = np.arange(P) * PS
         oracle_pages.append((O.h2f(O.paged_gather(kp, bt[b, :P], first, ks[0].astype(np.float32), False)),
                              O.h2f(O.paged_gather(vp, bt[b, :P], first, vs[0].astype(np.float32), True))))
-    return kside, vside, kt, vt, _t(bt, dev), oracle_pages
+        stats.append((O.h2f(kp["kmin"][bt[b, :P]]), O.h2f(kp["kmax"][bt[b, :P]])))
+    return kside, vside, kt, vt, _t(bt, dev), oracle_pages, stats
 
 
 @pytest.mark.parametrize("gqa,select", [("mean", "union"), ("sum", "per_head"), ("mean", "per_head")])
@@ -252,7 +253,7 @@ def test_paged_decode_step_batch_equals_single_steps(dev, gqa, select):
     lens = [3000, 700, 16 * 97, 33, 2100]
     top_k = [40, 12, 30, 50, 25]
     group, sinks, pps = 7, 4, 9
-    kside, vside, kt, vt, btd, _ = _batch_pool(dev, lens, 16, 4)
+    kside, vside, kt, vt, btd, _, _ = _batch_pool(dev, lens, 16, 4)
     q = _t(RNG.standard_normal((len(lens), H * group, D)).astype(np.float16), dev)
     got = paged_decode_step_batch(q, kside, kt, vside, vt, btd, lens, top_k, sinks, gqa=gqa,
                                   select=select, pages_per_split=pps)
@@ -291,7 +292,7 @@ def test_paged_decode_attention_batch_vs_oracle(dev):
 
     lens, group, pps = [900, 1601, 40], 4, 5
     B = len(lens)
-    kside, vside, kt, vt, btd, opages = _batch_pool(dev, lens, 4, 16, spare=5)
+    kside, vside, kt, vt, btd, opages, _ = _batch_pool(dev, lens, 4, 16, spare=5)
     q = RNG.standard_normal((B, H * group, D)).astype(np.float16)
     sels, offs = [], [0]
     for T in lens:
@@ -317,3 +318,34 @@ def test_paged_decode_attention_batch_vs_oracle(dev):
         want = O.selected_attention(q[b].astype(np.float64), *opages[b], sels[b], lambda h: h // group,
                                     num_tokens=T)
         _check(out[b], want)
+
+
+@pytest.mark.parametrize("group", [7, 1])
+def test_paged_select_ragged_vs_oracle(dev, group):
+    """The ragged paged selection (one bound and one top-K launch for the
+    batch) against the oracle's group-summed bound and top-K with sinks over
+    each sequence's logical pages, bit for bit, scores included; a block-table
+    entry outside the pool scores -inf and is not chosen."""
+    from helix_kv.paged import paged_select_ragged
+
+    lens = [1000, 16 * 300, 50, 16 * 41 + 3]
+    top_k, sinks = [20, 100, 9, 30], 4
+    kside, _, _, _, btd, _, stats = _batch_pool(dev, lens, 16, 4)
+    bt = btd.cpu().numpy()
+    bt[1, 17] = -1
+    bt[3, 30] = 10**7
+    q = RNG.standard_normal((len(lens), H * group, D)).astype(np.float16)
+    sel, rows, scores = paged_select_ragged(_t(q, dev), kside, _t(bt, dev), lens, top_k, sinks)
+    sel, scores = sel.cpu().numpy(), scores.cpu().numpy()
+    p0 = 0
+    for b, T in enumerate(lens):
+        P = -(-T // PS)
+        want = O.page_bound_group(q[b], *stats[b], group)
+        bad = bt[b, :P] < 0
+        bad |= bt[b, :P] >= kside.num_blocks
+        want[bad] = -np.inf
+        assert np.array_equal(scores[:, p0:p0 + P], want.T), b
+        got = sel[rows[b]:rows[b + 1]]
+        assert np.array_equal(got, O.topk_sinks(want, top_k[b], sinks)), b
+        assert not np.isin(got, np.flatnonzero(bad)).any(), b
+        p0 += P
