@@ -168,12 +168,21 @@ unpack_compact_kernel(const uint8_t* __restrict__ packed, const int32_t* __restr
     load_csr(Ln, Cn);
     process(wt, Lc, Cc);
   };
-  for (int64_t wt = wt0; wt < nwtiles; wt += 3 * nwaves) {
+  // Whole rounds of three tiles with no exit between the steps (an exit
+  // there leaves a join at the loop head through which the compiler waits
+  // for every outstanding access, the last tile's stores included, before
+  // the next loads), then the last one or two tiles.  At each round's start
+  // L0, L1 hold tiles wt, wt + nwaves and C0 tile wt's entries.
+  int64_t wt = wt0;
+  for (; wt + 2 * nwaves < nwtiles; wt += 3 * nwaves) {
     step(wt, L0, C0, L1, C1, L2);
-    if (wt + nwaves >= nwtiles) break;
     step(wt + nwaves, L1, C1, L2, C2, L0);
-    if (wt + 2 * nwaves >= nwtiles) break;
     step(wt + 2 * nwaves, L2, C2, L0, C0, L1);
+  }
+  if (wt < nwtiles) {
+    load_csr(L1, C1);
+    process(wt, L0, C0);
+    if (wt + nwaves < nwtiles) process(wt + nwaves, L1, C1);
   }
 }
 
@@ -235,7 +244,15 @@ HKV_DEV void unpack_d128_body(const uint8_t* __restrict__ packed, const int32_t*
     uint32_t c[kU128Passes], v[kU128Passes];  // entry ra + cg of each pass's row
   };
   const int64_t nwaves = (int64_t)nblk * NW;
-  const uint32_t cap32 = (uint32_t)(cap < 0x7fffffff ? cap : 0x7fffffff);  // row_ptr entries are int32
+  // The CSR entry, position and output accesses below are unconditional: a
+  // branch around any of them makes the compiler's waits allow for the path
+  // without it, and a wait for an earlier load then also waits for the
+  // previous tile's stores.  With no entries the entry loads read row_ptr's
+  // first bytes (it has at least two entries).
+  const uint8_t* colp = cap > 0 ? col : reinterpret_cast<const uint8_t*>(row_ptr);
+  const char* valp = cap > 0 ? reinterpret_cast<const char*>(val) : reinterpret_cast<const char*>(row_ptr);
+  // row_ptr entries are int32
+  const uint32_t cap32 = cap <= 0 ? 1u : (uint32_t)(cap < 0x7fffffff ? cap : 0x7fffffff);
   const int rows32 = (int)sc.rows;  // the host checks H * rows * 80 < 2^31 for this kernel
   auto load_tile = [&](int64_t wt, TileLoad& L) {
     int64_t rbase;
@@ -258,9 +275,11 @@ HKV_DEV void unpack_d128_body(const uint8_t* __restrict__ packed, const int32_t*
       L.rp[p] = *reinterpret_cast<const int2*>(reinterpret_cast<const char*>(rp) + 4u * o);
       if constexpr (PT) {
         const int k = (int)(o >> lgH), h = (int)(o & (H - 1));
+        // without a position array the load reads row_ptr's first 8 bytes
+        const int64_t ap = sc.positions ? sc.positions[t0 + k]
+                                        : *reinterpret_cast<const int64_t*>(row_ptr);
         int pos;
         if (sc.positions) {
-          const int64_t ap = sc.positions[t0 + k];
           pos = ap < 0 ? 0 : (ap > rows32 - 1 ? rows32 - 1 : (int)ap);
         } else {
           pos = p0c + k;
@@ -272,13 +291,12 @@ HKV_DEV void unpack_d128_body(const uint8_t* __restrict__ packed, const int32_t*
     }
   };
   auto load_csr = [&](const TileLoad& L, TileCsr& C) {
-    if (cap <= 0) return;
 #pragma unroll
     for (int p = 0; p < kU128Passes; ++p) {
       uint32_t i = (uint32_t)(L.rp[p].x > 0 ? L.rp[p].x : 0) + (uint32_t)cg;
       i = i < cap32 ? i : cap32 - 1u;
-      C.c[p] = col[i];
-      C.v[p] = *reinterpret_cast<const uint16_t*>(reinterpret_cast<const char*>(val) + 2u * i);
+      C.c[p] = colp[i];
+      C.v[p] = *reinterpret_cast<const uint16_t*>(valp + 2u * i);
     }
   };
   auto process = [&](int64_t wt, const TileLoad& L, const TileCsr& C) {
@@ -330,9 +348,11 @@ HKV_DEV void unpack_d128_body(const uint8_t* __restrict__ packed, const int32_t*
     uint16_t* ob = out + rbase * D;
 #pragma unroll
     for (int p = 0; p < kU128Passes; ++p) {
+      // a row past the end stores row lim's values again (same lane column,
+      // same data), so the store needs no branch
       const int rr = p * RW + rw;
-      if (rr > lim) continue;
-      store_stream(ob + (uint32_t)(rr * D + 8 * cg), *reinterpret_cast<const uint4*>(seg + rr * D + 8 * cg));
+      const int rs = rr > lim ? lim : rr;
+      store_stream(ob + (uint32_t)(rs * D + 8 * cg), *reinterpret_cast<const uint4*>(seg + rs * D + 8 * cg));
     }
     wave_sync();
   };
@@ -349,12 +369,18 @@ HKV_DEV void unpack_d128_body(const uint8_t* __restrict__ packed, const int32_t*
     load_csr(Ln, Cn);
     process(wt, Lc, Cc);
   };
-  for (int64_t wt = wt0; wt < nwtiles; wt += 3 * nwaves) {
+  // Whole rounds of three tiles, then the last one or two (as in
+  // unpack_compact_kernel).
+  int64_t wt = wt0;
+  for (; wt + 2 * nwaves < nwtiles; wt += 3 * nwaves) {
     step(wt, L0, C0, L1, C1, L2);
-    if (wt + nwaves >= nwtiles) break;
     step(wt + nwaves, L1, C1, L2, C2, L0);
-    if (wt + 2 * nwaves >= nwtiles) break;
     step(wt + 2 * nwaves, L2, C2, L0, C0, L1);
+  }
+  if (wt < nwtiles) {
+    load_csr(L1, C1);
+    process(wt, L0, C0);
+    if (wt + nwaves < nwtiles) process(wt + nwaves, L1, C1);
   }
 }
 
