@@ -179,7 +179,7 @@ HKV_DEV uint32_t pos_zero2(uint32_t v) {  // -0 -> +0 in both halves
 // group, written for the wave's head.  STATS (K): page min / max of the
 // dequantised values.
 template <int NB, bool PT, int BITS, bool STATS>
-__global__ void __launch_bounds__(kPT)
+__global__ void __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(PT ? 5 : 3)))
 paged_write_kernel(PagedWriteArgs A) {
   constexpr int RB = kPD * BITS / 8;    // packed bytes per row
   constexpr int TW = 20;                // staged table words per row
