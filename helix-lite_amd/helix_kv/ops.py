@@ -720,7 +720,7 @@ def decode_step_batch(queries: torch.Tensor, k: CompactCodes, kt: NuqLayerTables
     forward handles batch 1 only (src/kvquant/compact_backend.py:184-203).
 
     When the sequences lie back to back (each starts on the page after the
-    previous one's last) and B <= 64, the step is one ragged Quest selection
+    previous one's last), each batch of up to 64 is one ragged Quest selection
     (hkv_quest_select_ragged), the per-sequence union of the heads' pages for
     select="union" (hkv_union_pages_ragged) and one batched decode + merge
     (hkv_decode_attn_batch); each sequence's result equals decode_step's with
@@ -749,7 +749,13 @@ def decode_step_batch(queries: torch.Tensor, k: CompactCodes, kt: NuqLayerTables
     T, H, D = k.shape
     pages = [-(-n // 16) for n in lens]
     back_to_back = all(starts[b + 1] == starts[b] + 16 * pages[b] for b in range(B - 1))
-    if B > 64 or not back_to_back or starts[-1] + lens[-1] > T or v.shape != (T, H, D):
+    if back_to_back and B > 64 and starts[-1] + lens[-1] <= T and v.shape == (T, H, D):
+        for c in range(0, B, 64):  # batches of 64 (each one launch of the decode)
+            decode_step_batch(queries[c:c + 64], k, kt, v, vt, K_min, K_max, starts[c:c + 64],
+                              lens[c:c + 64], ks[c:c + 64], sink_pages, gqa=gqa, select=select,
+                              scale=scale, out=out[c:c + 64], pages_per_split=pages_per_split)
+        return out
+    if not back_to_back or starts[-1] + lens[-1] > T or v.shape != (T, H, D):
         for b, (t0, n) in enumerate(zip(starts, lens)):
             p0, p1 = t0 // 16, (t0 + n + 15) // 16
             decode_step(queries[b], compact_view(k, t0, t0 + n), kt, compact_view(v, t0, t0 + n), vt,

@@ -366,15 +366,16 @@ def paged_decode_step_batch(queries: torch.Tensor, kside: PagedSide, kt: NuqLaye
                             out: torch.Tensor | None = None,
                             out_dtype: torch.dtype = torch.float16,
                             pages_per_split: int | None = None) -> torch.Tensor:
-    """paged_decode_step for B <= 64 sequences of one pool, with no host reads:
+    """paged_decode_step for B sequences of one pool, with no host reads:
     sequence b has seq_lens[b] tokens, query queries[b] and its logical page p
     in block block_tables[b, p] (block_tables (B, M) as the attention
     metadata's block table, M >= ceil(seq_lens[b] / 16)).  One ragged Quest
     selection (hkv_quest_select_paged_ragged; one paged selection per sequence
     where the pool has more than 4 KV heads), the per-sequence union of the
     heads' pages for select="union" (hkv_union_pages_ragged), then one batched
-    decode + merge (hkv_paged_decode_attn_batch); each sequence's result equals
-    paged_decode_step's with the same pages_per_split.  The reference forward
+    decode + merge (hkv_paged_decode_attn_batch), per batch of up to 64
+    sequences; each sequence's result equals paged_decode_step's with the
+    same pages_per_split.  The reference forward
     falls back to dense attention for batches above one
     (src/kvquant/compact_backend.py:195-203).  top_k: one int, or one per
     sequence.  queries (B, Hq, 128) fp16; returns (B, Hq, 128)."""
@@ -390,8 +391,20 @@ def paged_decode_step_batch(queries: torch.Tensor, kside: PagedSide, kt: NuqLaye
     Hq = int(queries.shape[1])
     if Hq % H or queries.dtype != torch.float16:
         raise ValueError(f"queries {tuple(queries.shape)} {queries.dtype}: fp16 with a multiple of {H} heads")
-    if B < 1 or B > 64:
-        raise ValueError(f"1 to 64 sequences, got {B}")
+    if B < 1:
+        raise ValueError("no sequences")
+    if B > 64:  # batches of 64 (each one launch of the decode)
+        if out is None:
+            out = torch.empty((B, Hq, HEAD_DIM), dtype=out_dtype, device=queries.device)
+        ks_all = [int(top_k)] * B if not hasattr(top_k, '__len__') else [int(x) for x in top_k]
+        if len(ks_all) != B:
+            raise ValueError("one top_k per sequence")
+        for c in range(0, B, 64):
+            paged_decode_step_batch(queries[c:c + 64], kside, kt, vside, vt, block_tables[c:c + 64],
+                                    lens[c:c + 64], ks_all[c:c + 64], sink_pages, gqa=gqa,
+                                    select=select, scale=scale, out=out[c:c + 64], out_dtype=out_dtype,
+                                    pages_per_split=pages_per_split)
+        return out
     if any(n < 1 for n in lens):
         raise ValueError("sequence lengths must be positive")
     ks = [int(top_k)] * B if not hasattr(top_k, '__len__') else [int(x) for x in top_k]

@@ -420,18 +420,21 @@ def test_union_pages_vs_numpy_on_a_reused_workspace(dev):
         assert np.array_equal(got, want), (P, n, H)
 
 
-@pytest.mark.parametrize("layout", ["back_to_back", "gapped"])
+@pytest.mark.parametrize("layout", ["back_to_back", "gapped", "many"])
 def test_decode_step_batch_equals_single_steps(dev, layout):
     """The batched step (one ragged selection, one union, one decode launch;
-    the gapped layout takes the per-sequence path) equals decode_step on each
-    sequence's view with the same pages_per_split, bit for bit, in both select
-    modes; and a HIP graph of the batched step replays it exactly."""
+    the gapped layout takes the per-sequence path; 70 sequences run as
+    batches of 64 and 6) equals decode_step on each sequence's view with the
+    same pages_per_split, bit for bit, in both select modes; and a HIP graph
+    of the batched step replays it exactly."""
     from helix_kv.ops import (NuqLayerTables, compact_view, decode_step, decode_step_batch,
                               nuq_pack_compact)
 
     H, group, D, top_k, sinks, pps = 4, 7, 128, 20, 4, 8
     lens = [700, 1601, 40, 2100, 16]
-    gap = 0 if layout == "back_to_back" else 32
+    if layout == "many":
+        lens = [int(n) for n in np.random.default_rng(70).integers(1, 300, 70)]
+    gap = 32 if layout == "gapped" else 0
     starts = [0]
     for n in lens[:-1]:
         starts.append(starts[-1] + -(-n // PS) * PS + gap)

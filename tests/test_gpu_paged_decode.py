@@ -282,6 +282,24 @@ def test_paged_decode_step_batch_equals_single_steps(dev, gqa, select):
         torch.cuda.synchronize()
 
 
+def test_paged_decode_step_batch_above_64_sequences(dev):
+    """70 sequences run as batches of 64 and 6: each result equals
+    paged_decode_step on its own, bit for bit, in both select modes."""
+    from helix_kv.paged import paged_decode_step, paged_decode_step_batch
+
+    lens = [int(n) for n in np.random.default_rng(71).integers(1, 200, 70)]
+    kside, vside, kt, vt, btd, _, _ = _batch_pool(dev, lens, 4, 16)
+    q = _t(RNG.standard_normal((len(lens), H * 2, D)).astype(np.float16), dev)
+    for select in ("union", "per_head"):
+        got = paged_decode_step_batch(q, kside, kt, vside, vt, btd, lens, 3, 2, select=select,
+                                      pages_per_split=2)
+        for b, T in enumerate(lens):
+            P = -(-T // PS)
+            want = paged_decode_step(q[b], kside, kt, vside, vt, btd[b, :P], T, 3, 2, select=select,
+                                     pages_per_split=2)
+            assert torch.equal(got[b], want), (select, b)
+
+
 def test_paged_decode_attention_batch_vs_oracle(dev):
     """The batched paged decode (hkv_paged_decode_attn_batch) over given
     selections, nuq2 K / nuq4 V, against the oracle's float64 attention over
