@@ -807,6 +807,23 @@ HKV_DEV void merge_body(const float* __restrict__ pm, const float* __restrict__ 
   __shared__ float s_red[kW];
   __shared__ float s_acc[kDT];
   const int hq = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int d = blockIdx.y * kMergeCh + (tid % kMergeCh), sub = tid / kMergeCh;
+  // Up to kMergeRegs splits a thread: their partial outputs and maxima are
+  // requested first (clamped indexes, unconditional), so the max and sum
+  // passes below overlap them instead of following them.
+  constexpr int kMergeRegs = 16;
+  const bool in_regs = splits <= (int64_t)kMergeRegs * kMergeSub;
+  const int dc = d < Dv ? d : Dv - 1;
+  float pov[kMergeRegs], pmv[kMergeRegs];
+  if (in_regs) {
+#pragma unroll
+    for (int i = 0; i < kMergeRegs; ++i) {
+      int64_t s = sub + (int64_t)i * kMergeSub;
+      s = s < splits ? s : splits - 1;
+      pmv[i] = pm[s * Hq + hq];
+      pov[i] = po[(s * Hq + hq) * Dv + dc];
+    }
+  }
   float mx = -__builtin_inff();
   for (int64_t s = tid; s < splits; s += kDT) mx = fmaxf(mx, pm[s * Hq + hq]);
 #pragma unroll
@@ -828,9 +845,18 @@ HKV_DEV void merge_body(const float* __restrict__ pm, const float* __restrict__ 
   __syncthreads();
   float L = 0.0f;
   for (int w = 0; w < kW; ++w) L += s_red[w];
-  const int d = blockIdx.y * kMergeCh + (tid % kMergeCh), sub = tid / kMergeCh;
   float acc = 0.0f;
-  if (d < Dv && M != -__builtin_inff()) {
+  if (in_regs) {
+    if (d < Dv && M != -__builtin_inff()) {
+#pragma unroll
+      for (int i = 0; i < kMergeRegs; ++i) {
+        if (sub + (int64_t)i * kMergeSub < splits) {
+          const float w = pmv[i] == -__builtin_inff() ? 0.0f : exp2f(pmv[i] - M);
+          acc += w * pov[i];
+        }
+      }
+    }
+  } else if (d < Dv && M != -__builtin_inff()) {
 #pragma unroll 4
     for (int64_t s = sub; s < splits; s += kMergeSub) {
       const float ms = pm[s * Hq + hq];
