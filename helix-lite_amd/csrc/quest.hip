@@ -2465,8 +2465,10 @@ int select_ragged(const void* q, int q_dtype, int B, int Hq, const void* kmin, c
   for (int b = 0; b <= B; ++b) sg.out_off[b] = out_offsets[b];
   const int64_t Ptot = page_offsets[B];
   if (Ptot * H >= ((int64_t)1 << 31) || Ptot * H * D >= ((int64_t)1 << 32)) return HKV_ERR_SHAPE;
-  // paged: the pool's statistics rows are addressed in 32 bits, a lane's head fixed
-  if (bt && (nstat < 1 || nstat * H * D >= ((int64_t)1 << 31) || (64 / G) % H)) return HKV_ERR_SHAPE;
+  // paged: the pool's statistics rows are addressed in 32 bits, a lane's head
+  // fixed (the heads divide a block's rows per row group, 256 / G)
+  if (bt && (nstat < 1 || nstat * H * D >= ((int64_t)1 << 31) || G > 64 || (256 / G) % H))
+    return HKV_ERR_SHAPE;
   if (Ptot == 0) return HKV_OK;
   if (!q || !kmin || !kmax || !scores || (out_offsets[B] > 0 && !out)) return HKV_ERR_ARG;
   if (((uintptr_t)kmin | (uintptr_t)kmax) & 15u) return HKV_ERR_ARG;
@@ -2489,7 +2491,10 @@ int select_ragged(const void* q, int q_dtype, int B, int Hq, const void* kmin, c
   }
   const unsigned gx = (unsigned)sg.blk[B];
   const int64_t q_bytes = (int64_t)Hq * D * (q_dtype == HKV_DT_F32 ? 4 : 2);
-  const bool hfix = (64 / G) % H == 0;
+  // a lane's head is fixed when the heads divide the rows of a block's row
+  // group (256 / G): a lane keeps its row of every group; the compact path
+  // keeps the stricter wave rule it was measured with
+  const bool hfix = bt ? true : (64 / G) % H == 0;
   auto mn = (const uint16_t*)kmin;
   auto mx = (const uint16_t*)kmax;
   const int group = Hq / H;

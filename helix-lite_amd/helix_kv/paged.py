@@ -243,8 +243,8 @@ def paged_select_ragged(queries: torch.Tensor, kside: PagedSide, block_tables: t
     if queries.dim() != 3 or int(queries.shape[0]) != B or int(queries.shape[2]) != HEAD_DIM or \
             int(queries.shape[1]) % H:
         raise ValueError(f"queries {tuple(queries.shape)} incompatible with {B} sequences, {H} KV heads")
-    if 4 % H:
-        raise ValueError(f"the ragged paged selection needs 1, 2 or 4 KV heads, not {H}")
+    if 16 % H:
+        raise ValueError(f"the ragged paged selection needs 1, 2, 4, 8 or 16 KV heads, not {H}")
     pages = [-(-n // PAGE) for n in lens]
     if block_tables.dim() != 2 or int(block_tables.shape[0]) != B or \
             int(block_tables.shape[1]) < max(pages, default=0):
@@ -371,7 +371,7 @@ def paged_decode_step_batch(queries: torch.Tensor, kside: PagedSide, kt: NuqLaye
     in block block_tables[b, p] (block_tables (B, M) as the attention
     metadata's block table, M >= ceil(seq_lens[b] / 16)).  One ragged Quest
     selection (hkv_quest_select_paged_ragged; one paged selection per sequence
-    where the pool has more than 4 KV heads), the per-sequence union of the
+    where the pool's KV heads do not divide 16), the per-sequence union of the
     heads' pages for select="union" (hkv_union_pages_ragged), then one batched
     decode + merge (hkv_paged_decode_attn_batch), per batch of up to 64
     sequences; each sequence's result equals paged_decode_step's with the
@@ -436,7 +436,7 @@ def paged_decode_step_batch(queries: torch.Tensor, kside: PagedSide, kt: NuqLaye
     offs = [0]
     for P in pages:
         offs.append(offs[-1] + P)
-    if 4 % H == 0:
+    if 16 % H == 0:
         sel, rows, _ = paged_select_ragged(qs, kside, bt, lens, ks, sp)
     else:  # a bound lane cannot hold a fixed head: one selection per sequence
         from .ops import _ragged_rows

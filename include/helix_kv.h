@@ -603,8 +603,8 @@ int hkv_quest_select_ragged(const void *q, int q_dtype, int B, int Hq, const voi
  * (a block outside the pool gets bound -inf), as hkv_quest_select_paged per
  * sequence (src/kvquant/quest_selector.py:38-90 per sequence).  scores (H,
  * page_offsets[B]) fp32.  bt_offsets (B) is a HOST array, block_table a
- * device array.  kside->heads must divide 4 (1, 2 or 4: a bound lane's KV
- * head is fixed); HKV_ERR_SHAPE otherwise.
+ * device array.  kside->heads must divide 16 (1, 2, 4, 8 or 16: a bound
+ * lane's KV head is fixed); HKV_ERR_SHAPE otherwise.
  */
 int hkv_quest_select_paged_ragged(const void *q, int q_dtype, int B, int Hq,
                                   const hkv_paged_side *kside, const int64_t *block_table,

@@ -367,3 +367,58 @@ def test_paged_select_ragged_vs_oracle(dev, group):
         assert np.array_equal(got, O.topk_sinks(want, top_k[b], sinks)), b
         assert not np.isin(got, np.flatnonzero(bad)).any(), b
         p0 += P
+
+
+@pytest.mark.parametrize("H8", [8, 16])
+def test_paged_select_ragged_and_batch_step_more_heads(dev, H8):
+    """Pools with 8 and 16 KV heads: the ragged paged selection (a bound lane
+    still holds one head: the heads divide a block's 16 rows) against the
+    oracle's group-summed bound and top-K with sinks, bit for bit; the
+    batched paged step equal to paged_decode_step per sequence."""
+    from helix_kv.ops import NuqLayerTables
+    from helix_kv.paged import (PagedSide, paged_decode_step, paged_decode_step_batch, paged_select_ragged,
+                                paged_write)
+
+    lens, top_k, sinks, group = [700, 1300, 90], [30, 60, 5], 4, 2
+    pages = [-(-n // PS) for n in lens]
+    NB = sum(pages) + 9
+    perm = RNG.permutation(NB).astype(np.int64)
+    bt = np.full((len(lens), max(pages) + 1), -1, np.int64)
+    kpol = np.sort(RNG.standard_normal((H8, D, 16)), axis=-1).astype(np.float16)
+    kup = np.full((H8, D), 1.2, np.float16)
+    vpol = np.sort(RNG.standard_normal((H8, 2048, 4)), axis=-1).astype(np.float16)
+    vup = np.full((H8, 2048), 1.2, np.float16)
+    kt = NuqLayerTables(_t(kpol, dev), _t(kup, dev), _t(-kup, dev), per_token=False)
+    vt = NuqLayerTables(_t(vpol, dev), _t(vup, dev), _t(-vup, dev), per_token=True)
+    kside = PagedSide.empty(NB, H8, 4, 256, dev, stats=True, n_chunks=NB * H8)
+    vside = PagedSide.empty(NB, H8, 2, 256, dev, n_chunks=NB * H8)
+    kp = O.paged_empty(NB, H8, D, 4, 256, stats=True)
+    o = 0
+    for b, (T, P) in enumerate(zip(lens, pages)):
+        bt[b, :P] = perm[o:o + P]
+        o += P
+        slots = bt[b, np.arange(T) // PS] * PS + np.arange(T) % PS
+        k = (RNG.standard_t(3, (T, H8, D)) * 0.7).astype(np.float16)
+        v = (RNG.standard_t(3, (T, H8, D)) * 0.7).astype(np.float16)
+        paged_write(kside, _t(k, dev), kt, _t(slots, dev))
+        paged_write(vside, _t(v, dev), vt, _t(slots, dev), _t(np.arange(T), dev))
+        O.paged_write(kp, k, slots, [kpol.astype(np.float32), kup.astype(np.float32),
+                                     (-kup).astype(np.float32)], False)
+    q = RNG.standard_normal((len(lens), H8 * group, D)).astype(np.float16)
+    qd, btd = _t(q, dev), _t(bt, dev)
+    sel, rows, scores = paged_select_ragged(qd, kside, btd, lens, top_k, sinks)
+    sel, scores = sel.cpu().numpy(), scores.cpu().numpy()
+    p0 = 0
+    for b, P in enumerate(pages):
+        mn, mx = O.h2f(kp["kmin"][bt[b, :P]]), O.h2f(kp["kmax"][bt[b, :P]])
+        want = O.page_bound_group(q[b], mn, mx, group)
+        assert np.array_equal(scores[:, p0:p0 + P], want.T), b
+        assert np.array_equal(sel[rows[b]:rows[b + 1]], O.topk_sinks(want, top_k[b], sinks)), b
+        p0 += P
+    for select in ("union", "per_head"):
+        got = paged_decode_step_batch(qd, kside, kt, vside, vt, btd, lens, top_k, sinks, gqa="sum",
+                                      select=select, pages_per_split=7)
+        for b, (T, P) in enumerate(zip(lens, pages)):
+            want = paged_decode_step(qd[b], kside, kt, vside, vt, btd[b, :P], T, top_k[b], sinks, gqa="sum",
+                                     select=select, pages_per_split=7)
+            assert torch.equal(got[b], want), (select, b)
