@@ -1835,8 +1835,10 @@ int page_bound(const void* q, int q_dtype, int Hq, const void* kmin, const void*
   if (lds > 64 * 1024) return HKV_ERR_SHAPE;
   const int G = D / 8;
   // (the fp16 kernel indexes elements r * D in 32 bits; with page ids, a lane's
-  // head must be fixed and the statistics' rows too must fit)
-  const bool hfix = G <= 64 && G > 0 && (64 / G) % H == 0;
+  // head must be fixed and the statistics' rows too must fit).  A lane's head
+  // is fixed when the heads divide the rows of a block's row group (256 / G):
+  // the lane keeps its row of every group.
+  const bool hfix = G <= 64 && G > 0 && (256 / G) % H == 0;
   if ((!page_ids || (hfix && page_ids && nstat * H * D < ((int64_t)1 << 31))) &&
       k_dtype == HKV_DT_F16 && D % 8 == 0 && (G & (G - 1)) == 0 && G <= 64 &&
       rows * D < ((int64_t)1 << 32)) {
@@ -2118,7 +2120,7 @@ int page_bound_u8(const void* q, int q_dtype, int Hq, const uint8_t* kmin, const
   if (!fdt(q_dtype) && q_dtype != HKV_DT_BF16) return HKV_ERR_DTYPE;
   if (P < 0 || H < 1 || D < 8 || D % 8 || Hq < H || Hq % H) return HKV_ERR_SHAPE;
   const int G = D / 8;
-  if ((G & (G - 1)) || G > 64 || (64 / G) % H) return HKV_ERR_SHAPE;
+  if ((G & (G - 1)) || G > 64 || (256 / G) % H) return HKV_ERR_SHAPE;  // a lane's head fixed
   if (P * H * D >= ((int64_t)1 << 32) || P * H >= ((int64_t)1 << 31)) return HKV_ERR_SHAPE;
   if (P == 0) return HKV_OK;
   if (!q || !kmin || !kmax || !lo || !step || !out) return HKV_ERR_ARG;
@@ -2492,9 +2494,8 @@ int select_ragged(const void* q, int q_dtype, int B, int Hq, const void* kmin, c
   const unsigned gx = (unsigned)sg.blk[B];
   const int64_t q_bytes = (int64_t)Hq * D * (q_dtype == HKV_DT_F32 ? 4 : 2);
   // a lane's head is fixed when the heads divide the rows of a block's row
-  // group (256 / G): a lane keeps its row of every group; the compact path
-  // keeps the stricter wave rule it was measured with
-  const bool hfix = bt ? true : (64 / G) % H == 0;
+  // group (256 / G): a lane keeps its row of every group
+  const bool hfix = (256 / G) % H == 0;
   auto mn = (const uint16_t*)kmin;
   auto mx = (const uint16_t*)kmax;
   const int group = Hq / H;

@@ -45,7 +45,8 @@ def test_page_stats_vs_oracle(dev, dt, P, S, H, D):
 @pytest.mark.parametrize("kdt", [np.float16, np.float32])
 @pytest.mark.parametrize("P,H,D,g", [(512, 4, 128, 1), (300, 4, 128, 7), (77, 2, 32, 1),
                                      (50, 3, 128, 2), (33, 5, 64, 1),
-                                     (40, 1, 20, 3), (16, 2, 8, 1)])
+                                     (40, 1, 20, 3), (16, 2, 8, 1),
+                                     (200, 8, 128, 2), (101, 16, 128, 1)])
 def test_bound_bit_exact_vs_oracle(dev, kdt, P, H, D, g):
     from helix_kv.ops import quest_page_bound
 
@@ -157,6 +158,9 @@ def test_fused_select_small_and_per_kv_head(dev):
     # more slice blocks than CUs: the two-kernel form (threshold by the last block, then a write kernel)
     (40960, 64, 1, 10240, 4, "normal", 8),     # 5 slices x 64 heads
     (540000, 16, 2, 135000, 4, "normal", 32),  # 17 slices of 32768 x 16 heads (KPT 32)
+    # 8 and 16 KV heads at head dim 128: a bound lane keeps its head (the heads divide a block's rows)
+    (65536, 8, 4, 16384, 4, "normal"),
+    (20000, 16, 2, 5000, 4, "normal"),
 ]])
 def test_multiblock_select_vs_oracle(dev, P, H, g, k, s, mode, D):
     """The multi-block top-K (fp16 statistics, large columns) against the
@@ -197,6 +201,7 @@ def test_multiblock_select_vs_oracle(dev, P, H, g, k, s, mode, D):
     (40000, 4, 1, 100, 0, "heavy", np.float16),      # Student-t tails: wide ranges, dense bins
     (300, 1, 3, 50, 2, "const", np.float16),         # constant channels (step 1, codes 0)
     (5000, 4, 7, 1000, 4, "nonfinite", np.float16),  # NaN / inf statistics code as the full range
+    (20000, 8, 4, 5000, 4, "normal", np.float16),    # 8 KV heads
 ])
 def test_u8_metadata_select_vs_oracle(dev, P, H, g, k, s, mode, dt):
     """Compact u8 page metadata: the conversion bit-exact against the oracle,
