@@ -1117,6 +1117,7 @@ HKV_DEV uint4 mb_excl_scan4(uint4 v, uint4* red) {
 HKV_DEV void wait_stores() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 constexpr uint32_t kMBStage = 8192;     // pages staged in LDS per round of the ordered write
+constexpr uint32_t kMBSpan = (1u << 27) - 1u;  // ordered keys the histogram bins span at most
 constexpr int kMBSpinLimit = 1 << 22;   // polls of the fused form's wait for a head's slices
 
 // Block j's part of the output: the selected pages of slice j -- every key
@@ -1224,6 +1225,13 @@ topk_mb_hist(const float* scores, int64_t P, int64_t s, int64_t keff, int64_t* o
   }
   for (int b = tid; b < kMBBins; b += kMBThreads) sh.hist[b] = 0u;  // ordered by mb_minmax's barriers
   mb_minmax(mn, mx, sh.red);
+  // Bins over at most the top kMBSpan ordered keys below the largest (16
+  // binades of one sign): a few keys far below the rest (a bound of the
+  // other sign lies about 2^31 keys away) would otherwise put most keys in
+  // the threshold's bin and send the selection to the single-block
+  // fallback.  Keys below the range share bin 0, whose key range is then
+  // open below.
+  if (mx - mn > kMBSpan) mn = mx - kMBSpan;
   const uint32_t range = mx - mn;
   const int wbits = range ? 32 - __builtin_clz(range) : 0;
   const int sh1 = wbits > 12 ? wbits - 12 : 0;
@@ -1515,10 +1523,11 @@ topk_mb_hist(const float* scores, int64_t P, int64_t s, int64_t keff, int64_t* o
     __syncthreads();
   }
   const uint32_t r = need - above1;  // 1 <= r <= cnt1
-  const uint32_t lo1 = mn + (b1 << sh1);
+  const uint32_t lo1b = mn + (b1 << sh1);  // first key of bin b1's range
   // last key of bin b1, saturated (the top bin can end past 2^32 - 1)
-  const uint64_t hi1w = (uint64_t)lo1 + ((1ull << sh1) - 1ull);
+  const uint64_t hi1w = (uint64_t)lo1b + ((1ull << sh1) - 1ull);
   const uint32_t hi1 = hi1w > 0xffffffffull ? 0xffffffffu : (uint32_t)hi1w;
+  const uint32_t lo1 = b1 == 0 ? 0u : lo1b;  // bin 0 also holds the keys below the range
   if (cnt1 > (uint32_t)kMBCand) {
     // a huge bin: the single-block selector over the whole column (block 0
     // of the head in the fused form)

@@ -161,6 +161,11 @@ def test_fused_select_small_and_per_kv_head(dev):
     # 8 and 16 KV heads at head dim 128: a bound lane keeps its head (the heads divide a block's rows)
     (65536, 8, 4, 16384, 4, "normal"),
     (20000, 16, 2, 5000, 4, "normal"),
+    # a few bounds of the other sign (2^31 ordered keys below the rest): bins over the top 2^27 keys,
+    # the threshold inside them, or (nearly every page kept) in bin 0, open below
+    (65536, 4, 4, 16384, 4, "signs"),
+    (65536, 4, 4, 65530, 4, "signs"),
+    (65536, 2, 7, 30000, 0, "signs"),
 ]])
 def test_multiblock_select_vs_oracle(dev, P, H, g, k, s, mode, D):
     """The multi-block top-K (fp16 statistics, large columns) against the
@@ -179,6 +184,9 @@ def test_multiblock_select_vs_oracle(dev, P, H, g, k, s, mode, D):
     else:
         mn = RNG.standard_normal((P, H, D)).astype(np.float16)
         mx = (mn + np.abs(RNG.standard_normal((P, H, D))).astype(np.float16)).astype(np.float16)
+    if mode == "signs":  # pages whose bound is +-8 x the group's query sum: bounds of both signs
+        mn[100:102] = mx[100:102] = -8.0
+        mn[102:104] = mx[102:104] = 8.0
     if mode == "nan":  # 300 pages whose bound is NaN
         bad = RNG.choice(P, 300, replace=False)
         mn[bad, :, 5] = np.nan
